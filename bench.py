@@ -1,0 +1,314 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized matrix-product path on one MI355X.
+
+One step = one int8 GEMM C += A.B at M = N = K = 4096 (i.i.d. uniform int8 inputs, seed 2026),
+inputs resident in HBM.  `value` is TOPS = 2*M*N*K / time over `--steps` back-to-back launches
+timed with HIP events on the launch stream.  The same JSON line carries:
+  roofline      the GEMM kernel against the dense int8 MFMA peak (5.0 POPS), plus the HBM bytes
+                per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/ (if any);
+  cpu_baseline  the reference's scalar gemm_ref_i8 (built from its sources into oracle/_ref, or the
+                oracle's restatement when that is absent) on a bounded row sample, 1 core;
+  extra         the other measured shapes: skinny 8x4096x4096 GEMM, Q4_0 / Q4_K / Q3_K GEMV at
+                M = 1 and 4, the Qwen3-30B-A3B MoE decode layer at M = 1 and 4, each beside its
+                scalar CPU time.  GEMV and MoE run back-to-back in a captured graph over weight
+                copies totalling more than 256 MB (so the 256 MB Infinity Cache cannot hold them);
+                single-launch latency is reported separately.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "x100-gemm_amd"))
+
+import synth  # noqa: E402
+import x100hip  # noqa: E402
+
+METRIC = "int8 GEMM TOPS; Q4/Q3_K GEMV GB/s (% HBM peak); MoE decode layer µs"
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def read_traffic(kernel_key):
+    """HBM bytes per launch for a kernel from profiles/traffic.txt ("key bytes" lines)."""
+    path = os.path.join(ROOT, "profiles", "traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) >= 2 and parts[0] == kernel_key:
+            try:
+                return float(parts[1])
+            except ValueError:
+                return None
+    return None
+
+
+class Timer:
+    """HIP events on the current (launch) stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, reps, warm):
+        t = self.torch
+        for _ in range(warm):
+            fn()
+        t.cuda.synchronize()
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        t.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps   # microseconds per call
+
+    def graph(self, fns, replays=3):
+        """Capture fns back to back in one graph; microseconds per fn, averaged over replays."""
+        t = self.torch
+        for f in fns[:2]:
+            f()
+        t.cuda.synchronize()
+        g = t.cuda.CUDAGraph()
+        side = t.cuda.Stream()
+        with t.cuda.stream(side):
+            with t.cuda.graph(g, stream=side):
+                for f in fns:
+                    f()
+        t.cuda.synchronize()
+        g.replay()
+        t.cuda.synchronize()
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        t.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (replays * len(fns))
+
+    def single(self, fn, reps=10):
+        """Isolated-launch latency: synchronise around every call."""
+        t = self.torch
+        best = []
+        for _ in range(reps):
+            t.cuda.synchronize()
+            e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            t.cuda.synchronize()
+            best.append(e0.elapsed_time(e1) * 1e3)
+        return float(np.median(best))
+
+
+# ------------------------------------------------------------------------------------------------
+# CPU baseline (oracle / reference build; the checker, never the product)
+# ------------------------------------------------------------------------------------------------
+def cpu_gemm_baseline(K=4096, N=4096, target_s=10.0):
+    import oracle_lib as ol
+    ref = ol.reference()
+    kind = "reference" if ref is not None else "port"
+    fn = ref.gemm_ref_i8 if ref is not None else ol.oracle().gemm_ref_i8
+    A, B = synth.gemm_inputs(4096, N, K, seed=2026)
+
+    def run(rows):
+        C = np.zeros((rows, N), np.int32)
+        t0 = time.perf_counter()
+        fn(rows, N, K, A.ctypes.data, B.ctypes.data, C.ctypes.data)
+        return time.perf_counter() - t0
+
+    probe_rows = 8
+    t = run(probe_rows)
+    rows = int(max(probe_rows, min(4096, probe_rows * target_s / max(t, 1e-6))))
+    t = run(rows)
+    tops = 2.0 * rows * N * K / t / 1e12
+    return {"value": tops, "unit": "TOPS", "cores": 1, "kind": kind,
+            "sample": "gemm_ref_i8 on rows 0..%d of the 4096^3 workload (%.1f s, nproc=%d)" % (
+                rows, t, os.cpu_count() or 0)}
+
+
+def cpu_time(fn, min_s=0.5):
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            return dt / n * 1e6   # microseconds
+
+
+# ------------------------------------------------------------------------------------------------
+def bench_gemm(torch, timer, dev, args):
+    M = N = K = 4096
+    A, B = synth.gemm_inputs(M, N, K, seed=2026)
+    dA = torch.from_numpy(A).to(dev)
+    dB = torch.from_numpy(B).to(dev)
+    dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    ops = 2.0 * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+    log("gemm 4096^3: %.2f us/launch  %.1f TOPS  (wall %.3f s for %d steps)" % (ms * 1e3, tops, wall, args.steps))
+    traffic = read_traffic("gemm_i8_4096")
+    roof = {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+            "frac": tops / PEAK_INT8_TOPS, "traffic": traffic,
+            "kernel": "k_gemm_mfma<4,4,2,2> (256x256 tile)", "algorithmic_ops_per_launch": ops}
+    return ms, tops, roof
+
+
+def bench_extra(torch, timer, dev, args):
+    import oracle_lib as ol
+    extra = {}
+    s = torch.cuda.current_stream().cuda_stream
+
+    # ---- skinny speculative-verify GEMM -------------------------------------------------------
+    M, N, K = 8, 4096, 4096
+    A, B = synth.gemm_inputs(M, N, K, seed=2027)
+    dA, dB = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    nb = 16
+    dBs = torch.stack([torch.roll(dB, i, 0) for i in range(nb)])   # 16 x 16 MB copies
+    dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    fns = [lambda i=i: x100hip.gemm_dev(M, N, K, dA.data_ptr(), dBs[i].data_ptr(), dC.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream) for i in range(nb)]
+    us = timer.graph(fns)
+    lat = timer.single(fns[0])
+    byts = M * K + K * N + 2 * M * N * 4
+    Cc = np.zeros((M, N), np.int32)
+    cpu_us = cpu_time(lambda: ol.oracle().gemm_ref_i8(M, N, K, A.ctypes.data, B.ctypes.data, Cc.ctypes.data))
+    extra["gemm_i8_8x4096x4096"] = {"us": us, "TOPS": 2.0 * M * N * K / us / 1e6, "GB/s": byts / us / 1e3,
+                                    "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS, "single_launch_us": lat,
+                                    "cpu_us_1core": cpu_us}
+    log("gemm 8x4096x4096: %.2f us  %.0f GB/s (single %.2f us)" % (us, byts / us / 1e3, lat))
+    del dBs
+
+    # ---- dequant GEMV ---------------------------------------------------------------------------
+    for qt, name, N, K in [(synth.Q4_0, "q4_0", 4096, 4096), (synth.Q4_K, "q4_K", 6144, 2048),
+                           (synth.Q3_K, "q3_K", 6144, 2048)]:
+        W = synth.quant_weight(qt, N, K, seed=100 + qt)
+        raw = torch.from_numpy(W.view(np.uint8).reshape(-1)).to(dev)
+        pb = x100hip.packed_bytes(qt, N, K)
+        copies = int(300e6 // pb) + 1
+        packs = torch.empty((copies, (pb + 255) // 256 * 256), dtype=torch.uint8, device=dev)
+        for i in range(copies):
+            x100hip.pack(qt, N, K, raw.data_ptr(), packs[i].data_ptr(), s)
+        for M in (1, 4):
+            x = synth.normal_f32(7 + M, (M, K))
+            dx = torch.from_numpy(x).to(dev)
+            dy = torch.empty((M, N), dtype=torch.float32, device=dev)
+            fns = [lambda i=i: x100hip.qgemv(qt, M, N, K, packs[i].data_ptr(), dx.data_ptr(), dy.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream) for i in range(copies)]
+            us = timer.graph(fns)
+            lat = timer.single(fns[0])
+            byts = raw.numel() + M * K * 4 + M * N * 4
+            cpu_us = cpu_time(lambda: ol.qgemv(qt, W, x))
+            key = "%s_gemv_%dx%d_m%d" % (name, N, K, M)
+            extra[key] = {"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                          "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
+                          "cpu_us_1core": cpu_us}
+            log("%s: %.2f us  %.0f GB/s  (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
+                key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
+        del packs, raw
+
+    # ---- MoE decode layer ----------------------------------------------------------------------
+    n_exp, d, ff, n_act = 128, 2048, 768, 8
+    Wg, Wu, Wd = synth.moe_weights(n_exp, d, ff, seed=500)
+    R = synth.moe_router(n_exp, d, seed=501)
+    layers = []
+    base = [torch.from_numpy(np.ascontiguousarray(w).view(np.uint8).reshape(-1)).to(dev) for w in (Wg, Wu, Wd)]
+    for li in range(3):   # 3 layers x 340 MB of experts: well beyond the 256 MB Infinity Cache
+        layers.append([b.clone() for b in base] if li else base)
+    dR = torch.from_numpy(R).to(dev)
+    n_h = 48
+    for M in (1, 4):
+        hns = synth.normal_f32(900 + M, (n_h, M, d))
+        dh = torch.from_numpy(hns).to(dev)
+        out = torch.empty((M, d), dtype=torch.float32, device=dev)
+        sel = torch.empty((n_h, M, n_act), dtype=torch.int32, device=dev)
+
+        def call(i, with_sel=False):
+            L = layers[i % 3]
+            x100hip.moe_layer(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
+                              L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False,
+                              sel[i].data_ptr() if with_sel else None, None,
+                              torch.cuda.current_stream().cuda_stream)
+
+        for i in range(n_h):
+            call(i, True)
+        torch.cuda.synchronize()
+        U = np.array([len(set(r.ravel().tolist())) for r in sel.cpu().numpy()])
+        us = timer.graph([lambda i=i: call(i) for i in range(n_h)])
+        lat = timer.single(lambda: call(0))
+        byts = float(n_exp * d * 4 + U.mean() * 3 * (ff * d // 256 * 144) + M * d * 4 * 2)
+        cpu_us = cpu_time(lambda: ol.moe_layer(hns[0], R, Wg, Wu, Wd, n_act), min_s=0.3)
+        key = "moe_layer_qwen3_30b_a3b_m%d" % M
+        extra[key] = {"us_per_layer": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                      "single_launch_us": lat, "experts_union_mean": float(U.mean()),
+                      "bytes_per_layer": byts, "cpu_us_1core": cpu_us}
+        log("%s: %.2f us/layer  U=%.1f  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
+            key, us, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
+    return extra
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this backend has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import torch
+
+    dev = torch.device("cuda:0")
+    x100hip.lib()
+    caps = x100hip.caps()
+    if not caps.is_gfx950:
+        raise SystemExit("not a gfx950 device: %s" % caps.arch.decode())
+    timer = Timer(torch)
+    ms, tops, roof = bench_gemm(torch, timer, dev, args)
+    extra = {} if args.no_extra else bench_extra(torch, timer, dev, args)
+    cpu = None if args.no_cpu else cpu_gemm_baseline()
+    line = {
+        "metric": METRIC, "value": tops, "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 (int32 accumulate)", "data": "synthetic (seeded uniform int8)",
+        "config": {"workload": "int8 GEMM C += A.B, M=N=K=4096, row-major, int32 out",
+                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
+        "roofline": roof, "cpu_baseline": cpu, "extra": extra,
+        "device": {"name": caps.name.decode(), "arch": caps.arch.decode(), "cus": caps.cu_count},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

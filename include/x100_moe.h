@@ -1,0 +1,37 @@
+/*
+ * x100_moe.h -- Qwen3-MoE decode layer entry point of libx100hip (gfx950).
+ *
+ * The FFN block of the reference's forward() (qwen_moe.c:294-311; qwen_moe_hp.c:1512-1570) for
+ * M <= 8 token rows (decode or speculative verify), one call per layer:
+ *   logits = R . hn (fp32), softmax over all n_exp experts, top-n_act (ties -> lower expert id),
+ *   renormalised weights; for each selected expert: g = Wg[e].hn, u = Wu[e].hn, act = silu(g)*u,
+ *   y = Wd[e].act; out = sum_a w_a * y_a  (plus out's old value when residual != 0).
+ * Experts are Q4_K blocks in the ggml 3-D layout, experts outermost (qwen_moe.c:220-222):
+ *   Wg, Wu: [n_exp][ff][d/256] blocks, Wd: [n_exp][d][ff/256] blocks.
+ * Activations are quantized to Q8_K per row (hn before gate/up, act before down) with the
+ * scalar path's rounding; rows that pick the same expert share one pass over its weights.
+ *
+ * All pointers are device pointers.  sel / sw (may be NULL) receive [M][n_act] expert ids and
+ * renormalised weights.  Limits: 1 <= M <= 8, 1 <= n_act <= 8, n_act <= n_exp <= 256,
+ * d % 256 == 0, ff % 256 == 0, d <= 4096, ff <= 4096.  The library keeps a device workspace per
+ * GPU (allocated on the first call with a given shape); calls that overlap on one GPU must use
+ * the same stream.
+ */
+#ifndef X100_HIP_MOE_H
+#define X100_HIP_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int moe_layer_hip(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                  const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
+                  int *sel, float *sw, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

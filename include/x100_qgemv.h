@@ -1,0 +1,53 @@
+/*
+ * x100_qgemv.h -- block-quantized dequant-GEMV entry points of libx100hip (gfx950).
+ *
+ * y[M][N] = W[N][K] . x[M][K]^T for M <= 8 token rows, W in ggml block formats, x and y fp32.
+ * Each x row is quantized inside the call (Q8_0 for Q4_0 weights, Q8_K for Q4_K / Q3_K) with the
+ * scalar path's rounding (quantize_q8_0_native, reference qwen_moe_hp.c:408-414; pack_A_q3k,
+ * qwen_moe_q3k.c:612-624), each block's dot product is exact integer arithmetic, and the result
+ * is scaled in fp32.
+ *
+ * Replaces the reference's per-linear matmul `lin_mm(const Lin*, const float *x, float *y, ...)`
+ * (qwen_moe.c:101-107, qwen_moe_hp.c:712-718) and the vendor kernel family
+ * `gemm_kernel_i8i4* / i8i3k*` (reference/spacemit-backend/ime2_kernels.cpp:127-436): weights are
+ * repacked once at load (as the vendor backend repacks in repack.cpp), then every call streams
+ * them from HBM.
+ *
+ * All pointers are device pointers; stream is a hipStream_t passed as void* (NULL = default).
+ */
+#ifndef X100_HIP_QGEMV_H
+#define X100_HIP_QGEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (reference bench/gguf_dump.c:12-13). */
+#define X100_Q4_0  2
+#define X100_Q3_K 11
+#define X100_Q4_K 12
+
+/* Bytes of N rows x K columns in GGUF-native blocks (Q4_0 18 B / 32, Q4_K 144 B / 256,
+ * Q3_K 110 B / 256); 0 for an unsupported type or K not a multiple of the block size. */
+size_t x100q_gguf_bytes(int qtype, int N, int K);
+
+/* Bytes of the device layout produced by x100q_pack. */
+size_t x100q_packed_bytes(int qtype, int N, int K);
+
+/* Repack GGUF-native blocks (device pointer w_gguf, row n at n*row_bytes) into the device
+ * layout used by qgemv_hip (w_packed, x100q_packed_bytes bytes).  Done once per weight, like the
+ * reference's load-time repack (repack.cpp:292, 452, 928). */
+int x100q_pack(int qtype, int N, int K, const void *w_gguf, void *w_packed, void *stream);
+
+/* y[M][N] = W . x^T.  1 <= M <= 8; K % 32 == 0 (Q4_0) or K % 256 == 0 (K-quants); x 16-byte
+ * aligned.  Asynchronous on stream. */
+int qgemv_hip(int qtype, int M, int N, int K, const void *w_packed, const float *x, float *y,
+              void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

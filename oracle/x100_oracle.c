@@ -1,0 +1,584 @@
+/*
+ * x100_oracle.c -- CPU restatement of the reference's quantized matrix-product path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see x100_oracle.h).  Built with -ffp-contract=off so that every
+ * fp32 expression rounds after each operation, exactly as written.
+ */
+#include "x100_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------------------------------------
+ * fp16 helpers
+ * ------------------------------------------------------------------------------------------- */
+
+/* Round-to-nearest-even fp32 -> fp16.  Replaces the truncating f32_to_f16 of
+ * qwen_moe_hp.c:71-79 (see header).  Checked against numpy.float16 in tests/test_oracle.py. */
+uint16_t orc_f32_to_f16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) {                       /* inf / nan */
+        if (ax == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+        return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    }
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   /* >= 65520 rounds to inf */
+    if (ax < 0x38800000u) {                        /* below 2^-14: fp16 subnormal or zero */
+        if (ax < 0x33000000u) return (uint16_t)sign;            /* <= 2^-25 rounds to 0 */
+        uint32_t e = ax >> 23;
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - e;                 /* value / 2^-24 = m >> shift */
+        uint32_t r = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (r & 1u))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = (ax >> 13) - ((127u - 15u) << 10);
+    uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+    return (uint16_t)(sign | r);
+}
+
+/* Exact fp16 -> fp32; same decoding as f16_to_f32 in qwen_moe_hp.c:80-86 and f16f in
+ * qwen_moe.c:115-118. */
+float orc_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu, bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do { e++; mant <<= 1; } while (!(mant & 0x400u));
+            mant &= 0x3ffu;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp - 15u + 127u) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * int8 GEMM
+ * ------------------------------------------------------------------------------------------- */
+
+/* src/gemm_ref.c:17-26: i-k-j order, C += A*B, int32 accumulate. */
+void gemm_ref_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C)
+{
+    for (int i = 0; i < M; i++)
+        for (int k = 0; k < K; k++) {
+            int32_t a = A[(size_t)i * K + k];
+            const int8_t *b = &B[(size_t)k * N];
+            int32_t *c = &C[(size_t)i * N];
+            for (int j = 0; j < N; j++) c[j] += a * (int32_t)b[j];
+        }
+}
+
+void orc_gemm_i8_mt(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
+                    int nthreads)
+{
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int i = 0; i < M; i++)
+        for (int k = 0; k < K; k++) {
+            int32_t a = A[(size_t)i * K + k];
+            const int8_t *b = &B[(size_t)k * N];
+            int32_t *c = &C[(size_t)i * N];
+            for (int j = 0; j < N; j++) c[j] += a * (int32_t)b[j];
+        }
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * Block formats (Appendix of the block-format layouts used by ggml; reference restatements at
+ * qwen_moe_hp.c:98, qwen_moe_q3k.c:531, repack.cpp:222-233)
+ * ------------------------------------------------------------------------------------------- */
+
+typedef struct { uint16_t d; uint8_t qs[16]; } orc_q4_0;                       /*  18 B */
+typedef struct { uint16_t d; int8_t qs[32]; } orc_q8_0;                        /*  34 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } orc_q4_K; /* 144 B */
+typedef struct { uint8_t hmask[32]; uint8_t qs[64]; uint8_t scales[12]; uint16_t d; } orc_q3_K; /* 110 B */
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } orc_q8_K;        /* 292 B */
+
+size_t orc_block_bytes(int qtype)
+{
+    switch (qtype) {
+    case ORC_Q4_0: return sizeof(orc_q4_0);
+    case ORC_Q8_0: return sizeof(orc_q8_0);
+    case ORC_Q4_K: return sizeof(orc_q4_K);
+    case ORC_Q3_K: return sizeof(orc_q3_K);
+    case ORC_Q8_K: return sizeof(orc_q8_K);
+    default: return 0;
+    }
+}
+
+int orc_block_elems(int qtype)
+{
+    switch (qtype) {
+    case ORC_Q4_0: case ORC_Q8_0: return 32;
+    case ORC_Q4_K: case ORC_Q3_K: case ORC_Q8_K: return 256;
+    default: return 0;
+    }
+}
+
+size_t orc_row_bytes(int qtype, int K)
+{
+    int qk = orc_block_elems(qtype);
+    if (qk == 0 || K % qk) return 0;
+    return (size_t)(K / qk) * orc_block_bytes(qtype);
+}
+
+/* get_scale_min_k4 (repack.cpp:222-233; same unpack as q5k_get_scale_min, qwen_moe_q3k.c:534-537). */
+static void scale_min_k4(int j, const uint8_t *q, int *sc, int *m)
+{
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* Q3_K 6-bit scale unpack exactly as dequantize_q3_K_block does it (qwen_moe_q3k.c:559-563):
+ * bytes 0..11 viewed as three little-endian u32, low nibbles + 2-bit high parts. */
+static void q3k_scales(const uint8_t *s12, int8_t out[16])
+{
+    const uint32_t kmask1 = 0x03030303u, kmask2 = 0x0f0f0f0fu;
+    uint32_t aux[4];
+    memcpy(aux, s12, 12);
+    uint32_t tmp = aux[2];
+    aux[2] = ((aux[0] >> 4) & kmask2) | (((tmp >> 4) & kmask1) << 4);
+    aux[3] = ((aux[1] >> 4) & kmask2) | (((tmp >> 6) & kmask1) << 4);
+    aux[0] = (aux[0] & kmask2) | (((tmp >> 0) & kmask1) << 4);
+    aux[1] = (aux[1] & kmask2) | (((tmp >> 2) & kmask1) << 4);
+    memcpy(out, aux, 16);
+}
+
+/* Q3_K element value index helpers (qwen_moe_q3k.c:565-575): element e = 128*h + 32*j + l
+ * (h in 0..1, j in 0..3, l in 0..31) takes bits (2j, 2j+1) of qs[32h + l], the high bit from
+ * hmask[l] bit (4h + j) (set -> +0, clear -> -4), and sub-block scale index 8h + 2j + l/16. */
+static int q3k_value(const orc_q3_K *b, int e)
+{
+    int h = e >> 7, j = (e >> 5) & 3, l = e & 31;
+    int lo = (b->qs[32 * h + l] >> (2 * j)) & 3;
+    int hb = (b->hmask[l] >> (4 * h + j)) & 1;
+    return lo - (hb ? 0 : 4);
+}
+
+int orc_dequant_row(int qtype, const void *blocks, int K, float *out)
+{
+    int qk = orc_block_elems(qtype);
+    if (qk == 0 || K % qk) return -1;
+    int nb = K / qk;
+    switch (qtype) {
+    case ORC_Q4_0: {                                   /* qwen_moe.c:164-165 */
+        const orc_q4_0 *b = (const orc_q4_0 *)blocks;
+        for (int ib = 0; ib < nb; ib++) {
+            float d = orc_f16_to_f32(b[ib].d);
+            for (int j = 0; j < 32; j++) {
+                int nib = (j < 16) ? (b[ib].qs[j] & 0xf) : (b[ib].qs[j - 16] >> 4);
+                out[ib * 32 + j] = (float)(nib - 8) * d;
+            }
+        }
+        return 0;
+    }
+    case ORC_Q8_0: {                                   /* qwen_moe.c:162-163 */
+        const orc_q8_0 *b = (const orc_q8_0 *)blocks;
+        for (int ib = 0; ib < nb; ib++) {
+            float d = orc_f16_to_f32(b[ib].d);
+            for (int j = 0; j < 32; j++) out[ib * 32 + j] = (float)b[ib].qs[j] * d;
+        }
+        return 0;
+    }
+    case ORC_Q4_K: {                                   /* repack.cpp:950-970 decode */
+        const orc_q4_K *b = (const orc_q4_K *)blocks;
+        for (int ib = 0; ib < nb; ib++) {
+            float d = orc_f16_to_f32(b[ib].d), dmin = orc_f16_to_f32(b[ib].dmin);
+            for (int j = 0; j < 8; j++) {
+                int sc, m;
+                scale_min_k4(j, b[ib].scales, &sc, &m);
+                float d1 = d * (float)sc, m1 = dmin * (float)m;
+                const uint8_t *q = b[ib].qs + 32 * (j / 2);
+                for (int l = 0; l < 32; l++) {
+                    int nib = (j & 1) ? (q[l] >> 4) : (q[l] & 0xf);
+                    out[ib * 256 + 32 * j + l] = d1 * (float)nib - m1;
+                }
+            }
+        }
+        return 0;
+    }
+    case ORC_Q3_K: {                                   /* qwen_moe_q3k.c:557-577 */
+        const orc_q3_K *b = (const orc_q3_K *)blocks;
+        for (int ib = 0; ib < nb; ib++) {
+            int8_t sc[16];
+            q3k_scales(b[ib].scales, sc);
+            float dall = orc_f16_to_f32(b[ib].d);
+            for (int e = 0; e < 256; e++) {
+                int is = 8 * (e >> 7) + 2 * ((e >> 5) & 3) + ((e & 31) >> 4);
+                float dl = dall * (float)(sc[is] - 32);
+                out[ib * 256 + e] = dl * (float)q3k_value(&b[ib], e);
+            }
+        }
+        return 0;
+    }
+    case ORC_Q8_K: {
+        const orc_q8_K *b = (const orc_q8_K *)blocks;
+        for (int ib = 0; ib < nb; ib++)
+            for (int j = 0; j < 256; j++) out[ib * 256 + j] = (float)b[ib].qs[j] * b[ib].d;
+        return 0;
+    }
+    }
+    return -1;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * Quantizers
+ * ------------------------------------------------------------------------------------------- */
+
+/* quantize_q8_0_native, qwen_moe_hp.c:408-414 (fp16 d rounded to nearest even). */
+void orc_quantize_q8_0(const float *x, int K, void *out)
+{
+    orc_q8_0 *b = (orc_q8_0 *)out;
+    for (int ib = 0; ib < K / 32; ib++) {
+        const float *w = x + (size_t)ib * 32;
+        float amax = 1e-6f;
+        for (int i = 0; i < 32; i++) {
+            float v = fabsf(w[i]);
+            if (v > amax) amax = v;
+        }
+        float d = amax / 127.0f;
+        float inv = d ? 1.0f / d : 0.0f;
+        b[ib].d = orc_f32_to_f16(d);
+        for (int i = 0; i < 32; i++) {
+            int q = (int)rintf(w[i] * inv);
+            if (q > 127) q = 127;
+            if (q < -128) q = -128;
+            b[ib].qs[i] = (int8_t)q;
+        }
+    }
+}
+
+/* pack_A_q3k, qwen_moe_q3k.c:612-624 (fp32 scale amax/127, roundf, clamp, 16-element sums),
+ * all-zero block as rvv_kernels.cpp:1820-1828.  Stored in ggml order with positive sums. */
+void orc_quantize_q8_K(const float *x, int K, void *out)
+{
+    orc_q8_K *b = (orc_q8_K *)out;
+    for (int ib = 0; ib < K / 256; ib++) {
+        const float *a = x + (size_t)ib * 256;
+        float amax = 0.0f;
+        for (int i = 0; i < 256; i++) {
+            float v = fabsf(a[i]);
+            if (v > amax) amax = v;
+        }
+        float d = amax / 127.0f;
+        float rep = d ? 1.0f / d : 0.0f;
+        b[ib].d = d;
+        for (int g = 0; g < 16; g++) {
+            int sum = 0;
+            for (int l = 0; l < 16; l++) {
+                int q = (int)roundf(a[g * 16 + l] * rep);
+                if (q > 127) q = 127;
+                if (q < -128) q = -128;
+                b[ib].qs[g * 16 + l] = (int8_t)q;
+                sum += q;
+            }
+            b[ib].bsums[g] = (int16_t)sum;
+        }
+    }
+}
+
+/* quantize_q4_0_native, qwen_moe_hp.c:100-109 (fp16 d rounded to nearest even). */
+void orc_quantize_q4_0(const float *w, int K, void *out)
+{
+    orc_q4_0 *b = (orc_q4_0 *)out;
+    for (int ib = 0; ib < K / 32; ib++) {
+        const float *x = w + (size_t)ib * 32;
+        float amax = 1e-6f;
+        for (int i = 0; i < 32; i++) {
+            float v = fabsf(x[i]);
+            if (v > amax) amax = v;
+        }
+        float d = amax / 8.0f;
+        float inv = d ? 1.0f / d : 0.0f;
+        int8_t q[32];
+        for (int i = 0; i < 32; i++) {
+            int v = (int)rintf(x[i] * inv);
+            if (v > 7) v = 7;
+            if (v < -8) v = -8;
+            q[i] = (int8_t)v;
+        }
+        b[ib].d = orc_f32_to_f16(d);
+        for (int l = 0; l < 16; l++) {
+            uint8_t lo = (uint8_t)(q[l] + 8), hi = (uint8_t)(q[l + 16] + 8);
+            b[ib].qs[l] = (uint8_t)((lo & 0xf) | ((hi & 0xf) << 4));
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * Quantized GEMV (integer dot per block, sequential fp32 combine per row)
+ * ------------------------------------------------------------------------------------------- */
+
+/* Q4_0 x Q8_0 row dot: ggml vec_dot_q4_0_q8_0 formula; nibble order of qwen_moe.c:165. */
+static float dot_q4_0_q8_0(const orc_q4_0 *w, const orc_q8_0 *x, int nb)
+{
+    float acc = 0.0f;
+    for (int ib = 0; ib < nb; ib++) {
+        int isum = 0;
+        for (int j = 0; j < 16; j++) {
+            isum += ((w[ib].qs[j] & 0xf) - 8) * x[ib].qs[j];
+            isum += ((w[ib].qs[j] >> 4) - 8) * x[ib].qs[j + 16];
+        }
+        float dd = orc_f16_to_f32(w[ib].d) * orc_f16_to_f32(x[ib].d);
+        acc = acc + (float)isum * dd;
+    }
+    return acc;
+}
+
+/* Q4_K x Q8_K row dot: y = sum_sb dx*d*sum_j sc_j*sum_l q*a - dx*dmin*sum_j m_j*(a-sum of j). */
+static float dot_q4_K_q8_K(const orc_q4_K *w, const orc_q8_K *x, int nb)
+{
+    float acc = 0.0f;
+    for (int ib = 0; ib < nb; ib++) {
+        int isc = 0, imn = 0;
+        for (int j = 0; j < 8; j++) {
+            int sc, m;
+            scale_min_k4(j, w[ib].scales, &sc, &m);
+            const uint8_t *q = w[ib].qs + 32 * (j / 2);
+            int dot = 0;
+            for (int l = 0; l < 32; l++) {
+                int nib = (j & 1) ? (q[l] >> 4) : (q[l] & 0xf);
+                dot += nib * x[ib].qs[32 * j + l];
+            }
+            isc += sc * dot;
+            imn += m * (x[ib].bsums[2 * j] + x[ib].bsums[2 * j + 1]);
+        }
+        float dd = x[ib].d * orc_f16_to_f32(w[ib].d);
+        float dm = x[ib].d * orc_f16_to_f32(w[ib].dmin);
+        acc = acc + (dd * (float)isc - dm * (float)imn);
+    }
+    return acc;
+}
+
+/* Q3_K x Q8_K row dot: y = sum_sb dx*d*sum_is (s_is-32)*sum_16 q3*a (decode of
+ * qwen_moe_q3k.c:557-577; exact integer form of gemm_kernel_i8i3k_mrow_ref,
+ * ime2_kernels.cpp:127-215, without its fp16 partial sums). */
+static float dot_q3_K_q8_K(const orc_q3_K *w, const orc_q8_K *x, int nb)
+{
+    float acc = 0.0f;
+    for (int ib = 0; ib < nb; ib++) {
+        int8_t sc[16];
+        q3k_scales(w[ib].scales, sc);
+        int sub[16] = {0};
+        for (int e = 0; e < 256; e++) {
+            int is = 8 * (e >> 7) + 2 * ((e >> 5) & 3) + ((e & 31) >> 4);
+            sub[is] += q3k_value(&w[ib], e) * x[ib].qs[e];
+        }
+        int isc = 0;
+        for (int is = 0; is < 16; is++) isc += (sc[is] - 32) * sub[is];
+        float dd = x[ib].d * orc_f16_to_f32(w[ib].d);
+        acc = acc + dd * (float)isc;
+    }
+    return acc;
+}
+
+int orc_qgemv_q(int qtype, int M, int N, int K, const void *W, const void *xq, float *y)
+{
+    size_t rb = orc_row_bytes(qtype, K);
+    if (!rb || M < 0 || N < 0) return -1;
+    int nb = K / orc_block_elems(qtype);
+    int xtype = (qtype == ORC_Q4_0) ? ORC_Q8_0 : ORC_Q8_K;
+    size_t xrb = orc_row_bytes(xtype, K);
+    for (int m = 0; m < M; m++) {
+        const uint8_t *xr = (const uint8_t *)xq + (size_t)m * xrb;
+        for (int n = 0; n < N; n++) {
+            const uint8_t *wr = (const uint8_t *)W + (size_t)n * rb;
+            float v;
+            if (qtype == ORC_Q4_0)
+                v = dot_q4_0_q8_0((const orc_q4_0 *)wr, (const orc_q8_0 *)xr, nb);
+            else if (qtype == ORC_Q4_K)
+                v = dot_q4_K_q8_K((const orc_q4_K *)wr, (const orc_q8_K *)xr, nb);
+            else if (qtype == ORC_Q3_K)
+                v = dot_q3_K_q8_K((const orc_q3_K *)wr, (const orc_q8_K *)xr, nb);
+            else
+                return -1;
+            y[(size_t)m * N + n] = v;
+        }
+    }
+    return 0;
+}
+
+int orc_qgemv(int qtype, int M, int N, int K, const void *W, const float *x, float *y)
+{
+    if (qtype != ORC_Q4_0 && qtype != ORC_Q4_K && qtype != ORC_Q3_K) return -1;
+    if (!orc_row_bytes(qtype, K)) return -1;
+    int xtype = (qtype == ORC_Q4_0) ? ORC_Q8_0 : ORC_Q8_K;
+    size_t xrb = orc_row_bytes(xtype, K);
+    uint8_t *xq = (uint8_t *)malloc(xrb * (size_t)(M > 0 ? M : 1));
+    if (!xq) return -1;
+    for (int m = 0; m < M; m++) {
+        if (xtype == ORC_Q8_0) orc_quantize_q8_0(x + (size_t)m * K, K, xq + (size_t)m * xrb);
+        else orc_quantize_q8_K(x + (size_t)m * K, K, xq + (size_t)m * xrb);
+    }
+    int rc = orc_qgemv_q(qtype, M, N, K, W, xq, y);
+    free(xq);
+    return rc;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * MoE decode layer
+ * ------------------------------------------------------------------------------------------- */
+
+/* Fixed fp32 summation order shared with the HIP kernels: 64 lane-strided partial sums (lane l
+ * takes elements 4l..4l+3, then +256, ...) and a butterfly over the 64 partials (pairs l, l^o for
+ * o = 32, 16, ..., 1).  The reference sums sequentially (qwen_moe.c:296) or with an RVV reduction
+ * (vdot_f32, qwen_moe_hp.c:881-890); the orders differ by rounding only.  n % 256 == 0. */
+static float butterfly64(float p[64])
+{
+    for (int o = 32; o > 0; o >>= 1) {
+        float q[64];
+        for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ o];
+        memcpy(p, q, sizeof q);
+    }
+    return p[0];
+}
+
+static float dot_lane64(const float *a, const float *b, int n)
+{
+    float p[64];
+    for (int l = 0; l < 64; l++) {
+        float s = 0.0f;
+        for (int k = 4 * l; k < n; k += 256) {
+            s += a[k] * b[k];
+            s += a[k + 1] * b[k + 1];
+            s += a[k + 2] * b[k + 2];
+            s += a[k + 3] * b[k + 3];
+        }
+        p[l] = s;
+    }
+    return butterfly64(p);
+}
+
+/* exp rounded once to binary32 from a binary64 evaluation (the reference calls libm expf; the
+ * two differ by at most one binary32 ulp). */
+static float exp_f32(float x) { return (float)exp((double)x); }
+
+/* softmax of qwen_moe.c:189: max-subtract, exp, multiply by 1/sum (sum in the order above, with
+ * expert e in lane e%64, slot e/64; n <= 256). */
+static void softmax_ref(float *x, int n)
+{
+    float m = -1e30f;
+    for (int i = 0; i < n; i++)
+        if (x[i] > m) m = x[i];
+    float p[64];
+    for (int l = 0; l < 64; l++) p[l] = 0.0f;
+    for (int i = 0; i < n; i++) x[i] = exp_f32(x[i] - m);
+    for (int l = 0; l < 64; l++)
+        for (int c = 0; c < 4; c++)
+            if (l + 64 * c < n) p[l] += x[l + 64 * c];
+    float s = butterfly64(p);
+    float inv = 1.0f / s;
+    for (int i = 0; i < n; i++) x[i] *= inv;
+}
+
+float orc_swiglu(float g, float u)
+{
+    float e = (float)exp(-(double)g);
+    return (g / (1.0f + e)) * u;
+}
+
+int orc_moe_route(int M, int d, int n_exp, int n_act, const float *hn, const float *R,
+                  float *logits, int *sel, float *sw)
+{
+    if (M < 0 || d <= 0 || d % 256 || n_exp <= 0 || n_exp > 256 || n_act <= 0 || n_act > n_exp) return -1;
+    float *p = (float *)malloc(sizeof(float) * (size_t)n_exp);
+    if (!p) return -1;
+    for (int m = 0; m < M; m++) {
+        const float *h = hn + (size_t)m * d;
+        for (int e = 0; e < n_exp; e++) {              /* qwen_moe.c:296 */
+            float s = dot_lane64(R + (size_t)e * d, h, d);
+            p[e] = s;
+            if (logits) logits[(size_t)m * n_exp + e] = s;
+        }
+        softmax_ref(p, n_exp);                        /* qwen_moe.c:298 */
+        int *sl = sel + (size_t)m * n_act;
+        float *wl = sw + (size_t)m * n_act;
+        for (int a = 0; a < n_act; a++) {              /* qwen_moe.c:299-300 */
+            int bi = -1;
+            float bv = -1;
+            for (int e = 0; e < n_exp; e++) {
+                int used = 0;
+                for (int b = 0; b < a; b++)
+                    if (sl[b] == e) used = 1;
+                if (!used && p[e] > bv) { bv = p[e]; bi = e; }
+            }
+            sl[a] = bi;
+            wl[a] = bv;
+        }
+        float ssum = 0;                                /* qwen_moe.c:301 */
+        for (int a = 0; a < n_act; a++) ssum += wl[a];
+        for (int a = 0; a < n_act; a++) wl[a] /= ssum;
+    }
+    free(p);
+    return 0;
+}
+
+int orc_moe_layer(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                  const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
+                  int *sel, float *sw)
+{
+    if (M < 0 || d % 256 || ff % 256 || n_act <= 0 || n_act > n_exp || n_act > 64) return -1;
+    size_t gu_rb = orc_row_bytes(ORC_Q4_K, d), dn_rb = orc_row_bytes(ORC_Q4_K, ff);
+    size_t gu_eb = gu_rb * (size_t)ff, dn_eb = dn_rb * (size_t)d;
+    int *sel_l = (int *)malloc(sizeof(int) * (size_t)(M > 0 ? M : 1) * n_act);
+    float *sw_l = (float *)malloc(sizeof(float) * (size_t)(M > 0 ? M : 1) * n_act);
+    float *g = (float *)malloc(sizeof(float) * (size_t)ff);
+    float *u = (float *)malloc(sizeof(float) * (size_t)ff);
+    float *y = (float *)malloc(sizeof(float) * (size_t)d);
+    float *eout = (float *)malloc(sizeof(float) * (size_t)d);
+    orc_q8_K *xq = (orc_q8_K *)malloc(sizeof(orc_q8_K) * (size_t)(d / 256));
+    orc_q8_K *aq = (orc_q8_K *)malloc(sizeof(orc_q8_K) * (size_t)(ff / 256));
+    int rc = -1;
+    if (!sel_l || !sw_l || !g || !u || !y || !eout || !xq || !aq) goto done;
+    if (orc_moe_route(M, d, n_exp, n_act, hn, R, NULL, sel_l, sw_l)) goto done;
+    for (int m = 0; m < M; m++) {
+        const float *h = hn + (size_t)m * d;
+        orc_quantize_q8_K(h, d, xq);                   /* activation packed once, qwen_moe.c:303 */
+        for (int i = 0; i < d; i++) eout[i] = 0;
+        for (int a = 0; a < n_act; a++) {
+            int e = sel_l[(size_t)m * n_act + a];
+            float w = sw_l[(size_t)m * n_act + a];
+            const uint8_t *ge = (const uint8_t *)Wg + (size_t)e * gu_eb;
+            const uint8_t *ue = (const uint8_t *)Wu + (size_t)e * gu_eb;
+            const uint8_t *de = (const uint8_t *)Wd + (size_t)e * dn_eb;
+            for (int i = 0; i < ff; i++) {             /* gate / up, qwen_moe.c:307 */
+                g[i] = dot_q4_K_q8_K((const orc_q4_K *)(ge + (size_t)i * gu_rb), xq, d / 256);
+                u[i] = dot_q4_K_q8_K((const orc_q4_K *)(ue + (size_t)i * gu_rb), xq, d / 256);
+            }
+            for (int i = 0; i < ff; i++) g[i] = orc_swiglu(g[i], u[i]);   /* :309 */
+            orc_quantize_q8_K(g, ff, aq);
+            for (int j = 0; j < d; j++)                /* down + weighted sum, :310 */
+                y[j] = dot_q4_K_q8_K((const orc_q4_K *)(de + (size_t)j * dn_rb), aq, ff / 256);
+            for (int j = 0; j < d; j++) eout[j] += w * y[j];
+        }
+        float *o = out + (size_t)m * d;
+        for (int j = 0; j < d; j++) o[j] = residual ? o[j] + eout[j] : eout[j];   /* :311 */
+    }
+    if (sel) memcpy(sel, sel_l, sizeof(int) * (size_t)M * n_act);
+    if (sw) memcpy(sw, sw_l, sizeof(float) * (size_t)M * n_act);
+    rc = 0;
+done:
+    free(sel_l); free(sw_l); free(g); free(u); free(y); free(eout); free(xq); free(aq);
+    return rc;
+}

@@ -1,0 +1,154 @@
+"""ctypes binding of oracle/liboracle.so -- the CPU restatement used as the parity checker.
+
+Test infrastructure only: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg, never by the product path.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_PATH = os.path.join(ROOT, "oracle", "_ref", "libx100ref.so")
+
+Q4_0, Q8_0, Q3_K, Q4_K, Q8_K = 2, 8, 11, 12, 15
+DT_Q8_0 = np.dtype([("d", "<u2"), ("qs", "i1", (32,))])
+DT_Q8_K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+assert DT_Q8_0.itemsize == 34 and DT_Q8_K.itemsize == 292
+
+_o = None
+_r = None
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def oracle():
+    global _o
+    if _o is None:
+        if not os.path.exists(ORACLE_PATH):
+            raise FileNotFoundError("oracle/liboracle.so not built (make -C oracle)")
+        L = ctypes.CDLL(ORACLE_PATH)
+        i, p, f = ctypes.c_int, ctypes.c_void_p, ctypes.c_float
+        L.orc_f32_to_f16.argtypes = [f]
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f16_to_f32.restype = f
+        L.gemm_ref_i8.argtypes = [i, i, i, p, p, p]
+        L.gemm_ref_i8.restype = None
+        L.orc_gemm_i8_mt.argtypes = [i, i, i, p, p, p, i]
+        L.orc_gemm_i8_mt.restype = None
+        L.orc_dequant_row.argtypes = [i, p, i, p]
+        L.orc_quantize_q8_0.argtypes = [p, i, p]
+        L.orc_quantize_q8_0.restype = None
+        L.orc_quantize_q8_K.argtypes = [p, i, p]
+        L.orc_quantize_q8_K.restype = None
+        L.orc_quantize_q4_0.argtypes = [p, i, p]
+        L.orc_quantize_q4_0.restype = None
+        L.orc_qgemv.argtypes = [i, i, i, i, p, p, p]
+        L.orc_qgemv_q.argtypes = [i, i, i, i, p, p, p]
+        L.orc_moe_layer.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p]
+        L.orc_moe_route.argtypes = [i, i, i, i, p, p, p, p, p]
+        L.orc_swiglu.argtypes = [f, f]
+        L.orc_swiglu.restype = f
+        _o = L
+    return _o
+
+
+def reference():
+    """The reference's own gemm_ref_i8 built from its sources (oracle/_ref), or None."""
+    global _r
+    if _r is None and os.path.exists(REF_PATH):
+        L = ctypes.CDLL(REF_PATH)
+        i, p = ctypes.c_int, ctypes.c_void_p
+        L.gemm_ref_i8.argtypes = [i, i, i, p, p, p]
+        L.gemm_ref_i8.restype = None
+        _r = L
+    return _r
+
+
+def gemm_ref_i8(A, B, C, threads=1):
+    """C += A.B (in place) with the oracle (threads > 1: row-parallel, same arithmetic)."""
+    M, K = A.shape
+    N = B.shape[1]
+    A = np.ascontiguousarray(A)
+    B = np.ascontiguousarray(B)
+    assert C.dtype == np.int32 and C.flags.c_contiguous
+    if threads > 1:
+        oracle().orc_gemm_i8_mt(M, N, K, _p(A), _p(B), _p(C), threads)
+    else:
+        oracle().gemm_ref_i8(M, N, K, _p(A), _p(B), _p(C))
+    return C
+
+
+def dequant_row(qtype, blocks, K):
+    out = np.empty(K, dtype=np.float32)
+    b = np.ascontiguousarray(blocks)
+    rc = oracle().orc_dequant_row(qtype, _p(b), K, _p(out))
+    assert rc == 0
+    return out
+
+
+def quantize_q8_0(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 32, dtype=DT_Q8_0)
+    oracle().orc_quantize_q8_0(_p(x), x.size, _p(out))
+    return out
+
+
+def quantize_q8_K(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 256, dtype=DT_Q8_K)
+    oracle().orc_quantize_q8_K(_p(x), x.size, _p(out))
+    return out
+
+
+def quantize_q4_0(w, dtype):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.zeros(w.size // 32, dtype=dtype)
+    oracle().orc_quantize_q4_0(_p(w), w.size, _p(out))
+    return out
+
+
+def qgemv(qtype, W, x):
+    """y (M x N) for GGUF blocks W (N rows) and fp32 x (M x K)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    N = W.shape[0]
+    y = np.empty((M, N), dtype=np.float32)
+    Wc = np.ascontiguousarray(W)
+    rc = oracle().orc_qgemv(qtype, M, N, K, _p(Wc), _p(x), _p(y))
+    assert rc == 0
+    return y
+
+
+def moe_layer(hn, R, Wg, Wu, Wd, n_act, out=None, residual=False):
+    hn = np.ascontiguousarray(hn, dtype=np.float32)
+    M, d = hn.shape
+    n_exp = R.shape[0]
+    ff = Wg.shape[1]
+    if out is None:
+        out = np.zeros((M, d), dtype=np.float32)
+    sel = np.zeros((M, n_act), dtype=np.int32)
+    sw = np.zeros((M, n_act), dtype=np.float32)
+    R = np.ascontiguousarray(R, dtype=np.float32)
+    rc = oracle().orc_moe_layer(M, d, ff, n_exp, n_act, _p(hn), _p(R), _p(np.ascontiguousarray(Wg)),
+                                _p(np.ascontiguousarray(Wu)), _p(np.ascontiguousarray(Wd)), _p(out),
+                                1 if residual else 0, _p(sel), _p(sw))
+    assert rc == 0
+    return out, sel, sw
+
+
+def moe_route(hn, R, n_act):
+    hn = np.ascontiguousarray(hn, dtype=np.float32)
+    M, d = hn.shape
+    n_exp = R.shape[0]
+    logits = np.zeros((M, n_exp), dtype=np.float32)
+    sel = np.zeros((M, n_act), dtype=np.int32)
+    sw = np.zeros((M, n_act), dtype=np.float32)
+    rc = oracle().orc_moe_route(M, d, n_exp, n_act, _p(hn), _p(np.ascontiguousarray(R, dtype=np.float32)),
+                                _p(logits), _p(sel), _p(sw))
+    assert rc == 0
+    return logits, sel, sw

@@ -1,0 +1,132 @@
+"""int8 GEMM on the GPU, bit-exact against the oracle gemm_ref_i8 (C += A.B)."""
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+import synth
+import x100hip
+
+pytestmark = pytest.mark.gpu
+
+
+def _stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def gpu_gemm(A, B, C0, dev, variant=x100hip.GEMM_AUTO, reps=1):
+    import torch
+    M, K = A.shape
+    N = B.shape[1]
+    dA = torch.from_numpy(np.ascontiguousarray(A)).to(dev)
+    dB = torch.from_numpy(np.ascontiguousarray(B)).to(dev)
+    dC = torch.from_numpy(np.ascontiguousarray(C0).copy()).to(dev)
+    for _ in range(reps):
+        x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), _stream(), variant)
+    torch.cuda.synchronize()
+    return dC.cpu().numpy()
+
+
+def oracle_gemm(A, B, C0, threads=16):
+    C = np.ascontiguousarray(C0).copy()
+    ol.gemm_ref_i8(A, B, C, threads=threads)
+    return C
+
+
+def test_gemm_256_cube(dev):
+    A, B = synth.gemm_inputs(256, 256, 256, seed=2026)
+    C0 = np.zeros((256, 256), np.int32)
+    assert np.array_equal(gpu_gemm(A, B, C0, dev), oracle_gemm(A, B, C0))
+    C0 = synth.rand_int8(1, (256, 256)).astype(np.int32) * 77
+    assert np.array_equal(gpu_gemm(A, B, C0, dev), oracle_gemm(A, B, C0))
+
+
+def test_gemm_4096_cube(dev):
+    A, B = synth.gemm_inputs(4096, 4096, 4096, seed=2026)
+    C0 = np.zeros((4096, 4096), np.int32)
+    got = gpu_gemm(A, B, C0, dev)
+    ref = oracle_gemm(A, B, C0)
+    assert np.array_equal(got, ref), "mismatches: %d" % int((got != ref).sum())
+
+
+def test_gemm_4096_accumulate_twice(dev):
+    A, B = synth.gemm_inputs(4096, 4096, 4096, seed=7)
+    C0 = np.zeros((4096, 4096), np.int32)
+    once = gpu_gemm(A, B, C0, dev)
+    twice = gpu_gemm(A, B, C0, dev, reps=2)
+    assert np.array_equal(twice, 2 * once)
+
+
+def test_gemm_skinny_8x4096x4096(dev):
+    A, B = synth.gemm_inputs(8, 4096, 4096, seed=2027)
+    C0 = synth.rand_int8(2, (8, 4096)).astype(np.int32)
+    assert np.array_equal(gpu_gemm(A, B, C0, dev), oracle_gemm(A, B, C0))
+
+
+SHAPES = [(1, 16, 16), (2, 32, 48), (8, 4096, 256), (16, 272, 528), (17, 48, 80), (33, 48, 80),
+          (128, 128, 64), (130, 144, 96), (255, 256, 256), (256, 256, 64), (300, 272, 1040),
+          (512, 512, 512), (257, 528, 336), (1024, 768, 256)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_shapes_auto(dev, M, N, K):
+    A, B = synth.gemm_inputs(M, N, K, seed=M + 3 * N + 7 * K)
+    C0 = synth.rand_int8(5, (M, N)).astype(np.int32)
+    assert np.array_equal(gpu_gemm(A, B, C0, dev), oracle_gemm(A, B, C0))
+
+
+@pytest.mark.parametrize("variant", [x100hip.GEMM_TILE256, x100hip.GEMM_TILE128, x100hip.GEMM_SKINNY,
+                                     x100hip.GEMM_GENERIC])
+@pytest.mark.parametrize("M,N,K", [(8, 256, 256), (16, 512, 320), (3, 48, 64), (256, 256, 512),
+                                   (40, 96, 144)])
+def test_gemm_forced_variants(dev, variant, M, N, K):
+    if variant == x100hip.GEMM_SKINNY and M > 16:
+        pytest.skip("skinny kernel takes M <= 16")
+    A, B = synth.gemm_inputs(M, N, K, seed=11 * M + N + K)
+    C0 = synth.rand_int8(6, (M, N)).astype(np.int32)
+    assert np.array_equal(gpu_gemm(A, B, C0, dev, variant), oracle_gemm(A, B, C0))
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 20, 40), (64, 30, 64), (9, 17, 33), (100, 100, 100)])
+def test_gemm_unaligned_shapes(dev, M, N, K):
+    # K or N not a multiple of 16: row starts are not 16-byte aligned -> generic kernel
+    A, B = synth.gemm_inputs(M, N, K, seed=M + N + K)
+    C0 = np.zeros((M, N), np.int32)
+    assert np.array_equal(gpu_gemm(A, B, C0, dev), oracle_gemm(A, B, C0))
+
+
+def test_gemm_extremes(dev):
+    K = 512
+    A = np.full((64, K), -128, np.int8)
+    B = np.full((K, 64), -128, np.int8)
+    C = gpu_gemm(A, B, np.zeros((64, 64), np.int32), dev)
+    assert np.all(C == 16384 * K)
+    A = np.full((64, K), 127, np.int8)
+    C = gpu_gemm(A, B, np.zeros((64, 64), np.int32), dev)
+    assert np.all(C == -127 * 128 * K)
+
+
+def test_gemm_empty_is_noop(dev):
+    import torch
+    dC = torch.ones((4, 4), dtype=torch.int32, device=dev)
+    x100hip.gemm_dev(4, 4, 0, 0, 0, dC.data_ptr(), _stream())
+    x100hip.gemm_dev(0, 4, 4, 0, 0, dC.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    assert int(dC.sum()) == 16
+
+
+def test_gemm_host_dropin(dev):
+    A, B = synth.gemm_inputs(96, 80, 64, seed=8)
+    C = synth.rand_int8(9, (96, 80)).astype(np.int32)
+    ref = oracle_gemm(A, B, C)
+    x100hip.gemm_host(A, B, C)
+    assert np.array_equal(C, ref)
+    # the void drop-in entry point (reference name)
+    C2 = np.zeros((96, 80), np.int32)
+    x100hip.lib().gemm_ime_i8(96, 80, 64, A.ctypes.data, B.ctypes.data, C2.ctypes.data)
+    assert np.array_equal(C2, oracle_gemm(A, B, np.zeros((96, 80), np.int32)))
+
+
+def test_gemm_rejects_bad_args(dev):
+    with pytest.raises(x100hip.X100Error):
+        x100hip.gemm_dev(-1, 4, 4, 1, 1, 1, _stream())

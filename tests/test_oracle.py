@@ -1,0 +1,455 @@
+"""Pins the CPU oracle (oracle/x100_oracle.c) before it is trusted as the parity checker.
+
+Each oracle function is checked against something other than itself:
+  gemm_ref_i8         numpy int64 matmul (closed form), the reference's own gemm_ref_i8 built from
+                      its sources (oracle/_ref), golden vectors from that build, invariants.
+  fp16 conversions    numpy.float16 (IEEE round-to-nearest-even), exhaustive over fp16.
+  Q8_0 / Q8_K         independent numpy restatements + hand-worked tie cases (rint vs roundf).
+  Q4_0 / Q4_K / Q3_K  hand-built blocks with known values; numpy encoders written from the block
+  dequant             layout (not from the C decoder); random blocks vs numpy decoders.
+  qgemv               float64 dequantize-then-dot of the same quantized operands (closed form);
+                      zero-scale / offset special cases; exact linearity in d.
+  moe_layer           float64 restatement from dequantized weights, tie-breaking, expert
+                      permutation invariance, M rows == M single-row calls, dense n_act = n_exp.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+import synth
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ------------------------------------------------------------------------------------------------
+# int8 GEMM
+# ------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (3, 5, 7), (16, 16, 16), (37, 29, 53), (64, 1, 300),
+                                   (1, 200, 96), (128, 96, 64)])
+def test_gemm_ref_closed_form(M, N, K):
+    A, B = synth.gemm_inputs(M, N, K, seed=M * 1000 + N * 10 + K)
+    C0 = synth.rand_int8(99, (M, N)).astype(np.int32)
+    C = C0.copy()
+    ol.gemm_ref_i8(A, B, C)
+    expect = C0.astype(np.int64) + A.astype(np.int64) @ B.astype(np.int64)
+    assert np.array_equal(C, expect.astype(np.int32))
+
+
+def test_gemm_ref_golden_from_reference_build():
+    """Vectors whose outputs the reference's own gemm_ref_i8 produced (tests/golden/make_golden.py)."""
+    g = np.load(os.path.join(GOLDEN, "gemm_ref_i8.npz"))
+    n = len([k for k in g.files if k.startswith("A")])
+    assert n >= 9
+    for i in range(n):
+        A, B, C0, C = g["A%d" % i], g["B%d" % i], g["C0_%d" % i], g["C%d" % i]
+        out = C0.copy()
+        ol.gemm_ref_i8(A, B, out)
+        assert np.array_equal(out, C), "golden case %d" % i
+
+
+def test_gemm_ref_matches_reference_library():
+    ref = ol.reference()
+    if ref is None:
+        pytest.skip("reference not built here (oracle/_ref needs /root/reference)")
+    A, B = synth.gemm_inputs(70, 90, 110, seed=5)
+    C1 = np.zeros((70, 90), np.int32)
+    C2 = np.zeros((70, 90), np.int32)
+    ol.gemm_ref_i8(A, B, C1)
+    ref.gemm_ref_i8(70, 90, 110, A.ctypes.data, B.ctypes.data, C2.ctypes.data)
+    assert np.array_equal(C1, C2)
+
+
+def test_gemm_ref_invariants():
+    A, B = synth.gemm_inputs(40, 24, 64, seed=3)
+    C = np.zeros((40, 24), np.int32)
+    ol.gemm_ref_i8(A, B, C)
+    once = C.copy()
+    ol.gemm_ref_i8(A, B, C)                      # accumulate: twice == 2 * product
+    assert np.array_equal(C, 2 * once)
+    # identity: A . I == A
+    I = np.eye(64, dtype=np.int8)
+    C = np.zeros((40, 64), np.int32)
+    ol.gemm_ref_i8(A, I, C)
+    assert np.array_equal(C, A.astype(np.int32))
+    # extremes: all -128 -> 16384*K per element
+    K = 300
+    C = np.zeros((3, 5), np.int32)
+    ol.gemm_ref_i8(np.full((3, K), -128, np.int8), np.full((K, 5), -128, np.int8), C)
+    assert np.all(C == 16384 * K)
+    # threaded variant is the same arithmetic
+    A, B = synth.gemm_inputs(96, 80, 200, seed=4)
+    C1 = np.zeros((96, 80), np.int32)
+    C2 = np.zeros((96, 80), np.int32)
+    ol.gemm_ref_i8(A, B, C1)
+    ol.gemm_ref_i8(A, B, C2, threads=4)
+    assert np.array_equal(C1, C2)
+
+
+# ------------------------------------------------------------------------------------------------
+# fp16
+# ------------------------------------------------------------------------------------------------
+def test_f16_to_f32_exhaustive():
+    o = ol.oracle()
+    h = np.arange(65536, dtype=np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = np.array([o.orc_f16_to_f32(int(v)) for v in h], dtype=np.float32)
+    finite = np.isfinite(ref)
+    assert np.array_equal(got[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(ref)]))
+    assert np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])
+
+
+def test_f32_to_f16_round_nearest_even():
+    o = ol.oracle()
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, size=200000, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0x00000000, 0x80000000, 0x33000000, 0x33000001, 0x337fffff, 0x33800000,
+                        0x38800000, 0x387fffff, 0x387fe000, 0x387ff000, 0x477fe000, 0x477fefff,
+                        0x477ff000, 0x477ff001, 0x7f800000, 0xff800000, 0x3f800000, 0x3f801000,
+                        0x3f803000, 0x3f802000, 0x3f806000], dtype=np.uint32)
+    # every halfway case in one binade and around the subnormal range
+    ties = (np.arange(0x3f800000, 0x3f800000 + (1 << 23), 0x1000, dtype=np.uint64) | 0x1000).astype(np.uint32)
+    sub = np.arange(0x33000000, 0x38900000, 0x800, dtype=np.uint32)
+    allb = np.concatenate([bits, special, ties[:4000], sub])
+    f = allb.view(np.float32)
+    keep = ~np.isnan(f)
+    f = f[keep]
+    ref = f.astype(np.float16).view(np.uint16)
+    got = np.array([o.orc_f32_to_f16(float(v)) for v in f], dtype=np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------------------------------------
+# activation quantizers
+# ------------------------------------------------------------------------------------------------
+def np_q8_0(x):
+    b = x.reshape(-1, 32).astype(np.float32)
+    amax = np.maximum(np.abs(b).max(axis=1), np.float32(1e-6)).astype(np.float32)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    inv = np.where(d != 0, np.float32(1.0) / d, np.float32(0)).astype(np.float32)
+    q = np.clip(np.rint(b * inv[:, None]), -128, 127).astype(np.int8)
+    return d.astype(np.float16).view(np.uint16), q
+
+
+def np_q8_K(x):
+    b = x.reshape(-1, 256).astype(np.float32)
+    amax = np.abs(b).max(axis=1).astype(np.float32)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        rep = np.where(d != 0, np.float32(1.0) / d, np.float32(0)).astype(np.float32)
+    v = (b * rep[:, None]).astype(np.float32).astype(np.float64)
+    q = np.clip(np.sign(v) * np.floor(np.abs(v) + 0.5), -128, 127).astype(np.int8)  # half away
+    bs = q.reshape(-1, 16, 16).astype(np.int32).sum(axis=2).astype(np.int16)
+    return d, q, bs
+
+
+def test_q8_0_matches_numpy_restatement():
+    x = np.concatenate([synth.normal_f32(7, (4096,)), synth.normal_f32(8, (256,)) * 1e-3,
+                        np.zeros(64, np.float32)])
+    blocks = ol.quantize_q8_0(x)
+    d, q = np_q8_0(x)
+    assert np.array_equal(blocks["d"], d)
+    assert np.array_equal(blocks["qs"], q)
+
+
+def test_q8_0_ties_round_half_even():
+    # amax = 127 -> d = 1, inv = 1: x*inv lands exactly on .5 -> rint rounds to even
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:7] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5]
+    b = ol.quantize_q8_0(x)
+    assert list(b["qs"][0][:7]) == [127, 2, 4, -2, -4, 0, 0]
+    assert b["d"][0] == np.float16(1.0).view(np.uint16)
+
+
+def test_q8_K_matches_numpy_restatement():
+    x = np.concatenate([synth.normal_f32(9, (2048,)), np.zeros(256, np.float32),
+                        synth.normal_f32(10, (256,)) * 1e-4])
+    blocks = ol.quantize_q8_K(x)
+    d, q, bs = np_q8_K(x)
+    assert np.array_equal(blocks["d"].view(np.uint32), d.view(np.uint32))
+    assert np.array_equal(blocks["qs"], q)
+    assert np.array_equal(blocks["bsums"], bs)
+    assert blocks["d"][8] == 0 and not blocks["qs"][8].any()   # all-zero block
+
+
+def test_q8_K_ties_round_half_away():
+    x = np.zeros(256, np.float32)
+    x[0] = 127.0
+    x[1:7] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5]
+    b = ol.quantize_q8_K(x)
+    assert list(b["qs"][0][:7]) == [127, 3, 4, -3, -4, 1, -1]
+    assert b["bsums"][0][0] == 127 + 3 + 4 - 3 - 4 + 1 - 1
+
+
+# ------------------------------------------------------------------------------------------------
+# block dequantization
+# ------------------------------------------------------------------------------------------------
+F16_ONE = int(np.float16(1.0).view(np.uint16))
+F16_HALF = int(np.float16(0.5).view(np.uint16))
+
+
+def test_q4_0_known_block():
+    # qs[j] = j | (15-j)<<4, d = 1: elements j<16 -> j-8 (low nibbles), j>=16 -> (15-(j-16))-8
+    blk = np.zeros(1, synth.DT_Q4_0)
+    blk["d"] = F16_ONE
+    blk["qs"][0] = [j | ((15 - j) << 4) for j in range(16)]
+    got = ol.dequant_row(ol.Q4_0, blk, 32)
+    expect = [j - 8 for j in range(16)] + [(15 - j) - 8 for j in range(16)]
+    assert got.tolist() == [float(v) for v in expect]
+
+
+def np_q4_K_encode_scales(sc, m):
+    """6-bit (sc, m) pairs of the 8 sub-blocks -> 12 bytes, written from the Q4_K layout:
+    bytes 0-3 / 4-7 hold sc0-3 / m0-3 in bits 0-5; bytes 8-11 hold the low nibbles of sc4-7
+    (bits 0-3) and m4-7 (bits 4-7); the top 2 bits of sc4-7 / m4-7 sit in bits 6-7 of bytes
+    0-3 / 4-7."""
+    s = np.zeros(12, np.uint8)
+    for j in range(4):
+        s[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        s[j + 4] = (m[j] & 63) | ((m[j + 4] >> 4) << 6)
+        s[j + 8] = (sc[j + 4] & 15) | ((m[j + 4] & 15) << 4)
+    return s
+
+
+def test_q4_K_known_block():
+    rng = np.random.default_rng(3)
+    sc = rng.integers(0, 64, 8)
+    m = rng.integers(0, 64, 8)
+    blk = np.zeros(1, synth.DT_Q4_K)
+    blk["d"] = F16_ONE
+    blk["dmin"] = F16_HALF
+    blk["scales"][0] = np_q4_K_encode_scales(sc, m)
+    q = rng.integers(0, 16, 256)   # element value nibble per (sub-block j, l)
+    qs = np.zeros(128, np.uint8)
+    for j in range(8):
+        for l in range(32):
+            byte = 32 * (j // 2) + l
+            qs[byte] |= (q[32 * j + l] << (4 if j % 2 else 0))
+    blk["qs"][0] = qs
+    got = ol.dequant_row(ol.Q4_K, blk, 256)
+    expect = np.array([1.0 * sc[e // 32] * q[e] - 0.5 * m[e // 32] for e in range(256)], np.float32)
+    assert np.array_equal(got, expect)
+
+
+def np_q3_K_encode_scales(s6):
+    """16 six-bit scales -> 12 bytes (Q3_K layout): low nibble of scale i (i<8) in bits 0-3 of
+    byte i, of scale i+8 in bits 4-7 of byte i; the top 2 bits of scale i in byte 8+(i%4),
+    bits 2*(i//4)."""
+    s = np.zeros(12, np.uint8)
+    for i in range(16):
+        lo, hi = s6[i] & 15, s6[i] >> 4
+        s[i % 8] |= lo << (4 * (i // 8))
+        s[8 + i % 4] |= hi << (2 * (i // 4))
+    return s
+
+
+def test_q3_K_known_block():
+    rng = np.random.default_rng(4)
+    s6 = rng.integers(0, 64, 16)
+    v = rng.integers(-4, 4, 256)       # element values in [-4, 3]
+    hmask = np.zeros(32, np.uint8)
+    qs = np.zeros(64, np.uint8)
+    for e in range(256):
+        h, j, l = e // 128, (e // 32) % 4, e % 32
+        low, hbit = (v[e] + 4) & 3, 1 if v[e] >= 0 else 0   # v = low - (hbit ? 0 : 4)
+        qs[32 * h + l] |= low << (2 * j)
+        hmask[l] |= hbit << (4 * h + j)
+    blk = np.zeros(1, synth.DT_Q3_K)
+    blk["hmask"][0], blk["qs"][0], blk["scales"][0], blk["d"] = hmask, qs, np_q3_K_encode_scales(s6), F16_ONE
+    got = ol.dequant_row(ol.Q3_K, blk, 256)
+    sub = [8 * (e // 128) + 2 * ((e // 32) % 4) + (e % 32) // 16 for e in range(256)]
+    expect = np.array([(s6[sub[e]] - 32) * v[e] for e in range(256)], np.float32)
+    assert np.array_equal(got, expect)
+
+
+def np_dequant(qtype, W):
+    """Vectorised numpy decoders of the three layouts (float64)."""
+    N, nb = W.shape
+    if qtype == synth.Q4_0:
+        d = W["d"].view(np.float16).astype(np.float64)
+        lo, hi = (W["qs"] & 15).astype(np.int64) - 8, (W["qs"] >> 4).astype(np.int64) - 8
+        return (np.concatenate([lo, hi], axis=2) * d[..., None]).reshape(N, nb * 32)
+    if qtype == synth.Q4_K:
+        d = W["d"].view(np.float16).astype(np.float64)
+        dmin = W["dmin"].view(np.float16).astype(np.float64)
+        s = W["scales"].astype(np.int64)
+        sc = np.zeros((N, nb, 8), np.int64)
+        mn = np.zeros((N, nb, 8), np.int64)
+        sc[..., :4], mn[..., :4] = s[..., 0:4] & 63, s[..., 4:8] & 63
+        sc[..., 4:] = (s[..., 8:12] & 15) | ((s[..., 0:4] >> 6) << 4)
+        mn[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
+        qs = W["qs"].reshape(N, nb, 4, 32).astype(np.int64)
+        q = np.stack([qs & 15, qs >> 4], axis=3).reshape(N, nb, 8, 32)   # sub-block 2p, 2p+1
+        val = d[..., None, None] * sc[..., None] * q - dmin[..., None, None] * mn[..., None]
+        return val.reshape(N, nb * 256)
+    if qtype == synth.Q3_K:
+        d = W["d"].view(np.float16).astype(np.float64)
+        s = W["scales"].astype(np.int64)
+        i = np.arange(16)
+        s6 = ((s[..., i % 8] >> (4 * (i // 8))) & 15) | (((s[..., 8 + i % 4] >> (2 * (i // 4))) & 3) << 4)
+        e = np.arange(256)
+        h, j, l = e // 128, (e // 32) % 4, e % 32
+        low = (W["qs"][..., 32 * h + l].astype(np.int64) >> (2 * j)) & 3
+        hb = (W["hmask"][..., l].astype(np.int64) >> (4 * h + j)) & 1
+        q = low - 4 * (1 - hb)
+        sub = 8 * h + 2 * j + l // 16
+        return (d[..., None] * (s6[..., sub] - 32) * q).reshape(N, nb * 256)
+    raise ValueError(qtype)
+
+
+@pytest.mark.parametrize("qtype,K", [(synth.Q4_0, 512), (synth.Q4_K, 1024), (synth.Q3_K, 1024)])
+def test_dequant_random_blocks_vs_numpy(qtype, K):
+    W = synth.quant_weight(qtype, 6, K, seed=21)
+    ref = np_dequant(qtype, W)
+    for n in range(6):
+        got = ol.dequant_row(qtype, W[n], K)
+        np.testing.assert_allclose(got, ref[n], rtol=2e-7, atol=1e-12)
+
+
+# ------------------------------------------------------------------------------------------------
+# quantized GEMV
+# ------------------------------------------------------------------------------------------------
+def q8_dequant(qtype, x):
+    """Quantize x rows with the oracle, return the float64 values actually multiplied."""
+    rows = []
+    for r in x:
+        if qtype == synth.Q4_0:
+            b = ol.quantize_q8_0(r)
+            rows.append((b["qs"].astype(np.float64) * b["d"].view(np.float16).astype(np.float64)[:, None]).ravel())
+        else:
+            b = ol.quantize_q8_K(r)
+            rows.append((b["qs"].astype(np.float64) * b["d"].astype(np.float64)[:, None]).ravel())
+    return np.array(rows)
+
+
+@pytest.mark.parametrize("qtype,N,K,M", [(synth.Q4_0, 64, 1024, 1), (synth.Q4_0, 33, 256, 3),
+                                         (synth.Q4_K, 48, 2048, 1), (synth.Q4_K, 20, 768, 4),
+                                         (synth.Q3_K, 48, 2048, 1), (synth.Q3_K, 17, 512, 4)])
+def test_qgemv_closed_form(qtype, N, K, M):
+    W = synth.quant_weight(qtype, N, K, seed=N + K)
+    x = synth.normal_f32(M * 7 + K, (M, K))
+    y = ol.qgemv(qtype, W, x)
+    ref = q8_dequant(qtype, x) @ np_dequant(qtype, W).T
+    err = np.abs(y - ref)
+    assert np.all(err <= 1e-5 * np.abs(ref) + 1e-4 * np.abs(ref).max() * 1e-3 + 1e-6), err.max()
+
+
+def test_qgemv_special_cases():
+    x = synth.normal_f32(1, (2, 512))
+    # Q4_0 with every nibble 8 -> all elements 0 -> y == 0 exactly
+    W = synth.quant_weight(synth.Q4_0, 5, 512, seed=2)
+    W["qs"] = 0x88
+    assert not ol.qgemv(synth.Q4_0, W, x).any()
+    # Q4_K with all scales / mins 0 -> y == 0
+    W = synth.quant_weight(synth.Q4_K, 5, 512, seed=3)
+    W["scales"] = 0
+    assert not ol.qgemv(synth.Q4_K, W, x).any()
+    # Q3_K with every 6-bit scale 32 -> (s - 32) == 0 -> y == 0
+    W = synth.quant_weight(synth.Q3_K, 5, 512, seed=4)
+    W["scales"] = np_q3_K_encode_scales(np.full(16, 32))
+    assert not ol.qgemv(synth.Q3_K, W, x).any()
+    # Q4_K dmin-only: sc = 0, m = 1 -> y = -dmin * dx * sum(qx)
+    W = synth.quant_weight(synth.Q4_K, 3, 256, seed=5)
+    W["scales"] = np_q4_K_encode_scales(np.zeros(8, int), np.ones(8, int))
+    y = ol.qgemv(synth.Q4_K, W, x[:1, :256])
+    xb = ol.quantize_q8_K(x[0, :256])
+    expect = -(xb["d"][0] * W["dmin"][:, 0].view(np.float16).astype(np.float32)) * xb["qs"][0].astype(np.int32).sum()
+    np.testing.assert_allclose(y[0], expect, rtol=1e-6)
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q4_K, synth.Q3_K])
+def test_qgemv_linear_in_scale(qtype):
+    K = 512
+    W = synth.quant_weight(qtype, 8, K, seed=6)
+    W["d"] = np.float16(0.25).view(np.uint16)
+    x = synth.normal_f32(2, (1, K))
+    y1 = ol.qgemv(qtype, W, x)
+    W2 = W.copy()
+    W2["d"] = np.float16(0.5).view(np.uint16)
+    if qtype == synth.Q4_K:
+        W2["dmin"] = (W["dmin"].view(np.float16) * np.float16(2)).view(np.uint16)
+    y2 = ol.qgemv(qtype, W2, x)
+    assert np.array_equal(y2, 2 * y1)   # powers of two: exact
+
+
+# ------------------------------------------------------------------------------------------------
+# MoE layer
+# ------------------------------------------------------------------------------------------------
+def small_moe(seed, n_exp=16, d=512, ff=256):
+    Wg, Wu, Wd = synth.moe_weights(n_exp, d, ff, seed)
+    R = synth.moe_router(n_exp, d, seed + 1)
+    return Wg, Wu, Wd, R
+
+
+def np_moe(hn, R, Wg, Wu, Wd, n_act):
+    """float64 restatement of the layer from dequantized weights and the oracle's quantizers."""
+    out = np.zeros(hn.shape, np.float64)
+    for m, h in enumerate(hn):
+        lg = R.astype(np.float64) @ h.astype(np.float64)
+        p = np.exp(lg - lg.max())
+        p /= p.sum()
+        sel = sorted(range(len(p)), key=lambda e: (-p[e], e))[:n_act]
+        w = p[sel] / p[sel].sum()
+        xq = q8_dequant(synth.Q4_K, h[None])[0]
+        for a, e in enumerate(sel):
+            g = np_dequant(synth.Q4_K, Wg[e]) @ xq
+            u = np_dequant(synth.Q4_K, Wu[e]) @ xq
+            act = (g / (1 + np.exp(-g)) * u).astype(np.float32)
+            aq = q8_dequant(synth.Q4_K, act[None])[0]
+            out[m] += w[a] * (np_dequant(synth.Q4_K, Wd[e]) @ aq)
+    return out
+
+
+def test_moe_matches_float64_restatement():
+    Wg, Wu, Wd, R = small_moe(30)
+    hn = synth.normal_f32(31, (2, 512))
+    out, sel, sw = ol.moe_layer(hn, R, Wg, Wu, Wd, n_act=4)
+    ref = np_moe(hn, R, Wg, Wu, Wd, 4)
+    # activation re-quantization may flip a rounding at a .5 boundary; compare at 1e-3 of scale
+    assert np.abs(out - ref).max() <= 2e-3 * np.abs(ref).max()
+    np.testing.assert_allclose(sw.sum(axis=1), 1.0, rtol=1e-6)
+
+
+def test_moe_router_ties_lower_index_wins():
+    n_exp, d = 8, 256
+    R = np.zeros((n_exp, d), np.float32)
+    R[[2, 5, 6]] = 1.0           # three equal top logits
+    hn = np.ones((1, d), np.float32)
+    _, sel, sw = ol.moe_route(hn, R, 4)
+    assert sel[0].tolist()[:3] == [2, 5, 6]
+    assert sel[0][3] == 0         # remaining experts tie at the next value: lowest id first
+    assert abs(sw[0][:3].sum() + sw[0][3] - 1) < 1e-6
+
+
+def test_moe_rows_independent_and_permutation_invariant():
+    Wg, Wu, Wd, R = small_moe(40)
+    hn = synth.normal_f32(41, (3, 512))
+    out, sel, sw = ol.moe_layer(hn, R, Wg, Wu, Wd, n_act=4)
+    for m in range(3):   # M rows == M single-row calls (per-row activation quantization)
+        o1, s1, w1 = ol.moe_layer(hn[m:m + 1], R, Wg, Wu, Wd, n_act=4)
+        assert np.array_equal(o1[0], out[m]) and np.array_equal(s1[0], sel[m])
+    perm = np.random.default_rng(0).permutation(R.shape[0])
+    outp, selp, _ = ol.moe_layer(hn, R[perm], Wg[perm], Wu[perm], Wd[perm], n_act=4)
+    assert np.array_equal(perm[selp], sel)
+    np.testing.assert_allclose(outp, out, rtol=1e-5, atol=1e-5 * np.abs(out).max())
+
+
+def test_moe_residual_flag():
+    Wg, Wu, Wd, R = small_moe(50)
+    hn = synth.normal_f32(51, (1, 512))
+    base = synth.normal_f32(52, (1, 512))
+    out, _, _ = ol.moe_layer(hn, R, Wg, Wu, Wd, n_act=2)
+    res, _, _ = ol.moe_layer(hn, R, Wg, Wu, Wd, n_act=2, out=base.copy(), residual=True)
+    assert np.array_equal(res, base + out)
+
+
+def test_swiglu_is_exact_silu_product():
+    o = ol.oracle()
+    for g, u in [(0.0, 3.0), (1.5, -2.0), (-30.0, 1.0), (12.0, 0.5), (-0.25, 4.0)]:
+        g32, u32 = np.float32(g), np.float32(u)
+        e = np.float32(np.exp(-np.float64(g32)))
+        expect = np.float32(np.float32(g32 / np.float32(1 + e)) * u32)
+        assert np.float32(o.orc_swiglu(g32, u32)) == expect

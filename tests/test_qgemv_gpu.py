@@ -1,0 +1,75 @@
+"""Q4_0 / Q4_K / Q3_K dequant-GEMV on the GPU against the oracle (rel 1e-3 / abs 1e-4 in fp32;
+the K-quant kernels reduce in the oracle's order and are expected to match bit for bit)."""
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+import synth
+import x100hip
+
+pytestmark = pytest.mark.gpu
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def gpu_qgemv(qtype, W, x, dev):
+    import torch
+    N = W.shape[0]
+    M, K = x.shape
+    s = torch.cuda.current_stream().cuda_stream
+    raw = torch.from_numpy(np.ascontiguousarray(W).view(np.uint8).reshape(-1)).to(dev)
+    packed = torch.empty(x100hip.packed_bytes(qtype, N, K), dtype=torch.uint8, device=dev)
+    x100hip.pack(qtype, N, K, raw.data_ptr(), packed.data_ptr(), s)
+    dx = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dev)
+    dy = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    x100hip.qgemv(qtype, M, N, K, packed.data_ptr(), dx.data_ptr(), dy.data_ptr(), s)
+    torch.cuda.synchronize()
+    return dy.cpu().numpy()
+
+
+def check(qtype, N, K, M, seed, dev, exact=None):
+    W = synth.quant_weight(qtype, N, K, seed)
+    x = synth.normal_f32(seed + 1, (M, K))
+    got = gpu_qgemv(qtype, W, x, dev)
+    ref = ol.qgemv(qtype, W, x)
+    err = np.abs(got - ref)
+    bad = err > ATOL + RTOL * np.abs(ref)
+    assert not bad.any(), "qtype %d N=%d K=%d M=%d: %d outside tolerance, max err %g" % (
+        qtype, N, K, M, int(bad.sum()), float(err.max()))
+    if exact is None:
+        exact = qtype != synth.Q4_0
+    if exact:
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "not bit-identical"
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_q4_0_4096(dev, M):
+    check(synth.Q4_0, 4096, 4096, M, seed=300 + M, dev=dev)
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q3_K])
+@pytest.mark.parametrize("M", [1, 4])
+def test_kquant_6144x2048(dev, qtype, M):
+    check(qtype, 6144, 2048, M, seed=400 + M + qtype, dev=dev)
+
+
+@pytest.mark.parametrize("qtype,N,K,M", [
+    (synth.Q4_0, 1, 32, 1), (synth.Q4_0, 7, 96, 2), (synth.Q4_0, 300, 2048, 3), (synth.Q4_0, 64, 8192, 8),
+    (synth.Q4_0, 33, 16384, 1), (synth.Q4_K, 1, 256, 1), (synth.Q4_K, 5, 768, 2), (synth.Q4_K, 2048, 768, 8),
+    (synth.Q4_K, 100, 4096, 3), (synth.Q4_K, 9, 8192, 1), (synth.Q3_K, 1, 256, 1), (synth.Q3_K, 13, 768, 5),
+    (synth.Q3_K, 700, 4096, 8), (synth.Q3_K, 3, 16384, 2)])
+def test_qgemv_shapes(dev, qtype, N, K, M):
+    check(qtype, N, K, M, seed=N + K + M, dev=dev)
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q4_K, synth.Q3_K])
+def test_qgemv_zero_activation(dev, qtype):
+    W = synth.quant_weight(qtype, 64, 512, seed=9)
+    y = gpu_qgemv(qtype, W, np.zeros((2, 512), np.float32), dev)
+    assert not y.any()
+
+
+def test_qgemv_rejects_bad_shapes(dev):
+    with pytest.raises(x100hip.X100Error):
+        x100hip.qgemv(synth.Q4_K, 1, 16, 100, 1 << 20, 1 << 20, 1 << 20)
+    with pytest.raises(x100hip.X100Error):
+        x100hip.qgemv(synth.Q4_0, 9, 16, 64, 1 << 20, 1 << 20, 1 << 20)

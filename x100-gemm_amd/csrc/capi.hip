@@ -1,0 +1,274 @@
+// C-ABI of libx100hip: argument checking, device state and the host-pointer convenience paths.
+// The kernels live in gemm_i8.hip, qgemv.hip and moe.hip.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+// Only the extern "C" entry points are exported (the library is built with -fvisibility=hidden).
+#pragma GCC visibility push(default)
+#include "x100_gemm.h"
+#include "x100_moe.h"
+#include "x100_qgemv.h"
+#pragma GCC visibility pop
+#include "x100_internal.h"
+
+namespace {
+
+thread_local hipError_t g_last_hip = hipSuccess;
+
+int hip_fail(hipError_t e)
+{
+    g_last_hip = e;
+    if (e == hipErrorOutOfMemory) return X100_ENOMEM;
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) return X100_ENODEV;
+    return X100_EHIP;
+}
+
+#define X100_TRY(expr)                                                                             \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess) return hip_fail(e_);                                                 \
+    } while (0)
+
+// Every entry point checks once per thread that the current device is a gfx950 part: the kernels
+// are built for gfx950 only, and there is no CPU fallback.
+int check_device()
+{
+    thread_local int checked_dev = -1;
+    int dev = 0;
+    X100_TRY(hipGetDevice(&dev));
+    if (dev == checked_dev) return X100_OK;
+    hipDeviceProp_t p;
+    X100_TRY(hipGetDeviceProperties(&p, dev));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+        g_last_hip = hipErrorInvalidDeviceFunction;
+        return X100_ENODEV;
+    }
+    checked_dev = dev;
+    return X100_OK;
+}
+
+// Per-device MoE workspace (grown on demand, zero-filled so completion counters start at 0).
+struct Workspace {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+Workspace g_moe_ws[64];
+
+int moe_workspace(size_t need, void **out)
+{
+    int dev = 0;
+    X100_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return X100_ENODEV;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Workspace &w = g_moe_ws[dev];
+    if (w.bytes < need) {
+        if (w.ptr) {
+            X100_TRY(hipDeviceSynchronize());
+            X100_TRY(hipFree(w.ptr));
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        void *p = nullptr;
+        X100_TRY(hipMalloc(&p, need));
+        X100_TRY(hipMemset(p, 0, need));
+        X100_TRY(hipDeviceSynchronize());
+        w.ptr = p;
+        w.bytes = need;
+    }
+    *out = w.ptr;
+    return X100_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------------------------------------
+// int8 GEMM
+// ---------------------------------------------------------------------------------------------
+int gemm_hip_i8_dev_variant(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
+                            void *stream, int variant)
+{
+    if (M < 0 || N < 0 || K < 0 || variant < 0 || variant > 4) return X100_EINVAL;
+    if (M == 0 || N == 0 || K == 0) return X100_OK;  // C += (empty product) leaves C unchanged
+    if (!dA || !dB || !dC) return X100_EINVAL;
+    if (K >= (1 << 17)) return X100_EINVAL;          // keeps |sum| < 2^31 (no int32 wrap)
+    int rc = check_device();
+    if (rc) return rc;
+    hipError_t e = x100_gemm_i8_launch(M, N, K, dA, dB, dC, (hipStream_t)stream, variant);
+    if (e == hipErrorInvalidValue) return X100_EINVAL;
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
+int gemm_hip_i8_dev(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
+                    void *stream)
+{
+    return gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, 0);
+}
+
+int gemm_hip_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C)
+{
+    if (M < 0 || N < 0 || K < 0) return X100_EINVAL;
+    if (M == 0 || N == 0 || K == 0) return X100_OK;
+    if (!A || !B || !C) return X100_EINVAL;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t sa = (size_t)M * K, sb = (size_t)K * N, sc = (size_t)M * N * sizeof(int32_t);
+    int8_t *dA = nullptr, *dB = nullptr;
+    int32_t *dC = nullptr;
+    hipError_t e = hipMalloc((void **)&dA, sa);
+    if (e == hipSuccess) e = hipMalloc((void **)&dB, sb);
+    if (e == hipSuccess) e = hipMalloc((void **)&dC, sc);
+    if (e == hipSuccess) e = hipMemcpy(dA, A, sa, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dB, B, sb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dC, C, sc, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        rc = gemm_hip_i8_dev(M, N, K, dA, dB, dC, nullptr);
+        if (rc == X100_OK) {
+            e = hipMemcpy(C, dC, sc, hipMemcpyDeviceToHost);
+            if (e == hipSuccess) e = hipDeviceSynchronize();
+        }
+    }
+    if (dA) (void)hipFree(dA);
+    if (dB) (void)hipFree(dB);
+    if (dC) (void)hipFree(dC);
+    if (rc != X100_OK) return rc;
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
+void gemm_ime_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C)
+{
+    int rc = gemm_hip_i8(M, N, K, A, B, C);
+    if (rc != X100_OK) {
+        fprintf(stderr, "gemm_ime_i8 (libx100hip): %s\n", x100_hip_strerror(rc));
+        abort();
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// caps / errors
+// ---------------------------------------------------------------------------------------------
+int x100_hip_detect(x100_hip_caps_t *caps)
+{
+    if (!caps) return X100_EINVAL;
+    memset(caps, 0, sizeof(*caps));
+    int n = 0;
+    X100_TRY(hipGetDeviceCount(&n));
+    if (n <= 0) return X100_ENODEV;
+    int dev = 0;
+    X100_TRY(hipGetDevice(&dev));
+    hipDeviceProp_t p;
+    X100_TRY(hipGetDeviceProperties(&p, dev));
+    caps->device = dev;
+    snprintf(caps->name, sizeof caps->name, "%s", p.name);
+    snprintf(caps->arch, sizeof caps->arch, "%s", p.gcnArchName);
+    caps->cu_count = p.multiProcessorCount;
+    caps->clock_khz = p.clockRate;
+    caps->hbm_bytes = p.totalGlobalMem;
+    caps->lds_bytes = (int)p.sharedMemPerBlock;
+    caps->l2_bytes = p.l2CacheSize;
+    caps->is_gfx950 = strncmp(p.gcnArchName, "gfx950", 6) == 0;
+    return X100_OK;
+}
+
+void x100_hip_caps_print(const x100_hip_caps_t *c)
+{
+    if (!c) return;
+    printf("device %d: %s (%s)\n", c->device, c->name, c->arch);
+    printf("  CUs %d  clock %.0f MHz  HBM %.1f GiB  LDS/block %d KiB  L2 %d KiB  gfx950 %s\n",
+           c->cu_count, c->clock_khz / 1000.0, c->hbm_bytes / 1073741824.0, c->lds_bytes / 1024,
+           c->l2_bytes / 1024, c->is_gfx950 ? "yes" : "no");
+}
+
+const char *x100_hip_strerror(int code)
+{
+    switch (code) {
+    case X100_OK: return "ok";
+    case X100_EINVAL: return "invalid argument or unsupported shape";
+    case X100_ENODEV: return g_last_hip != hipSuccess ? hipGetErrorString(g_last_hip)
+                                                      : "no gfx950 device";
+    case X100_ENOMEM: return "device allocation failed";
+    case X100_EHIP: return hipGetErrorString(g_last_hip);
+    }
+    return "unknown error";
+}
+
+// ---------------------------------------------------------------------------------------------
+// quantized GEMV
+// ---------------------------------------------------------------------------------------------
+static int qk_of(int qtype)
+{
+    return qtype == X100_Q4_0 ? 32 : (qtype == X100_Q4_K || qtype == X100_Q3_K) ? 256 : 0;
+}
+
+size_t x100q_gguf_bytes(int qtype, int N, int K)
+{
+    const int qk = qk_of(qtype);
+    if (!qk || N < 0 || K <= 0 || K % qk) return 0;
+    const size_t bb = qtype == X100_Q4_0 ? 18 : qtype == X100_Q4_K ? 144 : 110;
+    return (size_t)N * (K / qk) * bb;
+}
+
+size_t x100q_packed_bytes(int qtype, int N, int K)
+{
+    if (!x100q_gguf_bytes(qtype, N, K)) return 0;
+    return x100_q_packed_bytes(qtype, N, K);
+}
+
+int x100q_pack(int qtype, int N, int K, const void *w_gguf, void *w_packed, void *stream)
+{
+    if (!x100q_gguf_bytes(qtype, N, K) || !w_gguf || !w_packed) return X100_EINVAL;
+    int rc = check_device();
+    if (rc) return rc;
+    hipError_t e = x100_q_pack_launch(qtype, N, K, w_gguf, w_packed, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
+int qgemv_hip(int qtype, int M, int N, int K, const void *w_packed, const float *x, float *y,
+              void *stream)
+{
+    if (!x100q_gguf_bytes(qtype, N, K) || M < 1 || M > 8) return X100_EINVAL;
+    if (N == 0) return X100_OK;
+    if (!w_packed || !x || !y || ((uintptr_t)x & 15) || ((uintptr_t)w_packed & 255)) return X100_EINVAL;
+    int rc = check_device();
+    if (rc) return rc;
+    hipError_t e = x100_qgemv_launch(qtype, M, N, K, w_packed, x, y, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return X100_EINVAL;
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// MoE decode layer
+// ---------------------------------------------------------------------------------------------
+int moe_layer_hip(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                  const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
+                  int *sel, float *sw, void *stream)
+{
+    if (M < 1 || M > 8 || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return X100_EINVAL;
+    if (d <= 0 || ff <= 0 || d % 256 || ff % 256 || d > 4096 || ff > 4096) return X100_EINVAL;
+    if (!hn || !R || !Wg || !Wu || !Wd || !out) return X100_EINVAL;
+    if (((uintptr_t)hn & 15) || ((uintptr_t)R & 15) || ((uintptr_t)Wg & 15) ||
+        ((uintptr_t)Wu & 15) || ((uintptr_t)Wd & 15))
+        return X100_EINVAL;
+    int rc = check_device();
+    if (rc) return rc;
+    void *ws = nullptr;
+    rc = moe_workspace(x100_moe_workspace_bytes(M, d, ff, n_exp, n_act), &ws);
+    if (rc) return rc;
+    hipError_t e = x100_moe_launch(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw,
+                                   ws, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return X100_EINVAL;
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
+}  // extern "C"

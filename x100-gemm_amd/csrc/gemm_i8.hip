@@ -1,0 +1,377 @@
+// int8 x int8 -> int32 GEMM for gfx950:  C[MxN] += A[MxK] . B[KxN], all row-major.
+//
+// Replaces the reference's gemm_ime_i8 (src/gemm_ime_i8.c:60-89) whose IME micro-kernel is a stub
+// that falls back to the scalar gemm_ref_i8 (src/gemm_ref.c:17-26).  Integer arithmetic is exact,
+// so every kernel here is bit-identical to gemm_ref_i8 for any K below 2^17 (|sum| < 2^31).
+//
+// Three kernels:
+//   k_gemm_mfma    tiled MFMA kernel (v_mfma_i32_32x32x32_i8).  A tiles go to LDS row-major with
+//                  an XOR swizzle on 16-byte chunks; B tiles are transposed in registers
+//                  (v_perm_b32) into "k-quad" dwords (4 consecutive k of one column) so that both
+//                  MFMA operands are k-contiguous.  Double-buffered LDS, C loaded into the
+//                  accumulators (C += A.B), XCD-aware grouped tile order.
+//   k_gemm_skinny  M <= 16 rows (speculative-verify shapes): HBM-bound on B.  Split-K over
+//                  256-row chunks, B streamed once through LDS, dot4 on transposed k-quads,
+//                  int32 atomics into C (exact and order independent).
+//   k_gemm_generic any shape / alignment (byte loads); correctness fallback.
+#include "x100_common.h"
+#include "x100_internal.h"
+
+namespace {
+
+constexpr int BK = 64;  // k bytes per pipeline stage
+
+// Tile order: blocks are dealt to the 8 XCDs round-robin, so block b runs on XCD b%8.  Give each
+// XCD a contiguous range of tile ids, and walk tile ids in groups of GROUP_M tile rows so the
+// tiles of one XCD share A row panels and B column panels in its L2.
+X100_DEV void tile_coords(int bid, int nblk, int tiles_m, int tiles_n, int &tm, int &tn)
+{
+    int t = bid;
+    if ((nblk & 7) == 0) t = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    constexpr int GROUP_M = 4;
+    int per_group = GROUP_M * tiles_n;
+    int g = t / per_group;
+    int first_m = g * GROUP_M;
+    int gsize = min(tiles_m - first_m, GROUP_M);
+    int r = t - g * per_group;
+    tm = first_m + r % gsize;
+    tn = r / gsize;
+}
+
+// A tile in LDS: BM rows x 64 bytes; 16-byte chunk c of row r stored at chunk c ^ ((r>>1)&3)
+// so that 8 consecutive lanes reading one chunk column hit 8 distinct 16-byte bank groups.
+X100_DEV int a_lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 3)) << 4); }
+
+template <int FM, int FN, int WM, int WN, bool EDGE>
+__global__ __launch_bounds__(WM *WN * 64) void k_gemm_mfma(int M, int N, int K,
+                                                           const int8_t *__restrict__ A,
+                                                           const int8_t *__restrict__ B,
+                                                           int32_t *__restrict__ C, int tiles_m,
+                                                           int tiles_n)
+{
+    constexpr int NT = WM * WN * 64;
+    constexpr int BM = WM * FM * 32;
+    constexpr int BN = WN * FN * 32;
+    constexpr int A_IT = BM * 4 / NT;             // 16-byte A chunks per thread per stage
+    constexpr int B_UNITS = BN;                   // (k-quad, 16 columns) units per stage
+    constexpr int B_IT = (B_UNITS + NT - 1) / NT;
+    static_assert(A_IT * NT == BM * 4, "A tile must split evenly over the threads");
+
+    __shared__ __attribute__((aligned(16))) int8_t As[2][BM * BK];
+    __shared__ __attribute__((aligned(16))) uint32_t Bs[2][16 * BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int lcol = lane & 31, lgrp = lane >> 5;
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    // EDGE = false is only launched when M % BM == 0, N % BN == 0 and K % BK == 0.
+    const bool full_mn = !EDGE || ((m0 + BM <= M) && (n0 + BN <= N));
+
+    // Accumulators start from C (C += A.B).  32x32 MFMA output layout: lane l, register r holds
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int gn = n0 + wn * FN * 32 + 32 * j + lcol;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int gm = m0 + wm * FM * 32 + 32 * i + 8 * (r >> 2) + 4 * lgrp + (r & 3);
+                acc[i][j][r] = (full_mn || (gm < M && gn < N)) ? C[(size_t)gm * N + gn] : 0;
+            }
+        }
+
+    v4i ra[A_IT];
+    v4i rb[B_IT][4];
+
+    auto gload = [&](int kt) {
+        const int k0 = kt * BK;
+        const bool full = !EDGE || (full_mn && (k0 + BK <= K));
+#pragma unroll
+        for (int p = 0; p < A_IT; p++) {
+            const int ch = tid + p * NT, r = ch >> 2, c = ch & 3;
+            const int gm = m0 + r, gk = k0 + 16 * c;
+            if (full || (gm < M && gk < K))
+                ra[p] = *(const v4i *)(A + (size_t)gm * K + gk);
+            else
+                ra[p] = v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int p = 0; p < B_IT; p++) {
+            const int u = tid + p * NT;
+            if (B_UNITS % NT == 0 || u < B_UNITS) {
+                const int kq = u / (BN / 16), nc = u % (BN / 16);
+                const int gn = n0 + 16 * nc;
+#pragma unroll
+                for (int rr = 0; rr < 4; rr++) {
+                    const int gk = k0 + 4 * kq + rr;
+                    if (full || (gk < K && gn < N))
+                        rb[p][rr] = *(const v4i *)(B + (size_t)gk * N + gn);
+                    else
+                        rb[p][rr] = v4i{0, 0, 0, 0};
+                }
+            }
+        }
+    };
+
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < A_IT; p++) {
+            const int ch = tid + p * NT, r = ch >> 2, c = ch & 3;
+            *(v4i *)(&As[buf][a_lds_off(r, c)]) = ra[p];
+        }
+#pragma unroll
+        for (int p = 0; p < B_IT; p++) {
+            const int u = tid + p * NT;
+            if (B_UNITS % NT == 0 || u < B_UNITS) {
+                const int kq = u / (BN / 16), nc = u % (BN / 16);
+                uint32_t o[16];
+#pragma unroll
+                for (int cg = 0; cg < 4; cg++)
+                    transpose4x4((uint32_t)rb[p][0][cg], (uint32_t)rb[p][1][cg],
+                                 (uint32_t)rb[p][2][cg], (uint32_t)rb[p][3][cg], o[4 * cg + 0],
+                                 o[4 * cg + 1], o[4 * cg + 2], o[4 * cg + 3]);
+                v4u *dst = (v4u *)(&Bs[buf][kq * BN + 16 * nc]);
+                dst[0] = v4u{o[0], o[1], o[2], o[3]};
+                dst[1] = v4u{o[4], o[5], o[6], o[7]};
+                dst[2] = v4u{o[8], o[9], o[10], o[11]};
+                dst[3] = v4u{o[12], o[13], o[14], o[15]};
+            }
+        }
+    };
+
+    const int nk = (K + BK - 1) / BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            v4i af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const int r = wm * FM * 32 + 32 * i + lcol;
+                af[i] = *(const v4i *)(&As[buf][a_lds_off(r, 2 * kk + lgrp)]);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int n = wn * FN * 32 + 32 * j + lcol;
+                const int kq = 8 * kk + 4 * lgrp;
+                const uint32_t *bp = &Bs[buf][kq * BN + n];
+                bf[j] = v4i{(int)bp[0], (int)bp[BN], (int)bp[2 * BN], (int)bp[3 * BN]};
+            }
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int gn = n0 + wn * FN * 32 + 32 * j + lcol;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int gm = m0 + wm * FM * 32 + 32 * i + 8 * (r >> 2) + 4 * lgrp + (r & 3);
+                if (full_mn || (gm < M && gn < N)) C[(size_t)gm * N + gn] = acc[i][j][r];
+            }
+        }
+}
+
+// Skinny GEMM, M <= MR rows.  Block = 4 waves over columns [n0, n0+256) and k rows
+// [k0, k0+256); wave w owns rows k0+64w .. +63.  Each lane streams 16 x 16 bytes of B (one
+// 256-byte row slice per 16 lanes, fully coalesced), the wave stages its 16 KB slice in LDS, then
+// each lane owns 4 columns: it reads 4 rows' dwords, transposes them to k-quads and runs dot4
+// against the A k-quads (wave-uniform LDS broadcast).  The 4 waves' partial sums are reduced in
+// LDS and added to C with int32 atomics.
+template <int MR>
+__global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K,
+                                                    const int8_t *__restrict__ A,
+                                                    const int8_t *__restrict__ B,
+                                                    int32_t *__restrict__ C)
+{
+    __shared__ __attribute__((aligned(16))) uint32_t Bs[4][64 * 64];  // 64 KB: 4 x (64 rows x 256 B)
+    __shared__ __attribute__((aligned(16))) uint32_t As[MR][64];      // A[m][k0..k0+256) as dwords
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n0 = blockIdx.x * 256, k0 = blockIdx.y * 256;
+    const bool full = (n0 + 256 <= N) && (k0 + 256 <= K);
+
+    // Issue all B loads first (16 per lane) so the whole slice is in flight.
+    v4i rb[16];
+    const int nc = lane & 15;
+    const int gn = n0 + 16 * nc;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int gk = k0 + 64 * w + 4 * i + (lane >> 4);
+        if (full || (gk < K && gn < N))
+            rb[i] = *(const v4i *)(B + (size_t)gk * N + gn);
+        else
+            rb[i] = v4i{0, 0, 0, 0};
+    }
+    // A slice (zero padded) into LDS.
+    for (int idx = tid; idx < MR * 64; idx += 256) {
+        const int m = idx >> 6, kq = idx & 63;
+        uint32_t v = 0;
+        if (m < M) {
+            const int gk = k0 + 4 * kq;
+            const int8_t *ap = A + (size_t)m * K + gk;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (gk + e < K) v |= (uint32_t)(uint8_t)ap[e] << (8 * e);
+        }
+        As[m][kq] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int row = 4 * i + (lane >> 4);
+        *(v4i *)(&Bs[w][row * 64 + 4 * nc]) = rb[i];
+    }
+    __syncthreads();
+
+    int acc[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[m][e] = 0;
+
+    const uint32_t *bw = Bs[w];
+#pragma unroll 4
+    for (int kq = 0; kq < 16; kq++) {
+        uint32_t o0, o1, o2, o3;
+        transpose4x4(bw[(4 * kq + 0) * 64 + lane], bw[(4 * kq + 1) * 64 + lane],
+                     bw[(4 * kq + 2) * 64 + lane], bw[(4 * kq + 3) * 64 + lane], o0, o1, o2, o3);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            const int a = (int)As[m][16 * w + kq];
+            acc[m][0] = dot4((int)o0, a, acc[m][0]);
+            acc[m][1] = dot4((int)o1, a, acc[m][1]);
+            acc[m][2] = dot4((int)o2, a, acc[m][2]);
+            acc[m][3] = dot4((int)o3, a, acc[m][3]);
+        }
+    }
+    __syncthreads();
+
+    // Cross-wave reduction through LDS (reuses the B staging area).
+    int *red = (int *)&Bs[0][0];  // [4 waves][MR][256 columns]
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+        *(v4i *)(&red[(w * MR + m) * 256 + 4 * lane]) = v4i{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+    __syncthreads();
+    const int col = n0 + tid;
+    if (col < N) {
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            if (m < M) {
+                int s = red[(0 * MR + m) * 256 + tid] + red[(1 * MR + m) * 256 + tid] +
+                        red[(2 * MR + m) * 256 + tid] + red[(3 * MR + m) * 256 + tid];
+                atomicAdd(&C[(size_t)m * N + col], s);
+            }
+        }
+    }
+}
+
+// Generic fallback: 64x64 tile, 256 threads (4x4 outputs each), 32-deep byte tiles in LDS.
+__global__ __launch_bounds__(256) void k_gemm_generic(int M, int N, int K, const int8_t *__restrict__ A,
+                                                      const int8_t *__restrict__ B,
+                                                      int32_t *__restrict__ C)
+{
+    __shared__ int As[64][33];
+    __shared__ int Bs[32][65];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    int acc[4][4] = {};
+    for (int k0 = 0; k0 < K; k0 += 32) {
+        for (int idx = tid; idx < 64 * 32; idx += 256) {
+            int r = idx >> 5, c = idx & 31;
+            int gm = m0 + r, gk = k0 + c;
+            As[r][c] = (gm < M && gk < K) ? (int)A[(size_t)gm * K + gk] : 0;
+            int kr = idx >> 6, nc2 = idx & 63;
+            int gk2 = k0 + kr, gn = n0 + nc2;
+            Bs[kr][nc2] = (gk2 < K && gn < N) ? (int)B[(size_t)gk2 * N + gn] : 0;
+        }
+        __syncthreads();
+        for (int k = 0; k < 32; k++) {
+            int a[4], b[4];
+            for (int i = 0; i < 4; i++) a[i] = As[ty * 4 + i][k];
+            for (int j = 0; j < 4; j++) b[j] = Bs[k][tx * 4 + j];
+            for (int i = 0; i < 4; i++)
+                for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
+        }
+        __syncthreads();
+    }
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++) {
+            int gm = m0 + ty * 4 + i, gn = n0 + tx * 4 + j;
+            if (gm < M && gn < N) C[(size_t)gm * N + gn] += acc[i][j];
+        }
+}
+
+template <int FM, int FN, int WM, int WN>
+hipError_t launch_mfma(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
+                       hipStream_t s)
+{
+    constexpr int BM = WM * FM * 32, BN = WN * FN * 32;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const bool edge = (M % BM) || (N % BN) || (K % BK);
+    if (edge)
+        hipLaunchKernelGGL((k_gemm_mfma<FM, FN, WM, WN, true>), dim3(tiles_m * tiles_n),
+                           dim3(WM * WN * 64), 0, s, M, N, K, A, B, C, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((k_gemm_mfma<FM, FN, WM, WN, false>), dim3(tiles_m * tiles_n),
+                           dim3(WM * WN * 64), 0, s, M, N, K, A, B, C, tiles_m, tiles_n);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Kernel selection.  Returns the HIP launch status.
+hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
+                               hipStream_t s, int variant)
+{
+    const bool aligned = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) &&
+                         (((uintptr_t)B & 15) == 0) && (((uintptr_t)C & 15) == 0);
+    if (variant == X100_GEMM_AUTO) {
+        if (!aligned)
+            variant = X100_GEMM_GENERIC;
+        else if (M <= 16)
+            variant = X100_GEMM_SKINNY;
+        else if ((long)M * N >= 1024L * 1024L)
+            variant = X100_GEMM_TILE256;
+        else
+            variant = X100_GEMM_TILE128;
+    }
+    if (!aligned && variant != X100_GEMM_GENERIC) return hipErrorInvalidValue;
+    switch (variant) {
+    case X100_GEMM_TILE256:
+        // The 256x256 tile is register-tight; shapes that need edge guards use the 128x128 tile.
+        if (M % 256 || N % 256 || K % BK) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
+        return launch_mfma<4, 4, 2, 2>(M, N, K, A, B, C, s);
+    case X100_GEMM_TILE128: return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
+    case X100_GEMM_SKINNY: {
+        if (M > 16) return hipErrorInvalidValue;
+        dim3 grid((N + 255) / 256, (K + 255) / 256);
+        if (M <= 8)
+            hipLaunchKernelGGL(k_gemm_skinny<8>, grid, dim3(256), 0, s, M, N, K, A, B, C);
+        else
+            hipLaunchKernelGGL(k_gemm_skinny<16>, grid, dim3(256), 0, s, M, N, K, A, B, C);
+        return hipGetLastError();
+    }
+    case X100_GEMM_GENERIC: {
+        dim3 grid((N + 63) / 64, (M + 63) / 64);
+        hipLaunchKernelGGL(k_gemm_generic, grid, dim3(256), 0, s, M, N, K, A, B, C);
+        return hipGetLastError();
+    }
+    }
+    return hipErrorInvalidValue;
+}

@@ -1,0 +1,574 @@
+// Block-quantized dequant-GEMV for gfx950:  y[M][N] = W[N][K] . x[M][K]^T,  M <= 8.
+//
+// Weights are block-quantized (Q4_0, Q4_K, Q3_K); each x row is quantized inside the kernel
+// (Q8_0 for Q4_0, Q8_K for the K-quants) with the same fp32 operations as the scalar path
+// (quantize_q8_0_native, qwen_moe_hp.c:408-414; pack_A_q3k, qwen_moe_q3k.c:612-624), then every
+// block's dot product is done in exact integer arithmetic with v_dot4 and scaled in fp32.
+//
+// At M <= 8 the work is bandwidth bound: every lane issues all of its 16-byte weight loads before
+// it quantizes x, so a block's whole weight slice is in flight at once; no MFMA.
+//
+// Device weight layouts (made once at upload by x100q_pack):
+//   Q4_K  GGUF-native 144-byte blocks (16-byte aligned fields, consumed as is).
+//   Q4_0  split into d[N*K/32] (fp16) and qs[N*K/32][16], so nibble rows are 16-byte aligned.
+//   Q3_K  split into hq[N*K/256][96] (hmask 32 + qs 64), sc[N*K/256][12], d[N*K/256] (fp16).
+// Same byte count as the GGUF blocks (plus alignment padding between the arrays).
+//
+// The K-quant kernels reduce each row in the same order as the scalar oracle (sequential over
+// super-blocks, no fused multiply-add), so their fp32 outputs are bit-identical to it; Q4_0 sums
+// lane partials in a tree (fp32 reassociation only).
+#include "x100_common.h"
+#include "x100_internal.h"
+
+namespace {
+
+// ------------------------------------------------------------------------------------------------
+// In-kernel activation quantizers (x rows -> LDS).
+// ------------------------------------------------------------------------------------------------
+
+// Q8_0 per 32 elements, one element per thread, 32-lane groups (K % 32 == 0).
+// LDS: xlo/xhi [m][nb][16] bytes (elements 0..15 / 16..31), xd [m][nb] (fp16-rounded d as
+// float), xs [m][nb] (sum of q).
+X100_DEV void quantize_q8_0_lds(const float *__restrict__ x, int M, int K, int8_t *xlo,
+                                int8_t *xhi, float *xd, int *xs)
+{
+    const int nb = K / 32;
+    const int tid = threadIdx.x;
+    for (int m = 0; m < M; m++) {
+        for (int e0 = 0; e0 < K; e0 += blockDim.x) {
+            const int e = e0 + tid;
+            const bool in = e < K;  // uniform per 32-lane group because K % 32 == 0
+            const float v = in ? x[(size_t)m * K + e] : 0.0f;
+            float a = fabsf(v);
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+            const float amax = fmaxf(a, 1e-6f);
+            const float d = amax / 127.0f;
+            const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+            const int q = clamp_i8((int)rintf(v * inv));
+            int s = q;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);
+            if (in) {
+                const int b = e >> 5, pos = e & 31;
+                if (pos < 16)
+                    xlo[(m * nb + b) * 16 + pos] = (int8_t)q;
+                else
+                    xhi[(m * nb + b) * 16 + pos - 16] = (int8_t)q;
+                if (pos == 0) {
+                    xd[m * nb + b] = h2f(f2h(d));
+                    xs[m * nb + b] = s;
+                }
+            }
+        }
+    }
+}
+
+// Q8_K per 256 elements: one wave per block, 4 consecutive elements per lane.
+// LDS: xq [m][nsb][256] int8, xbs [m][nsb][16] int, xd [m][nsb] float.
+X100_DEV void quantize_q8_K_rows(const float *__restrict__ x, int M, int K, int8_t *xq, int *xbs,
+                                 float *xd)
+{
+    const int nsb = K / 256;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int blk = w; blk < M * nsb; blk += nw) {
+        const int m = blk / nsb, sb = blk - m * nsb;
+        const float4 v = *(const float4 *)(x + (size_t)m * K + sb * 256 + 4 * lane);
+        float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        const float amax = wave_max_f(a);
+        const float d = amax / 127.0f;
+        const float rep = d != 0.0f ? 1.0f / d : 0.0f;
+        const int q0 = clamp_i8((int)roundf(v.x * rep)), q1 = clamp_i8((int)roundf(v.y * rep));
+        const int q2 = clamp_i8((int)roundf(v.z * rep)), q3 = clamp_i8((int)roundf(v.w * rep));
+        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+        ((uint32_t *)(xq + (size_t)blk * 256))[lane] = packed;
+        int s = q0 + q1 + q2 + q3;
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        if ((lane & 3) == 0) xbs[blk * 16 + (lane >> 2)] = s;
+        if (lane == 0) xd[blk] = d;
+    }
+}
+
+// get_scale_min_k4 (repack.cpp:222-233) on the 12 scale bytes held in dwords s0, s1, s2.
+X100_DEV uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int k)
+{
+    const uint32_t w = k < 4 ? s0 : (k < 8 ? s1 : s2);
+    return (w >> (8 * (k & 3))) & 0xffu;
+}
+X100_DEV void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &m)
+{
+    if (j < 4) {
+        sc = sbyte(s0, s1, s2, j) & 63;
+        m = sbyte(s0, s1, s2, j + 4) & 63;
+    } else {
+        sc = (sbyte(s0, s1, s2, j + 4) & 0xf) | ((sbyte(s0, s1, s2, j - 4) >> 6) << 4);
+        m = (sbyte(s0, s1, s2, j + 4) >> 4) | ((sbyte(s0, s1, s2, j) >> 6) << 4);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Q4_0 x Q8_0
+// ------------------------------------------------------------------------------------------------
+// Block = 4 waves; wave w owns rows row0 + w*RPW .. +RPW-1; lane l owns blocks l, l+64, ...
+// (BPL per row).  All RPW*BPL nibble loads (16 B) and scale loads are issued first.
+template <int MR, int RPW, int BPL>
+__global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_t *__restrict__ wd,
+                                              const uint8_t *__restrict__ wq,
+                                              const float *__restrict__ x, float *__restrict__ y)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nb = K / 32;
+    int8_t *xlo = (int8_t *)smem;
+    int8_t *xhi = xlo + MR * nb * 16;
+    float *xd = (float *)(xhi + MR * nb * 16);
+    int *xs = (int *)(xd + MR * nb);
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int rowb = blockIdx.x * 4 * RPW + w * RPW;
+
+    v4i q[RPW][BPL];
+    uint16_t dwb[RPW][BPL];
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+#pragma unroll
+        for (int c = 0; c < BPL; c++) {
+            const int row = rowb + r, b = lane + 64 * c;
+            if (row < N && b < nb) {
+                const size_t blk = (size_t)row * nb + b;
+                q[r][c] = *(const v4i *)(wq + blk * 16);
+                dwb[r][c] = wd[blk];
+            } else {
+                q[r][c] = v4i{0, 0, 0, 0};
+                dwb[r][c] = 0;
+            }
+        }
+
+    quantize_q8_0_lds(x, M, K, xlo, xhi, xd, xs);
+    __syncthreads();
+
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const int row = rowb + r;
+        float acc[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < BPL; c++) {
+            const int b = lane + 64 * c;
+            if (b < nb) {
+                const v4i qq = q[r][c];
+                const float dwf = h2f(dwb[r][c]);
+                int lo[4], hi[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    lo[t] = qq[t] & 0x0F0F0F0F;
+                    hi[t] = (qq[t] >> 4) & 0x0F0F0F0F;
+                }
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    if (m < M) {
+                        const v4i xl = *(const v4i *)(xlo + (m * nb + b) * 16);
+                        const v4i xh = *(const v4i *)(xhi + (m * nb + b) * 16);
+                        int s = 0;
+#pragma unroll
+                        for (int t = 0; t < 4; t++) {
+                            s = dot4(lo[t], xl[t], s);
+                            s = dot4(hi[t], xh[t], s);
+                        }
+                        s -= 8 * xs[m * nb + b];  // nibble offset: (q-8).x = q.x - 8*sum(x)
+                        acc[m] += (float)s * (dwf * xd[m * nb + b]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            if (m < M) {
+                float v = acc[m];
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+                if (lane == 0 && row < N) y[(size_t)m * N + row] = v;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Q4_K x Q8_K
+// ------------------------------------------------------------------------------------------------
+// Work unit = (row, super-block), 8 lanes per unit: lane i of the unit loads the block header
+// (d, dmin, scales: 16 B) and qs bytes [16i, 16i+16): low nibbles = sub-block 2*(i/2), high
+// nibbles = sub-block 2*(i/2)+1, elements 16*(i%2) .. +15 of each.  A block of R rows has
+// R*nsb units; wave w takes units w*8 + lane/8 + 32*c.
+template <int MR, int UPL>
+__global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R,
+                                              const uint8_t *__restrict__ W,
+                                              const float *__restrict__ x, float *__restrict__ y)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nsb = K / 256;
+    int8_t *xq = (int8_t *)smem;                   // [MR][nsb][256]
+    int *xbs = (int *)(xq + MR * nsb * 256);       // [MR][nsb][16]
+    float *xd = (float *)(xbs + MR * nsb * 16);    // [MR][nsb]
+    float *tv = xd + MR * nsb;                     // [MR][R*nsb]
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int i = lane & 7, p = i >> 1, h = i & 1;
+    const int row0 = blockIdx.x * R;
+    const int nrows = min(R, N - row0);
+    const int U = nrows * nsb;
+
+    v4i hdr[UPL], qs[UPL];
+#pragma unroll
+    for (int c = 0; c < UPL; c++) {
+        const int u = w * 8 + (lane >> 3) + 32 * c;
+        if (u < U) {
+            const uint8_t *blk = W + ((size_t)row0 * nsb + u) * 144;
+            hdr[c] = *(const v4i *)blk;
+            qs[c] = *(const v4i *)(blk + 16 + 16 * i);
+        } else {
+            hdr[c] = v4i{0, 0, 0, 0};
+            qs[c] = v4i{0, 0, 0, 0};
+        }
+    }
+
+    quantize_q8_K_rows(x, M, K, xq, xbs, xd);
+    __syncthreads();
+
+#pragma unroll
+    for (int c = 0; c < UPL; c++) {
+        const int u = w * 8 + (lane >> 3) + 32 * c;
+        const bool valid = u < U;  // uniform over the 8 lanes of a unit
+        const int sb = valid ? u % nsb : 0;
+        const uint32_t h0 = (uint32_t)hdr[c][0];
+        const float d = h2f((uint16_t)(h0 & 0xffff)), dmin = h2f((uint16_t)(h0 >> 16));
+        int sc0, m0, sc1, m1;
+        scale_min_k4(2 * p, (uint32_t)hdr[c][1], (uint32_t)hdr[c][2], (uint32_t)hdr[c][3], sc0, m0);
+        scale_min_k4(2 * p + 1, (uint32_t)hdr[c][1], (uint32_t)hdr[c][2], (uint32_t)hdr[c][3], sc1, m1);
+        int lo[4], hi[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            lo[t] = qs[c][t] & 0x0F0F0F0F;
+            hi[t] = (qs[c][t] >> 4) & 0x0F0F0F0F;
+        }
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            if (m < M) {
+                const int8_t *xb = xq + (m * nsb + sb) * 256;
+                const v4i xa = *(const v4i *)(xb + 64 * p + 16 * h);
+                const v4i xc = *(const v4i *)(xb + 64 * p + 32 + 16 * h);
+                int d0 = 0, d1 = 0;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    d0 = dot4(lo[t], xa[t], d0);
+                    d1 = dot4(hi[t], xc[t], d1);
+                }
+                const int *bs = xbs + (m * nsb + sb) * 16;
+                int isc = sc0 * d0 + sc1 * d1;
+                int imn = m0 * bs[4 * p + h] + m1 * bs[4 * p + 2 + h];
+#pragma unroll
+                for (int o = 1; o < 8; o <<= 1) {
+                    isc += __shfl_xor(isc, o, 64);
+                    imn += __shfl_xor(imn, o, 64);
+                }
+                if (valid && i == 0) {
+                    const float dx = xd[m * nsb + sb];
+                    const float dd = dx * d, dm = dx * dmin;
+                    tv[m * R * nsb + u] = dd * (float)isc - dm * (float)imn;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // Sequential combine over super-blocks (same order and operations as the oracle).
+    for (int t = threadIdx.x; t < MR * nrows; t += blockDim.x) {
+        const int m = t / nrows, r = t - m * nrows;
+        if (m < M) {
+            float acc = 0.0f;
+            for (int sb = 0; sb < nsb; sb++) acc = acc + tv[m * R * nsb + r * nsb + sb];
+            y[(size_t)m * N + row0 + r] = acc;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Q3_K x Q8_K
+// ------------------------------------------------------------------------------------------------
+// Work unit = (row, super-block), 4 lanes per unit: lane i (hh = i/2, lh = i%2) loads qs bytes
+// [32hh + 16lh, +16) and hmask bytes [16lh, +16) and decodes the 64 elements
+// 128hh + 32j + 16lh + (0..15), j = 0..3 (shift 2j, hmask bit 4hh+j, scale index 8hh+2j+lh),
+// as in dequantize_q3_K_block (qwen_moe_q3k.c:565-575).  Wave w takes units w*16 + lane/4 + 64*c.
+template <int MR, int UPL>
+__global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
+                                              const uint8_t *__restrict__ hq,
+                                              const uint8_t *__restrict__ scl,
+                                              const uint16_t *__restrict__ wdd,
+                                              const float *__restrict__ x, float *__restrict__ y)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nsb = K / 256;
+    int8_t *xq = (int8_t *)smem;
+    int *xbs = (int *)(xq + MR * nsb * 256);
+    float *xd = (float *)(xbs + MR * nsb * 16);
+    float *tv = xd + MR * nsb;
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int i = lane & 3, hh = i >> 1, lh = i & 1;
+    const int row0 = blockIdx.x * R;
+    const int nrows = min(R, N - row0);
+    const int U = nrows * nsb;
+
+    v4i qv[UPL], hv[UPL];
+    uint32_t s0[UPL], s1[UPL], s2[UPL];
+    uint16_t dv[UPL];
+#pragma unroll
+    for (int c = 0; c < UPL; c++) {
+        const int u = w * 16 + (lane >> 2) + 64 * c;
+        if (u < U) {
+            const size_t rec = (size_t)row0 * nsb + u;
+            qv[c] = *(const v4i *)(hq + rec * 96 + 32 + 32 * hh + 16 * lh);
+            hv[c] = *(const v4i *)(hq + rec * 96 + 16 * lh);
+            const uint32_t *sp = (const uint32_t *)(scl + rec * 12);
+            s0[c] = sp[0];
+            s1[c] = sp[1];
+            s2[c] = sp[2];
+            dv[c] = wdd[rec];
+        } else {
+            qv[c] = hv[c] = v4i{0, 0, 0, 0};
+            s0[c] = s1[c] = s2[c] = 0;
+            dv[c] = 0;
+        }
+    }
+
+    quantize_q8_K_rows(x, M, K, xq, xbs, xd);
+    __syncthreads();
+
+#pragma unroll
+    for (int c = 0; c < UPL; c++) {
+        const int u = w * 16 + (lane >> 2) + 64 * c;
+        const bool valid = u < U;
+        const int sb = valid ? u % nsb : 0;
+        int scl_j[4];
+        int v[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            // 6-bit scale of sub-block is = 8hh + 2j + lh: low nibble of byte (2j+lh) (hh = 0) or
+            // its high nibble (hh = 1); high 2 bits from byte 8 + is%4 at bit 2*(is/4).
+            const int k = 2 * j + lh;
+            const uint32_t low4 = (sbyte(s0[c], s1[c], s2[c], k) >> (4 * hh)) & 0xf;
+            const int is = 8 * hh + k;
+            const uint32_t high2 = (sbyte(s0[c], s1[c], s2[c], 8 + (is & 3)) >> (2 * (is >> 2))) & 3;
+            scl_j[j] = (int)(low4 | (high2 << 4)) - 32;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t lo2 = ((uint32_t)qv[c][t] >> (2 * j)) & 0x03030303u;
+                const uint32_t hb = ((uint32_t)hv[c][t] >> (4 * hh + j)) & 0x01010101u;
+                v[j][t] = (int)(lo2 | (hb << 2));   // 3-bit value q + 4, q in [-4, 3]
+            }
+        }
+        const float dw = h2f(dv[c]);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            if (m < M) {
+                const int8_t *xb = xq + (m * nsb + sb) * 256 + 128 * hh + 16 * lh;
+                const int *bs = xbs + (m * nsb + sb) * 16 + 8 * hh + lh;
+                int isc = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const v4i xv = *(const v4i *)(xb + 32 * j);
+                    int dsum = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) dsum = dot4(v[j][t], xv[t], dsum);
+                    dsum -= 4 * bs[2 * j];
+                    isc += scl_j[j] * dsum;
+                }
+                isc += __shfl_xor(isc, 1, 64);
+                isc += __shfl_xor(isc, 2, 64);
+                if (valid && i == 0) {
+                    const float dx = xd[m * nsb + sb];
+                    tv[m * R * nsb + u] = (dx * dw) * (float)isc;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    for (int t = threadIdx.x; t < MR * nrows; t += blockDim.x) {
+        const int m = t / nrows, r = t - m * nrows;
+        if (m < M) {
+            float acc = 0.0f;
+            for (int sb = 0; sb < nsb; sb++) acc = acc + tv[m * R * nsb + r * nsb + sb];
+            y[(size_t)m * N + row0 + r] = acc;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Weight packing (GGUF-native blocks -> device layout)
+// ------------------------------------------------------------------------------------------------
+__global__ void k_pack_q4_0(size_t nblk, const uint8_t *__restrict__ src, uint16_t *__restrict__ d,
+                            uint8_t *__restrict__ qs)
+{
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    const uint8_t *s = src + b * 18;
+    d[b] = (uint16_t)(s[0] | (s[1] << 8));
+    uint8_t *o = qs + b * 16;
+#pragma unroll
+    for (int j = 0; j < 16; j++) o[j] = s[2 + j];
+}
+
+__global__ void k_pack_q3_K(size_t nblk, const uint8_t *__restrict__ src, uint8_t *__restrict__ hq,
+                            uint8_t *__restrict__ scl, uint16_t *__restrict__ d)
+{
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    const uint8_t *s = src + b * 110;
+    for (int j = 0; j < 96; j++) hq[b * 96 + j] = s[j];
+    for (int j = 0; j < 12; j++) scl[b * 12 + j] = s[96 + j];
+    d[b] = (uint16_t)(s[108] | (s[109] << 8));
+}
+
+constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------
+// Host-side layout helpers and launchers
+// ------------------------------------------------------------------------------------------------
+size_t x100_q_packed_bytes(int qtype, int N, int K)
+{
+    switch (qtype) {
+    case X100_Q4_0: {
+        const size_t nblk = (size_t)N * (K / 32);
+        return align256(nblk * 2) + nblk * 16;
+    }
+    case X100_Q4_K: return (size_t)N * (K / 256) * 144;
+    case X100_Q3_K: {
+        const size_t nblk = (size_t)N * (K / 256);
+        return nblk * 96 + nblk * 12 + nblk * 2;
+    }
+    }
+    return 0;
+}
+
+hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *dst, hipStream_t s)
+{
+    switch (qtype) {
+    case X100_Q4_0: {
+        const size_t nblk = (size_t)N * (K / 32);
+        uint16_t *d = (uint16_t *)dst;
+        uint8_t *qs = (uint8_t *)dst + align256(nblk * 2);
+        hipLaunchKernelGGL(k_pack_q4_0, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, nblk,
+                           (const uint8_t *)src, d, qs);
+        return hipGetLastError();
+    }
+    case X100_Q4_K:
+        return hipMemcpyAsync(dst, src, (size_t)N * (K / 256) * 144, hipMemcpyDeviceToDevice, s);
+    case X100_Q3_K: {
+        const size_t nblk = (size_t)N * (K / 256);
+        uint8_t *hq = (uint8_t *)dst;
+        uint8_t *scl = hq + nblk * 96;
+        uint16_t *d = (uint16_t *)(scl + nblk * 12);
+        hipLaunchKernelGGL(k_pack_q3_K, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, nblk,
+                           (const uint8_t *)src, hq, scl, d);
+        return hipGetLastError();
+    }
+    }
+    return hipErrorInvalidValue;
+}
+
+namespace {
+
+template <int MR>
+hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
+{
+    const int nb = K / 32;
+    const size_t nblk = (size_t)N * nb;
+    const uint16_t *wd = (const uint16_t *)w;
+    const uint8_t *wq = (const uint8_t *)w + align256(nblk * 2);
+    const size_t lds = (size_t)MR * nb * 40;
+    constexpr int RPW = 4;
+    const dim3 grid((N + 4 * RPW - 1) / (4 * RPW));
+    if (nb <= 64)
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, 1>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+    else if (nb <= 128)
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, 2>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+    else if (nb <= 256)
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, 4>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+    else
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, 8>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+    return hipGetLastError();
+}
+
+// One K-quant launch with a compile-time number of work units per lane.
+template <int MR, int UPL>
+hipError_t launch_kq_upl(int qtype, dim3 grid, size_t lds, int M, int N, int K, int R, const void *w,
+                         const float *x, float *y, hipStream_t s)
+{
+    if (qtype == X100_Q4_K) {
+        hipLaunchKernelGGL((k_q4_K<MR, UPL>), grid, dim3(256), lds, s, M, N, K, R,
+                           (const uint8_t *)w, x, y);
+    } else {
+        const size_t nblk = (size_t)N * (K / 256);
+        const uint8_t *hq = (const uint8_t *)w;
+        const uint8_t *scl = hq + nblk * 96;
+        const uint16_t *dd = (const uint16_t *)(scl + nblk * 12);
+        hipLaunchKernelGGL((k_q3_K<MR, UPL>), grid, dim3(256), lds, s, M, N, K, R, hq, scl, dd, x, y);
+    }
+    return hipGetLastError();
+}
+
+// Rows per block R for the K-quant kernels: about 256 blocks, each lane holding UPL <= 8 units
+// (Q4_K: 8 lanes per unit, Q3_K: 4 lanes per unit).
+template <int MR, int LANES_PER_UNIT>
+hipError_t launch_kq(int qtype, int M, int N, int K, const void *w, const float *x, float *y,
+                     hipStream_t s)
+{
+    const int nsb = K / 256;
+    constexpr int UNITS_PER_PASS = 256 / LANES_PER_UNIT;
+    int R = (N + 255) / 256;
+    if (R < 1) R = 1;
+    if (R * nsb > 8 * UNITS_PER_PASS) R = (8 * UNITS_PER_PASS) / nsb;
+    if (R < 1) return hipErrorInvalidValue;  // a single row does not fit in one pass
+    int upl = (R * nsb + UNITS_PER_PASS - 1) / UNITS_PER_PASS;
+    const dim3 grid((N + R - 1) / R);
+    const size_t lds = (size_t)MR * nsb * (256 + 64 + 4) + (size_t)MR * R * nsb * 4;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if (upl <= 1) return launch_kq_upl<MR, 1>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    if (upl <= 2) return launch_kq_upl<MR, 2>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    if (upl <= 3) return launch_kq_upl<MR, 3>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    if (upl <= 4) return launch_kq_upl<MR, 4>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    if (upl <= 6) return launch_kq_upl<MR, 6>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    return launch_kq_upl<MR, 8>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+}
+
+}  // namespace
+
+hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, const float *x, float *y,
+                             hipStream_t s)
+{
+    if (M < 1 || M > 8) return hipErrorInvalidValue;
+    if (qtype == X100_Q4_0) {
+        if (K % 32 || K / 32 > 512) return hipErrorInvalidValue;
+        if ((size_t)(M <= 1 ? 1 : (M <= 4 ? 4 : 8)) * (K / 32) * 40 > 160 * 1024) return hipErrorInvalidValue;
+        if (M == 1) return launch_q4_0<1>(M, N, K, w, x, y, s);
+        if (M <= 4) return launch_q4_0<4>(M, N, K, w, x, y, s);
+        return launch_q4_0<8>(M, N, K, w, x, y, s);
+    }
+    if (qtype == X100_Q4_K || qtype == X100_Q3_K) {
+        if (K % 256) return hipErrorInvalidValue;
+        if (qtype == X100_Q4_K) {
+            if (M == 1) return launch_kq<1, 8>(qtype, M, N, K, w, x, y, s);
+            if (M <= 4) return launch_kq<4, 8>(qtype, M, N, K, w, x, y, s);
+            return launch_kq<8, 8>(qtype, M, N, K, w, x, y, s);
+        }
+        if (M == 1) return launch_kq<1, 4>(qtype, M, N, K, w, x, y, s);
+        if (M <= 4) return launch_kq<4, 4>(qtype, M, N, K, w, x, y, s);
+        return launch_kq<8, 4>(qtype, M, N, K, w, x, y, s);
+    }
+    return hipErrorInvalidValue;
+}

@@ -1,0 +1,25 @@
+// Internal launch interfaces between the C-ABI layer (capi.hip) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+enum {
+    X100_GEMM_AUTO = 0,
+    X100_GEMM_TILE256 = 1,
+    X100_GEMM_TILE128 = 2,
+    X100_GEMM_SKINNY = 3,
+    X100_GEMM_GENERIC = 4,
+};
+
+hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
+                               hipStream_t s, int variant);
+
+size_t x100_q_packed_bytes(int qtype, int N, int K);
+hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *dst, hipStream_t s);
+hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, const float *x, float *y,
+                             hipStream_t s);
+
+size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act);
+hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
+                           int *sel, float *sw, void *workspace, hipStream_t s);

@@ -1,0 +1,116 @@
+"""Deterministic synthetic inputs for the quantized matrix-product path.
+
+One generator family for every workload: splitmix64 for uniform bits, Box-Muller for N(0,1).
+The same seeds give the same bytes in tests, bench.py and smoke().  Block layouts are the
+GGUF-native ones (Q4_0 18 B / 32, Q4_K 144 B / 256, Q3_K 110 B / 256).
+
+Workloads (sizes as named by the reference's measured shapes):
+  int8 GEMM    A (MxK), B (KxN) i.i.d. uniform int8 in [-128, 127]
+  Q4_0 weight  per 32-block: fp16 d = |N(0,1)|*0.01, 16 random bytes of nibbles
+  Q4_K weight  per 256-block: fp16 d, dmin = |N(0,1)|*0.01, 12 random scale bytes, 128 nibble bytes
+  Q3_K weight  per 256-block: 32 hmask + 64 qs + 12 scale random bytes, fp16 d = |N(0,1)|*0.01
+  activations  fp32 N(0,1);  MoE router fp32 N(0, 0.02)
+"""
+import numpy as np
+
+_GOLD = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+
+Q4_0, Q3_K, Q4_K = 2, 11, 12
+BLOCK_BYTES = {Q4_0: 18, Q4_K: 144, Q3_K: 110}
+BLOCK_ELEMS = {Q4_0: 32, Q4_K: 256, Q3_K: 256}
+
+DT_Q4_0 = np.dtype([("d", "<u2"), ("qs", "u1", (16,))])
+DT_Q4_K = np.dtype([("d", "<u2"), ("dmin", "<u2"), ("scales", "u1", (12,)), ("qs", "u1", (128,))])
+DT_Q3_K = np.dtype([("hmask", "u1", (32,)), ("qs", "u1", (64,)), ("scales", "u1", (12,)), ("d", "<u2")])
+assert DT_Q4_0.itemsize == 18 and DT_Q4_K.itemsize == 144 and DT_Q3_K.itemsize == 110
+
+
+def splitmix64(seed, n):
+    """n consecutive splitmix64 outputs for a 64-bit seed (uint64 array)."""
+    with np.errstate(over="ignore"):
+        i = np.arange(1, n + 1, dtype=np.uint64)
+        z = np.uint64(seed & 0xFFFFFFFFFFFFFFFF) + i * _GOLD
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        return z ^ (z >> np.uint64(31))
+
+
+def rand_bytes(seed, n):
+    """n uniform random bytes (uint8)."""
+    words = splitmix64(seed, (n + 7) // 8)
+    return words.view(np.uint8)[:n].copy()
+
+
+def rand_int8(seed, shape):
+    n = int(np.prod(shape))
+    return rand_bytes(seed, n).view(np.int8).reshape(shape)
+
+
+def rand_normal(seed, n):
+    """n standard normals (float64) by Box-Muller on 53-bit uniforms."""
+    m = (n + 1) // 2
+    z = splitmix64(seed, 2 * m)
+    u1 = (z[0::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+    u2 = (z[1::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+    r = np.sqrt(-2.0 * np.log1p(-u1))
+    t = 2.0 * np.pi * u2
+    out = np.empty(2 * m, dtype=np.float64)
+    out[0::2] = r * np.cos(t)
+    out[1::2] = r * np.sin(t)
+    return out[:n]
+
+
+def normal_f32(seed, shape, std=1.0):
+    n = int(np.prod(shape))
+    return (rand_normal(seed, n) * std).astype(np.float32).reshape(shape)
+
+
+def _scale_f16(seed, n):
+    return (np.abs(rand_normal(seed, n)) * 0.01).astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+def gemm_inputs(M, N, K, seed=2026):
+    """A (MxK) and B (KxN) int8 uniform in [-128, 127]."""
+    return rand_int8(seed, (M, K)), rand_int8(seed + 1, (K, N))
+
+
+def quant_weight(qtype, N, K, seed):
+    """N x K weight matrix as GGUF-native blocks: structured array of shape (N, K // QK)."""
+    qk = BLOCK_ELEMS[qtype]
+    if K % qk:
+        raise ValueError("K must be a multiple of %d" % qk)
+    nb = N * (K // qk)
+    if qtype == Q4_0:
+        w = np.zeros(nb, dtype=DT_Q4_0)
+        w["d"] = _scale_f16(seed, nb)
+        w["qs"] = rand_bytes(seed + 1, nb * 16).reshape(nb, 16)
+    elif qtype == Q4_K:
+        w = np.zeros(nb, dtype=DT_Q4_K)
+        w["d"] = _scale_f16(seed, nb)
+        w["dmin"] = _scale_f16(seed + 1, nb)
+        w["scales"] = rand_bytes(seed + 2, nb * 12).reshape(nb, 12)
+        w["qs"] = rand_bytes(seed + 3, nb * 128).reshape(nb, 128)
+    elif qtype == Q3_K:
+        w = np.zeros(nb, dtype=DT_Q3_K)
+        w["hmask"] = rand_bytes(seed + 2, nb * 32).reshape(nb, 32)
+        w["qs"] = rand_bytes(seed + 3, nb * 64).reshape(nb, 64)
+        w["scales"] = rand_bytes(seed + 4, nb * 12).reshape(nb, 12)
+        w["d"] = _scale_f16(seed, nb)
+    else:
+        raise ValueError("unsupported qtype %r" % qtype)
+    return w.reshape(N, K // qk)
+
+
+def moe_weights(n_exp, d, ff, seed):
+    """Expert tensors in the ggml 3-D layout (experts outermost), Q4_K:
+    gate, up: (n_exp, ff, d/256) blocks; down: (n_exp, d, ff/256) blocks."""
+    wg = quant_weight(Q4_K, n_exp * ff, d, seed).reshape(n_exp, ff, d // 256)
+    wu = quant_weight(Q4_K, n_exp * ff, d, seed + 100).reshape(n_exp, ff, d // 256)
+    wd = quant_weight(Q4_K, n_exp * d, ff, seed + 200).reshape(n_exp, d, ff // 256)
+    return wg, wu, wd
+
+
+def moe_router(n_exp, d, seed):
+    return normal_f32(seed, (n_exp, d), std=0.02)

@@ -1,0 +1,144 @@
+"""ctypes binding of libx100hip.so (the C ABI declared in include/x100_*.h).
+
+Thin host-side mirror used by the tests, bench.py and smoke(): every call goes straight to the
+gfx950 kernels through the C entry points; there is no CPU fallback.  Device memory and streams
+come from the caller (torch tensors are convenient: pass tensor.data_ptr() and
+torch.cuda.current_stream().cuda_stream).
+
+Entry points and what they replace in the reference:
+  gemm_ime_i8 / gemm_hip_i8 / gemm_hip_i8_dev   include/x100_gemm.h:60-61 (C += A*B, int8->int32)
+  qgemv_hip (+ x100q_pack)                      lin_mm of qwen_moe.c:101-107 on Q4_0/Q4_K/Q3_K
+  moe_layer_hip                                 the MoE block of qwen_moe.c:294-311
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libx100hip.so")
+
+Q4_0, Q3_K, Q4_K = 2, 11, 12
+
+X100_OK, X100_EINVAL, X100_ENODEV, X100_EHIP, X100_ENOMEM = 0, -1, -2, -3, -4
+
+# Every symbol declared in include/x100_gemm.h, x100_qgemv.h, x100_moe.h.
+EXPORTS = (
+    "gemm_ime_i8", "gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant",
+    "x100_hip_detect", "x100_hip_caps_print", "x100_hip_strerror",
+    "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip",
+    "moe_layer_hip",
+)
+
+GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC = 0, 1, 2, 3, 4
+
+
+class X100Error(RuntimeError):
+    def __init__(self, fn, code, text):
+        super().__init__("%s failed: %d (%s)" % (fn, code, text))
+        self.code = code
+
+
+class Caps(ctypes.Structure):
+    _fields_ = [
+        ("device", ctypes.c_int), ("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64),
+        ("cu_count", ctypes.c_int), ("clock_khz", ctypes.c_int), ("hbm_bytes", ctypes.c_size_t),
+        ("lds_bytes", ctypes.c_int), ("l2_bytes", ctypes.c_int), ("is_gfx950", ctypes.c_int),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    """Load libx100hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError("libx100hip.so not built: run __graft_entry__.build() "
+                                "(make -C x100-gemm_amd)")
+    L = ctypes.CDLL(LIB_PATH)
+    i, p, sz = ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+    L.gemm_ime_i8.argtypes = [i, i, i, p, p, p]
+    L.gemm_ime_i8.restype = None
+    L.gemm_hip_i8.argtypes = [i, i, i, p, p, p]
+    L.gemm_hip_i8_dev.argtypes = [i, i, i, p, p, p, p]
+    L.gemm_hip_i8_dev_variant.argtypes = [i, i, i, p, p, p, p, i]
+    L.x100_hip_detect.argtypes = [ctypes.POINTER(Caps)]
+    L.x100_hip_caps_print.argtypes = [ctypes.POINTER(Caps)]
+    L.x100_hip_caps_print.restype = None
+    L.x100_hip_strerror.argtypes = [i]
+    L.x100_hip_strerror.restype = ctypes.c_char_p
+    L.x100q_gguf_bytes.argtypes = [i, i, i]
+    L.x100q_gguf_bytes.restype = sz
+    L.x100q_packed_bytes.argtypes = [i, i, i]
+    L.x100q_packed_bytes.restype = sz
+    L.x100q_pack.argtypes = [i, i, i, p, p, p]
+    L.qgemv_hip.argtypes = [i, i, i, i, p, p, p, p]
+    L.moe_layer_hip.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p]
+    for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant", "x100_hip_detect",
+                 "x100q_pack", "qgemv_hip", "moe_layer_hip"):
+        getattr(L, name).restype = i
+    _lib = L
+    return L
+
+
+def _check(fn, rc):
+    if rc != X100_OK:
+        raise X100Error(fn, rc, lib().x100_hip_strerror(rc).decode())
+    return rc
+
+
+def strerror(code):
+    return lib().x100_hip_strerror(code).decode()
+
+
+def caps():
+    c = Caps()
+    _check("x100_hip_detect", lib().x100_hip_detect(ctypes.byref(c)))
+    return c
+
+
+# ---- int8 GEMM ---------------------------------------------------------------------------------
+def gemm_dev(M, N, K, dA, dB, dC, stream=None, variant=GEMM_AUTO):
+    """C += A*B on device pointers (ints); asynchronous on stream."""
+    return _check("gemm_hip_i8_dev_variant",
+                  lib().gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, variant))
+
+
+def gemm_host(A, B, C):
+    """Drop-in host path: C (int32, MxN) += A (int8, MxK) . B (int8, KxN), numpy arrays."""
+    M, K = A.shape
+    K2, N = B.shape
+    assert K == K2 and C.shape == (M, N)
+    A = np.ascontiguousarray(A, dtype=np.int8)
+    B = np.ascontiguousarray(B, dtype=np.int8)
+    assert C.dtype == np.int32 and C.flags.c_contiguous
+    return _check("gemm_hip_i8", lib().gemm_hip_i8(M, N, K, A.ctypes.data, B.ctypes.data,
+                                                   C.ctypes.data))
+
+
+# ---- quantized GEMV ----------------------------------------------------------------------------
+def gguf_bytes(qtype, N, K):
+    return lib().x100q_gguf_bytes(qtype, N, K)
+
+
+def packed_bytes(qtype, N, K):
+    return lib().x100q_packed_bytes(qtype, N, K)
+
+
+def pack(qtype, N, K, d_src, d_dst, stream=None):
+    return _check("x100q_pack", lib().x100q_pack(qtype, N, K, d_src, d_dst, stream))
+
+
+def qgemv(qtype, M, N, K, d_w, d_x, d_y, stream=None):
+    return _check("qgemv_hip", lib().qgemv_hip(qtype, M, N, K, d_w, d_x, d_y, stream))
+
+
+# ---- MoE layer ---------------------------------------------------------------------------------
+def moe_layer(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residual=False,
+              d_sel=None, d_sw=None, stream=None):
+    return _check("moe_layer_hip",
+                  lib().moe_layer_hip(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out,
+                                      1 if residual else 0, d_sel, d_sw, stream))
