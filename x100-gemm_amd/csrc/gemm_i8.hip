@@ -188,6 +188,241 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm_mfma(int M, int N, int K,
         }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Large-tile kernel: 256x256 output tile per block, NW waves (2 x NW/2; 8 waves = two per SIMD,
+// 128x64 each), K step 64.
+//
+// * Operands reach LDS by direct global->LDS DMA (global_load_lds_dwordx4: lane l's 16 bytes land
+//   at M0 + 16*l), through a 4-stage ring refilled as soon as a stage is consumed; the loads are
+//   issued from inline asm so the compiler does not drain them at every barrier, and each
+//   iteration waits with an exact s_waitcnt vmcnt for the stage it is about to read.
+// * A tile: 256 rows x 64 bytes, 16-byte chunk c of row r stored at chunk big_a_chunk(r, c);
+//   fragments read with ds_read_b128 (k-contiguous rows, conflict-free).
+// * B tile: 64 k-rows x 256 bytes, row-major as in memory, chunk c of k-row k stored at
+//   big_b_chunk(k, c);
+//   fragments read with ds_read_b64_tr_b8 (lane c of each 16-lane group receives column c of an
+//   8x16 byte block), two reads give the 16 consecutive k of one column that MFMA wants.
+// * MFMA operands are swapped (B fragment first) so the accumulator holds C^T: each lane owns
+//   4 consecutive C columns per register quad, and C is read and written 16 bytes at a time.
+// * C += A.B: the accumulators start at zero; the old C is prefetched a quarter of the tile at a
+//   time (before the K loop, then at 1/4, 1/2, 3/4 of it) and added when the next quarter is
+//   fetched, so C reads overlap the MFMA work.
+// Requires M % 256 == 0, N % 256 == 0, K % 64 == 0, K >= 512, 16-byte aligned pointers.
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+
+X100_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(const lds_u8 *)p; }
+
+// LDS swizzles for a 64-bank (256 bytes per cycle) LDS: ds_read_b128 serves 16 lanes and
+// ds_read_b64_tr_b8 32 lanes per cycle, so those lanes must hit distinct 16-byte granules of a
+// 256-byte bank row.
+//   A (64-byte rows): 16 consecutive rows, same chunk c -> granule 4*(r&3) + (c ^ ((r>>2)&3)).
+//   B (256-byte k-rows): 8 consecutive k, chunks c and c+1 (c even) -> c ^ 2*(k&7) and its ^1.
+X100_DEV int big_a_chunk(int r, int c) { return c ^ ((r >> 2) & 3); }
+X100_DEV int big_b_chunk(int k, int c) { return c ^ (2 * (k & 7)); }
+
+X100_DEV void dma16(const void *gsrc, uint32_t lds_base)
+{
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(gsrc)
+                 : "memory", "m0");
+}
+
+template <int N> X100_DEV void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// Wait until at most n of this wave's vector-memory operations are outstanding.
+X100_DEV void wait_vmcnt_le(int n)
+{
+    // Largest listed count <= n (waiting for more completions than needed is always safe).
+    if (n >= 56) wait_vmcnt<56>();
+    else if (n >= 48) wait_vmcnt<48>();
+    else if (n >= 40) wait_vmcnt<40>();
+    else if (n >= 32) wait_vmcnt<32>();
+    else if (n >= 24) wait_vmcnt<24>();
+    else if (n >= 16) wait_vmcnt<16>();
+    else if (n >= 12) wait_vmcnt<12>();
+    else if (n >= 8) wait_vmcnt<8>();
+    else if (n >= 4) wait_vmcnt<4>();
+    else wait_vmcnt<0>();
+}
+
+X100_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const int8_t *__restrict__ A,
+                                                     const int8_t *__restrict__ B,
+                                                     int32_t *__restrict__ C, int tiles_m, int tiles_n)
+{
+    // NW waves as 2 x NW/2; each wave owns 128 rows x FN*32 columns of the 256x256 tile.
+    constexpr int NS = 4, STAGE = 32768, BOFF = 16384;
+    constexpr int WN = NW / 2, FN = 8 / WN;   // column fragments per wave
+    constexpr int OPS = 16 / NW;              // DMA ops per wave per operand per stage
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wm = w / WN, wn = w % WN, lcol = lane & 31, lgrp = lane >> 5;
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * 256, n0 = tn * 256;
+    const int nk = K / 64;
+
+    // DMA sources: A op p covers tile rows 16*(NW*p+w) .. +15 (lane -> row lane/4, chunk lane%4),
+    // B op p covers k-rows 4*(NW*p+w) .. +3 (lane -> row lane/16, chunk lane%16); each lane fetches
+    // the logical chunk whose swizzled position is its own.
+    const int8_t *Ab = A + (size_t)m0 * K;
+    const int8_t *Bb = B + n0;
+    uint32_t aoff[OPS], boff[OPS];
+#pragma unroll
+    for (int p = 0; p < OPS; p++) {
+        const int ra = 16 * (NW * p + w) + (lane >> 2);
+        aoff[p] = (uint32_t)(ra * K + 16 * big_a_chunk(ra, lane & 3));
+        const int rb = 4 * (NW * p + w) + (lane >> 4);
+        boff[p] = (uint32_t)(rb * N + 16 * big_b_chunk(rb, lane & 15));
+    }
+    const uint32_t sbase = lds_addr(smem);
+    auto issue = [&](int kt) {
+        const uint32_t sb = sbase + (uint32_t)((kt & (NS - 1)) * STAGE);
+        const int8_t *ak = Ab + (size_t)kt * 64;
+        const int8_t *bk = Bb + (size_t)kt * 64 * N;
+#pragma unroll
+        for (int p = 0; p < OPS; p++)
+            dma16(ak + aoff[p], __builtin_amdgcn_readfirstlane(sb + (uint32_t)(16 * (NW * p + w) * 64)));
+#pragma unroll
+        for (int p = 0; p < OPS; p++)
+            dma16(bk + boff[p], __builtin_amdgcn_readfirstlane(sb + BOFF + (uint32_t)(4 * (NW * p + w) * 256)));
+    };
+
+    // C prefetch by quarters: quarter i = accumulator row-tile i (C rows crow0 + 32i); the lane
+    // holds C[row][col .. col+3] for col = ccol0 + 32j + 8q.
+    v4i cbuf[FN][4];
+    const int crow0 = m0 + wm * 128 + lcol;
+    const int ccol0 = n0 + wn * FN * 32 + 4 * lgrp;
+    auto load_c = [&](int i) {  // i may be a run-time value: one base pointer, immediate offsets
+        const int32_t *cp = C + (size_t)(crow0 + 32 * i) * N + ccol0;
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) cbuf[j][q] = *(const v4i *)(cp + 32 * j + 8 * q);
+    };
+
+    v16i acc[4][FN];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+    auto add_c = [&](int i) {
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    // Integer add written as asm: a plain += makes the register allocator move
+                    // all 256 accumulators out of AGPRs (and spill); this keeps them resident.
+                    int x = acc[i][j][4 * q + p];
+                    asm volatile("v_add_u32 %0, %0, %1" : "+v"(x) : "v"(cbuf[j][q][p]));
+                    acc[i][j][4 * q + p] = x;
+                }
+    };
+
+    // B fragment addressing for ds_read_b64_tr_b8: 16-lane group G = lane/16 covers columns
+    // 16*(G&1) .. +15 of the 32-column fragment and k-rows 16*(G>>1) + 8t + (lane%16)/2.
+    const int q16 = lane & 15, r8 = q16 >> 1, h8 = q16 & 1, ch = (lane >> 4) & 1;
+    auto read_frags = [&](int slot, int kk, v4i (&af)[4], v4i (&bf)[FN]) {
+        const uint8_t *As = smem + slot * STAGE;
+        const uint8_t *Bs = As + BOFF;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = wm * 128 + 32 * i + lcol;
+            af[i] = *(const v4i *)(As + r * 64 + 16 * big_a_chunk(r, 2 * kk + lgrp));
+        }
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int c = 2 * FN * wn + 2 * j + ch;
+            const int k0 = 32 * kk + 16 * lgrp + r8;
+            const uint8_t *p0 = Bs + k0 * 256 + 16 * big_b_chunk(r8, c) + 8 * h8;
+            const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(const lds_u8 *)p0);
+            const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(const lds_u8 *)(p0 + 8 * 256));
+            bf[j] = v4i{lo.x, lo.y, hi.x, hi.y};
+        }
+    };
+    auto mma = [&](const v4i (&af)[4], const v4i (&bf)[FN]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+    };
+
+    // Software pipeline.  Iteration kt: read k-half 1 of stage kt, MFMAs on k-half 0; wait for
+    // stage kt+1 and barrier (all waves are then done reading stage kt, whose slot is refilled
+    // with stage kt+4); read k-half 0 of stage kt+1; MFMAs on k-half 1.  LDS reads are always
+    // one MFMA group ahead of their use.
+    // C quarter q is added at the end of loop segment q (segments end at nk/4, nk/2, 3nk/4, nk),
+    // when quarter q+1 is prefetched.
+    const int ev1 = nk / 4, ev2 = nk / 2, ev3 = 3 * nk / 4;
+    constexpr int DPS = 2 * OPS;   // DMA ops per wave per stage
+    constexpr int CQ = 4 * FN;     // C loads per wave per quarter
+    // Vector-memory operations of this wave issued after stage s+1's DMAs when iteration s waits
+    // for them: stages s+2 and s+3 (if they exist), C quarter 0 (issued after the prologue's 4
+    // stages) and C quarters issued at the end of iterations before s.
+    auto pending_after = [&](int s) {
+        int n = DPS * min(2, nk - 2 - s);
+        if (s <= 2) {
+            n += CQ;
+            n += (ev1 - 1 <= s - 1 ? CQ : 0) + (ev2 - 1 <= s - 1 ? CQ : 0) + (ev3 - 1 <= s - 1 ? CQ : 0);
+        } else {
+            n += (ev1 - 1 >= s - 3 && ev1 - 1 <= s - 1) ? CQ : 0;
+            n += (ev2 - 1 >= s - 3 && ev2 - 1 <= s - 1) ? CQ : 0;
+            n += (ev3 - 1 >= s - 3 && ev3 - 1 <= s - 1) ? CQ : 0;
+        }
+        return n;
+    };
+    v4i a0[4], b0[FN], a1[4], b1[FN];
+    auto step = [&](int kt) {
+        read_frags(kt & (NS - 1), 1, a1, b1);
+        mma(a0, b0);
+        if (kt + 1 < nk) {
+            wait_vmcnt_le(pending_after(kt));
+            lds_barrier();
+            if (kt + 4 < nk) issue(kt + 4);
+            read_frags((kt + 1) & (NS - 1), 0, a0, b0);
+        }
+        mma(a1, b1);
+    };
+    issue(0);
+    issue(1);
+    issue(2);
+    issue(3);
+    load_c(0);
+    wait_vmcnt_le(3 * DPS + CQ);
+    lds_barrier();
+    read_frags(0, 0, a0, b0);
+    for (int kt = 0; kt < ev1; kt++) step(kt);
+    add_c(0);
+    load_c(1);
+    for (int kt = ev1; kt < ev2; kt++) step(kt);
+    add_c(1);
+    load_c(2);
+    for (int kt = ev2; kt < ev3; kt++) step(kt);
+    add_c(2);
+    load_c(3);
+    for (int kt = ev3; kt < nk; kt++) step(kt);
+    add_c(3);
+
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                *(v4i *)(C + (size_t)(crow0 + 32 * i) * N + ccol0 + 32 * j + 8 * q) =
+                    v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+}
+
 // Skinny GEMM, M <= MR rows.  Block = 4 waves over columns [n0, n0+256) and k rows
 // [k0, k0+256); wave w owns rows k0+64w .. +63.  Each lane streams 16 x 16 bytes of B (one
 // 256-byte row slice per 16 lanes, fully coalesced), the wave stages its 16 KB slice in LDS, then
@@ -353,10 +588,14 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
     }
     if (!aligned && variant != X100_GEMM_GENERIC) return hipErrorInvalidValue;
     switch (variant) {
-    case X100_GEMM_TILE256:
-        // The 256x256 tile is register-tight; shapes that need edge guards use the 128x128 tile.
-        if (M % 256 || N % 256 || K % BK) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
-        return launch_mfma<4, 4, 2, 2>(M, N, K, A, B, C, s);
+    case X100_GEMM_TILE256: {
+        // Full 256x256 tiles only; other shapes use the 128x128 tile with edge guards.
+        if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
+        const int tiles_m = M / 256, tiles_n = N / 256;
+        hipLaunchKernelGGL(k_gemm_big<8>, dim3(tiles_m * tiles_n), dim3(512), 0, s, M, N, K, A, B, C,
+                           tiles_m, tiles_n);
+        return hipGetLastError();
+    }
     case X100_GEMM_TILE128: return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
     case X100_GEMM_SKINNY: {
         if (M > 16) return hipErrorInvalidValue;
