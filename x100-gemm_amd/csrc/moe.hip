@@ -1,25 +1,24 @@
 // Qwen3-MoE decode layer (the FFN block of qwen_moe.c:294-311) for M <= 8 token rows.
 //
-//   k_moe_route    router logits R.hn (one wave per expert), Q8_K of every hn row; the last
-//                  block to finish does softmax / top-k / renormalise per row and groups the
-//                  (row, slot) pairs by expert (the expert union, as ggml MUL_MAT_ID does,
-//                  ime.cpp:667-697).
-//   k_moe_gate_up  one block per (selected expert, 8 rows of ff): streams those rows of the
-//                  expert's gate and up matrices once for all rows that chose it (Q4_K x Q8_K),
-//                  SwiGLU, writes the activation; the last block of an expert quantizes its
-//                  activations to Q8_K.
-//   k_moe_down     one block per (selected expert, 16 rows of d): down projection of every pair
-//                  of that expert; the last block of a row range combines the slots of each token
-//                  row in slot order a = 0..n_act-1 (out += w_a * y_a), so results do not depend
-//                  on block scheduling.
-// Completion is counted with device-scope atomics and fences; no block ever waits for another.
+// Four launches on one stream; each kernel only reads what an earlier launch wrote, so no block
+// ever waits for, or signals, another block (no fences, no atomics):
+//   k_moe_route    router logits R.hn (one wave per expert) and the Q8_K form of every hn row.
+//   k_moe_gate_up  grid (union slot, GU_ROWS rows of ff).  Every block re-derives softmax, top-k
+//                  and the expert union from the logits (a few hundred flops per row, cheaper
+//                  than another launch), then streams its GU_ROWS rows of the expert's gate and
+//                  up matrices once for all token rows that chose the expert (Q4_K x Q8_K, the
+//                  MUL_MAT_ID grouping of ime.cpp:667-697) and writes SwiGLU(g, u) per pair.
+//                  Block (0, 0) also publishes the routing (sel, sw, union) for the next launches.
+//   k_moe_down     grid (union slot, DN_ROWS rows of d).  Quantizes the expert's activation rows
+//                  (Q8_K, in LDS), down projection, writes y per (token row, slot) pair.
+//   k_moe_combine  out[m] (+)= sum over slots a = 0..n_act-1 of w_a * y_a, in slot order.
 #include "x100_common.h"
 #include "x100_internal.h"
 
 namespace {
 
-constexpr int GU_ROWS = 8;    // gate/up rows per block
-constexpr int DN_ROWS = 16;   // down rows per block
+constexpr int GU_ROWS = 8;    // gate/up rows of ff per block
+constexpr int DN_ROWS = 16;   // down rows of d per block
 
 // Workspace layout (device memory owned by the library, sized by x100_moe_workspace_bytes).
 struct MoeWs {
@@ -29,38 +28,32 @@ struct MoeWs {
     int *nuniq;           // [1]
     int *uniq;            // [P]          expert id of union slot u (P = M*n_act)
     int *ucnt;            // [P]          pairs in union slot u
-    int *upairs;          // [P][8]       pair ids (m*n_act + a) of union slot u
-    int8_t *xq;           // [M][d/256][256]
-    int *xbs;             // [M][d/256][16]
-    float *xd;            // [M][d/256]
+    int *upairs;          // [P][8]       pair ids (m*n_act + a) of union slot u, m ascending
+    uint8_t *xrec;        // [M][rec]: Q8_K of hn row m = q[nsb][256] | bsum[nsb][16] (int) |
+                          // d[nsb] (float), rec = that size rounded up to 16 bytes
     float *act;           // [P][ff]
-    int8_t *aq;           // [P][ff/256][256]
-    int *abs_;            // [P][ff/256][16]
-    float *ad;            // [P][ff/256]
     float *ydn;           // [P][d]
-    int *cnt_route;       // [1]
-    int *cnt_gu;          // [P]
-    int *cnt_dn;          // [d/DN_ROWS]
 };
 
 inline size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Quantize one 256-element block to Q8_K with one wave (same operations as pack_A_q3k).
-X100_DEV void q8k_block_wave(const float *src, int8_t *qs, int *bs, float *dout)
+// Bytes of one row's Q8_K record (nsb 256-element blocks).
+X100_DEV __host__ inline int q8k_rec_bytes(int nsb) { return (nsb * (256 + 64 + 4) + 15) & ~15; }
+
+// Quantize one 256-element block to Q8_K with one wave (same operations as pack_A_q3k): v is the
+// lane's float4 (elements 4*lane .. 4*lane+3).
+X100_DEV void q8k_wave(const float4 v, int8_t *qs, int *bs, float *dout)
 {
     const int lane = threadIdx.x & 63;
-    const float4 v = *(const float4 *)(src + 4 * lane);
-    float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    const float amax = wave_max_f(a);
+    const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    const float amax = wave_max_u(a);
     const float d = amax / 127.0f;
     const float rep = d != 0.0f ? 1.0f / d : 0.0f;
     const int q0 = clamp_i8((int)roundf(v.x * rep)), q1 = clamp_i8((int)roundf(v.y * rep));
     const int q2 = clamp_i8((int)roundf(v.z * rep)), q3 = clamp_i8((int)roundf(v.w * rep));
     ((uint32_t *)qs)[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
                              ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-    int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    const int s = sum4_i(q0 + q1 + q2 + q3);
     if ((lane & 3) == 0) bs[lane >> 2] = s;
     if (lane == 0) *dout = d;
 }
@@ -99,13 +92,8 @@ X100_DEV void q4k_unit_dot(const v4i &hdr, const v4i &qs, const int8_t *xq256, c
         d0 = dot4(qs[t] & 0x0F0F0F0F, xa[t], d0);
         d1 = dot4((qs[t] >> 4) & 0x0F0F0F0F, xc[t], d1);
     }
-    isc = sc0 * d0 + sc1 * d1;
-    imn = m0 * bs16[4 * p + h] + m1 * bs16[4 * p + 2 + h];
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-        isc += __shfl_xor(isc, o, 64);
-        imn += __shfl_xor(imn, o, 64);
-    }
+    isc = sum8_i(sc0 * d0 + sc1 * d1);
+    imn = sum8_i(m0 * bs16[4 * p + h] + m1 * bs16[4 * p + 2 + h]);
 }
 
 X100_DEV float q4k_combine(const v4i &hdr, float dx, int isc, int imn)
@@ -123,60 +111,85 @@ X100_DEV float swiglu(float g, float u)
 }
 
 // ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, int n_act,
-                                                   const float *__restrict__ hn,
-                                                   const float *__restrict__ R, MoeWs ws,
-                                                   int *__restrict__ sel_out,
-                                                   float *__restrict__ sw_out)
+// Router.  Waves 0 .. n_exp-1 compute one expert's logits for all M rows (qwen_moe.c:296; lane l
+// sums elements 4l..4l+3, +256, ... in order, then a butterfly over the lanes); waves n_exp ..
+// n_exp + M*d/256 - 1 quantize one 256-element block of hn to Q8_K.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, const float *__restrict__ hn,
+                                                   const float *__restrict__ R, MoeWs ws)
 {
-    __shared__ int s_last;
-    __shared__ int s_sel[8 * 8];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    float4 *s_hn = (float4 *)smem;   // [M][d/4]
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int nsb = d / 256;
 
-    // Router logits, one wave per expert (qwen_moe.c:296).
-    const int e = blockIdx.x * 4 + w;
-    if (e < n_exp) {
-        const float *rw = R + (size_t)e * d;
+    // The wave's router row (clamped expert; elements past d read as 0 and are not used).
+    const int e = min(wave, n_exp - 1);
+    const rsrc_t rr = buf_rsrc(R + (size_t)e * d, (uint32_t)d * 4u);
+    float4 rv[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
+
+    // hn -> LDS (all M rows; M*d/256 chunks of 1 KiB, one wave each), asynchronous.
+    for (int ch = threadIdx.x >> 6; ch < M * nsb; ch += 4)
+        dma_1k(hn + (size_t)ch * 256 + 4 * lane, smem + ch * 1024);
+    __syncthreads();
+
+    if (wave < n_exp) {
         for (int m = 0; m < M; m++) {
-            const float *h = hn + (size_t)m * d;
+            const float4 *h = s_hn + m * (d / 4);
             float s = 0.0f;
-            for (int k = 4 * lane; k < d; k += 256) {
-                const float4 a = *(const float4 *)(rw + k);
-                const float4 b = *(const float4 *)(h + k);
-                s += a.x * b.x;
-                s += a.y * b.y;
-                s += a.z * b.z;
-                s += a.w * b.w;
-            }
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if (j < nsb) {
+                    const float4 hv = h[lane + 64 * j];
+                    s += rv[j].x * hv.x;
+                    s += rv[j].y * hv.y;
+                    s += rv[j].z * hv.z;
+                    s += rv[j].w * hv.w;
+                }
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-            if (lane == 0) ws.logits[m * n_exp + e] = s;
+            if (lane == 0) ws.logits[m * n_exp + wave] = s;
         }
+    } else if (wave < n_exp + M * nsb) {
+        const int q = wave - n_exp, m = q / nsb, sb = q - m * nsb;
+        uint8_t *rec = ws.xrec + (size_t)m * q8k_rec_bytes(nsb);
+        q8k_wave(s_hn[q * 64 + lane], (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16,
+                 (float *)(rec + nsb * 320) + sb);
     }
-    // Q8_K of the hn rows (input of every expert's gate/up).
-    for (int q = blockIdx.x * 4 + w; q < M * nsb; q += gridDim.x * 4)
-        q8k_block_wave(hn + (size_t)q * 256, ws.xq + (size_t)q * 256, ws.xbs + q * 16, ws.xd + q);
+}
 
-    __threadfence();  // every thread releases its own writes before the block is counted
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(ws.cnt_route, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+// ------------------------------------------------------------------------------------------------
+// Routing of all M rows from the logits, computed identically by every gate/up block.
+// Softmax over all experts (max-subtract, exp, times 1/sum; lane l of a wave holds experts
+// l, l+64, l+128, l+192 and the sum is lane-partial then butterfly), top-n_act by repeated
+// argmax with the lower expert id kept on ties (qwen_moe.c:298-300), renormalise (:301).
+// Outputs in LDS: s_sel/s_w [M][n_act] (slot order), s_uniq[U] = distinct experts ascending.
+// ------------------------------------------------------------------------------------------------
+struct RouteLds {
+    int sel[8 * 8];
+    float w[8 * 8];
+    int uniq[64];
+    int wcnt[4];
+    int U;
+};
 
-    // Softmax over all experts, top-n_act by repeated argmax (ties -> lower index), renormalise
-    // (qwen_moe.c:298-301).  One wave per token row; lane l holds experts l, l+64, l+128, l+192.
+X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     for (int m = w; m < M; m += 4) {
         float p[4];
         float mx = -1e30f;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int ex = lane + 64 * c;
-            p[c] = ex < n_exp ? ws.logits[m * n_exp + ex] : -1e30f;
+            const float lv = logits[m * n_exp + min(ex, n_exp - 1)];   // unconditional load
+            p[c] = ex < n_exp ? lv : -1e30f;
             mx = fmaxf(mx, p[c]);
         }
-        mx = wave_max_f(mx);
+        mx = wave_max_u(mx);
         float s = 0.0f;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -194,22 +207,17 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, int 
             const float pv = p[c] * inv;
             p[c] = (lane + 64 * c) < n_exp ? (pv == pv ? pv : 0.0f) : -2.0f;
         }
-
         float wsel[8];
         int isel[8];
         for (int a = 0; a < n_act; a++) {
-            float bv = -1.0f;
-            int bi = 0x7fffffff;
+            // Largest probability (DPP maximum), then the lowest expert id holding it: experts
+            // lane + 64c, so the first c whose ballot is non-empty, its lowest lane.
+            const float bv = wave_max_u(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])));
+            int bi = 0;
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int ex = lane + 64 * c;
-                if (p[c] > bv) { bv = p[c]; bi = ex; }   // c ascending: lower index kept on ties
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const int oi = __shfl_xor(bi, o, 64);
-                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            for (int c = 3; c >= 0; c--) {
+                const uint64_t hit = __ballot(p[c] == bv);
+                if (hit) bi = 64 * c + __ffsll((unsigned long long)hit) - 1;
             }
             wsel[a] = bv;
             isel[a] = bi;
@@ -221,52 +229,74 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, int 
             float ssum = 0.0f;
             for (int a = 0; a < n_act; a++) ssum += wsel[a];
             for (int a = 0; a < n_act; a++) {
-                const float wv = wsel[a] / ssum;
-                s_sel[m * n_act + a] = isel[a];
-                ws.sel[m * n_act + a] = isel[a];
-                ws.sw[m * n_act + a] = wv;
-                if (sel_out) sel_out[m * n_act + a] = isel[a];
-                if (sw_out) sw_out[m * n_act + a] = wv;
+                rl.sel[m * n_act + a] = isel[a];
+                rl.w[m * n_act + a] = wsel[a] / ssum;
             }
         }
     }
     __syncthreads();
-    // Expert union: union slot per distinct expert, with the (row, slot) pairs that use it.
-    if (threadIdx.x == 0) {
-        int U = 0;
-        for (int pr = 0; pr < M * n_act; pr++) {
-            const int ex = s_sel[pr];
-            int u = 0;
-            while (u < U && ws.uniq[u] != ex) u++;
-            if (u == U) {
-                ws.uniq[U] = ex;
-                ws.ucnt[U] = 0;
-                U++;
-            }
-            if (ws.ucnt[u] < 8) {   // distinct experts per row => at most M <= 8 pairs
-                ws.upairs[u * 8 + ws.ucnt[u]] = pr;
-                ws.ucnt[u]++;
-            }
-        }
-        *ws.nuniq = U;
-        *ws.cnt_route = 0;
+    // Union slots in ascending expert id: slot of expert e = number of selected experts below e.
+    bool chosen = false;
+    for (int t = 0; t < M * n_act; t++) chosen |= rl.sel[t] == (int)threadIdx.x;
+    const uint64_t bal = __ballot(chosen);
+    if (lane == 0) rl.wcnt[w] = __popcll(bal);
+    __syncthreads();
+    if (chosen) {
+        int slot = __popcll(bal & ((1ull << lane) - 1ull));
+        for (int v = 0; v < w; v++) slot += rl.wcnt[v];
+        rl.uniq[slot] = threadIdx.x;
     }
+    if (threadIdx.x == 0) rl.U = rl.wcnt[0] + rl.wcnt[1] + rl.wcnt[2] + rl.wcnt[3];
+    __syncthreads();
 }
 
 // ------------------------------------------------------------------------------------------------
 // grid (U_max, ff / GU_ROWS).  Units (matrix g/u, row, super-block) = 2*GU_ROWS*nsb, 8 lanes each.
+// ------------------------------------------------------------------------------------------------
 template <int UPL>
-__global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n_act,
+__global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
                                                      const uint8_t *__restrict__ Wg,
-                                                     const uint8_t *__restrict__ Wu, MoeWs ws)
+                                                     const uint8_t *__restrict__ Wu, MoeWs ws,
+                                                     int *__restrict__ sel_out, float *__restrict__ sw_out)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int s_pairs[8], s_cnt, s_last;
-    const int u = blockIdx.x;
-    if (u >= *ws.nuniq) return;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, i = lane & 7;
+    __shared__ RouteLds rl;
+    __shared__ int s_pairs[8], s_cnt;
     const int nsb = d / 256;
-    const int ex = ws.uniq[u], cnt = ws.ucnt[u];
+    const int rec = q8k_rec_bytes(nsb);
+
+    // Q8_K records of all M hn rows -> LDS [M][rec], asynchronous (1 KiB chunks, one wave each;
+    // sources clamped to the records, the LDS area is padded to whole chunks).
+    const int totv = M * rec / 16;
+    for (int ch = threadIdx.x >> 6; ch * 64 < totv; ch += 4)
+        dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
+
+    route_block(M, n_exp, n_act, ws.logits, rl);
+    const int u = blockIdx.x;
+    const int U = rl.U;
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        const int t = threadIdx.x;
+        if (t < M * n_act) {
+            ws.sel[t] = rl.sel[t];
+            ws.sw[t] = rl.w[t];
+            if (sel_out) sel_out[t] = rl.sel[t];
+            if (sw_out) sw_out[t] = rl.w[t];
+        }
+        if (t < U) {
+            const int ex = rl.uniq[t];
+            int c = 0;
+            for (int m = 0; m < M; m++)
+                for (int a = 0; a < n_act; a++)
+                    if (rl.sel[m * n_act + a] == ex) ws.upairs[t * 8 + c++] = m * n_act + a;
+            ws.uniq[t] = ex;
+            ws.ucnt[t] = c;
+        }
+        if (t == 0) *ws.nuniq = U;
+    }
+    if (u >= U) return;
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, i = lane & 7;
+    const int ex = rl.uniq[u];
     const int r0 = blockIdx.y * GU_ROWS;
     const int nunits = 2 * GU_ROWS * nsb;
     const size_t erow = (size_t)nsb * 144;               // bytes per row
@@ -275,40 +305,28 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
     v4i hdr[UPL], qs[UPL];
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int un = c * 32 + w * 8 + (lane >> 3);
-        if (un < nunits) {
-            const int mat = un / (GU_ROWS * nsb), rem = un - mat * GU_ROWS * nsb;
-            const int r = rem / nsb, sb = rem - r * nsb;
-            const uint8_t *blk = (mat ? Wu : Wg) + ex * emat + (size_t)(r0 + r) * erow + sb * 144;
-            hdr[c] = *(const v4i *)blk;
-            qs[c] = *(const v4i *)(blk + 16 + 16 * i);
-        } else {
-            hdr[c] = qs[c] = v4i{0, 0, 0, 0};
-        }
+        // Unconditional loads (unit clamped; results of units beyond nunits are discarded), so
+        // every load of the lane is in flight before the first one is waited for.
+        const int un = min(c * 32 + w * 8 + (lane >> 3), nunits - 1);
+        const int mat = un / (GU_ROWS * nsb), rem = un - mat * GU_ROWS * nsb;
+        const int r = rem / nsb, sb = rem - r * nsb;
+        const uint8_t *blk = (mat ? Wu : Wg) + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
+        hdr[c] = *(const v4i *)blk;
+        qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
     }
 
-    // Q8_K of the hn rows of this expert's pairs -> LDS.
-    int8_t *xq = (int8_t *)smem;                    // [8][nsb][256]
-    int *xbs = (int *)(xq + 8 * nsb * 256);         // [8][nsb][16]
-    float *xd = (float *)(xbs + 8 * nsb * 16);      // [8][nsb]
-    float *tv = xd + 8 * nsb;                       // [8][2][GU_ROWS][nsb]
-    if (threadIdx.x < 8) s_pairs[threadIdx.x] = threadIdx.x < cnt ? ws.upairs[u * 8 + threadIdx.x] : 0;
-    if (threadIdx.x == 0) s_cnt = cnt;
-    __syncthreads();
-    for (int t = threadIdx.x; t < cnt * nsb * 64; t += 256) {
-        const int k = t / (nsb * 64), rem = t - k * nsb * 64;
-        const int m = s_pairs[k] / n_act;
-        ((uint32_t *)xq)[k * nsb * 64 + rem] = ((const uint32_t *)ws.xq)[m * nsb * 64 + rem];
-    }
-    for (int t = threadIdx.x; t < cnt * nsb * 16; t += 256) {
-        const int k = t / (nsb * 16), rem = t - k * nsb * 16;
-        xbs[k * nsb * 16 + rem] = ws.xbs[(s_pairs[k] / n_act) * nsb * 16 + rem];
-    }
-    for (int t = threadIdx.x; t < cnt * nsb; t += 256) {
-        const int k = t / nsb, rem = t - k * nsb;
-        xd[k * nsb + rem] = ws.xd[(s_pairs[k] / n_act) * nsb + rem];
+    // Pairs (token row m, slot a) of this expert, m ascending (distinct experts per row, so at
+    // most one slot per row).
+    if (threadIdx.x == 0) {
+        int c = 0;
+        for (int m = 0; m < M; m++)
+            for (int a = 0; a < n_act; a++)
+                if (rl.sel[m * n_act + a] == ex) s_pairs[c++] = m * n_act + a;
+        s_cnt = c;
     }
     __syncthreads();
+    const int cnt = s_cnt;
+    float *tv = (float *)(smem + ((size_t)M * rec + 1023) / 1024 * 1024);   // [8][2][GU_ROWS][nsb]
 
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
@@ -316,9 +334,12 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
         const bool valid = un < nunits;
         const int sb = valid ? un % nsb : 0;
         for (int k = 0; k < cnt; k++) {
+            const uint8_t *xr = smem + (size_t)(s_pairs[k] / n_act) * rec;
             int isc, imn;
-            q4k_unit_dot(hdr[c], qs[c], xq + (k * nsb + sb) * 256, xbs + (k * nsb + sb) * 16, i, isc, imn);
-            if (valid && i == 0) tv[k * 2 * GU_ROWS * nsb + un] = q4k_combine(hdr[c], xd[k * nsb + sb], isc, imn);
+            q4k_unit_dot(hdr[c], qs[c], (const int8_t *)xr + sb * 256, (const int *)(xr + nsb * 256) + sb * 16,
+                         i, isc, imn);
+            if (valid && i == 0)
+                tv[k * 2 * GU_ROWS * nsb + un] = q4k_combine(hdr[c], ((const float *)(xr + nsb * 320))[sb], isc, imn);
         }
     }
     __syncthreads();
@@ -333,39 +354,23 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
         for (int sb = 0; sb < nsb; sb++) up = up + tu[sb];
         ws.act[(size_t)s_pairs[k] * ff + r0 + r] = swiglu(g, up);
     }
-
-    // The last block of this expert quantizes the expert's activations to Q8_K.
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(&ws.cnt_gu[u], 1) == (int)gridDim.y - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int nsf = ff / 256;
-    for (int q = w; q < s_cnt * nsf; q += 4) {
-        const int k = q / nsf, sb = q - k * nsf;
-        const int pr = s_pairs[k];
-        q8k_block_wave(ws.act + (size_t)pr * ff + sb * 256, ws.aq + ((size_t)pr * nsf + sb) * 256,
-                       ws.abs_ + (pr * nsf + sb) * 16, ws.ad + pr * nsf + sb);
-    }
-    if (threadIdx.x == 0) ws.cnt_gu[u] = 0;
 }
 
 // ------------------------------------------------------------------------------------------------
 // grid (U_max, d / DN_ROWS).  Units (row, super-block) = DN_ROWS*nsf, 8 lanes each.
+// ------------------------------------------------------------------------------------------------
 template <int UPL>
-__global__ __launch_bounds__(256) void k_moe_down(int M, int d, int ff, int n_act,
-                                                  const uint8_t *__restrict__ Wd, MoeWs ws,
-                                                  float *__restrict__ out, int residual)
+__global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *__restrict__ Wd, MoeWs ws)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int s_pairs[8], s_last;
     const int u = blockIdx.x;
+    // Union slot metadata in one round trip (entries of slots >= U are stale and unused).
     const int U = *ws.nuniq;
+    const int ex = ws.uniq[u], cnt = ws.ucnt[u];
+    const int prl = ws.upairs[u * 8 + (threadIdx.x & 7)];   // lane l holds pair l % 8 of the slot
     if (u >= U) return;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, i = lane & 7;
     const int nsf = ff / 256;
-    const int ex = ws.uniq[u], cnt = ws.ucnt[u];
     const int r0 = blockIdx.y * DN_ROWS;
     const int nunits = DN_ROWS * nsf;
     const size_t erow = (size_t)nsf * 144;
@@ -374,35 +379,44 @@ __global__ __launch_bounds__(256) void k_moe_down(int M, int d, int ff, int n_ac
     v4i hdr[UPL], qs[UPL];
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int un = c * 32 + w * 8 + (lane >> 3);
-        if (un < nunits) {
-            const int r = un / nsf, sb = un - r * nsf;
-            const uint8_t *blk = Wd + ex * emat + (size_t)(r0 + r) * erow + sb * 144;
-            hdr[c] = *(const v4i *)blk;
-            qs[c] = *(const v4i *)(blk + 16 + 16 * i);
-        } else {
-            hdr[c] = qs[c] = v4i{0, 0, 0, 0};
-        }
+        const int un = min(c * 32 + w * 8 + (lane >> 3), nunits - 1);   // clamped, as in gate/up
+        const int r = un / nsf, sb = un - r * nsf;
+        const uint8_t *blk = Wd + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
+        hdr[c] = *(const v4i *)blk;
+        qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
     }
 
+    // Q8_K of this expert's activation rows (one wave per 256-element block) -> LDS.
     int8_t *aq = (int8_t *)smem;                    // [8][nsf][256]
     int *abs_ = (int *)(aq + 8 * nsf * 256);        // [8][nsf][16]
     float *ad = (float *)(abs_ + 8 * nsf * 16);     // [8][nsf]
     float *tv = ad + 8 * nsf;                       // [8][DN_ROWS][nsf]
-    if (threadIdx.x < 8) s_pairs[threadIdx.x] = threadIdx.x < cnt ? ws.upairs[u * 8 + threadIdx.x] : 0;
-    __syncthreads();
-    for (int t = threadIdx.x; t < cnt * nsf * 64; t += 256) {
-        const int k = t / (nsf * 64), rem = t - k * nsf * 64;
-        ((uint32_t *)aq)[k * nsf * 64 + rem] = ((const uint32_t *)ws.aq)[s_pairs[k] * nsf * 64 + rem];
+    // 16 blocks per pass (4 per wave), each pass's loads issued before its math; the first pass is
+    // straight-line code so that its loads go out right behind the weight loads.
+    const int nq = cnt * nsf;
+    float4 v[4];
+#define X100_ACT_LOADS(q0)                                                                        \
+    _Pragma("unroll") for (int j = 0; j < 4; j++) {                                               \
+        const int q = min((q0) + 4 * j + w, nq - 1); /* clamped; only q < nq is used */           \
+        const int k = q / nsf, sb = q - k * nsf;                                                  \
+        v[j] = *(const float4 *)(ws.act + (size_t)__builtin_amdgcn_readlane(prl, k) * ff + sb * 256 + 4 * lane); \
     }
-    for (int t = threadIdx.x; t < cnt * nsf * 16; t += 256) {
-        const int k = t / (nsf * 16), rem = t - k * nsf * 16;
-        abs_[k * nsf * 16 + rem] = ws.abs_[s_pairs[k] * nsf * 16 + rem];
+#define X100_ACT_QUANT(q0)                                                                        \
+    _Pragma("unroll") for (int j = 0; j < 4; j++) {                                               \
+        const int q = (q0) + 4 * j + w;                                                           \
+        if (q < nq) q8k_wave(v[j], aq + q * 256, abs_ + q * 16, ad + q);                          \
     }
-    for (int t = threadIdx.x; t < cnt * nsf; t += 256) {
-        const int k = t / nsf, rem = t - k * nsf;
-        ad[k * nsf + rem] = ws.ad[s_pairs[k] * nsf + rem];
+    X100_ACT_LOADS(0)
+    __builtin_amdgcn_sched_barrier(0);
+    X100_ACT_QUANT(0)
+    for (int q0 = 16; q0 < nq; q0 += 16) {
+        X100_ACT_LOADS(q0)
+        X100_ACT_QUANT(q0)
     }
+#undef X100_ACT_LOADS
+#undef X100_ACT_QUANT
+    __shared__ int s_pr[8];
+    if (threadIdx.x < 8) s_pr[threadIdx.x] = prl;
     __syncthreads();
 
 #pragma unroll
@@ -421,32 +435,37 @@ __global__ __launch_bounds__(256) void k_moe_down(int M, int d, int ff, int n_ac
         const int k = t / DN_ROWS, r = t - k * DN_ROWS;
         float y = 0.0f;
         for (int sb = 0; sb < nsf; sb++) y = y + tv[k * nunits + r * nsf + sb];
-        ws.ydn[(size_t)s_pairs[k] * d + r0 + r] = y;
+        ws.ydn[(size_t)s_pr[k] * d + r0 + r] = y;
     }
+}
 
-    // The last expert block of this row range combines the slots in order (qwen_moe.c:310-311).
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(&ws.cnt_dn[blockIdx.y], 1) == U - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int t = threadIdx.x; t < M * DN_ROWS; t += 256) {
-        const int m = t / DN_ROWS, r = t - m * DN_ROWS;
-        const int row = r0 + r;
-        float eo = 0.0f;
-        for (int a = 0; a < n_act; a++)
-            eo = eo + ws.sw[m * n_act + a] * ws.ydn[(size_t)(m * n_act + a) * d + row];
-        float *o = out + (size_t)m * d + row;
-        *o = residual ? *o + eo : eo;
-    }
-    if (threadIdx.x == 0) ws.cnt_dn[blockIdx.y] = 0;
+// ------------------------------------------------------------------------------------------------
+// out[m][j] (+)= sum_a sw[m][a] * y[m*n_act + a][j], a ascending (qwen_moe.c:310-311).
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_moe_combine(int M, int d, int n_act, MoeWs ws,
+                                                     float *__restrict__ out, int residual)
+{
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= M * d) return;
+    const int m = t / d, j = t - m * d;
+    float wv[8], yv[8];
+#pragma unroll
+    for (int a = 0; a < 8; a++)
+        if (a < n_act) {
+            wv[a] = ws.sw[m * n_act + a];
+            yv[a] = ws.ydn[(size_t)(m * n_act + a) * d + j];
+        }
+    float eo = 0.0f;
+#pragma unroll
+    for (int a = 0; a < 8; a++)
+        if (a < n_act) eo = eo + wv[a] * yv[a];
+    out[t] = residual ? out[t] + eo : eo;
 }
 
 MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *total)
 {
     const int P = M * n_act;
-    const int nsb = d / 256, nsf = ff / 256;
+    const int nsb = d / 256;
     size_t off = 0;
     MoeWs ws;
     auto take = [&](size_t bytes) {
@@ -454,10 +473,6 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
         off += al(bytes);
         return r;
     };
-    // Counters first so that a zero-filled fresh workspace has them at 0.
-    ws.cnt_route = (int *)take(sizeof(int));
-    ws.cnt_gu = (int *)take(sizeof(int) * 64);
-    ws.cnt_dn = (int *)take(sizeof(int) * 4096);
     ws.logits = (float *)take(sizeof(float) * M * n_exp);
     ws.sel = (int *)take(sizeof(int) * P);
     ws.sw = (float *)take(sizeof(float) * P);
@@ -465,13 +480,8 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     ws.uniq = (int *)take(sizeof(int) * P);
     ws.ucnt = (int *)take(sizeof(int) * P);
     ws.upairs = (int *)take(sizeof(int) * P * 8);
-    ws.xq = (int8_t *)take((size_t)M * nsb * 256);
-    ws.xbs = (int *)take(sizeof(int) * M * nsb * 16);
-    ws.xd = (float *)take(sizeof(float) * M * nsb);
+    ws.xrec = (uint8_t *)take((size_t)M * q8k_rec_bytes(nsb));
     ws.act = (float *)take(sizeof(float) * (size_t)P * ff);
-    ws.aq = (int8_t *)take((size_t)P * nsf * 256);
-    ws.abs_ = (int *)take(sizeof(int) * P * nsf * 16);
-    ws.ad = (float *)take(sizeof(float) * P * nsf);
     ws.ydn = (float *)take(sizeof(float) * (size_t)P * d);
     if (total) *total = off;
     return ws;
@@ -491,27 +501,29 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
                            int *sel, float *sw, void *workspace, hipStream_t s)
 {
     if (M < 1 || M > 8 || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return hipErrorInvalidValue;
-    if (d % 256 || ff % 256 || d / DN_ROWS > 4096 || d % DN_ROWS || ff % GU_ROWS) return hipErrorInvalidValue;
+    if (d % 256 || ff % 256 || d > 4096 || ff > 4096 || d % DN_ROWS || ff % GU_ROWS) return hipErrorInvalidValue;
     const int nsb = d / 256, nsf = ff / 256;
     if (2 * GU_ROWS * nsb > 8 * 32 || DN_ROWS * nsf > 8 * 32) return hipErrorInvalidValue;
     MoeWs ws = carve((uintptr_t)workspace, M, d, ff, n_exp, n_act, nullptr);
     const int Umax = min(M * n_act, n_exp);
 
-    hipLaunchKernelGGL(k_moe_route, dim3((n_exp + 3) / 4), dim3(256), 0, s, M, d, n_exp, n_act, hn, R,
-                       ws, sel, sw);
+    const int nwaves = n_exp + M * nsb;
+    hipLaunchKernelGGL(k_moe_route, dim3((nwaves + 3) / 4), dim3(256), (size_t)M * d * 4, s, M, d, n_exp, hn, R, ws);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
 
-    const size_t lds_gu = (size_t)8 * nsb * (256 + 64 + 4) + (size_t)8 * 2 * GU_ROWS * nsb * 4;
+    const size_t lds_gu = ((size_t)M * q8k_rec_bytes(nsb) + 1023) / 1024 * 1024 + (size_t)8 * 2 * GU_ROWS * nsb * 4;
     const int upl_gu = (2 * GU_ROWS * nsb + 31) / 32;
     const dim3 g_gu(Umax, ff / GU_ROWS);
     const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
+#define X100_GU(U) hipLaunchKernelGGL(k_moe_gate_up<U>, g_gu, dim3(256), lds_gu, s, M, d, ff, n_exp, n_act, wg, wu, ws, sel, sw)
     switch (upl_gu) {
-    case 1: hipLaunchKernelGGL(k_moe_gate_up<1>, g_gu, dim3(256), lds_gu, s, M, d, ff, n_act, wg, wu, ws); break;
-    case 2: hipLaunchKernelGGL(k_moe_gate_up<2>, g_gu, dim3(256), lds_gu, s, M, d, ff, n_act, wg, wu, ws); break;
-    case 3: case 4: hipLaunchKernelGGL(k_moe_gate_up<4>, g_gu, dim3(256), lds_gu, s, M, d, ff, n_act, wg, wu, ws); break;
-    default: hipLaunchKernelGGL(k_moe_gate_up<8>, g_gu, dim3(256), lds_gu, s, M, d, ff, n_act, wg, wu, ws); break;
+    case 1: X100_GU(1); break;
+    case 2: X100_GU(2); break;
+    case 3: case 4: X100_GU(4); break;
+    default: X100_GU(8); break;
     }
+#undef X100_GU
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
@@ -520,10 +532,14 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     const dim3 g_dn(Umax, d / DN_ROWS);
     const uint8_t *wd = (const uint8_t *)Wd;
     switch (upl_dn) {
-    case 1: hipLaunchKernelGGL(k_moe_down<1>, g_dn, dim3(256), lds_dn, s, M, d, ff, n_act, wd, ws, out, residual); break;
-    case 2: hipLaunchKernelGGL(k_moe_down<2>, g_dn, dim3(256), lds_dn, s, M, d, ff, n_act, wd, ws, out, residual); break;
-    case 3: case 4: hipLaunchKernelGGL(k_moe_down<4>, g_dn, dim3(256), lds_dn, s, M, d, ff, n_act, wd, ws, out, residual); break;
-    default: hipLaunchKernelGGL(k_moe_down<8>, g_dn, dim3(256), lds_dn, s, M, d, ff, n_act, wd, ws, out, residual); break;
+    case 1: hipLaunchKernelGGL(k_moe_down<1>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 2: hipLaunchKernelGGL(k_moe_down<2>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 3: case 4: hipLaunchKernelGGL(k_moe_down<4>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    default: hipLaunchKernelGGL(k_moe_down<8>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
     }
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+
+    hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
     return hipGetLastError();
 }

@@ -22,75 +22,6 @@
 
 namespace {
 
-// ------------------------------------------------------------------------------------------------
-// In-kernel activation quantizers (x rows -> LDS).
-// ------------------------------------------------------------------------------------------------
-
-// Q8_0 per 32 elements, one element per thread, 32-lane groups (K % 32 == 0).
-// LDS: xlo/xhi [m][nb][16] bytes (elements 0..15 / 16..31), xd [m][nb] (fp16-rounded d as
-// float), xs [m][nb] (sum of q).
-X100_DEV void quantize_q8_0_lds(const float *__restrict__ x, int M, int K, int8_t *xlo,
-                                int8_t *xhi, float *xd, int *xs)
-{
-    const int nb = K / 32;
-    const int tid = threadIdx.x;
-    for (int m = 0; m < M; m++) {
-        for (int e0 = 0; e0 < K; e0 += blockDim.x) {
-            const int e = e0 + tid;
-            const bool in = e < K;  // uniform per 32-lane group because K % 32 == 0
-            const float v = in ? x[(size_t)m * K + e] : 0.0f;
-            float a = fabsf(v);
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
-            const float amax = fmaxf(a, 1e-6f);
-            const float d = amax / 127.0f;
-            const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-            const int q = clamp_i8((int)rintf(v * inv));
-            int s = q;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);
-            if (in) {
-                const int b = e >> 5, pos = e & 31;
-                if (pos < 16)
-                    xlo[(m * nb + b) * 16 + pos] = (int8_t)q;
-                else
-                    xhi[(m * nb + b) * 16 + pos - 16] = (int8_t)q;
-                if (pos == 0) {
-                    xd[m * nb + b] = h2f(f2h(d));
-                    xs[m * nb + b] = s;
-                }
-            }
-        }
-    }
-}
-
-// Q8_K per 256 elements: one wave per block, 4 consecutive elements per lane.
-// LDS: xq [m][nsb][256] int8, xbs [m][nsb][16] int, xd [m][nsb] float.
-X100_DEV void quantize_q8_K_rows(const float *__restrict__ x, int M, int K, int8_t *xq, int *xbs,
-                                 float *xd)
-{
-    const int nsb = K / 256;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int blk = w; blk < M * nsb; blk += nw) {
-        const int m = blk / nsb, sb = blk - m * nsb;
-        const float4 v = *(const float4 *)(x + (size_t)m * K + sb * 256 + 4 * lane);
-        float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        const float amax = wave_max_f(a);
-        const float d = amax / 127.0f;
-        const float rep = d != 0.0f ? 1.0f / d : 0.0f;
-        const int q0 = clamp_i8((int)roundf(v.x * rep)), q1 = clamp_i8((int)roundf(v.y * rep));
-        const int q2 = clamp_i8((int)roundf(v.z * rep)), q3 = clamp_i8((int)roundf(v.w * rep));
-        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-        ((uint32_t *)(xq + (size_t)blk * 256))[lane] = packed;
-        int s = q0 + q1 + q2 + q3;
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        if ((lane & 3) == 0) xbs[blk * 16 + (lane >> 2)] = s;
-        if (lane == 0) xd[blk] = d;
-    }
-}
-
 // get_scale_min_k4 (repack.cpp:222-233) on the 12 scale bytes held in dwords s0, s1, s2.
 X100_DEV uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int k)
 {
@@ -128,24 +59,32 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int rowb = blockIdx.x * 4 * RPW + w * RPW;
 
+    constexpr int XPT = MR == 1 ? 4 : 16;
+    const int total4 = M * K / 4;
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
+    float4 xv[XPT];
+    x_load<XPT>(xr, 0, xv);
+
+    // Unconditional loads (indices clamped into the matrix; out-of-range results are discarded),
+    // so every load of the lane is in flight before the first one is waited for.
     v4i q[RPW][BPL];
-    uint16_t dwb[RPW][BPL];
+    uint32_t dwb[RPW][BPL];
 #pragma unroll
     for (int r = 0; r < RPW; r++)
 #pragma unroll
         for (int c = 0; c < BPL; c++) {
-            const int row = rowb + r, b = lane + 64 * c;
-            if (row < N && b < nb) {
-                const size_t blk = (size_t)row * nb + b;
-                q[r][c] = *(const v4i *)(wq + blk * 16);
-                dwb[r][c] = wd[blk];
-            } else {
-                q[r][c] = v4i{0, 0, 0, 0};
-                dwb[r][c] = 0;
-            }
+            const int row = min(rowb + r, N - 1), b = min(lane + 64 * c, nb - 1);
+            const size_t blk = (size_t)row * nb + b;
+            q[r][c] = __builtin_nontemporal_load((const v4i *)(wq + blk * 16));
+            dwb[r][c] = wd[blk];
         }
 
-    quantize_q8_0_lds(x, M, K, xlo, xhi, xd, xs);
+    __builtin_amdgcn_sched_barrier(0);   // keep every load above ahead of the quantizer's math
+    q8_0_from_regs<XPT>(xv, 0, total4, K, xlo, xhi, xd, xs);
+    for (int c0 = 256 * XPT; c0 < total4; c0 += 256 * XPT) {
+        x_load<XPT>(xr, c0, xv);
+        q8_0_from_regs<XPT>(xv, c0, total4, K, xlo, xhi, xd, xs);
+    }
     __syncthreads();
 
 #pragma unroll
@@ -159,7 +98,7 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
             const int b = lane + 64 * c;
             if (b < nb) {
                 const v4i qq = q[r][c];
-                const float dwf = h2f(dwb[r][c]);
+                const float dwf = h2f((uint16_t)dwb[r][c]);
                 int lo[4], hi[4];
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
@@ -186,9 +125,7 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
 #pragma unroll
         for (int m = 0; m < MR; m++) {
             if (m < M) {
-                float v = acc[m];
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+                const float v = wave_sum_uf(acc[m]);
                 if (lane == 0 && row < N) y[(size_t)m * N + row] = v;
             }
         }
@@ -220,21 +157,27 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R,
     const int nrows = min(R, N - row0);
     const int U = nrows * nsb;
 
+    constexpr int XPT = MR == 1 ? 4 : 16;
+    const int total4 = M * K / 4;
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
+    float4 xv[XPT];
+    x_load<XPT>(xr, 0, xv);
+
     v4i hdr[UPL], qs[UPL];
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int u = w * 8 + (lane >> 3) + 32 * c;
-        if (u < U) {
-            const uint8_t *blk = W + ((size_t)row0 * nsb + u) * 144;
-            hdr[c] = *(const v4i *)blk;
-            qs[c] = *(const v4i *)(blk + 16 + 16 * i);
-        } else {
-            hdr[c] = v4i{0, 0, 0, 0};
-            qs[c] = v4i{0, 0, 0, 0};
-        }
+        const int u = min(w * 8 + (lane >> 3) + 32 * c, U - 1);   // clamped: see k_q4_0
+        const uint8_t *blk = W + ((size_t)row0 * nsb + u) * 144;
+        hdr[c] = *(const v4i *)blk;
+        qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
     }
 
-    quantize_q8_K_rows(x, M, K, xq, xbs, xd);
+    __builtin_amdgcn_sched_barrier(0);   // keep every load above ahead of the quantizer's math
+    q8_K_from_regs<XPT>(xv, 0, total4, xq, xbs, xd);
+    for (int c0 = 256 * XPT; c0 < total4; c0 += 256 * XPT) {
+        x_load<XPT>(xr, c0, xv);
+        q8_K_from_regs<XPT>(xv, c0, total4, xq, xbs, xd);
+    }
     __syncthreads();
 
 #pragma unroll
@@ -266,13 +209,8 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R,
                     d1 = dot4(hi[t], xc[t], d1);
                 }
                 const int *bs = xbs + (m * nsb + sb) * 16;
-                int isc = sc0 * d0 + sc1 * d1;
-                int imn = m0 * bs[4 * p + h] + m1 * bs[4 * p + 2 + h];
-#pragma unroll
-                for (int o = 1; o < 8; o <<= 1) {
-                    isc += __shfl_xor(isc, o, 64);
-                    imn += __shfl_xor(imn, o, 64);
-                }
+                const int isc = sum8_i(sc0 * d0 + sc1 * d1);
+                const int imn = sum8_i(m0 * bs[4 * p + h] + m1 * bs[4 * p + 2 + h]);
                 if (valid && i == 0) {
                     const float dx = xd[m * nsb + sb];
                     const float dd = dx * d, dm = dx * dmin;
@@ -321,29 +259,34 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
     const int nrows = min(R, N - row0);
     const int U = nrows * nsb;
 
+    constexpr int XPT = MR == 1 ? 4 : 16;
+    const int total4 = M * K / 4;
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
+    float4 xv[XPT];
+    x_load<XPT>(xr, 0, xv);
+
     v4i qv[UPL], hv[UPL];
     uint32_t s0[UPL], s1[UPL], s2[UPL];
-    uint16_t dv[UPL];
+    uint32_t dv[UPL];
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int u = w * 16 + (lane >> 2) + 64 * c;
-        if (u < U) {
-            const size_t rec = (size_t)row0 * nsb + u;
-            qv[c] = *(const v4i *)(hq + rec * 96 + 32 + 32 * hh + 16 * lh);
-            hv[c] = *(const v4i *)(hq + rec * 96 + 16 * lh);
-            const uint32_t *sp = (const uint32_t *)(scl + rec * 12);
-            s0[c] = sp[0];
-            s1[c] = sp[1];
-            s2[c] = sp[2];
-            dv[c] = wdd[rec];
-        } else {
-            qv[c] = hv[c] = v4i{0, 0, 0, 0};
-            s0[c] = s1[c] = s2[c] = 0;
-            dv[c] = 0;
-        }
+        const int u = min(w * 16 + (lane >> 2) + 64 * c, U - 1);  // clamped: see k_q4_0
+        const size_t rec = (size_t)row0 * nsb + u;
+        qv[c] = __builtin_nontemporal_load((const v4i *)(hq + rec * 96 + 32 + 32 * hh + 16 * lh));
+        hv[c] = *(const v4i *)(hq + rec * 96 + 16 * lh);
+        const uint32_t *sp = (const uint32_t *)(scl + rec * 12);
+        s0[c] = sp[0];
+        s1[c] = sp[1];
+        s2[c] = sp[2];
+        dv[c] = wdd[rec];
     }
 
-    quantize_q8_K_rows(x, M, K, xq, xbs, xd);
+    __builtin_amdgcn_sched_barrier(0);   // keep every load above ahead of the quantizer's math
+    q8_K_from_regs<XPT>(xv, 0, total4, xq, xbs, xd);
+    for (int c0 = 256 * XPT; c0 < total4; c0 += 256 * XPT) {
+        x_load<XPT>(xr, c0, xv);
+        q8_K_from_regs<XPT>(xv, c0, total4, xq, xbs, xd);
+    }
     __syncthreads();
 
 #pragma unroll
@@ -369,7 +312,7 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
                 v[j][t] = (int)(lo2 | (hb << 2));   // 3-bit value q + 4, q in [-4, 3]
             }
         }
-        const float dw = h2f(dv[c]);
+        const float dw = h2f((uint16_t)dv[c]);
 #pragma unroll
         for (int m = 0; m < MR; m++) {
             if (m < M) {
@@ -385,8 +328,7 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
                     dsum -= 4 * bs[2 * j];
                     isc += scl_j[j] * dsum;
                 }
-                isc += __shfl_xor(isc, 1, 64);
-                isc += __shfl_xor(isc, 2, 64);
+                isc = sum4_i(isc);
                 if (valid && i == 0) {
                     const float dx = xd[m * nsb + sb];
                     tv[m * R * nsb + u] = (dx * dw) * (float)isc;

@@ -61,9 +61,179 @@ X100_DEV float wave_max_f(float v)
     return v;
 }
 
+// ------------------------------------------------------------------------------------------------
+// Lane reductions with DPP (data-parallel primitives: a VALU operand read from another lane of
+// the same row of 16, a few cycles) instead of ds_bpermute shuffles.
+//   quad_perm 0xB1 = lanes [1,0,3,2] (xor 1), 0x4E = [2,3,0,1] (xor 2);
+//   row_half_mirror 0x141: lane i <- lane 7-i within each group of 8;
+//   row_shr:n 0x110+n; row_bcast:15 0x142 / row_bcast:31 0x143 (lane 15 / 31 of the previous
+//   row(s) into the rows enabled by the row mask).
+// A lane whose source lane is invalid (row_shr at the start of a row) or whose row is masked off
+// receives `old` instead: v itself for a maximum, 0 for a sum.
+// ------------------------------------------------------------------------------------------------
+template <int CTRL, int ROWM = 0xf, int BANKM = 0xf>
+X100_DEV int dpp_i(int old, int v)
+{
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWM, BANKM, false);
+}
+template <int CTRL, int ROWM = 0xf, int BANKM = 0xf>
+X100_DEV float dpp_f(float old, float v)
+{
+    return __int_as_float(dpp_i<CTRL, ROWM, BANKM>(__float_as_int(old), __float_as_int(v)));
+}
+// Sum / max over each aligned group of 4 or 8 lanes, result in every lane of the group.
+X100_DEV int sum4_i(int v)
+{
+    v += dpp_i<0xB1>(0, v);
+    v += dpp_i<0x4E>(0, v);
+    return v;
+}
+X100_DEV int sum8_i(int v)
+{
+    v = sum4_i(v);
+    v += dpp_i<0x141>(0, v);
+    return v;
+}
+X100_DEV float max8_f(float v)
+{
+    v = fmaxf(v, dpp_f<0xB1>(v, v));
+    v = fmaxf(v, dpp_f<0x4E>(v, v));
+    v = fmaxf(v, dpp_f<0x141>(v, v));
+    return v;
+}
+// Maximum over the 64 lanes, returned wave-uniform (prefix maximum into lane 63, then readlane).
+X100_DEV float wave_max_u(float v)
+{
+    v = fmaxf(v, dpp_f<0x111>(v, v));
+    v = fmaxf(v, dpp_f<0x112>(v, v));
+    v = fmaxf(v, dpp_f<0x114>(v, v));
+    v = fmaxf(v, dpp_f<0x118>(v, v));
+    v = fmaxf(v, dpp_f<0x142, 0xa>(v, v));
+    v = fmaxf(v, dpp_f<0x143, 0xc>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// Sum over the 64 lanes, wave-uniform: prefix sum of rows (row_shr 1, 2, 4, 8), then rows
+// combined into lane 63.  For integers, or floats whose summation order is not prescribed.
+X100_DEV int wave_sum_u(int v)
+{
+    v += dpp_i<0x111>(0, v);
+    v += dpp_i<0x112>(0, v);
+    v += dpp_i<0x114>(0, v);
+    v += dpp_i<0x118>(0, v);
+    v += dpp_i<0x142, 0xa>(0, v);
+    v += dpp_i<0x143, 0xc>(0, v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+X100_DEV float wave_sum_uf(float v)
+{
+    v += dpp_f<0x111>(0.0f, v);
+    v += dpp_f<0x112>(0.0f, v);
+    v += dpp_f<0x114>(0.0f, v);
+    v += dpp_f<0x118>(0.0f, v);
+    v += dpp_f<0x142, 0xa>(0.0f, v);
+    v += dpp_f<0x143, 0xc>(0.0f, v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Device-side Q8 activation formats (kept in LDS or a workspace; internal to the library).
 //   Q8_0 (per 32): fp16 d, int8 q[32], int sum(q)     -- quantize_q8_0_native rounding
 //   Q8_K (per 256): fp32 d, int8 q[256], int bsum[16] -- pack_A_q3k rounding
 // Quantize one 32-element block held by one thread (values v[0..31]).
 X100_DEV float q8_0_scale(float amax) { return amax / 127.0f; }
 X100_DEV int clamp_i8(int q) { return q > 127 ? 127 : (q < -128 ? -128 : q); }
+
+// Raw buffer resource over [p, p + bytes): loads at byte offsets >= bytes return 0 instead of
+// touching memory, so bounds-checked loads need no branch (word 3 = gfx9 raw buffer format).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+X100_DEV rsrc_t buf_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+X100_DEV float4 buf_load_f4(rsrc_t r, uint32_t byte_off)
+{
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                       __uint_as_float(v[3]));
+}
+
+// Asynchronous global -> LDS copy of 1 KiB per wave (global_load_lds_dwordx4): lane l copies the
+// 16 bytes at its own src to lds_base + 16*l.  lds_base must be the same for the whole wave.  The
+// compiler counts these loads like any other (a __syncthreads() waits for them).
+X100_DEV void dma_1k(const void *src, void *lds_base)
+{
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_base, 16, 0, 0);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Activation quantizers for a 256-thread block.  The M x K fp32 rows are read as float4 (float4
+// f = c0 + tid + 256*i holds elements 4f .. 4f+3 of the flattened rows) in chunks of XPT float4
+// per thread: x_load issues a chunk's loads (through a buffer resource of M*K*4 bytes, so
+// elements past the end read as 0), the *_from_regs functions quantize the chunk into LDS.
+// Kernels issue chunk 0 before their weight loads so that it arrives while the weights are still
+// in flight.
+//   Q8_0 (quantize_q8_0_native rounding): a 32-element block is 8 consecutive threads.
+//   Q8_K (pack_A_q3k rounding): a 256-element block is one wave (64 threads).
+// ------------------------------------------------------------------------------------------------
+template <int XPT>
+X100_DEV void x_load(rsrc_t xr, int c0, float4 (&v)[XPT])
+{
+#pragma unroll
+    for (int i = 0; i < XPT; i++) v[i] = buf_load_f4(xr, (uint32_t)(c0 + threadIdx.x + 256 * i) * 16u);
+}
+
+template <int XPT>
+X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, int8_t *xlo,
+                             int8_t *xhi, float *xd, int *xs)
+{
+    const int nb = K / 32;
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int f = c0 + threadIdx.x + 256 * i;
+        const float a = max8_f(fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        const float amax = fmaxf(a, 1e-6f);
+        const float d = amax / 127.0f;
+        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        const int q0 = clamp_i8((int)rintf(v[i].x * inv)), q1 = clamp_i8((int)rintf(v[i].y * inv));
+        const int q2 = clamp_i8((int)rintf(v[i].z * inv)), q3 = clamp_i8((int)rintf(v[i].w * inv));
+        const int s = sum8_i(q0 + q1 + q2 + q3);
+        if (f < total4) {   // uniform per 8-thread block: total4 is a multiple of 8
+            const int e = 4 * f, m = e / K, k = e - m * K;
+            const int b = m * nb + k / 32, pos = k & 31;
+            const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                    ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+            if (pos < 16)
+                ((uint32_t *)(xlo + b * 16))[pos / 4] = packed;
+            else
+                ((uint32_t *)(xhi + b * 16))[(pos - 16) / 4] = packed;
+            if (pos == 0) {
+                xd[b] = h2f(f2h(d));
+                xs[b] = s;
+            }
+        }
+    }
+}
+
+template <int XPT>
+X100_DEV void q8_K_from_regs(const float4 (&v)[XPT], int c0, int total4, int8_t *xq, int *xbs, float *xd)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int f = c0 + threadIdx.x + 256 * i;
+        const float a = fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
+        const float amax = wave_max_u(a);
+        const float d = amax / 127.0f;
+        const float rep = d != 0.0f ? 1.0f / d : 0.0f;
+        const int q0 = clamp_i8((int)roundf(v[i].x * rep)), q1 = clamp_i8((int)roundf(v[i].y * rep));
+        const int q2 = clamp_i8((int)roundf(v[i].z * rep)), q3 = clamp_i8((int)roundf(v[i].w * rep));
+        const int s = sum4_i(q0 + q1 + q2 + q3);
+        if (f < total4) {   // uniform per wave: total4 is a multiple of 64
+            const int blk = f / 64;   // flattened (row, super-block) index
+            ((uint32_t *)(xq + blk * 256))[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                                   ((uint32_t)(q2 & 0xff) << 16) |
+                                                   ((uint32_t)(q3 & 0xff) << 24);
+            if ((lane & 3) == 0) xbs[blk * 16 + (lane >> 2)] = s;
+            if (lane == 0) xd[blk] = d;
+        }
+    }
+}
