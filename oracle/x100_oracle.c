@@ -99,6 +99,48 @@ void orc_gemm_i8_mt(int M, int N, int K, const int8_t *A, const int8_t *B, int32
         }
 }
 
+/* ---- integer tile GEMV ---------------------------------------------------------------------- */
+
+/* bench/q4_gemv.c:101-103: plain dot per (m, n). */
+void orc_gemv_int(int M, int N, int K, const int8_t *W, const int8_t *x, int32_t *y)
+{
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            int32_t a = 0;
+            for (int k = 0; k < K; k++) a += (int32_t)W[(size_t)n * K + k] * (int32_t)x[(size_t)m * K + k];
+            y[(size_t)m * N + n] = a;
+        }
+}
+
+/* bench/q4_gemv.c:37-48: tile (nb, kp) of 128 bytes; byte 16n+k holds W[8nb+n][32kp+k] in the low
+ * nibble and W[8nb+n][32kp+16+k] in the high nibble. */
+int orc_pack_w_int4(int N, int K, const int8_t *W, uint8_t *Wq)
+{
+    if (N % 8 || K % 32) return -1;
+    const int nkp = K / 32;
+    for (int nb = 0; nb < N / 8; nb++)
+        for (int kp = 0; kp < nkp; kp++)
+            for (int j = 0; j < 128; j++) {
+                const int n = j / 16, k = j % 16;
+                const int8_t lo = W[(size_t)(8 * nb + n) * K + 32 * kp + k];
+                const int8_t hi = W[(size_t)(8 * nb + n) * K + 32 * kp + 16 + k];
+                Wq[((size_t)nb * nkp + kp) * 128 + j] = (uint8_t)((lo & 0xf) | ((hi & 0xf) << 4));
+            }
+    return 0;
+}
+
+/* bench/q4_gemv.c:55-62: tile (nb, kb) of 128 bytes; byte 16n+k = W[8nb+n][16kb+k]. */
+int orc_pack_w_int8(int N, int K, const int8_t *W, int8_t *Wp)
+{
+    if (N % 8 || K % 16) return -1;
+    const int nkb = K / 16;
+    for (int nb = 0; nb < N / 8; nb++)
+        for (int kb = 0; kb < nkb; kb++)
+            for (int j = 0; j < 128; j++)
+                Wp[((size_t)nb * nkb + kb) * 128 + j] = W[(size_t)(8 * nb + j / 16) * K + 16 * kb + j % 16];
+    return 0;
+}
+
 /* ---------------------------------------------------------------------------------------------
  * Block formats (Appendix of the block-format layouts used by ggml; reference restatements at
  * qwen_moe_hp.c:98, qwen_moe_q3k.c:531, repack.cpp:222-233)

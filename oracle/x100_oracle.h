@@ -56,6 +56,14 @@ void gemm_ref_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t 
 void orc_gemm_i8_mt(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
                     int nthreads);
 
+/* ---- integer tile GEMV (bench/q4_gemv.c) --------------------------------------------------- */
+/* y[M][N] = W[N][K] . x[M][K]^T, int32 exact: ref_gemv, bench/q4_gemv.c:101-103. */
+void orc_gemv_int(int M, int N, int K, const int8_t *W, const int8_t *x, int32_t *y);
+/* Packed weight layouts of pack_w_int4 (bench/q4_gemv.c:37-48) and pack_w_int8 (:55-62).
+ * Return 0, or -1 for N % 8 / K % 32 (int4) / K % 16 (int8). */
+int orc_pack_w_int4(int N, int K, const int8_t *W, uint8_t *Wq);
+int orc_pack_w_int8(int N, int K, const int8_t *W, int8_t *Wp);
+
 /* ---- block formats ------------------------------------------------------------------------- */
 size_t orc_block_bytes(int qtype);   /* 18, 34, 110, 144, 292 */
 int    orc_block_elems(int qtype);   /* 32 or 256 */

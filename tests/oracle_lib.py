@@ -51,6 +51,10 @@ def oracle():
         L.orc_qgemv_q.argtypes = [i, i, i, i, p, p, p]
         L.orc_moe_layer.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p]
         L.orc_moe_route.argtypes = [i, i, i, i, p, p, p, p, p]
+        L.orc_gemv_int.argtypes = [i, i, i, p, p, p]
+        L.orc_gemv_int.restype = None
+        L.orc_pack_w_int4.argtypes = [i, i, p, p]
+        L.orc_pack_w_int8.argtypes = [i, i, p, p]
         L.orc_swiglu.argtypes = [f, f]
         L.orc_swiglu.restype = f
         _o = L
@@ -152,3 +156,28 @@ def moe_route(hn, R, n_act):
                                 _p(logits), _p(sel), _p(sw))
     assert rc == 0
     return logits, sel, sw
+
+
+def gemv_int(W, x):
+    """y[M][N] = W[N][K] . x[M][K]^T (int32 exact), bench/q4_gemv.c:101-103."""
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    N, K = W.shape
+    M = x.shape[0]
+    y = np.zeros((M, N), np.int32)
+    oracle().orc_gemv_int(M, N, K, _p(W), _p(x), _p(y))
+    return y
+
+
+def pack_w(int4, W):
+    """Packed tile layout of pack_w_int4 / pack_w_int8 (bench/q4_gemv.c:37-62)."""
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    N, K = W.shape
+    if int4:
+        out = np.zeros(N * K // 2, np.uint8)
+        rc = oracle().orc_pack_w_int4(N, K, _p(W), _p(out))
+    else:
+        out = np.zeros(N * K, np.int8)
+        rc = oracle().orc_pack_w_int8(N, K, _p(W), _p(out))
+    assert rc == 0
+    return out

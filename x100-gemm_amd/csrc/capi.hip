@@ -1,5 +1,5 @@
 // C-ABI of libx100hip: argument checking, device state and the host-pointer convenience paths.
-// The kernels live in gemm_i8.hip, qgemv.hip and moe.hip.
+// The kernels live in gemm_i8.hip, gemv_tile.hip, qgemv.hip and moe.hip.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -10,6 +10,7 @@
 // Only the extern "C" entry points are exported (the library is built with -fvisibility=hidden).
 #pragma GCC visibility push(default)
 #include "x100_gemm.h"
+#include "x100_gemv_tile.h"
 #include "x100_moe.h"
 #include "x100_qgemv.h"
 #pragma GCC visibility pop
@@ -244,6 +245,66 @@ int qgemv_hip(int qtype, int M, int N, int K, const void *w_packed, const float 
     if (e == hipErrorInvalidValue) return X100_EINVAL;
     if (e != hipSuccess) return hip_fail(e);
     return X100_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// integer tile GEMV (int4 / int8 weights)
+// ---------------------------------------------------------------------------------------------
+size_t x100_tile_bytes(int int4, int N, int K)
+{
+    if (N <= 0 || K <= 0 || N % 8 || K % (int4 ? 32 : 16)) return 0;
+    return int4 ? (size_t)N * K / 2 : (size_t)N * K;
+}
+
+int x100_pack_w_int4(int N, int K, const int8_t *W, uint8_t *Wq)
+{
+    if (!x100_tile_bytes(1, N, K) || !W || !Wq) return X100_EINVAL;
+    const int kp_n = K / 32;
+    for (int nb = 0; nb < N / 8; nb++)
+        for (int kp = 0; kp < kp_n; kp++) {
+            uint8_t *t = Wq + ((size_t)nb * kp_n + kp) * 128;
+            for (int n = 0; n < 8; n++) {
+                const int8_t *row = W + (size_t)(8 * nb + n) * K + 32 * kp;
+                for (int k = 0; k < 16; k++)
+                    t[16 * n + k] = (uint8_t)((row[k] & 0xf) | ((row[16 + k] & 0xf) << 4));
+            }
+        }
+    return X100_OK;
+}
+
+int x100_pack_w_int8(int N, int K, const int8_t *W, int8_t *Wp)
+{
+    if (!x100_tile_bytes(0, N, K) || !W || !Wp) return X100_EINVAL;
+    const int kb_n = K / 16;
+    for (int nb = 0; nb < N / 8; nb++)
+        for (int kb = 0; kb < kb_n; kb++) {
+            int8_t *t = Wp + ((size_t)nb * kb_n + kb) * 128;
+            for (int n = 0; n < 8; n++) memcpy(t + 16 * n, W + (size_t)(8 * nb + n) * K + 16 * kb, 16);
+        }
+    return X100_OK;
+}
+
+static int gemv_tile(int int4, int M, int N, int K, const void *W, const int8_t *x, int32_t *y, void *stream)
+{
+    if (!x100_tile_bytes(int4, N, K) || M < 1 || M > 8) return X100_EINVAL;
+    if ((size_t)M * K + 16 + ((size_t)M * (K / 16) + 1) * 4 > 64 * 1024) return X100_EINVAL;
+    if (!W || !x || !y || ((uintptr_t)W & 15) || ((uintptr_t)x & 15)) return X100_EINVAL;
+    int rc = check_device();
+    if (rc) return rc;
+    hipError_t e = x100_gemv_tile_launch(int4, M, N, K, W, x, y, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return X100_EINVAL;
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
+int gemv_int4_hip(int M, int N, int K, const uint8_t *Wq, const int8_t *x, int32_t *y, void *stream)
+{
+    return gemv_tile(1, M, N, K, Wq, x, y, stream);
+}
+
+int gemv_int8_hip(int M, int N, int K, const int8_t *Wp, const int8_t *x, int32_t *y, void *stream)
+{
+    return gemv_tile(0, M, N, K, Wp, x, y, stream);
 }
 
 // ---------------------------------------------------------------------------------------------

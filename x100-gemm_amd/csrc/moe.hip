@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     float4 *s_hn = (float4 *)smem;   // [M][d/4]
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wave = blockIdx.x * 4 + wave_id();
     const int nsb = d / 256;
 
     // The wave's router row (clamped expert; elements past d read as 0 and are not used).
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
     for (int j = 0; j < 16; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
 
     // hn -> LDS (all M rows; M*d/256 chunks of 1 KiB, one wave each), asynchronous.
-    for (int ch = threadIdx.x >> 6; ch < M * nsb; ch += 4)
+    for (int ch = wave_id(); ch < M * nsb; ch += 4)
         dma_1k(hn + (size_t)ch * 256 + 4 * lane, smem + ch * 1024);
     __syncthreads();
 
@@ -178,7 +178,7 @@ struct RouteLds {
 
 X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
 {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     for (int m = w; m < M; m += 4) {
         float p[4];
         float mx = -1e30f;
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
     // Q8_K records of all M hn rows -> LDS [M][rec], asynchronous (1 KiB chunks, one wave each;
     // sources clamped to the records, the LDS area is padded to whole chunks).
     const int totv = M * rec / 16;
-    for (int ch = threadIdx.x >> 6; ch * 64 < totv; ch += 4)
+    for (int ch = wave_id(); ch * 64 < totv; ch += 4)
         dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
 
     route_block(M, n_exp, n_act, ws.logits, rl);
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
     }
     if (u >= U) return;
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, i = lane & 7;
+    const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
     const int ex = rl.uniq[u];
     const int r0 = blockIdx.y * GU_ROWS;
     const int nunits = 2 * GU_ROWS * nsb;
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
     const int ex = ws.uniq[u], cnt = ws.ucnt[u];
     const int prl = ws.upairs[u * 8 + (threadIdx.x & 7)];   // lane l holds pair l % 8 of the slot
     if (u >= U) return;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, i = lane & 7;
+    const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
     const int nsf = ff / 256;
     const int r0 = blockIdx.y * DN_ROWS;
     const int nunits = DN_ROWS * nsf;

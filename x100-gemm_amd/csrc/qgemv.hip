@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
     float *xd = (float *)(xhi + MR * nb * 16);
     int *xs = (int *)(xd + MR * nb);
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int rowb = blockIdx.x * 4 * RPW + w * RPW;
 
     constexpr int XPT = MR == 1 ? 4 : 16;
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R,
     float *xd = (float *)(xbs + MR * nsb * 16);    // [MR][nsb]
     float *tv = xd + MR * nsb;                     // [MR][R*nsb]
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int i = lane & 7, p = i >> 1, h = i & 1;
     const int row0 = blockIdx.x * R;
     const int nrows = min(R, N - row0);
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
     float *xd = (float *)(xbs + MR * nsb * 16);
     float *tv = xd + MR * nsb;
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int i = lane & 3, hh = i >> 1, lh = i & 1;
     const int row0 = blockIdx.x * R;
     const int nrows = min(R, N - row0);

@@ -47,6 +47,10 @@ X100_DEV void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, u
     o3 = perm(x23h, x01h, 0x07060302u);
 }
 
+// Index of the calling wave in its block, as a wave-uniform (scalar) value: addresses derived from
+// it (buffer resources, M0) stay in scalar registers.
+X100_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // Wave-wide (64 lanes) reductions.
 X100_DEV int wave_sum_i(int v)
 {

@@ -23,3 +23,6 @@ size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act);
 hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                            const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
                            int *sel, float *sw, void *workspace, hipStream_t s);
+
+hipError_t x100_gemv_tile_launch(int int4, int M, int N, int K, const void *W, const int8_t *x, int32_t *y,
+                                 hipStream_t s);

@@ -9,6 +9,7 @@ Entry points and what they replace in the reference:
   gemm_ime_i8 / gemm_hip_i8 / gemm_hip_i8_dev   include/x100_gemm.h:60-61 (C += A*B, int8->int32)
   qgemv_hip (+ x100q_pack)                      lin_mm of qwen_moe.c:101-107 on Q4_0/Q4_K/Q3_K
   moe_layer_hip                                 the MoE block of qwen_moe.c:294-311
+  gemv_int4_hip / gemv_int8_hip (+ packers)     gemv_nb_int4 / gemv_nb_int8 of bench/q4_gemv.c:67-99
 """
 import ctypes
 import os
@@ -22,10 +23,11 @@ Q4_0, Q3_K, Q4_K = 2, 11, 12
 
 X100_OK, X100_EINVAL, X100_ENODEV, X100_EHIP, X100_ENOMEM = 0, -1, -2, -3, -4
 
-# Every symbol declared in include/x100_gemm.h, x100_qgemv.h, x100_moe.h.
+# Every symbol declared in include/x100_gemm.h, x100_gemv_tile.h, x100_qgemv.h, x100_moe.h.
 EXPORTS = (
     "gemm_ime_i8", "gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant",
     "x100_hip_detect", "x100_hip_caps_print", "x100_hip_strerror",
+    "x100_tile_bytes", "x100_pack_w_int4", "x100_pack_w_int8", "gemv_int4_hip", "gemv_int8_hip",
     "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip",
     "moe_layer_hip",
 )
@@ -77,8 +79,15 @@ def lib():
     L.x100q_pack.argtypes = [i, i, i, p, p, p]
     L.qgemv_hip.argtypes = [i, i, i, i, p, p, p, p]
     L.moe_layer_hip.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p]
+    L.x100_tile_bytes.argtypes = [i, i, i]
+    L.x100_tile_bytes.restype = sz
+    L.x100_pack_w_int4.argtypes = [i, i, p, p]
+    L.x100_pack_w_int8.argtypes = [i, i, p, p]
+    L.gemv_int4_hip.argtypes = [i, i, i, p, p, p, p]
+    L.gemv_int8_hip.argtypes = [i, i, i, p, p, p, p]
     for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant", "x100_hip_detect",
-                 "x100q_pack", "qgemv_hip", "moe_layer_hip"):
+                 "x100q_pack", "qgemv_hip", "moe_layer_hip", "x100_pack_w_int4", "x100_pack_w_int8",
+                 "gemv_int4_hip", "gemv_int8_hip"):
         getattr(L, name).restype = i
     _lib = L
     return L
@@ -142,3 +151,27 @@ def moe_layer(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residu
     return _check("moe_layer_hip",
                   lib().moe_layer_hip(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out,
                                       1 if residual else 0, d_sel, d_sw, stream))
+
+
+# ---- integer tile GEMV (int4 / int8 weights) ---------------------------------------------------
+def tile_bytes(int4, N, K):
+    return lib().x100_tile_bytes(1 if int4 else 0, N, K)
+
+
+def pack_w(int4, W):
+    """Host packer with the reference's tile layout (pack_w_int4 / pack_w_int8); W int8 N x K."""
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    N, K = W.shape
+    out = np.zeros(tile_bytes(int4, N, K), np.uint8 if int4 else np.int8)
+    if int4:
+        _check("x100_pack_w_int4", lib().x100_pack_w_int4(N, K, W.ctypes.data, out.ctypes.data))
+    else:
+        _check("x100_pack_w_int8", lib().x100_pack_w_int8(N, K, W.ctypes.data, out.ctypes.data))
+    return out
+
+
+def gemv_tile(int4, M, N, K, d_w, d_x, d_y, stream=None):
+    """y[M][N] (int32) = W . x^T on device pointers; W packed by pack_w."""
+    if int4:
+        return _check("gemv_int4_hip", lib().gemv_int4_hip(M, N, K, d_w, d_x, d_y, stream))
+    return _check("gemv_int8_hip", lib().gemv_int8_hip(M, N, K, d_w, d_x, d_y, stream))
