@@ -15,6 +15,8 @@ timed with HIP events on the launch stream.  The same JSON line carries:
                 single-launch latency is reported separately.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
+       python bench.py --probe     (for rocprofv3 --pmc: `--steps` GEMM 4096^3 launches, then one
+                                    256 MiB device-to-device copy as the byte-count calibration)
 """
 import argparse
 import json
@@ -177,7 +179,7 @@ def bench_gemm(torch, timer, dev, args):
     traffic = read_traffic("gemm_i8_4096")
     roof = {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
             "frac": tops / PEAK_INT8_TOPS, "traffic": traffic,
-            "kernel": "k_gemm_mfma<4,4,2,2> (256x256 tile)", "algorithmic_ops_per_launch": ops}
+            "kernel": "k_gemm_big<8> (256x256 tile, 8 waves)", "algorithmic_ops_per_launch": ops}
     return ms, tops, roof
 
 
@@ -274,6 +276,23 @@ def bench_extra(torch, timer, dev, args):
     return extra
 
 
+def probe(torch, dev, args):
+    """Launches to read hardware counters from: GEMM 4096^3 x steps, then a 256 MiB copy."""
+    M = N = K = 4096
+    A, B = synth.gemm_inputs(M, N, K, seed=2026)
+    dA, dB = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    for _ in range(args.steps):
+        x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
+    torch.cuda.synchronize()
+    src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log("probe: %d x gemm 4096^3, 1 x copy of %d bytes" % (args.steps, src.numel()))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -281,6 +300,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this backend has no multi-GPU path "
@@ -295,6 +315,9 @@ def main():
     if not caps.is_gfx950:
         raise SystemExit("not a gfx950 device: %s" % caps.arch.decode())
     timer = Timer(torch)
+    if args.probe:
+        probe(torch, dev, args)
+        return
     ms, tops, roof = bench_gemm(torch, timer, dev, args)
     extra = {} if args.no_extra else bench_extra(torch, timer, dev, args)
     cpu = None if args.no_cpu else cpu_gemm_baseline()
