@@ -236,6 +236,42 @@ def bench_extra(torch, timer, dev, args):
                 key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
         del packs, raw
 
+    # ---- integer tile GEMV (bench/q4_gemv.c defaults: N = 4864, K = 896) ----------------------
+    N, K = 4864, 896
+    r = synth.rand_bytes(77, N * K)
+    Wt = (r.astype(np.int32) % 15 - 7).astype(np.int8).reshape(N, K)
+    for int4 in (True, False):
+        packed = x100hip.pack_w(int4, Wt)
+        pb = packed.nbytes
+        copies = int(300e6 // pb) + 1
+        dws = torch.from_numpy(packed.view(np.uint8)).to(dev).repeat(copies, 1)
+        for M in (1, 8):
+            xt = synth.rand_int8(78 + M, (M, K))
+            dx = torch.from_numpy(xt).to(dev)
+            dy = torch.empty((M, N), dtype=torch.int32, device=dev)
+            fns = [lambda i=i: x100hip.gemv_tile(int4, M, N, K, dws[i].data_ptr(), dx.data_ptr(), dy.data_ptr(),
+                                                 torch.cuda.current_stream().cuda_stream) for i in range(copies)]
+            us = timer.graph(fns)
+            lat = timer.single(fns[0])
+            byts = pb + M * K + 4 * M * N
+            cpu_us = cpu_time(lambda: ol.gemv_int(Wt, xt), min_s=0.3)
+            key = "%s_gemv_%dx%d_m%d" % ("int4" if int4 else "int8", N, K, M)
+            extra[key] = {"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                          "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
+                          "cpu_us_1core": cpu_us}
+            log("%s: %.2f us  %.0f GB/s  single %.2f us  cpu %.0f us" % (key, us, byts / us / 1e3, lat, cpu_us))
+        del dws
+
+    # ---- host-pointer drop-in gemm_ime_i8 at 4096^3 (PCIe copies + allocation included) ---------
+    A, B = synth.gemm_inputs(4096, 4096, 4096, seed=2026)
+    Ch = np.zeros((4096, 4096), np.int32)
+    x100hip.gemm_host(A, B, Ch)
+    t0 = time.perf_counter()
+    x100hip.gemm_host(A, B, Ch)
+    host_ms = (time.perf_counter() - t0) * 1e3
+    extra["gemm_ime_i8_host_4096"] = {"ms": host_ms, "TOPS_incl_pcie": 2.0 * 4096 ** 3 / host_ms / 1e9}
+    log("gemm_ime_i8 host path 4096^3: %.1f ms (PCIe copies + allocation included)" % host_ms)
+
     # ---- MoE decode layer ----------------------------------------------------------------------
     n_exp, d, ff, n_act = 128, 2048, 768, 8
     Wg, Wu, Wd = synth.moe_weights(n_exp, d, ff, seed=500)
