@@ -49,6 +49,13 @@ def test_gemm_4096_cube(dev):
     assert np.array_equal(got, ref), "mismatches: %d" % int((got != ref).sum())
 
 
+@pytest.mark.parametrize("variant", [x100hip.GEMM_TILE256, x100hip.GEMM_TILE256_W4])
+def test_gemm_4096_cube_variants(dev, variant):
+    A, B = synth.gemm_inputs(4096, 4096, 4096, seed=2028)
+    C0 = synth.rand_int8(8, (4096, 4096)).astype(np.int32) * 1000
+    assert np.array_equal(gpu_gemm(A, B, C0, dev, variant), oracle_gemm(A, B, C0))
+
+
 def test_gemm_4096_accumulate_twice(dev):
     A, B = synth.gemm_inputs(4096, 4096, 4096, seed=7)
     C0 = np.zeros((4096, 4096), np.int32)
@@ -76,9 +83,9 @@ def test_gemm_shapes_auto(dev, M, N, K):
 
 
 @pytest.mark.parametrize("variant", [x100hip.GEMM_TILE256, x100hip.GEMM_TILE128, x100hip.GEMM_SKINNY,
-                                     x100hip.GEMM_GENERIC])
+                                     x100hip.GEMM_GENERIC, x100hip.GEMM_TILE256_W4])
 @pytest.mark.parametrize("M,N,K", [(8, 256, 256), (16, 512, 320), (3, 48, 64), (256, 256, 512),
-                                   (40, 96, 144)])
+                                   (40, 96, 144), (512, 768, 1024), (768, 512, 576)])
 def test_gemm_forced_variants(dev, variant, M, N, K):
     if variant == x100hip.GEMM_SKINNY and M > 16:
         pytest.skip("skinny kernel takes M <= 16")

@@ -14,6 +14,8 @@
 //                  256-row chunks, B streamed once through LDS, dot4 on transposed k-quads,
 //                  int32 atomics into C (exact and order independent).
 //   k_gemm_generic any shape / alignment (byte loads); correctness fallback.
+#include <type_traits>
+
 #include "x100_common.h"
 #include "x100_internal.h"
 
@@ -248,6 +250,16 @@ X100_DEV void wait_vmcnt_le(int n)
 
 X100_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (indices usable as constants).
+template <int I, int N, class F> X100_DEV void static_for_impl(F &&f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for_impl<I + 1, N>(f);
+    }
+}
+template <int N, class F> X100_DEV void static_for(F &&f) { static_for_impl<0, N>(f); }
+
 template <int NW>
 __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const int8_t *__restrict__ A,
                                                      const int8_t *__restrict__ B,
@@ -280,10 +292,13 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         boff[p] = (uint32_t)(rb * N + 16 * big_b_chunk(rb, lane & 15));
     }
     const uint32_t sbase = lds_addr(smem);
-    auto issue = [&](int kt) {
+    // Stage kt (clamped to the last stage: the loop issues 4 stages ahead unconditionally, and a
+    // stage past the end is never read) into ring slot kt % NS.
+    auto issue = [&](int kt) __attribute__((always_inline)) {
         const uint32_t sb = sbase + (uint32_t)((kt & (NS - 1)) * STAGE);
-        const int8_t *ak = Ab + (size_t)kt * 64;
-        const int8_t *bk = Bb + (size_t)kt * 64 * N;
+        const int kc = min(kt, nk - 1);
+        const int8_t *ak = Ab + (size_t)kc * 64;
+        const int8_t *bk = Bb + (size_t)kc * 64 * N;
 #pragma unroll
         for (int p = 0; p < OPS; p++)
             dma16(ak + aoff[p], __builtin_amdgcn_readfirstlane(sb + (uint32_t)(16 * (NW * p + w) * 64)));
@@ -292,17 +307,20 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
             dma16(bk + boff[p], __builtin_amdgcn_readfirstlane(sb + BOFF + (uint32_t)(4 * (NW * p + w) * 256)));
     };
 
-    // C prefetch by quarters: quarter i = accumulator row-tile i (C rows crow0 + 32i); the lane
-    // holds C[row][col .. col+3] for col = ccol0 + 32j + 8q.
-    v4i cbuf[FN][4];
+    // C prefetch by parts: part p = accumulator row-tile i = p / (FN/2) (C rows crow0 + 32i) and
+    // column fragments j0 = 2*(p % (FN/2)), j0 + 1; the lane holds C[row][col .. col+3] for
+    // col = ccol0 + 32j + 8q.
+    constexpr int NPART = 2 * FN;
+    v4i cbuf[2][4];
     const int crow0 = m0 + wm * 128 + lcol;
     const int ccol0 = n0 + wn * FN * 32 + 4 * lgrp;
-    auto load_c = [&](int i) {  // i may be a run-time value: one base pointer, immediate offsets
-        const int32_t *cp = C + (size_t)(crow0 + 32 * i) * N + ccol0;
+    auto load_c = [&](int p) __attribute__((always_inline)) {  // p may be a run-time value: one base pointer, immediate offsets
+        const int i = p / (FN / 2), j0 = 2 * (p % (FN / 2));
+        const int32_t *cp = C + (size_t)(crow0 + 32 * i) * N + ccol0 + 32 * j0;
 #pragma unroll
-        for (int j = 0; j < FN; j++)
+        for (int jj = 0; jj < 2; jj++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) cbuf[j][q] = *(const v4i *)(cp + 32 * j + 8 * q);
+            for (int q = 0; q < 4; q++) cbuf[jj][q] = *(const v4i *)(cp + 32 * jj + 8 * q);
     };
 
     v16i acc[4][FN];
@@ -313,25 +331,40 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-    auto add_c = [&](int i) {
+    auto add_c = [&](auto pc) __attribute__((always_inline)) {   // pc: compile-time part index
+        constexpr int p = decltype(pc)::value;
+        constexpr int i = p / (FN / 2), j0 = 2 * (p % (FN / 2));
+        // The adds below are inline asm, for which the compiler inserts no hazard wait states:
+        // keep every MFMA above this point and wait out the MFMA-result-to-VALU latency (a
+        // 16-pass MFMA needs 18 wait states; 32 are given) before reading accumulators.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < FN; j++)
+        for (int jj = 0; jj < 2; jj++)
 #pragma unroll
             for (int q = 0; q < 4; q++)
 #pragma unroll
-                for (int p = 0; p < 4; p++) {
+                for (int e = 0; e < 4; e++) {
                     // Integer add written as asm: a plain += makes the register allocator move
-                    // all 256 accumulators out of AGPRs (and spill); this keeps them resident.
-                    int x = acc[i][j][4 * q + p];
-                    asm volatile("v_add_u32 %0, %0, %1" : "+v"(x) : "v"(cbuf[j][q][p]));
-                    acc[i][j][4 * q + p] = x;
+                    // all the accumulators between register files (and spill); this keeps them
+                    // where the MFMAs want them (ArchVGPRs with 8 waves, AGPRs with 4).
+                    int x = acc[i][j0 + jj][4 * q + e];
+                    if constexpr (NW == 8) {
+                        asm volatile("v_add_u32 %0, %0, %1" : "+v"(x) : "v"(cbuf[jj][q][e]));
+                    } else {
+                        int t;
+                        asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_add_u32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+                                     : "+a"(x), "=&v"(t) : "v"(cbuf[jj][q][e]));
+                    }
+                    acc[i][j0 + jj][4 * q + e] = x;
                 }
     };
 
     // B fragment addressing for ds_read_b64_tr_b8: 16-lane group G = lane/16 covers columns
     // 16*(G&1) .. +15 of the 32-column fragment and k-rows 16*(G>>1) + 8t + (lane%16)/2.
     const int q16 = lane & 15, r8 = q16 >> 1, h8 = q16 & 1, ch = (lane >> 4) & 1;
-    auto read_frags = [&](int slot, int kk, v4i (&af)[4], v4i (&bf)[FN]) {
+    auto read_frags = [&](int slot, int kk, v4i (&af)[4], v4i (&bf)[FN]) __attribute__((always_inline)) {
         const uint8_t *As = smem + slot * STAGE;
         const uint8_t *Bs = As + BOFF;
 #pragma unroll
@@ -349,7 +382,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
             bf[j] = v4i{lo.x, lo.y, hi.x, hi.y};
         }
     };
-    auto mma = [&](const v4i (&af)[4], const v4i (&bf)[FN]) {
+    auto mma = [&](const v4i (&af)[4], const v4i (&bf)[FN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -361,36 +394,51 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     // stage kt+1 and barrier (all waves are then done reading stage kt, whose slot is refilled
     // with stage kt+4); read k-half 0 of stage kt+1; MFMAs on k-half 1.  LDS reads are always
     // one MFMA group ahead of their use.
-    // C quarter q is added at the end of loop segment q (segments end at nk/4, nk/2, 3nk/4, nk),
-    // when quarter q+1 is prefetched.
-    const int ev1 = nk / 4, ev2 = nk / 2, ev3 = 3 * nk / 4;
+    // The K loop runs in NPART segments; C part p is added at the end of segment p, when part
+    // p+1 is prefetched (part 0 right after the prologue's DMAs).
     constexpr int DPS = 2 * OPS;   // DMA ops per wave per stage
-    constexpr int CQ = 4 * FN;     // C loads per wave per quarter
+    constexpr int CQ = 8;          // C loads per wave per part
     // Vector-memory operations of this wave issued after stage s+1's DMAs when iteration s waits
-    // for them: stages s+2 and s+3 (if they exist), C quarter 0 (issued after the prologue's 4
-    // stages) and C quarters issued at the end of iterations before s.
-    auto pending_after = [&](int s) {
-        int n = DPS * min(2, nk - 2 - s);
-        if (s <= 2) {
-            n += CQ;
-            n += (ev1 - 1 <= s - 1 ? CQ : 0) + (ev2 - 1 <= s - 1 ? CQ : 0) + (ev3 - 1 <= s - 1 ? CQ : 0);
-        } else {
-            n += (ev1 - 1 >= s - 3 && ev1 - 1 <= s - 1) ? CQ : 0;
-            n += (ev2 - 1 >= s - 3 && ev2 - 1 <= s - 1) ? CQ : 0;
-            n += (ev3 - 1 >= s - 3 && ev3 - 1 <= s - 1) ? CQ : 0;
+    // for them: stages s+2 and s+3 (always issued: the prologue issues 0..3, step t issues t+4),
+    // C part 0 (issued after the prologue's 4 stages, so after stage s+1 when s+1 <= 3) and every
+    // C part p >= 1 whose load (after step ev_p - 1) lies between stage s+1's issue (prologue,
+    // or step s-3) and step s.
+    auto pending_after = [&](int s) __attribute__((always_inline)) {
+        int n = 2 * DPS;
+        if (s + 1 <= 3) n += CQ;
+        for (int p = 1; p < NPART; p++) {
+            const int t = p * nk / NPART - 1;
+            if ((s + 1 <= 3 || t >= s - 3) && t <= s - 1) n += CQ;
         }
         return n;
     };
+    // Instruction order inside each half-step: the ds_reads of the next fragments alternate with
+    // the MFMAs of the current ones, so LDS latency hides behind the matrix pipe even with one
+    // wave per SIMD.
+    constexpr int NRD = 4 + 2 * FN, NMF = 4 * FN;
+    auto interleave = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < NRD; r++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        }
+        if constexpr (NMF > NRD) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
+    };
     v4i a0[4], b0[FN], a1[4], b1[FN];
-    auto step = [&](int kt) {
+    auto step = [&](int kt) __attribute__((always_inline)) {   // kt < nk - 1
         read_frags(kt & (NS - 1), 1, a1, b1);
         mma(a0, b0);
-        if (kt + 1 < nk) {
-            wait_vmcnt_le(pending_after(kt));
-            lds_barrier();
-            if (kt + 4 < nk) issue(kt + 4);
-            read_frags((kt + 1) & (NS - 1), 0, a0, b0);
-        }
+        interleave();
+        wait_vmcnt_le(pending_after(kt));
+        lds_barrier();
+        issue(kt + 4);
+        read_frags((kt + 1) & (NS - 1), 0, a0, b0);
+        mma(a1, b1);
+        interleave();
+    };
+    auto last_step = [&]() __attribute__((always_inline)) {   // kt = nk - 1
+        read_frags((nk - 1) & (NS - 1), 1, a1, b1);
+        mma(a0, b0);
         mma(a1, b1);
     };
     issue(0);
@@ -401,17 +449,19 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     wait_vmcnt_le(3 * DPS + CQ);
     lds_barrier();
     read_frags(0, 0, a0, b0);
-    for (int kt = 0; kt < ev1; kt++) step(kt);
-    add_c(0);
-    load_c(1);
-    for (int kt = ev1; kt < ev2; kt++) step(kt);
-    add_c(1);
-    load_c(2);
-    for (int kt = ev2; kt < ev3; kt++) step(kt);
-    add_c(2);
-    load_c(3);
-    for (int kt = ev3; kt < nk; kt++) step(kt);
-    add_c(3);
+    static_for<NPART>([&](auto pc) __attribute__((always_inline)) {
+        constexpr int p = decltype(pc)::value;
+        const int kb = p * nk / NPART, ke = (p + 1) * nk / NPART;
+        if constexpr (p + 1 < NPART) {
+            for (int kt = kb; kt < ke; kt++) step(kt);
+            add_c(pc);
+            load_c(p + 1);
+        } else {
+            for (int kt = kb; kt < ke - 1; kt++) step(kt);
+            last_step();
+            add_c(pc);
+        }
+    });
 
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -593,6 +643,13 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
         if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
         const int tiles_m = M / 256, tiles_n = N / 256;
         hipLaunchKernelGGL(k_gemm_big<8>, dim3(tiles_m * tiles_n), dim3(512), 0, s, M, N, K, A, B, C,
+                           tiles_m, tiles_n);
+        return hipGetLastError();
+    }
+    case X100_GEMM_TILE256_W4: {
+        if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
+        const int tiles_m = M / 256, tiles_n = N / 256;
+        hipLaunchKernelGGL(k_gemm_big<4>, dim3(tiles_m * tiles_n), dim3(256), 0, s, M, N, K, A, B, C,
                            tiles_m, tiles_n);
         return hipGetLastError();
     }

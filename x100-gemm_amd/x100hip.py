@@ -32,7 +32,7 @@ EXPORTS = (
     "moe_layer_hip",
 )
 
-GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC = 0, 1, 2, 3, 4
+GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC, GEMM_TILE256_W4 = 0, 1, 2, 3, 4, 5
 
 
 class X100Error(RuntimeError):
