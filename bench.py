@@ -9,8 +9,9 @@ timed with HIP events on the launch stream.  The same JSON line carries:
   cpu_baseline  the reference's scalar gemm_ref_i8 (built from its sources into oracle/_ref, or the
                 oracle's restatement when that is absent) on a bounded row sample, 1 core;
   extra         the other measured shapes: skinny 8x4096x4096 GEMM, Q4_0 / Q4_K / Q3_K GEMV at
-                M = 1 and 4, the Qwen3-30B-A3B MoE decode layer at M = 1 and 4, each beside its
-                scalar CPU time.  GEMV and MoE run back-to-back in a captured graph over weight
+                M = 1 and 4, the int4 / int8 tile GEMV of bench/q4_gemv.c, the Qwen3-30B-A3B MoE
+                decode layer at M = 1 and 4, each beside its scalar CPU time, and the per-token
+                decode weight stream of bench/moe_decode.c (x100-gemm_amd/moe_decode.py).  GEMV and MoE run back-to-back in a captured graph over weight
                 copies totalling more than 256 MB (so the 256 MB Infinity Cache cannot hold them);
                 single-launch latency is reported separately.
 
@@ -261,6 +262,14 @@ def bench_extra(torch, timer, dev, args):
                           "cpu_us_1core": cpu_us}
             log("%s: %.2f us  %.0f GB/s  single %.2f us  cpu %.0f us" % (key, us, byts / us / 1e3, lat, cpu_us))
         del dws
+
+    # ---- Qwen3-30B-A3B decode weight stream (bench/moe_decode.c), q4 and q8 ----------------------
+    import moe_decode
+    md = moe_decode.run(torch, L=48, reps=3, us=(8, 24, 64), verbose=False)
+    for name, r in md.items():
+        extra["moe_decode_stream_" + name] = r
+        log("moe_decode %s: M=1 %.3f ms/tok (%.1f tok/s, %.0f GB/s); M=8 U=24 %.3f ms/pass (%.1f tok/s)" % (
+            name, r["m1_ms_per_token"], r["m1_tok_s"], r["m1_GB_s"], r["m8_u24_ms_per_pass"], r["m8_u24_tok_s"]))
 
     # ---- host-pointer drop-in gemm_ime_i8 at 4096^3 (PCIe copies + allocation included) ---------
     A, B = synth.gemm_inputs(4096, 4096, 4096, seed=2026)
