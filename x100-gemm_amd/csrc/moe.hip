@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
 // Outputs in LDS: s_sel/s_w [M][n_act] (slot order), s_uniq[U] = distinct experts ascending.
 // ------------------------------------------------------------------------------------------------
 struct RouteLds {
-    int sel[8 * 8];
+    __attribute__((aligned(16))) int sel[8 * 8];
     float w[8 * 8];
     int uniq[64];
     int wcnt[4];
@@ -200,44 +200,56 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
         const float inv = 1.0f / s;
-        // Probabilities are >= 0 (NaN from bad input is treated as 0), used/absent experts -2, so
-        // every pass below selects a distinct valid expert.
+        // Selection keys: the bits of the probability (>= 0, so integer order = float order; NaN
+        // from bad input is treated as 0); absent or already chosen experts are INT_MIN, so every
+        // pass selects a distinct valid expert.
+        int key[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const float pv = p[c] * inv;
-            p[c] = (lane + 64 * c) < n_exp ? (pv == pv ? pv : 0.0f) : -2.0f;
+            key[c] = (lane + 64 * c) < n_exp ? __float_as_int(pv == pv ? pv : 0.0f) : INT_MIN;
         }
         float wsel[8];
-        int isel[8];
-        for (int a = 0; a < n_act; a++) {
-            // Largest probability (DPP maximum), then the lowest expert id holding it: experts
-            // lane + 64c, so the first c whose ballot is non-empty, its lowest lane.
-            const float bv = wave_max_u(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])));
-            int bi = 0;
 #pragma unroll
-            for (int c = 3; c >= 0; c--) {
-                const uint64_t hit = __ballot(p[c] == bv);
-                if (hit) bi = 64 * c + __ffsll((unsigned long long)hit) - 1;
-            }
-            wsel[a] = bv;
-            isel[a] = bi;
+        for (int a = 0; a < 8; a++) {
+            wsel[a] = 0.0f;
+            if (a < n_act) {
+                // Largest probability (wave maximum of the keys), then the lowest expert id holding
+                // it: experts lane + 64c, so the first c whose ballot is non-empty, its lowest lane.
+                const int km = wave_max_iu(max(max(key[0], key[1]), max(key[2], key[3])));
+                const uint64_t h0 = __ballot(key[0] == km), h1 = __ballot(key[1] == km);
+                const uint64_t h2 = __ballot(key[2] == km), h3 = __ballot(key[3] == km);
+                const int bi = h0 ? __ffsll((unsigned long long)h0) - 1
+                             : h1 ? 64 + __ffsll((unsigned long long)h1) - 1
+                             : h2 ? 128 + __ffsll((unsigned long long)h2) - 1
+                                  : 192 + __ffsll((unsigned long long)h3) - 1;
+                wsel[a] = __int_as_float(km);
+                if (lane == 0) rl.sel[m * n_act + a] = bi;
 #pragma unroll
-            for (int c = 0; c < 4; c++)
-                if (lane + 64 * c == bi) p[c] = -2.0f;
-        }
-        if (lane == 0) {
-            float ssum = 0.0f;
-            for (int a = 0; a < n_act; a++) ssum += wsel[a];
-            for (int a = 0; a < n_act; a++) {
-                rl.sel[m * n_act + a] = isel[a];
-                rl.w[m * n_act + a] = wsel[a] / ssum;
+                for (int c = 0; c < 4; c++)
+                    if (lane + 64 * c == bi) key[c] = INT_MIN;
             }
         }
+        // Renormalise (qwen_moe.c:301): the sum in slot order, then one division per slot, lane a
+        // doing slot a.
+        float ssum = 0.0f;
+#pragma unroll
+        for (int a = 0; a < 8; a++)
+            if (a < n_act) ssum += wsel[a];
+        float mine = wsel[0];
+#pragma unroll
+        for (int a = 1; a < 8; a++) mine = lane == a ? wsel[a] : mine;
+        if (lane < n_act) rl.w[m * n_act + lane] = mine / ssum;
     }
     __syncthreads();
     // Union slots in ascending expert id: slot of expert e = number of selected experts below e.
     bool chosen = false;
-    for (int t = 0; t < M * n_act; t++) chosen |= rl.sel[t] == (int)threadIdx.x;
+    const int P = M * n_act;
+    for (int t0 = 0; t0 < P; t0 += 4) {
+        const v4i q = *(const v4i *)(rl.sel + t0);   // rl.sel is padded to a multiple of 4
+#pragma unroll
+        for (int k = 0; k < 4; k++) chosen |= (t0 + k < P) && q[k] == (int)threadIdx.x;
+    }
     const uint64_t bal = __ballot(chosen);
     if (lane == 0) rl.wcnt[w] = __popcll(bal);
     __syncthreads();
@@ -354,6 +366,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
         for (int sb = 0; sb < nsb; sb++) up = up + tu[sb];
         ws.act[(size_t)s_pairs[k] * ff + r0 + r] = swiglu(g, up);
     }
+    __syncthreads();
 }
 
 // ------------------------------------------------------------------------------------------------

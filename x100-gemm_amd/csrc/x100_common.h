@@ -116,6 +116,17 @@ X100_DEV float wave_max_u(float v)
     v = fmaxf(v, dpp_f<0x143, 0xc>(v, v));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// Integer maximum over the 64 lanes, wave-uniform.
+X100_DEV int wave_max_iu(int v)
+{
+    v = max(v, dpp_i<0x111>(v, v));
+    v = max(v, dpp_i<0x112>(v, v));
+    v = max(v, dpp_i<0x114>(v, v));
+    v = max(v, dpp_i<0x118>(v, v));
+    v = max(v, dpp_i<0x142, 0xa>(v, v));
+    v = max(v, dpp_i<0x143, 0xc>(v, v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
 // Sum over the 64 lanes, wave-uniform: prefix sum of rows (row_shr 1, 2, 4, 8), then rows
 // combined into lane 63.  For integers, or floats whose summation order is not prescribed.
 X100_DEV int wave_sum_u(int v)
