@@ -260,7 +260,7 @@ template <int I, int N, class F> X100_DEV void static_for_impl(F &&f)
 }
 template <int N, class F> X100_DEV void static_for(F &&f) { static_for_impl<0, N>(f); }
 
-template <int NW>
+template <int NW, int SUPER>
 __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const int8_t *__restrict__ A,
                                                      const int8_t *__restrict__ B,
                                                      int32_t *__restrict__ C, int tiles_m, int tiles_n)
@@ -441,11 +441,73 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         mma(a0, b0);
         mma(a1, b1);
     };
+    // Two stages per barrier (SUPER == 2, K % 128 == 0): superstage u = stages 2u, 2u+1.  On
+    // entry slots hold 2u, 2u+1 (complete) and 2u+2, 2u+3 (in flight); before the only barrier of
+    // the superstage the wave waits for 2u+2 and 2u+3, and after it refills the slots of 2u and
+    // 2u+1 with 2u+4 and 2u+5.  Outstanding operations allowed at that wait: C parts loaded after
+    // stage 2u+3 was issued (at the previous superstage's barrier), i.e. part 0 for u = 0 and a
+    // part p loaded at the end of superstage u-1.
+    const int nsup = nk / 2;
+    auto pending_super = [&](int u) __attribute__((always_inline)) {
+        int n = u == 0 ? CQ : 0;
+        for (int p = 1; p < NPART; p++)
+            if (p * nsup / NPART - 1 == u - 1) n += CQ;
+        return n;
+    };
+    auto superstep = [&](int u) __attribute__((always_inline)) {   // u < nsup - 1
+        const int s0 = (2 * u) & (NS - 1), s1 = (2 * u + 1) & (NS - 1);
+        read_frags(s0, 1, a1, b1);
+        mma(a0, b0);
+        interleave();
+        read_frags(s1, 0, a0, b0);
+        mma(a1, b1);
+        interleave();
+        read_frags(s1, 1, a1, b1);
+        mma(a0, b0);
+        interleave();
+        wait_vmcnt_le(pending_super(u));
+        lds_barrier();
+        issue(2 * u + 4);
+        issue(2 * u + 5);
+        read_frags((2 * u + 2) & (NS - 1), 0, a0, b0);
+        mma(a1, b1);
+        interleave();
+    };
+    auto last_super = [&]() __attribute__((always_inline)) {   // u = nsup - 1
+        const int s0 = (nk - 2) & (NS - 1), s1 = (nk - 1) & (NS - 1);
+        read_frags(s0, 1, a1, b1);
+        mma(a0, b0);
+        interleave();
+        read_frags(s1, 0, a0, b0);
+        mma(a1, b1);
+        interleave();
+        read_frags(s1, 1, a1, b1);
+        mma(a0, b0);
+        mma(a1, b1);
+    };
     issue(0);
     issue(1);
     issue(2);
     issue(3);
     load_c(0);
+    if constexpr (SUPER == 2) {
+        wait_vmcnt_le(2 * DPS + CQ);   // stages 0 and 1 complete
+        lds_barrier();
+        read_frags(0, 0, a0, b0);
+        static_for<NPART>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int p = decltype(pc)::value;
+            const int ub = p * nsup / NPART, ue = (p + 1) * nsup / NPART;
+            if constexpr (p + 1 < NPART) {
+                for (int u = ub; u < ue; u++) superstep(u);
+                add_c(pc);
+                load_c(p + 1);
+            } else {
+                for (int u = ub; u < ue - 1; u++) superstep(u);
+                last_super();
+                add_c(pc);
+            }
+        });
+    } else {
     wait_vmcnt_le(3 * DPS + CQ);
     lds_barrier();
     read_frags(0, 0, a0, b0);
@@ -462,6 +524,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
             add_c(pc);
         }
     });
+    }
 
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -642,14 +705,18 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
         // Full 256x256 tiles only; other shapes use the 128x128 tile with edge guards.
         if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
         const int tiles_m = M / 256, tiles_n = N / 256;
-        hipLaunchKernelGGL(k_gemm_big<8>, dim3(tiles_m * tiles_n), dim3(512), 0, s, M, N, K, A, B, C,
-                           tiles_m, tiles_n);
+        if ((K / BK) % 8 == 0)   // whole superstages in each of the 4 C parts
+            hipLaunchKernelGGL((k_gemm_big<8, 2>), dim3(tiles_m * tiles_n), dim3(512), 0, s, M, N, K, A, B, C,
+                               tiles_m, tiles_n);
+        else
+            hipLaunchKernelGGL((k_gemm_big<8, 1>), dim3(tiles_m * tiles_n), dim3(512), 0, s, M, N, K, A, B, C,
+                               tiles_m, tiles_n);
         return hipGetLastError();
     }
     case X100_GEMM_TILE256_W4: {
         if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
         const int tiles_m = M / 256, tiles_n = N / 256;
-        hipLaunchKernelGGL(k_gemm_big<4>, dim3(tiles_m * tiles_n), dim3(256), 0, s, M, N, K, A, B, C,
+        hipLaunchKernelGGL((k_gemm_big<4, 1>), dim3(tiles_m * tiles_n), dim3(256), 0, s, M, N, K, A, B, C,
                            tiles_m, tiles_n);
         return hipGetLastError();
     }
