@@ -526,14 +526,29 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     });
     }
 
+    // Epilogue: each 32-row accumulator tile goes through a wave-private LDS area (the ring is free
+    // once every wave has passed the barrier) so that every global store writes whole row segments
+    // of the wave's FN*128-byte column range: 1 KiB contiguous per instruction instead of 32 rows
+    // x 32 bytes.  Row pitch FN*128 + 16 bytes keeps both LDS access patterns conflict-free.
+    lds_barrier();
+    constexpr int PB = FN * 128 + 16;   // LDS row pitch (bytes)
+    constexpr int CPR = FN * 8;         // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;       // rows per store instruction
+    uint8_t *cst = smem + w * (32 * PB);
+    const int sr = lane / CPR, sc = lane % CPR;
+    int32_t *cw = C + (size_t)(m0 + wm * 128 + sr) * N + n0 + wn * FN * 32 + 4 * sc;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
 #pragma unroll
         for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                *(v4i *)(C + (size_t)(crow0 + 32 * i) * N + ccol0 + 32 * j + 8 * q) =
+                *(v4i *)(cst + lcol * PB + 4 * (32 * j + 8 * q + 4 * lgrp)) =
                     v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+#pragma unroll
+        for (int t = 0; t < 32 / RPI; t++)
+            *(v4i *)(cw + (size_t)(32 * i + RPI * t) * N) = *(const v4i *)(cst + (RPI * t + sr) * PB + 16 * sc);
+    }
 }
 
 // Skinny GEMM, M <= MR rows.  Block = 4 waves over columns [n0, n0+256) and k rows

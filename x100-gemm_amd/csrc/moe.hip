@@ -38,7 +38,7 @@ struct MoeWs {
 inline size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Bytes of one row's Q8_K record (nsb 256-element blocks).
-X100_DEV __host__ inline int q8k_rec_bytes(int nsb) { return (nsb * (256 + 64 + 4) + 15) & ~15; }
+__host__ __device__ inline int q8k_rec_bytes(int nsb) { return (nsb * (256 + 64 + 4) + 15) & ~15; }
 
 // Quantize one 256-element block to Q8_K with one wave (same operations as pack_A_q3k): v is the
 // lane's float4 (elements 4*lane .. 4*lane+3).
