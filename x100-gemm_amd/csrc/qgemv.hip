@@ -30,14 +30,21 @@ X100_DEV uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int k)
 }
 X100_DEV void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &m)
 {
-    if (j < 4) {
-        sc = sbyte(s0, s1, s2, j) & 63;
-        m = sbyte(s0, s1, s2, j + 4) & 63;
-    } else {
-        sc = (sbyte(s0, s1, s2, j + 4) & 0xf) | ((sbyte(s0, s1, s2, j - 4) >> 6) << 4);
-        m = (sbyte(s0, s1, s2, j + 4) >> 4) | ((sbyte(s0, s1, s2, j) >> 6) << 4);
-    }
+    // Both forms computed and selected (j is lane-dependent here: a branch would split the
+    // unrolled loop); byte indices are taken modulo 12 so every read stays in the 12 bytes.
+    const uint32_t bj = sbyte(s0, s1, s2, j), bj4 = sbyte(s0, s1, s2, (j + 4) % 12);
+    const uint32_t bjm4 = sbyte(s0, s1, s2, (j + 8) % 12);   // byte j - 4 for j >= 4
+    const int sc_lo = (int)(bj & 63), m_lo = (int)(bj4 & 63);
+    const int sc_hi = (int)((bj4 & 0xf) | ((bjm4 >> 6) << 4));
+    const int m_hi = (int)((bj4 >> 4) | ((bj >> 6) << 4));
+    sc = j < 4 ? sc_lo : sc_hi;
+    m = j < 4 ? m_lo : m_hi;
 }
+
+// u / d and u % d for 0 <= u < 2^16 and 1 <= d <= 2^16 with the multiplier mg = ceil(2^32 / d)
+// (exact in that range).
+X100_DEV int fast_div(uint32_t u, uint32_t mg) { return (int)__umulhi(u, mg); }
+inline uint32_t div_magic(uint32_t d) { return (uint32_t)((0x100000000ull + d - 1) / d); }
 
 // ------------------------------------------------------------------------------------------------
 // Q4_0 x Q8_0
@@ -51,10 +58,11 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nb = K / 32;
+    const int nb1 = MR * nb + 1;                 // + the quantizer's spare block
     int8_t *xlo = (int8_t *)smem;
-    int8_t *xhi = xlo + MR * nb * 16;
-    float *xd = (float *)(xhi + MR * nb * 16);
-    int *xs = (int *)(xd + MR * nb);
+    int8_t *xhi = xlo + nb1 * 16;
+    float *xd = (float *)(xhi + nb1 * 16);
+    int *xs = (int *)(xd + nb1);
 
     const int lane = threadIdx.x & 63, w = wave_id();
     const int rowb = blockIdx.x * 4 * RPW + w * RPW;
@@ -95,31 +103,32 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
         for (int m = 0; m < MR; m++) acc[m] = 0.0f;
 #pragma unroll
         for (int c = 0; c < BPL; c++) {
-            const int b = lane + 64 * c;
-            if (b < nb) {
-                const v4i qq = q[r][c];
-                const float dwf = h2f((uint16_t)dwb[r][c]);
-                int lo[4], hi[4];
+            // Branch-free (the scheduler interleaves the unrolled blocks): a lane past the last
+            // block reads block nb-1 and adds 0.  Rows m >= M compute on unused LDS and are not
+            // stored.
+            const bool inb = lane + 64 * c < nb;
+            const int b = min(lane + 64 * c, nb - 1);
+            const v4i qq = q[r][c];
+            const float dwf = h2f((uint16_t)dwb[r][c]);
+            int lo[4], hi[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                lo[t] = qq[t] & 0x0F0F0F0F;
+                hi[t] = (qq[t] >> 4) & 0x0F0F0F0F;
+            }
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const v4i xl = *(const v4i *)(xlo + (m * nb + b) * 16);
+                const v4i xh = *(const v4i *)(xhi + (m * nb + b) * 16);
+                int s = 0;
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    lo[t] = qq[t] & 0x0F0F0F0F;
-                    hi[t] = (qq[t] >> 4) & 0x0F0F0F0F;
+                    s = dot4(lo[t], xl[t], s);
+                    s = dot4(hi[t], xh[t], s);
                 }
-#pragma unroll
-                for (int m = 0; m < MR; m++) {
-                    if (m < M) {
-                        const v4i xl = *(const v4i *)(xlo + (m * nb + b) * 16);
-                        const v4i xh = *(const v4i *)(xhi + (m * nb + b) * 16);
-                        int s = 0;
-#pragma unroll
-                        for (int t = 0; t < 4; t++) {
-                            s = dot4(lo[t], xl[t], s);
-                            s = dot4(hi[t], xh[t], s);
-                        }
-                        s -= 8 * xs[m * nb + b];  // nibble offset: (q-8).x = q.x - 8*sum(x)
-                        acc[m] += (float)s * (dwf * xd[m * nb + b]);
-                    }
-                }
+                s -= 8 * xs[m * nb + b];  // nibble offset: (q-8).x = q.x - 8*sum(x)
+                const float term = (float)s * (dwf * xd[m * nb + b]);
+                acc[m] += inb ? term : 0.0f;
             }
         }
 #pragma unroll
@@ -140,16 +149,17 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
 // nibbles = sub-block 2*(i/2)+1, elements 16*(i%2) .. +15 of each.  A block of R rows has
 // R*nsb units; wave w takes units w*8 + lane/8 + 32*c.
 template <int MR, int UPL>
-__global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R,
+__global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R, uint32_t nsb_mg,
                                               const uint8_t *__restrict__ W,
                                               const float *__restrict__ x, float *__restrict__ y)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nsb = K / 256;
+    const int ns1 = MR * nsb + 1;                  // + the quantizer's spare block
     int8_t *xq = (int8_t *)smem;                   // [MR][nsb][256]
-    int *xbs = (int *)(xq + MR * nsb * 256);       // [MR][nsb][16]
-    float *xd = (float *)(xbs + MR * nsb * 16);    // [MR][nsb]
-    float *tv = xd + MR * nsb;                     // [MR][R*nsb]
+    int *xbs = (int *)(xq + ns1 * 256);            // [MR][nsb][16]
+    float *xd = (float *)(xbs + ns1 * 16);         // [MR][nsb]
+    float *tv = xd + ns1;                          // [MR][R*nsb] + one spare
 
     const int lane = threadIdx.x & 63, w = wave_id();
     const int i = lane & 7, p = i >> 1, h = i & 1;
@@ -184,7 +194,7 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R,
     for (int c = 0; c < UPL; c++) {
         const int u = w * 8 + (lane >> 3) + 32 * c;
         const bool valid = u < U;  // uniform over the 8 lanes of a unit
-        const int sb = valid ? u % nsb : 0;
+        const int sb = valid ? u - fast_div(u, nsb_mg) * nsb : 0;
         const uint32_t h0 = (uint32_t)hdr[c][0];
         const float d = h2f((uint16_t)(h0 & 0xffff)), dmin = h2f((uint16_t)(h0 >> 16));
         int sc0, m0, sc1, m1;
@@ -198,25 +208,23 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R,
         }
 #pragma unroll
         for (int m = 0; m < MR; m++) {
-            if (m < M) {
-                const int8_t *xb = xq + (m * nsb + sb) * 256;
-                const v4i xa = *(const v4i *)(xb + 64 * p + 16 * h);
-                const v4i xc = *(const v4i *)(xb + 64 * p + 32 + 16 * h);
-                int d0 = 0, d1 = 0;
+            // Branch-free: rows m >= M compute on unused LDS and are never combined; the 8 lanes
+            // of a unit hold the same sums and store the same value; invalid units use the spare.
+            const int8_t *xb = xq + (m * nsb + sb) * 256;
+            const v4i xa = *(const v4i *)(xb + 64 * p + 16 * h);
+            const v4i xc = *(const v4i *)(xb + 64 * p + 32 + 16 * h);
+            int d0 = 0, d1 = 0;
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    d0 = dot4(lo[t], xa[t], d0);
-                    d1 = dot4(hi[t], xc[t], d1);
-                }
-                const int *bs = xbs + (m * nsb + sb) * 16;
-                const int isc = sum8_i(sc0 * d0 + sc1 * d1);
-                const int imn = sum8_i(m0 * bs[4 * p + h] + m1 * bs[4 * p + 2 + h]);
-                if (valid && i == 0) {
-                    const float dx = xd[m * nsb + sb];
-                    const float dd = dx * d, dm = dx * dmin;
-                    tv[m * R * nsb + u] = dd * (float)isc - dm * (float)imn;
-                }
+            for (int t = 0; t < 4; t++) {
+                d0 = dot4(lo[t], xa[t], d0);
+                d1 = dot4(hi[t], xc[t], d1);
             }
+            const int *bs = xbs + (m * nsb + sb) * 16;
+            const int isc = sum8_i(sc0 * d0 + sc1 * d1);
+            const int imn = sum8_i(m0 * bs[4 * p + h] + m1 * bs[4 * p + 2 + h]);
+            const float dx = xd[m * nsb + sb];
+            const float dd = dx * d, dm = dx * dmin;
+            tv[valid ? m * R * nsb + u : MR * R * nsb] = dd * (float)isc - dm * (float)imn;
         }
     }
     __syncthreads();
@@ -240,7 +248,7 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R,
 // 128hh + 32j + 16lh + (0..15), j = 0..3 (shift 2j, hmask bit 4hh+j, scale index 8hh+2j+lh),
 // as in dequantize_q3_K_block (qwen_moe_q3k.c:565-575).  Wave w takes units w*16 + lane/4 + 64*c.
 template <int MR, int UPL>
-__global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
+__global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R, uint32_t nsb_mg,
                                               const uint8_t *__restrict__ hq,
                                               const uint8_t *__restrict__ scl,
                                               const uint16_t *__restrict__ wdd,
@@ -248,10 +256,11 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nsb = K / 256;
-    int8_t *xq = (int8_t *)smem;
-    int *xbs = (int *)(xq + MR * nsb * 256);
-    float *xd = (float *)(xbs + MR * nsb * 16);
-    float *tv = xd + MR * nsb;
+    const int ns1 = MR * nsb + 1;                  // + the quantizer's spare block
+    int8_t *xq = (int8_t *)smem;                   // [MR][nsb][256]
+    int *xbs = (int *)(xq + ns1 * 256);            // [MR][nsb][16]
+    float *xd = (float *)(xbs + ns1 * 16);         // [MR][nsb]
+    float *tv = xd + ns1;                          // [MR][R*nsb] + one spare
 
     const int lane = threadIdx.x & 63, w = wave_id();
     const int i = lane & 3, hh = i >> 1, lh = i & 1;
@@ -293,7 +302,7 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
     for (int c = 0; c < UPL; c++) {
         const int u = w * 16 + (lane >> 2) + 64 * c;
         const bool valid = u < U;
-        const int sb = valid ? u % nsb : 0;
+        const int sb = valid ? u - fast_div(u, nsb_mg) * nsb : 0;
         int scl_j[4];
         int v[4][4];
 #pragma unroll
@@ -315,25 +324,22 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R,
         const float dw = h2f((uint16_t)dv[c]);
 #pragma unroll
         for (int m = 0; m < MR; m++) {
-            if (m < M) {
-                const int8_t *xb = xq + (m * nsb + sb) * 256 + 128 * hh + 16 * lh;
-                const int *bs = xbs + (m * nsb + sb) * 16 + 8 * hh + lh;
-                int isc = 0;
+            // Branch-free, as in k_q4_K.
+            const int8_t *xb = xq + (m * nsb + sb) * 256 + 128 * hh + 16 * lh;
+            const int *bs = xbs + (m * nsb + sb) * 16 + 8 * hh + lh;
+            int isc = 0;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const v4i xv = *(const v4i *)(xb + 32 * j);
-                    int dsum = 0;
+            for (int j = 0; j < 4; j++) {
+                const v4i xv = *(const v4i *)(xb + 32 * j);
+                int dsum = 0;
 #pragma unroll
-                    for (int t = 0; t < 4; t++) dsum = dot4(v[j][t], xv[t], dsum);
-                    dsum -= 4 * bs[2 * j];
-                    isc += scl_j[j] * dsum;
-                }
-                isc = sum4_i(isc);
-                if (valid && i == 0) {
-                    const float dx = xd[m * nsb + sb];
-                    tv[m * R * nsb + u] = (dx * dw) * (float)isc;
-                }
+                for (int t = 0; t < 4; t++) dsum = dot4(v[j][t], xv[t], dsum);
+                dsum -= 4 * bs[2 * j];
+                isc += scl_j[j] * dsum;
             }
+            isc = sum4_i(isc);
+            const float dx = xd[m * nsb + sb];
+            tv[valid ? m * R * nsb + u : MR * R * nsb] = (dx * dw) * (float)isc;
         }
     }
     __syncthreads();
@@ -432,7 +438,7 @@ hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float
     const size_t nblk = (size_t)N * nb;
     const uint16_t *wd = (const uint16_t *)w;
     const uint8_t *wq = (const uint8_t *)w + align256(nblk * 2);
-    const size_t lds = (size_t)MR * nb * 40;
+    const size_t lds = ((size_t)MR * nb + 1) * 40;
     constexpr int RPW = 4;
     const dim3 grid((N + 4 * RPW - 1) / (4 * RPW));
     if (nb <= 64)
@@ -452,14 +458,14 @@ hipError_t launch_kq_upl(int qtype, dim3 grid, size_t lds, int M, int N, int K, 
                          const float *x, float *y, hipStream_t s)
 {
     if (qtype == X100_Q4_K) {
-        hipLaunchKernelGGL((k_q4_K<MR, UPL>), grid, dim3(256), lds, s, M, N, K, R,
+        hipLaunchKernelGGL((k_q4_K<MR, UPL>), grid, dim3(256), lds, s, M, N, K, R, div_magic(K / 256),
                            (const uint8_t *)w, x, y);
     } else {
         const size_t nblk = (size_t)N * (K / 256);
         const uint8_t *hq = (const uint8_t *)w;
         const uint8_t *scl = hq + nblk * 96;
         const uint16_t *dd = (const uint16_t *)(scl + nblk * 12);
-        hipLaunchKernelGGL((k_q3_K<MR, UPL>), grid, dim3(256), lds, s, M, N, K, R, hq, scl, dd, x, y);
+        hipLaunchKernelGGL((k_q3_K<MR, UPL>), grid, dim3(256), lds, s, M, N, K, R, div_magic(K / 256), hq, scl, dd, x, y);
     }
     return hipGetLastError();
 }
@@ -478,7 +484,7 @@ hipError_t launch_kq(int qtype, int M, int N, int K, const void *w, const float 
     if (R < 1) return hipErrorInvalidValue;  // a single row does not fit in one pass
     int upl = (R * nsb + UNITS_PER_PASS - 1) / UNITS_PER_PASS;
     const dim3 grid((N + R - 1) / R);
-    const size_t lds = (size_t)MR * nsb * (256 + 64 + 4) + (size_t)MR * R * nsb * 4;
+    const size_t lds = ((size_t)MR * nsb + 1) * (256 + 64 + 4) + ((size_t)MR * R * nsb + 1) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if (upl <= 1) return launch_kq_upl<MR, 1>(qtype, grid, lds, M, N, K, R, w, x, y, s);
     if (upl <= 2) return launch_kq_upl<MR, 2>(qtype, grid, lds, M, N, K, R, w, x, y, s);
@@ -496,7 +502,7 @@ hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, cons
     if (M < 1 || M > 8) return hipErrorInvalidValue;
     if (qtype == X100_Q4_0) {
         if (K % 32 || K / 32 > 512) return hipErrorInvalidValue;
-        if ((size_t)(M <= 1 ? 1 : (M <= 4 ? 4 : 8)) * (K / 32) * 40 > 160 * 1024) return hipErrorInvalidValue;
+        if (((size_t)(M <= 1 ? 1 : (M <= 4 ? 4 : 8)) * (K / 32) + 1) * 40 > 160 * 1024) return hipErrorInvalidValue;
         if (M == 1) return launch_q4_0<1>(M, N, K, w, x, y, s);
         if (M <= 4) return launch_q4_0<4>(M, N, K, w, x, y, s);
         return launch_q4_0<8>(M, N, K, w, x, y, s);

@@ -196,6 +196,9 @@ X100_DEV void x_load(rsrc_t xr, int c0, float4 (&v)[XPT])
     for (int i = 0; i < XPT; i++) v[i] = buf_load_f4(xr, (uint32_t)(c0 + threadIdx.x + 256 * i) * 16u);
 }
 
+// Branch-free stores (so the unrolled iterations can be interleaved by the scheduler): blocks past
+// the end go to the spare slot (index M*nb / M*nsb) that the LDS layout provides, and values that
+// several lanes hold (d, sum) are stored by all of them.
 template <int XPT>
 X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, int8_t *xlo,
                              int8_t *xhi, float *xd, int *xs)
@@ -211,20 +214,15 @@ X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, 
         const int q0 = clamp_i8((int)rintf(v[i].x * inv)), q1 = clamp_i8((int)rintf(v[i].y * inv));
         const int q2 = clamp_i8((int)rintf(v[i].z * inv)), q3 = clamp_i8((int)rintf(v[i].w * inv));
         const int s = sum8_i(q0 + q1 + q2 + q3);
-        if (f < total4) {   // uniform per 8-thread block: total4 is a multiple of 8
-            const int e = 4 * f, m = e / K, k = e - m * K;
-            const int b = m * nb + k / 32, pos = k & 31;
-            const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                                    ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-            if (pos < 16)
-                ((uint32_t *)(xlo + b * 16))[pos / 4] = packed;
-            else
-                ((uint32_t *)(xhi + b * 16))[(pos - 16) / 4] = packed;
-            if (pos == 0) {
-                xd[b] = h2f(f2h(d));
-                xs[b] = s;
-            }
-        }
+        const int e = 4 * f, m = e / K, k = e - m * K;
+        const int pos = k & 31;
+        const int b = f < total4 ? m * nb + k / 32 : total4 / 8;   // spare block past the end
+        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+        int8_t *dst = pos < 16 ? xlo + b * 16 + pos : xhi + b * 16 + (pos - 16);
+        *(uint32_t *)dst = packed;
+        xd[b] = h2f(f2h(d));   // the 8 lanes of a block hold the same d and sum
+        xs[b] = s;
     }
 }
 
@@ -242,13 +240,12 @@ X100_DEV void q8_K_from_regs(const float4 (&v)[XPT], int c0, int total4, int8_t 
         const int q0 = clamp_i8((int)roundf(v[i].x * rep)), q1 = clamp_i8((int)roundf(v[i].y * rep));
         const int q2 = clamp_i8((int)roundf(v[i].z * rep)), q3 = clamp_i8((int)roundf(v[i].w * rep));
         const int s = sum4_i(q0 + q1 + q2 + q3);
-        if (f < total4) {   // uniform per wave: total4 is a multiple of 64
-            const int blk = f / 64;   // flattened (row, super-block) index
-            ((uint32_t *)(xq + blk * 256))[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                                                   ((uint32_t)(q2 & 0xff) << 16) |
-                                                   ((uint32_t)(q3 & 0xff) << 24);
-            if ((lane & 3) == 0) xbs[blk * 16 + (lane >> 2)] = s;
-            if (lane == 0) xd[blk] = d;
-        }
+        // flattened (row, super-block) index, uniform per wave (total4 is a multiple of 64); the
+        // spare block total4/64 takes waves past the end
+        const int blk = min(f, total4) / 64;
+        ((uint32_t *)(xq + blk * 256))[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                               ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+        xbs[blk * 16 + (lane >> 2)] = s;   // the 4 lanes of a 16-group hold the same sum
+        xd[blk] = d;                       // d is wave-uniform
     }
 }
