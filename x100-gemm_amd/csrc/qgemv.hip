@@ -51,7 +51,7 @@ inline uint32_t div_magic(uint32_t d) { return (uint32_t)((0x100000000ull + d - 
 // ------------------------------------------------------------------------------------------------
 // Block = 4 waves; wave w owns rows row0 + w*RPW .. +RPW-1; lane l owns blocks l, l+64, ...
 // (BPL per row).  All RPW*BPL nibble loads (16 B) and scale loads are issued first.
-template <int MR, int RPW, int BPL>
+template <int MR, int RPW, int BPL, int XPT>
 __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_t *__restrict__ wd,
                                               const uint8_t *__restrict__ wq,
                                               const float *__restrict__ x, float *__restrict__ y)
@@ -67,7 +67,6 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
     const int lane = threadIdx.x & 63, w = wave_id();
     const int rowb = blockIdx.x * 4 * RPW + w * RPW;
 
-    constexpr int XPT = MR == 1 ? 4 : 16;
     const int total4 = M * K / 4;
     const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
     float4 xv[XPT];
@@ -148,7 +147,7 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
 // (d, dmin, scales: 16 B) and qs bytes [16i, 16i+16): low nibbles = sub-block 2*(i/2), high
 // nibbles = sub-block 2*(i/2)+1, elements 16*(i%2) .. +15 of each.  A block of R rows has
 // R*nsb units; wave w takes units w*8 + lane/8 + 32*c.
-template <int MR, int UPL>
+template <int MR, int UPL, int XPT>
 __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R, uint32_t nsb_mg,
                                               const uint8_t *__restrict__ W,
                                               const float *__restrict__ x, float *__restrict__ y)
@@ -167,7 +166,6 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R, uint32
     const int nrows = min(R, N - row0);
     const int U = nrows * nsb;
 
-    constexpr int XPT = MR == 1 ? 4 : 16;
     const int total4 = M * K / 4;
     const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
     float4 xv[XPT];
@@ -247,7 +245,7 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R, uint32
 // [32hh + 16lh, +16) and hmask bytes [16lh, +16) and decodes the 64 elements
 // 128hh + 32j + 16lh + (0..15), j = 0..3 (shift 2j, hmask bit 4hh+j, scale index 8hh+2j+lh),
 // as in dequantize_q3_K_block (qwen_moe_q3k.c:565-575).  Wave w takes units w*16 + lane/4 + 64*c.
-template <int MR, int UPL>
+template <int MR, int UPL, int XPT>
 __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R, uint32_t nsb_mg,
                                               const uint8_t *__restrict__ hq,
                                               const uint8_t *__restrict__ scl,
@@ -268,7 +266,6 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R, uint32
     const int nrows = min(R, N - row0);
     const int U = nrows * nsb;
 
-    constexpr int XPT = MR == 1 ? 4 : 16;
     const int total4 = M * K / 4;
     const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
     float4 xv[XPT];
@@ -431,8 +428,11 @@ hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *ds
 
 namespace {
 
-template <int MR>
-hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
+// Activation float4 per thread per load pass: enough for M*K <= 1024*XPT in one pass.
+inline int xpt_for(int M, int K) { const int need = (M * K + 1023) / 1024; return need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16; }
+
+template <int MR, int XPT>
+hipError_t launch_q4_0_x(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
 {
     const int nb = K / 32;
     const size_t nblk = (size_t)N * nb;
@@ -442,32 +442,55 @@ hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float
     constexpr int RPW = 4;
     const dim3 grid((N + 4 * RPW - 1) / (4 * RPW));
     if (nb <= 64)
-        hipLaunchKernelGGL((k_q4_0<MR, RPW, 1>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, 1, XPT>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
     else if (nb <= 128)
-        hipLaunchKernelGGL((k_q4_0<MR, RPW, 2>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, 2, XPT>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
     else if (nb <= 256)
-        hipLaunchKernelGGL((k_q4_0<MR, RPW, 4>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, 4, XPT>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
     else
-        hipLaunchKernelGGL((k_q4_0<MR, RPW, 8>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, 8, XPT>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
     return hipGetLastError();
 }
 
+template <int MR>
+hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
+{
+    switch (xpt_for(M, K)) {
+    case 2: return launch_q4_0_x<MR, 2>(M, N, K, w, x, y, s);
+    case 4: return launch_q4_0_x<MR, 4>(M, N, K, w, x, y, s);
+    case 8: return launch_q4_0_x<MR, 8>(M, N, K, w, x, y, s);
+    default: return launch_q4_0_x<MR, 16>(M, N, K, w, x, y, s);
+    }
+}
+
 // One K-quant launch with a compile-time number of work units per lane.
-template <int MR, int UPL>
-hipError_t launch_kq_upl(int qtype, dim3 grid, size_t lds, int M, int N, int K, int R, const void *w,
-                         const float *x, float *y, hipStream_t s)
+template <int MR, int UPL, int XPT>
+hipError_t launch_kq_upl_x(int qtype, dim3 grid, size_t lds, int M, int N, int K, int R, const void *w,
+                           const float *x, float *y, hipStream_t s)
 {
     if (qtype == X100_Q4_K) {
-        hipLaunchKernelGGL((k_q4_K<MR, UPL>), grid, dim3(256), lds, s, M, N, K, R, div_magic(K / 256),
+        hipLaunchKernelGGL((k_q4_K<MR, UPL, XPT>), grid, dim3(256), lds, s, M, N, K, R, div_magic(K / 256),
                            (const uint8_t *)w, x, y);
     } else {
         const size_t nblk = (size_t)N * (K / 256);
         const uint8_t *hq = (const uint8_t *)w;
         const uint8_t *scl = hq + nblk * 96;
         const uint16_t *dd = (const uint16_t *)(scl + nblk * 12);
-        hipLaunchKernelGGL((k_q3_K<MR, UPL>), grid, dim3(256), lds, s, M, N, K, R, div_magic(K / 256), hq, scl, dd, x, y);
+        hipLaunchKernelGGL((k_q3_K<MR, UPL, XPT>), grid, dim3(256), lds, s, M, N, K, R, div_magic(K / 256), hq, scl, dd, x, y);
     }
     return hipGetLastError();
+}
+
+template <int MR, int UPL>
+hipError_t launch_kq_upl(int qtype, dim3 grid, size_t lds, int M, int N, int K, int R, const void *w,
+                         const float *x, float *y, hipStream_t s)
+{
+    switch (xpt_for(M, K)) {
+    case 2: return launch_kq_upl_x<MR, UPL, 2>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    case 4: return launch_kq_upl_x<MR, UPL, 4>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    case 8: return launch_kq_upl_x<MR, UPL, 8>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    default: return launch_kq_upl_x<MR, UPL, 16>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    }
 }
 
 // Rows per block R for the K-quant kernels: about 256 blocks, each lane holding UPL <= 8 units
