@@ -54,8 +54,8 @@ X100_DEV void q8k_wave(const float4 v, int8_t *qs, int *bs, float *dout)
     ((uint32_t *)qs)[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
                              ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
     const int s = sum4_i(q0 + q1 + q2 + q3);
-    if ((lane & 3) == 0) bs[lane >> 2] = s;
-    if (lane == 0) *dout = d;
+    bs[lane >> 2] = s;   // the 4 lanes of a 16-group hold the same sum (no branch)
+    *dout = d;           // d is wave-uniform
 }
 
 // get_scale_min_k4 (repack.cpp:222-233) over the header dwords 1..3 of a Q4_K block.
@@ -66,13 +66,11 @@ X100_DEV uint32_t hbyte(const v4i &h, int k)
 }
 X100_DEV void gsm(const v4i &h, int j, int &sc, int &m)
 {
-    if (j < 4) {
-        sc = hbyte(h, j) & 63;
-        m = hbyte(h, j + 4) & 63;
-    } else {
-        sc = (hbyte(h, j + 4) & 0xf) | ((hbyte(h, j - 4) >> 6) << 4);
-        m = (hbyte(h, j + 4) >> 4) | ((hbyte(h, j) >> 6) << 4);
-    }
+    // Both forms computed and selected (j is lane-dependent: no branch in the unrolled loops);
+    // byte indices modulo 12 keep every read inside the 12 scale bytes.
+    const uint32_t bj = hbyte(h, j), bj4 = hbyte(h, (j + 4) % 12), bjm4 = hbyte(h, (j + 8) % 12);
+    sc = j < 4 ? (int)(bj & 63) : (int)((bj4 & 0xf) | ((bjm4 >> 6) << 4));
+    m = j < 4 ? (int)(bj4 & 63) : (int)((bj4 >> 4) | ((bj >> 6) << 4));
 }
 
 // Integer part of one Q4_K x Q8_K super-block dot over the 8 lanes of a unit (lane i of 8 holds
@@ -340,18 +338,21 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
     const int cnt = s_cnt;
     float *tv = (float *)(smem + ((size_t)M * rec + 1023) / 1024 * 1024);   // [8][2][GU_ROWS][nsb]
 
+    // Token rows outer, units inner (unrolled and branch-free so the scheduler interleaves them):
+    // the 8 lanes of a unit store the same value; invalid units write the spare slot.
+    const int tv_spare = 8 * 2 * GU_ROWS * nsb;
+    for (int k = 0; k < cnt; k++) {
+        const uint8_t *xr = smem + (size_t)(s_pairs[k] / n_act) * rec;
 #pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        const int un = c * 32 + w * 8 + (lane >> 3);
-        const bool valid = un < nunits;
-        const int sb = valid ? un % nsb : 0;
-        for (int k = 0; k < cnt; k++) {
-            const uint8_t *xr = smem + (size_t)(s_pairs[k] / n_act) * rec;
+        for (int c = 0; c < UPL; c++) {
+            const int un = c * 32 + w * 8 + (lane >> 3);
+            const bool valid = un < nunits;
+            const int sb = valid ? un % nsb : 0;
             int isc, imn;
             q4k_unit_dot(hdr[c], qs[c], (const int8_t *)xr + sb * 256, (const int *)(xr + nsb * 256) + sb * 16,
                          i, isc, imn);
-            if (valid && i == 0)
-                tv[k * 2 * GU_ROWS * nsb + un] = q4k_combine(hdr[c], ((const float *)(xr + nsb * 320))[sb], isc, imn);
+            tv[valid ? k * 2 * GU_ROWS * nsb + un : tv_spare] =
+                q4k_combine(hdr[c], ((const float *)(xr + nsb * 320))[sb], isc, imn);
         }
     }
     __syncthreads();
@@ -432,15 +433,16 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
     if (threadIdx.x < 8) s_pr[threadIdx.x] = prl;
     __syncthreads();
 
+    // As in gate/up: pairs outer, units inner, branch-free (spare slot 8 * nunits).
+    for (int k = 0; k < cnt; k++) {
 #pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        const int un = c * 32 + w * 8 + (lane >> 3);
-        const bool valid = un < nunits;
-        const int sb = valid ? un % nsf : 0;
-        for (int k = 0; k < cnt; k++) {
+        for (int c = 0; c < UPL; c++) {
+            const int un = c * 32 + w * 8 + (lane >> 3);
+            const bool valid = un < nunits;
+            const int sb = valid ? un % nsf : 0;
             int isc, imn;
             q4k_unit_dot(hdr[c], qs[c], aq + (k * nsf + sb) * 256, abs_ + (k * nsf + sb) * 16, i, isc, imn);
-            if (valid && i == 0) tv[k * nunits + un] = q4k_combine(hdr[c], ad[k * nsf + sb], isc, imn);
+            tv[valid ? k * nunits + un : 8 * nunits] = q4k_combine(hdr[c], ad[k * nsf + sb], isc, imn);
         }
     }
     __syncthreads();
@@ -525,7 +527,7 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
 
-    const size_t lds_gu = ((size_t)M * q8k_rec_bytes(nsb) + 1023) / 1024 * 1024 + (size_t)8 * 2 * GU_ROWS * nsb * 4;
+    const size_t lds_gu = ((size_t)M * q8k_rec_bytes(nsb) + 1023) / 1024 * 1024 + ((size_t)8 * 2 * GU_ROWS * nsb + 1) * 4;
     const int upl_gu = (2 * GU_ROWS * nsb + 31) / 32;
     const dim3 g_gu(Umax, ff / GU_ROWS);
     const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
@@ -540,7 +542,7 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
-    const size_t lds_dn = (size_t)8 * nsf * (256 + 64 + 4) + (size_t)8 * DN_ROWS * nsf * 4;
+    const size_t lds_dn = (size_t)8 * nsf * (256 + 64 + 4) + ((size_t)8 * DN_ROWS * nsf + 1) * 4;
     const int upl_dn = (DN_ROWS * nsf + 31) / 32;
     const dim3 g_dn(Umax, d / DN_ROWS);
     const uint8_t *wd = (const uint8_t *)Wd;
