@@ -180,7 +180,7 @@ def bench_gemm(torch, timer, dev, args):
     traffic = read_traffic("gemm_i8_4096")
     roof = {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
             "frac": tops / PEAK_INT8_TOPS, "traffic": traffic,
-            "kernel": "k_gemm_big<8> (256x256 tile, 8 waves)", "algorithmic_ops_per_launch": ops}
+            "kernel": "k_gemm_big<8, 2> (256x256 tile, 8 waves, 2 K stages per barrier)", "algorithmic_ops_per_launch": ops}
     return ms, tops, roof
 
 
