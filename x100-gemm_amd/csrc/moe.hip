@@ -455,6 +455,99 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
 }
 
 // ------------------------------------------------------------------------------------------------
+// M = 1: down projection and slot combine in one launch.  Block = DN1 rows of d for every union
+// slot (units (slot, row, super-block) = U*DN1*nsf, 8 lanes each), so each block has all the y
+// values its rows need and combines them in slot order; with one token row the union is the n_act
+// selected experts and each slot's activation row is act[a] of its slot a.
+// ------------------------------------------------------------------------------------------------
+constexpr int DN1 = 8;
+
+template <int UPL>
+__global__ __launch_bounds__(256) void k_moe_down_m1(int d, int ff, int n_act, const uint8_t *__restrict__ Wd,
+                                                     MoeWs ws, float *__restrict__ out, int residual)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float s_y[8][DN1];
+    __shared__ int s_slot_u[8];
+    __shared__ float s_w[8];
+    const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
+    const int U = *ws.nuniq;
+    const int nsf = ff / 256;
+    const int r0 = blockIdx.x * DN1;
+    const int nunits = U * DN1 * nsf;
+    const size_t erow = (size_t)nsf * 144;
+    const size_t emat = erow * d;
+    // lane l (< 8) holds slot a of union entry l, and the expert of each unit is read per lane:
+    // one round trip for all the metadata
+    const int pu = ws.upairs[min(lane, 7) * 8];
+
+    v4i hdr[UPL], qs[UPL];
+#pragma unroll
+    for (int c = 0; c < UPL; c++) {
+        const int un = min(c * 32 + w * 8 + (lane >> 3), nunits - 1);   // clamped: see k_moe_gate_up
+        const int u = un / (DN1 * nsf), rem = un - u * DN1 * nsf;
+        const int r = rem / nsf, sb = rem - r * nsf;
+        const int ex = ws.uniq[u];
+        const uint8_t *blk = Wd + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
+        hdr[c] = *(const v4i *)blk;
+        qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
+    }
+
+    // Q8_K of the U activation rows (one wave per 256-element block) -> LDS.
+    int8_t *aq = (int8_t *)smem;                    // [8][nsf][256]
+    int *abs_ = (int *)(aq + 8 * nsf * 256);        // [8][nsf][16]
+    float *ad = (float *)(abs_ + 8 * nsf * 16);     // [8][nsf]
+    float *tv = ad + 8 * nsf;                       // [8][DN1][nsf] + one spare
+    const int nq = U * nsf;
+    for (int q0 = 0; q0 < nq; q0 += 16) {
+        float4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int q = min(q0 + 4 * j + w, nq - 1);   // clamped; only q < nq is used
+            const int u = q / nsf, sb = q - u * nsf;
+            v[j] = *(const float4 *)(ws.act + (size_t)__builtin_amdgcn_readlane(pu, u) * ff + sb * 256 + 4 * lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int q = q0 + 4 * j + w;
+            if (q < nq) q8k_wave(v[j], aq + q * 256, abs_ + q * 16, ad + q);
+        }
+    }
+    if (threadIdx.x < U) s_slot_u[pu] = threadIdx.x;   // thread u < 8 is lane u of wave 0
+    if (threadIdx.x < n_act) s_w[threadIdx.x] = ws.sw[threadIdx.x];
+    __syncthreads();
+
+#pragma unroll
+    for (int c = 0; c < UPL; c++) {
+        const int un = c * 32 + w * 8 + (lane >> 3);
+        const bool valid = un < nunits;
+        const int unc = valid ? un : 0;
+        const int u = unc / (DN1 * nsf), rem = unc - u * DN1 * nsf;
+        const int sb = rem - (rem / nsf) * nsf;
+        int isc, imn;
+        q4k_unit_dot(hdr[c], qs[c], aq + (u * nsf + sb) * 256, abs_ + (u * nsf + sb) * 16, i, isc, imn);
+        tv[valid ? un : 8 * DN1 * nsf] = q4k_combine(hdr[c], ad[u * nsf + sb], isc, imn);
+    }
+    __syncthreads();
+    // y of each (slot, row): sequential over super-blocks (the oracle's order)
+    for (int t = threadIdx.x; t < U * DN1; t += 256) {
+        const int u = t / DN1, r = t - u * DN1;
+        float y = 0.0f;
+        for (int sb = 0; sb < nsf; sb++) y = y + tv[(u * DN1 + r) * nsf + sb];
+        s_y[u][r] = y;
+    }
+    __syncthreads();
+    // out (+)= sum over slots a = 0..n_act-1 of w_a * y_a (qwen_moe.c:310-311)
+    if (threadIdx.x < DN1) {
+        const int row = r0 + threadIdx.x;
+        float eo = 0.0f;
+        for (int a = 0; a < n_act; a++) eo = eo + s_w[a] * s_y[s_slot_u[a]][threadIdx.x];
+        out[row] = residual ? out[row] + eo : eo;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // out[m][j] (+)= sum_a sw[m][a] * y[m*n_act + a][j], a ascending (qwen_moe.c:310-311).
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_moe_combine(int M, int d, int n_act, MoeWs ws,
@@ -542,6 +635,21 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
+    if (M == 1 && d % DN1 == 0 && n_act * DN1 * nsf <= 8 * 32) {
+        // down + combine in one launch (see k_moe_down_m1)
+        const size_t lds1 = (size_t)8 * nsf * (256 + 64 + 4) + ((size_t)8 * DN1 * nsf + 1) * 4;
+        const int upl1 = (n_act * DN1 * nsf + 31) / 32;
+        const dim3 g1(d / DN1);
+        const uint8_t *wd1 = (const uint8_t *)Wd;
+        switch (upl1) {
+        case 1: hipLaunchKernelGGL(k_moe_down_m1<1>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
+        case 2: hipLaunchKernelGGL(k_moe_down_m1<2>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
+        case 3: case 4: hipLaunchKernelGGL(k_moe_down_m1<4>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
+        case 5: case 6: hipLaunchKernelGGL(k_moe_down_m1<6>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
+        default: hipLaunchKernelGGL(k_moe_down_m1<8>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
+        }
+        return hipGetLastError();
+    }
     const size_t lds_dn = (size_t)8 * nsf * (256 + 64 + 4) + ((size_t)8 * DN_ROWS * nsf + 1) * 4;
     const int upl_dn = (DN_ROWS * nsf + 31) / 32;
     const dim3 g_dn(Umax, d / DN_ROWS);
