@@ -223,10 +223,19 @@ X100_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(const l
 //   B (256-byte k-rows): 8 consecutive k, chunks c and c+1 (c even) -> c ^ 2*(k&7) and its ^1.
 X100_DEV int big_a_chunk(int r, int c) { return c ^ ((r >> 2) & 3); }
 X100_DEV int big_b_chunk(int k, int c) { return c ^ (2 * (k & 7)); }
+//   A of a two-stage superslot (128-byte rows, whole cache lines): 16 consecutive rows, same
+//   chunk c -> granule 8*(r&1) + (c ^ ((r>>1)&7)).
+X100_DEV int big_a2_chunk(int r, int c) { return c ^ ((r >> 1) & 7); }
 
 X100_DEV void dma16(const void *gsrc, uint32_t lds_base)
 {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(gsrc)
+                 : "memory", "m0");
+}
+// Same with a wave-uniform 64-bit base address and a 32-bit per-lane byte offset.
+X100_DEV void dma16s(uint32_t voff, const void *sbase, uint32_t lds_base)
+{
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_base), "v"(voff), "s"(sbase)
                  : "memory", "m0");
 }
 
@@ -270,6 +279,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     constexpr int WN = NW / 2, FN = 8 / WN;   // column fragments per wave
     constexpr int OPS = 16 / NW;              // DMA ops per wave per operand per stage
     __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t csm[NW * 4096];   // C staging, 4 KiB per wave
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w / WN, wn = w % WN, lcol = lane & 31, lgrp = lane >> 5;
@@ -283,15 +293,32 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     // the logical chunk whose swizzled position is its own.
     const int8_t *Ab = A + (size_t)m0 * K;
     const int8_t *Bb = B + n0;
-    uint32_t aoff[OPS], boff[OPS];
-#pragma unroll
-    for (int p = 0; p < OPS; p++) {
-        const int ra = 16 * (NW * p + w) + (lane >> 2);
-        aoff[p] = (uint32_t)(ra * K + 16 * big_a_chunk(ra, lane & 3));
-        const int rb = 4 * (NW * p + w) + (lane >> 4);
-        boff[p] = (uint32_t)(rb * N + 16 * big_b_chunk(rb, lane & 15));
+    // With SUPER == 2 the A rows of both stages of a superstage are fetched together as 128-byte
+    // rows (op p covers tile rows 8*(NW*p+w) .. +7: lane -> row lane/8, chunk lane%8), so every
+    // A fetch is a whole cache line instead of two half lines fetched a stage apart.
+    // Op p differs from op 0 by a whole number of swizzle periods of rows, so the per-lane offset
+    // is the same for every op and the op's row shift goes into the scalar base address.
+    constexpr int AOPS = SUPER == 2 ? 2 * OPS : OPS;
+    constexpr int AROWS = SUPER == 2 ? 8 : 16;   // tile rows per A op
+    uint32_t aoff, boff;
+    if constexpr (SUPER == 2) {
+        const int ra = 8 * w + (lane >> 3);
+        aoff = (uint32_t)(ra * K + 16 * big_a2_chunk(ra, lane & 7));
+    } else {
+        const int ra = 16 * w + (lane >> 2);
+        aoff = (uint32_t)(ra * K + 16 * big_a_chunk(ra, lane & 3));
+    }
+    {
+        const int rb = 4 * w + (lane >> 4);
+        boff = (uint32_t)(rb * N + 16 * big_b_chunk(rb, lane & 15));
     }
     const uint32_t sbase = lds_addr(smem);
+    auto dma_a = [&](const int8_t *ak, int p, uint32_t lds) __attribute__((always_inline)) {
+        dma16s(aoff, ak + (size_t)AROWS * NW * p * K, lds);
+    };
+    auto dma_b = [&](const int8_t *bk, int p, uint32_t lds) __attribute__((always_inline)) {
+        dma16s(boff, bk + (size_t)4 * NW * p * N, lds);
+    };
     // Stage kt (clamped to the last stage: the loop issues 4 stages ahead unconditionally, and a
     // stage past the end is never read) into ring slot kt % NS.
     auto issue = [&](int kt) __attribute__((always_inline)) {
@@ -301,26 +328,49 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         const int8_t *bk = Bb + (size_t)kc * 64 * N;
 #pragma unroll
         for (int p = 0; p < OPS; p++)
-            dma16(ak + aoff[p], __builtin_amdgcn_readfirstlane(sb + (uint32_t)(16 * (NW * p + w) * 64)));
+            dma_a(ak, p, __builtin_amdgcn_readfirstlane(sb + (uint32_t)(16 * (NW * p + w) * 64)));
 #pragma unroll
         for (int p = 0; p < OPS; p++)
-            dma16(bk + boff[p], __builtin_amdgcn_readfirstlane(sb + BOFF + (uint32_t)(4 * (NW * p + w) * 256)));
+            dma_b(bk, p, __builtin_amdgcn_readfirstlane(sb + BOFF + (uint32_t)(4 * (NW * p + w) * 256)));
+    };
+    // SUPER == 2: superstage u (stages 2u, 2u+1; clamped like issue) into superslot u % 2 =
+    // [A 256 rows x 128 bytes | B of stage 2u | B of stage 2u+1].
+    auto issue_super = [&](int u) __attribute__((always_inline)) {
+        const uint32_t sb = sbase + (uint32_t)((u & 1) * 2 * STAGE);
+        const int uc = min(u, nk / 2 - 1);
+        const int8_t *ak = Ab + (size_t)uc * 128;
+#pragma unroll
+        for (int p = 0; p < AOPS; p++)
+            dma_a(ak, p, __builtin_amdgcn_readfirstlane(sb + (uint32_t)(8 * (NW * p + w) * 128)));
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int8_t *bk = Bb + (size_t)(2 * uc + h) * 64 * N;
+#pragma unroll
+            for (int p = 0; p < OPS; p++)
+                dma_b(bk, p, __builtin_amdgcn_readfirstlane(sb + STAGE + h * BOFF + (uint32_t)(4 * (NW * p + w) * 256)));
+        }
     };
 
-    // C prefetch by parts: part p = accumulator row-tile i = p / (FN/2) (C rows crow0 + 32i) and
-    // column fragments j0 = 2*(p % (FN/2)), j0 + 1; the lane holds C[row][col .. col+3] for
-    // col = ccol0 + 32j + 8q.
-    constexpr int NPART = 2 * FN;
-    v4i cbuf[2][4];
-    const int crow0 = m0 + wm * 128 + lcol;
-    const int ccol0 = n0 + wn * FN * 32 + 4 * lgrp;
-    auto load_c = [&](int p) __attribute__((always_inline)) {  // p may be a run-time value: one base pointer, immediate offsets
-        const int i = p / (FN / 2), j0 = 2 * (p % (FN / 2));
-        const int32_t *cp = C + (size_t)(crow0 + 32 * i) * N + ccol0 + 32 * j0;
+    // C prefetch by parts: part p = accumulator fragment (i, j) = (p / FN, p % FN) of the wave,
+    // 32 C rows x 32 columns (128 bytes).  Each part reaches a
+    // wave-private 4 KiB LDS area by global->LDS DMA: 4 ops, each 8 rows x 128 bytes (whole cache
+    // lines), 16-byte chunk c of row r stored at chunk big_a2_chunk(r, c) so that the accumulator-
+    // layout reads below (16 rows, same chunk) are conflict-free.  No VGPRs hold C in flight.
+    constexpr int NPART = 4 * FN;
+    uint32_t coff[2];   // op t: row 8t + lane/8; ops t and t+2 differ by 16 rows (one swizzle period)
 #pragma unroll
-        for (int jj = 0; jj < 2; jj++)
+    for (int t = 0; t < 2; t++) {
+        const int r = 8 * t + (lane >> 3);
+        coff[t] = (uint32_t)(4 * ((wm * 128 + r) * N + wn * FN * 32 + 4 * big_a2_chunk(r, lane & 7)));
+    }
+    const uint32_t cl = lds_addr(csm) + (uint32_t)(w * 4096);
+    auto load_c = [&](int p) __attribute__((always_inline)) {
+        const int i = p / FN, j = p % FN;
+        const int32_t *cb = C + (size_t)(m0 + 32 * i) * N + n0 + 32 * j;
 #pragma unroll
-            for (int q = 0; q < 4; q++) cbuf[jj][q] = *(const v4i *)(cp + 32 * jj + 8 * q);
+        for (int t = 0; t < 4; t++)
+            dma16s(coff[t & 1], cb + (size_t)16 * (t >> 1) * N,
+                   __builtin_amdgcn_readfirstlane(cl + (uint32_t)(1024 * t)));
     };
 
     v16i acc[4][FN];
@@ -331,9 +381,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-    auto add_c = [&](auto pc) __attribute__((always_inline)) {   // pc: compile-time part index
+    // pend: vector-memory ops of this wave issued after part p's DMA (waited for exactly).
+    auto add_c = [&](auto pc, int pend) __attribute__((always_inline)) {   // pc: compile-time part index
         constexpr int p = decltype(pc)::value;
-        constexpr int i = p / (FN / 2), j0 = 2 * (p % (FN / 2));
+        constexpr int i = p / FN, j = p % FN;
+        wait_vmcnt_le(pend);
+        v4i cv[4];
+        const uint8_t *cw = csm + w * 4096 + lcol * 128;
+#pragma unroll
+        for (int q = 0; q < 4; q++) cv[q] = *(const v4i *)(cw + 16 * big_a2_chunk(lcol, 2 * q + lgrp));
         // The adds below are inline asm, for which the compiler inserts no hazard wait states:
         // keep every MFMA above this point and wait out the MFMA-result-to-VALU latency (a
         // 16-pass MFMA needs 18 wait states; 32 are given) before reading accumulators.
@@ -341,36 +397,37 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int jj = 0; jj < 2; jj++)
+        for (int q = 0; q < 4; q++)
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    // Integer add written as asm: a plain += makes the register allocator move
-                    // all the accumulators between register files (and spill); this keeps them
-                    // where the MFMAs want them (ArchVGPRs with 8 waves, AGPRs with 4).
-                    int x = acc[i][j0 + jj][4 * q + e];
-                    if constexpr (NW == 8) {
-                        asm volatile("v_add_u32 %0, %0, %1" : "+v"(x) : "v"(cbuf[jj][q][e]));
-                    } else {
-                        int t;
-                        asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_add_u32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
-                                     : "+a"(x), "=&v"(t) : "v"(cbuf[jj][q][e]));
-                    }
-                    acc[i][j0 + jj][4 * q + e] = x;
+            for (int e = 0; e < 4; e++) {
+                // Integer add written as asm: a plain += makes the register allocator move
+                // all the accumulators between register files (and spill); this keeps them
+                // where the MFMAs want them (ArchVGPRs with 8 waves, AGPRs with 4).
+                int x = acc[i][j][4 * q + e];
+                if constexpr (NW == 8) {
+                    asm volatile("v_add_u32 %0, %0, %1" : "+v"(x) : "v"(cv[q][e]));
+                } else {
+                    int t;
+                    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_add_u32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+                                 : "+a"(x), "=&v"(t) : "v"(cv[q][e]));
                 }
+                acc[i][j][4 * q + e] = x;
+            }
     };
 
     // B fragment addressing for ds_read_b64_tr_b8: 16-lane group G = lane/16 covers columns
     // 16*(G&1) .. +15 of the 32-column fragment and k-rows 16*(G>>1) + 8t + (lane%16)/2.
     const int q16 = lane & 15, r8 = q16 >> 1, h8 = q16 & 1, ch = (lane >> 4) & 1;
     auto read_frags = [&](int slot, int kk, v4i (&af)[4], v4i (&bf)[FN]) __attribute__((always_inline)) {
-        const uint8_t *As = smem + slot * STAGE;
-        const uint8_t *Bs = As + BOFF;
+        const uint8_t *As = SUPER == 2 ? smem + (slot >> 1) * 2 * STAGE : smem + slot * STAGE;
+        const uint8_t *Bs = SUPER == 2 ? As + STAGE + (slot & 1) * BOFF : As + BOFF;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = wm * 128 + 32 * i + lcol;
-            af[i] = *(const v4i *)(As + r * 64 + 16 * big_a_chunk(r, 2 * kk + lgrp));
+            if constexpr (SUPER == 2)
+                af[i] = *(const v4i *)(As + r * 128 + 16 * big_a2_chunk(r, 4 * (slot & 1) + 2 * kk + lgrp));
+            else
+                af[i] = *(const v4i *)(As + r * 64 + 16 * big_a_chunk(r, 2 * kk + lgrp));
         }
 #pragma unroll
         for (int j = 0; j < FN; j++) {
@@ -397,7 +454,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     // The K loop runs in NPART segments; C part p is added at the end of segment p, when part
     // p+1 is prefetched (part 0 right after the prologue's DMAs).
     constexpr int DPS = 2 * OPS;   // DMA ops per wave per stage
-    constexpr int CQ = 8;          // C loads per wave per part
+    constexpr int CQ = 4;          // C DMA ops per wave per part
     // Vector-memory operations of this wave issued after stage s+1's DMAs when iteration s waits
     // for them: stages s+2 and s+3 (always issued: the prologue issues 0..3, step t issues t+4),
     // C part 0 (issued after the prologue's 4 stages, so after stage s+1 when s+1 <= 3) and every
@@ -467,8 +524,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         interleave();
         wait_vmcnt_le(pending_super(u));
         lds_barrier();
-        issue(2 * u + 4);
-        issue(2 * u + 5);
+        issue_super(u + 2);
         read_frags((2 * u + 2) & (NS - 1), 0, a0, b0);
         mma(a1, b1);
         interleave();
@@ -485,10 +541,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         mma(a0, b0);
         mma(a1, b1);
     };
-    issue(0);
-    issue(1);
-    issue(2);
-    issue(3);
+    if constexpr (SUPER == 2) {
+        issue_super(0);
+        issue_super(1);
+    } else {
+        issue(0);
+        issue(1);
+        issue(2);
+        issue(3);
+    }
     load_c(0);
     if constexpr (SUPER == 2) {
         wait_vmcnt_le(2 * DPS + CQ);   // stages 0 and 1 complete
@@ -499,12 +560,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
             const int ub = p * nsup / NPART, ue = (p + 1) * nsup / NPART;
             if constexpr (p + 1 < NPART) {
                 for (int u = ub; u < ue; u++) superstep(u);
-                add_c(pc);
+                add_c(pc, 2 * DPS * (ue - ub));
                 load_c(p + 1);
             } else {
                 for (int u = ub; u < ue - 1; u++) superstep(u);
                 last_super();
-                add_c(pc);
+                add_c(pc, 2 * DPS * (ue - 1 - ub));
             }
         });
     } else {
@@ -516,12 +577,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         const int kb = p * nk / NPART, ke = (p + 1) * nk / NPART;
         if constexpr (p + 1 < NPART) {
             for (int kt = kb; kt < ke; kt++) step(kt);
-            add_c(pc);
+            add_c(pc, DPS * (ke - kb));
             load_c(p + 1);
         } else {
             for (int kt = kb; kt < ke - 1; kt++) step(kt);
             last_step();
-            add_c(pc);
+            add_c(pc, DPS * (ke - 1 - kb));
         }
     });
     }
