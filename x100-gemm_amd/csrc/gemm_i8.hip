@@ -511,6 +511,30 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
             if (p * nsup / NPART - 1 == u - 1) n += CQ;
         return n;
     };
+    // The last k-half of a superstep with superstage u's DMA ops (issue_super's, same order)
+    // spread between its MFMAs: issued as one burst after the barrier, the 8 waves' DMA ops back up
+    // the vector-memory queue and every wave stalls at issue while the matrix pipe runs dry.
+    auto mma_dma = [&](const v4i (&af)[4], const v4i (&bf)[FN], int u) __attribute__((always_inline)) {
+        const uint32_t sb = sbase + (uint32_t)((u & 1) * 2 * STAGE);
+        const int uc = min(u, nk / 2 - 1);
+        const int8_t *ak = Ab + (size_t)uc * 128;
+        static_for<4 * FN>([&](auto cc) __attribute__((always_inline)) {
+            constexpr int c = decltype(cc)::value, i = c / FN, j = c % FN;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<(AOPS + 2 * OPS) / (4 * FN)>([&](auto dd) __attribute__((always_inline)) {
+                constexpr int k = c * ((AOPS + 2 * OPS) / (4 * FN)) + decltype(dd)::value;
+                if constexpr (k < AOPS) {
+                    dma_a(ak, k, __builtin_amdgcn_readfirstlane(sb + (uint32_t)(8 * (NW * k + w) * 128)));
+                } else {
+                    constexpr int h = (k - AOPS) / OPS, q = (k - AOPS) % OPS;
+                    dma_b(Bb + (size_t)(2 * uc + h) * 64 * N, q,
+                          __builtin_amdgcn_readfirstlane(sb + STAGE + h * BOFF + (uint32_t)(4 * (NW * q + w) * 256)));
+                }
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
     auto superstep = [&](int u) __attribute__((always_inline)) {   // u < nsup - 1
         const int s0 = (2 * u) & (NS - 1), s1 = (2 * u + 1) & (NS - 1);
         read_frags(s0, 1, a1, b1);
@@ -524,10 +548,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         interleave();
         wait_vmcnt_le(pending_super(u));
         lds_barrier();
-        issue_super(u + 2);
         read_frags((2 * u + 2) & (NS - 1), 0, a0, b0);
-        mma(a1, b1);
-        interleave();
+        mma_dma(a1, b1, u + 2);
     };
     auto last_super = [&]() __attribute__((always_inline)) {   // u = nsup - 1
         const int s0 = (nk - 2) & (NS - 1), s1 = (nk - 1) & (NS - 1);
