@@ -18,6 +18,7 @@
 namespace {
 
 constexpr int GU_ROWS = 8;    // gate/up rows of ff per block
+constexpr int GU_NWV = 4;     // waves per block of k_moe_gate_up (more waves: fewer blocks resident per CU, each re-deriving the routing)
 constexpr int DN_ROWS = 16;   // down rows of d per block
 
 // Workspace layout (device memory owned by the library, sized by x100_moe_workspace_bytes).
@@ -174,10 +175,11 @@ struct RouteLds {
     int U;
 };
 
+template <int NWV>
 X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
 {
     const int lane = threadIdx.x & 63, w = wave_id();
-    for (int m = w; m < M; m += 4) {
+    for (int m = w; m < M; m += NWV) {
         float p[4];
         float mx = -1e30f;
 #pragma unroll
@@ -249,7 +251,7 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
         for (int k = 0; k < 4; k++) chosen |= (t0 + k < P) && q[k] == (int)threadIdx.x;
     }
     const uint64_t bal = __ballot(chosen);
-    if (lane == 0) rl.wcnt[w] = __popcll(bal);
+    if (lane == 0 && w < 4) rl.wcnt[w] = __popcll(bal);   // threads >= 256 >= n_exp are never chosen
     __syncthreads();
     if (chosen) {
         int slot = __popcll(bal & ((1ull << lane) - 1ull));
@@ -263,8 +265,8 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
 // ------------------------------------------------------------------------------------------------
 // grid (U_max, ff / GU_ROWS).  Units (matrix g/u, row, super-block) = 2*GU_ROWS*nsb, 8 lanes each.
 // ------------------------------------------------------------------------------------------------
-template <int UPL>
-__global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
+template <int UPL, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
                                                      const uint8_t *__restrict__ Wg,
                                                      const uint8_t *__restrict__ Wu, MoeWs ws,
                                                      int *__restrict__ sel_out, float *__restrict__ sw_out)
@@ -278,10 +280,10 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
     // Q8_K records of all M hn rows -> LDS [M][rec], asynchronous (1 KiB chunks, one wave each;
     // sources clamped to the records, the LDS area is padded to whole chunks).
     const int totv = M * rec / 16;
-    for (int ch = wave_id(); ch * 64 < totv; ch += 4)
+    for (int ch = wave_id(); ch * 64 < totv; ch += NWV)
         dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
 
-    route_block(M, n_exp, n_act, ws.logits, rl);
+    route_block<NWV>(M, n_exp, n_act, ws.logits, rl);
     const int u = blockIdx.x;
     const int U = rl.U;
     if (blockIdx.x == 0 && blockIdx.y == 0) {
@@ -317,7 +319,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
     for (int c = 0; c < UPL; c++) {
         // Unconditional loads (unit clamped; results of units beyond nunits are discarded), so
         // every load of the lane is in flight before the first one is waited for.
-        const int un = min(c * 32 + w * 8 + (lane >> 3), nunits - 1);
+        const int un = min(c * 8 * NWV + w * 8 + (lane >> 3), nunits - 1);
         const int mat = un / (GU_ROWS * nsb), rem = un - mat * GU_ROWS * nsb;
         const int r = rem / nsb, sb = rem - r * nsb;
         const uint8_t *blk = (mat ? Wu : Wg) + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
@@ -345,7 +347,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
         const uint8_t *xr = smem + (size_t)(s_pairs[k] / n_act) * rec;
 #pragma unroll
         for (int c = 0; c < UPL; c++) {
-            const int un = c * 32 + w * 8 + (lane >> 3);
+            const int un = c * 8 * NWV + w * 8 + (lane >> 3);
             const bool valid = un < nunits;
             const int sb = valid ? un % nsb : 0;
             int isc, imn;
@@ -358,7 +360,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(int M, int d, int ff, int n
     __syncthreads();
 
     // g, u sequential over super-blocks; SwiGLU (qwen_moe.c:309).
-    for (int t = threadIdx.x; t < cnt * GU_ROWS; t += 256) {
+    for (int t = threadIdx.x; t < cnt * GU_ROWS; t += 64 * NWV) {
         const int k = t / GU_ROWS, r = t - k * GU_ROWS;
         const float *tg = tv + k * 2 * GU_ROWS * nsb + r * nsb;
         const float *tu = tg + GU_ROWS * nsb;
@@ -461,9 +463,10 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
 // selected experts and each slot's activation row is act[a] of its slot a.
 // ------------------------------------------------------------------------------------------------
 constexpr int DN1 = 8;
+constexpr int DN1_NWV = 16;   // waves per block of k_moe_down_m1
 
-template <int UPL>
-__global__ __launch_bounds__(256) void k_moe_down_m1(int d, int ff, int n_act, const uint8_t *__restrict__ Wd,
+template <int UPL, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_moe_down_m1(int d, int ff, int n_exp, int n_act, const uint8_t *__restrict__ Wd,
                                                      MoeWs ws, float *__restrict__ out, int residual)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -477,42 +480,57 @@ __global__ __launch_bounds__(256) void k_moe_down_m1(int d, int ff, int n_act, c
     const int nunits = U * DN1 * nsf;
     const size_t erow = (size_t)nsf * 144;
     const size_t emat = erow * d;
-    // lane l (< 8) holds slot a of union entry l, and the expert of each unit is read per lane:
-    // one round trip for all the metadata
-    const int pu = ws.upairs[min(lane, 7) * 8];
+    // Lane l (< 8) holds slot a of union entry l, and the expert of each unit is read per lane.
+    // No address depends on U: entries past U are clamped to a valid slot / expert (their results
+    // are discarded), so U, the union and the pairs are fetched in one round trip.
+    const int pu = (int)min((unsigned)ws.upairs[min(lane, 7) * 8], (unsigned)(n_act - 1));
+    const int umax = n_act * DN1 * nsf;   // units of a full union (U <= n_act at M = 1)
+
+    // Q8_K of the U activation rows (one wave per 256-element block) -> LDS; slot 8*nsf is a
+    // spare that blocks past nq write, so the quantizations run unrolled and branch-free.
+    int8_t *aq = (int8_t *)smem;                    // [8*nsf + 1][256]
+    int *abs_ = (int *)(aq + (8 * nsf + 1) * 256);  // [8*nsf + 1][16]
+    float *ad = (float *)(abs_ + (8 * nsf + 1) * 16);   // [8*nsf + 1]
+    float *tv = ad + 8 * nsf + 1;                   // [8][DN1][nsf] + one spare
+    const int nq = U * nsf, qspare = 8 * nsf;
+    // All activation loads of the first pass (32 blocks: nsf <= 4 takes one pass), then all weight
+    // loads, then the quantizations: the quantizer waits only for the activations.
+    constexpr int QJ = 32 / NWV;   // activation blocks per wave per pass
+    auto act_loads = [&](int q0, float4 (&v)[QJ]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < QJ; j++) {
+            const int q = min(q0 + NWV * j + w, n_act * nsf - 1);   // clamped; only q < nq is kept
+            const int u = q / nsf, sb = q - u * nsf;
+            v[j] = *(const float4 *)(ws.act + (size_t)__builtin_amdgcn_readlane(pu, u) * ff + sb * 256 + 4 * lane);
+        }
+    };
+    auto act_quant = [&](int q0, const float4 (&v)[QJ]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < QJ; j++) {
+            const int q = q0 + NWV * j + w;
+            const int qd = q < nq ? q : qspare;
+            q8k_wave(v[j], aq + qd * 256, abs_ + qd * 16, ad + qd);
+        }
+    };
+    float4 av[QJ];
+    act_loads(0, av);
 
     v4i hdr[UPL], qs[UPL];
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int un = min(c * 32 + w * 8 + (lane >> 3), nunits - 1);   // clamped: see k_moe_gate_up
+        const int un = min(c * 8 * NWV + w * 8 + (lane >> 3), umax - 1);   // clamped: see k_moe_gate_up
         const int u = un / (DN1 * nsf), rem = un - u * DN1 * nsf;
         const int r = rem / nsf, sb = rem - r * nsf;
-        const int ex = ws.uniq[u];
+        const int ex = min((unsigned)ws.uniq[u], (unsigned)(n_exp - 1));
         const uint8_t *blk = Wd + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
         hdr[c] = *(const v4i *)blk;
         qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
     }
-
-    // Q8_K of the U activation rows (one wave per 256-element block) -> LDS.
-    int8_t *aq = (int8_t *)smem;                    // [8][nsf][256]
-    int *abs_ = (int *)(aq + 8 * nsf * 256);        // [8][nsf][16]
-    float *ad = (float *)(abs_ + 8 * nsf * 16);     // [8][nsf]
-    float *tv = ad + 8 * nsf;                       // [8][DN1][nsf] + one spare
-    const int nq = U * nsf;
-    for (int q0 = 0; q0 < nq; q0 += 16) {
-        float4 v[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int q = min(q0 + 4 * j + w, nq - 1);   // clamped; only q < nq is used
-            const int u = q / nsf, sb = q - u * nsf;
-            v[j] = *(const float4 *)(ws.act + (size_t)__builtin_amdgcn_readlane(pu, u) * ff + sb * 256 + 4 * lane);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int q = q0 + 4 * j + w;
-            if (q < nq) q8k_wave(v[j], aq + q * 256, abs_ + q * 16, ad + q);
-        }
+    __builtin_amdgcn_sched_barrier(0);
+    act_quant(0, av);
+    for (int q0 = 32; q0 < nq; q0 += 32) {
+        act_loads(q0, av);
+        act_quant(q0, av);
     }
     if (threadIdx.x < U) s_slot_u[pu] = threadIdx.x;   // thread u < 8 is lane u of wave 0
     if (threadIdx.x < n_act) s_w[threadIdx.x] = ws.sw[threadIdx.x];
@@ -520,7 +538,7 @@ __global__ __launch_bounds__(256) void k_moe_down_m1(int d, int ff, int n_act, c
 
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int un = c * 32 + w * 8 + (lane >> 3);
+        const int un = c * 8 * NWV + w * 8 + (lane >> 3);
         const bool valid = un < nunits;
         const int unc = valid ? un : 0;
         const int u = unc / (DN1 * nsf), rem = unc - u * DN1 * nsf;
@@ -531,7 +549,7 @@ __global__ __launch_bounds__(256) void k_moe_down_m1(int d, int ff, int n_act, c
     }
     __syncthreads();
     // y of each (slot, row): sequential over super-blocks (the oracle's order)
-    for (int t = threadIdx.x; t < U * DN1; t += 256) {
+    for (int t = threadIdx.x; t < U * DN1; t += 64 * NWV) {
         const int u = t / DN1, r = t - u * DN1;
         float y = 0.0f;
         for (int sb = 0; sb < nsf; sb++) y = y + tv[(u * DN1 + r) * nsf + sb];
@@ -611,7 +629,7 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     if (M < 1 || M > 8 || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return hipErrorInvalidValue;
     if (d % 256 || ff % 256 || d > 4096 || ff > 4096 || d % DN_ROWS || ff % GU_ROWS) return hipErrorInvalidValue;
     const int nsb = d / 256, nsf = ff / 256;
-    if (2 * GU_ROWS * nsb > 8 * 32 || DN_ROWS * nsf > 8 * 32) return hipErrorInvalidValue;
+    if (2 * GU_ROWS * nsb > 8 * 8 * GU_NWV || DN_ROWS * nsf > 8 * 32) return hipErrorInvalidValue;
     MoeWs ws = carve((uintptr_t)workspace, M, d, ff, n_exp, n_act, nullptr);
     const int Umax = min(M * n_act, n_exp);
 
@@ -621,10 +639,10 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     if (err != hipSuccess) return err;
 
     const size_t lds_gu = ((size_t)M * q8k_rec_bytes(nsb) + 1023) / 1024 * 1024 + ((size_t)8 * 2 * GU_ROWS * nsb + 1) * 4;
-    const int upl_gu = (2 * GU_ROWS * nsb + 31) / 32;
+    const int upl_gu = (2 * GU_ROWS * nsb + 8 * GU_NWV - 1) / (8 * GU_NWV);
     const dim3 g_gu(Umax, ff / GU_ROWS);
     const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
-#define X100_GU(U) hipLaunchKernelGGL(k_moe_gate_up<U>, g_gu, dim3(256), lds_gu, s, M, d, ff, n_exp, n_act, wg, wu, ws, sel, sw)
+#define X100_GU(U) hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV>), g_gu, dim3(64 * GU_NWV), lds_gu, s, M, d, ff, n_exp, n_act, wg, wu, ws, sel, sw)
     switch (upl_gu) {
     case 1: X100_GU(1); break;
     case 2: X100_GU(2); break;
@@ -635,19 +653,21 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
-    if (M == 1 && d % DN1 == 0 && n_act * DN1 * nsf <= 8 * 32) {
+    if (M == 1 && d % DN1 == 0 && n_act * DN1 * nsf <= 8 * 8 * DN1_NWV) {
         // down + combine in one launch (see k_moe_down_m1)
-        const size_t lds1 = (size_t)8 * nsf * (256 + 64 + 4) + ((size_t)8 * DN1 * nsf + 1) * 4;
-        const int upl1 = (n_act * DN1 * nsf + 31) / 32;
-        const dim3 g1(d / DN1);
+        const size_t lds1 = ((size_t)8 * nsf + 1) * (256 + 64 + 4) + ((size_t)8 * DN1 * nsf + 1) * 4;
+        const int upl1 = (n_act * DN1 * nsf + 8 * DN1_NWV - 1) / (8 * DN1_NWV);
+        const dim3 g1(d / DN1), b1(64 * DN1_NWV);
         const uint8_t *wd1 = (const uint8_t *)Wd;
+#define X100_DN1(U) hipLaunchKernelGGL((k_moe_down_m1<U, DN1_NWV>), g1, b1, lds1, s, d, ff, n_exp, n_act, wd1, ws, out, residual)
         switch (upl1) {
-        case 1: hipLaunchKernelGGL(k_moe_down_m1<1>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
-        case 2: hipLaunchKernelGGL(k_moe_down_m1<2>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
-        case 3: case 4: hipLaunchKernelGGL(k_moe_down_m1<4>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
-        case 5: case 6: hipLaunchKernelGGL(k_moe_down_m1<6>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
-        default: hipLaunchKernelGGL(k_moe_down_m1<8>, g1, dim3(256), lds1, s, d, ff, n_act, wd1, ws, out, residual); break;
+        case 1: X100_DN1(1); break;
+        case 2: X100_DN1(2); break;
+        case 3: case 4: X100_DN1(4); break;
+        case 5: case 6: X100_DN1(6); break;
+        default: X100_DN1(8); break;
         }
+#undef X100_DN1
         return hipGetLastError();
     }
     const size_t lds_dn = (size_t)8 * nsf * (256 + 64 + 4) + ((size_t)8 * DN_ROWS * nsf + 1) * 4;
