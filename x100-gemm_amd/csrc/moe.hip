@@ -148,8 +148,7 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
                     s += rv[j].z * hv.z;
                     s += rv[j].w * hv.w;
                 }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+            s = wave_sum_bfly_f(s);
             if (lane == 0) ws.logits[m * n_exp + wave] = s;
         }
     } else if (wave < n_exp + M * nsb) {
@@ -175,15 +174,20 @@ struct RouteLds {
     int U;
 };
 
-template <int NWV>
-X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
+// Softmax, top-k and expert union of the M token rows (qwen_moe.c:296-301), one wave per row;
+// KC = 64-expert groups per lane (2 for n_exp <= 128, else 4).
+template <int NWV, int KC>
+X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
 {
     const int lane = threadIdx.x & 63, w = wave_id();
+    bool picked[KC];   // experts lane + 64c chosen for row w (used when M == 1)
+#pragma unroll
+    for (int c = 0; c < KC; c++) picked[c] = false;
     for (int m = w; m < M; m += NWV) {
-        float p[4];
+        float p[KC];
         float mx = -1e30f;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int c = 0; c < KC; c++) {
             const int ex = lane + 64 * c;
             const float lv = logits[m * n_exp + min(ex, n_exp - 1)];   // unconditional load
             p[c] = ex < n_exp ? lv : -1e30f;
@@ -192,20 +196,19 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
         mx = wave_max_u(mx);
         float s = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int c = 0; c < KC; c++) {
             const int ex = lane + 64 * c;
             p[c] = ex < n_exp ? (float)exp((double)(p[c] - mx)) : 0.0f;
             s += p[c];
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        s = wave_sum_bfly_f(s);
         const float inv = 1.0f / s;
         // Selection keys: the bits of the probability (>= 0, so integer order = float order; NaN
         // from bad input is treated as 0); absent or already chosen experts are INT_MIN, so every
         // pass selects a distinct valid expert.
-        int key[4];
+        int key[KC];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int c = 0; c < KC; c++) {
             const float pv = p[c] * inv;
             key[c] = (lane + 64 * c) < n_exp ? __float_as_int(pv == pv ? pv : 0.0f) : INT_MIN;
         }
@@ -215,19 +218,26 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
             wsel[a] = 0.0f;
             if (a < n_act) {
                 // Largest probability (wave maximum of the keys), then the lowest expert id holding
-                // it: experts lane + 64c, so the first c whose ballot is non-empty, its lowest lane.
-                const int km = wave_max_iu(max(max(key[0], key[1]), max(key[2], key[3])));
-                const uint64_t h0 = __ballot(key[0] == km), h1 = __ballot(key[1] == km);
-                const uint64_t h2 = __ballot(key[2] == km), h3 = __ballot(key[3] == km);
-                const int bi = h0 ? __ffsll((unsigned long long)h0) - 1
-                             : h1 ? 64 + __ffsll((unsigned long long)h1) - 1
-                             : h2 ? 128 + __ffsll((unsigned long long)h2) - 1
-                                  : 192 + __ffsll((unsigned long long)h3) - 1;
-                wsel[a] = __int_as_float(km);
-                if (lane == 0) rl.sel[m * n_act + a] = bi;
+                // it: per group c the lowest lane whose key matches (all ones when none does, so
+                // the unsigned minimum picks the lowest group that has one).
+                int kl = key[0];
 #pragma unroll
-                for (int c = 0; c < 4; c++)
-                    if (lane + 64 * c == bi) key[c] = INT_MIN;
+                for (int c = 1; c < KC; c++) kl = max(kl, key[c]);
+                const int km = wave_max_iu(kl);
+                unsigned bi = 0xffffffffu;
+#pragma unroll
+                for (int c = 0; c < KC; c++) {
+                    const uint64_t h = __ballot(key[c] == km);
+                    bi = min(bi, (unsigned)(__ffsll((unsigned long long)h) - 1) | (unsigned)(64 * c));
+                }
+                wsel[a] = __int_as_float(km);
+                if (lane == 0) rl.sel[m * n_act + a] = (int)bi;
+#pragma unroll
+                for (int c = 0; c < KC; c++) {
+                    const bool hit = (unsigned)(lane + 64 * c) == bi;
+                    picked[c] = picked[c] || hit;
+                    key[c] = hit ? INT_MIN : key[c];
+                }
             }
         }
         // Renormalise (qwen_moe.c:301): the sum in slot order, then one division per slot, lane a
@@ -241,8 +251,24 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
         for (int a = 1; a < 8; a++) mine = lane == a ? wsel[a] : mine;
         if (lane < n_act) rl.w[m * n_act + lane] = mine / ssum;
     }
-    __syncthreads();
     // Union slots in ascending expert id: slot of expert e = number of selected experts below e.
+    if (M == 1) {
+        // One row: its wave holds the chosen experts as flags; prefix counts of the ballots.
+        if (w == 0) {
+            const uint64_t below = (1ull << lane) - 1ull;
+            int base = 0;
+#pragma unroll
+            for (int c = 0; c < KC; c++) {
+                const uint64_t bal = __ballot(picked[c]);
+                if (picked[c]) rl.uniq[base + __popcll(bal & below)] = lane + 64 * c;
+                base += __popcll(bal);
+            }
+            if (lane == 0) rl.U = base;
+        }
+        __syncthreads();
+        return;
+    }
+    __syncthreads();
     bool chosen = false;
     const int P = M * n_act;
     for (int t0 = 0; t0 < P; t0 += 4) {
@@ -260,6 +286,14 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
     }
     if (threadIdx.x == 0) rl.U = rl.wcnt[0] + rl.wcnt[1] + rl.wcnt[2] + rl.wcnt[3];
     __syncthreads();
+}
+template <int NWV>
+X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
+{
+    if (n_exp <= 128)
+        route_rows<NWV, 2>(M, n_exp, n_act, logits, rl);
+    else
+        route_rows<NWV, 4>(M, n_exp, n_act, logits, rl);
 }
 
 // ------------------------------------------------------------------------------------------------

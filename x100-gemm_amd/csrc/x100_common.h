@@ -116,16 +116,31 @@ X100_DEV float wave_max_u(float v)
     v = fmaxf(v, dpp_f<0x143, 0xc>(v, v));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
-// Integer maximum over the 64 lanes, wave-uniform.
+// Integer maximum over the 64 lanes, wave-uniform.  The "old" operand is INT_MIN, the identity
+// of max, so each step compiles to one v_max_i32_dpp.
 X100_DEV int wave_max_iu(int v)
 {
-    v = max(v, dpp_i<0x111>(v, v));
-    v = max(v, dpp_i<0x112>(v, v));
-    v = max(v, dpp_i<0x114>(v, v));
-    v = max(v, dpp_i<0x118>(v, v));
-    v = max(v, dpp_i<0x142, 0xa>(v, v));
-    v = max(v, dpp_i<0x143, 0xc>(v, v));
+    v = max(v, dpp_i<0x111>(INT_MIN, v));
+    v = max(v, dpp_i<0x112>(INT_MIN, v));
+    v = max(v, dpp_i<0x114>(INT_MIN, v));
+    v = max(v, dpp_i<0x118>(INT_MIN, v));
+    v = max(v, dpp_i<0x142, 0xa>(INT_MIN, v));
+    v = max(v, dpp_i<0x143, 0xc>(INT_MIN, v));
     return __builtin_amdgcn_readlane(v, 63);
+}
+// Sum over the 64 lanes in xor-butterfly order (lane l adds lane l^32, then l^16, l^8, l^4, l^2,
+// l^1): the value six __shfl_xor steps give, bit for bit.  After the first two levels a lane's
+// value depends only on l mod 16, after the third only on l mod 8, so row_ror:8 and row_ror:4
+// (rotations within a row of 16) deliver the l^8 and l^4 partners' values; quad_perm does l^2, l^1.
+X100_DEV float wave_sum_bfly_f(float s)
+{
+    s += __shfl_xor(s, 32, 64);
+    s += __shfl_xor(s, 16, 64);
+    s += dpp_f<0x128>(0.0f, s);
+    s += dpp_f<0x124>(0.0f, s);
+    s += dpp_f<0x4E>(0.0f, s);
+    s += dpp_f<0xB1>(0.0f, s);
+    return s;
 }
 // Sum over the 64 lanes, wave-uniform: prefix sum of rows (row_shr 1, 2, 4, 8), then rows
 // combined into lane 63.  For integers, or floats whose summation order is not prescribed.
