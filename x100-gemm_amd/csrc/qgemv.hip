@@ -146,9 +146,9 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
 // Work unit = (row, super-block), 8 lanes per unit: lane i of the unit loads the block header
 // (d, dmin, scales: 16 B) and qs bytes [16i, 16i+16): low nibbles = sub-block 2*(i/2), high
 // nibbles = sub-block 2*(i/2)+1, elements 16*(i%2) .. +15 of each.  A block of R rows has
-// R*nsb units; wave w takes units w*8 + lane/8 + 32*c.
-template <int MR, int UPL, int XPT>
-__global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R, uint32_t nsb_mg,
+// R*nsb units; wave w takes units w*8 + lane/8 + (NT/8)*c.
+template <int MR, int UPL, int XPT, int NT>
+__global__ __launch_bounds__(NT) void k_q4_K(int M, int N, int K, int R, uint32_t nsb_mg,
                                               const uint8_t *__restrict__ W,
                                               const float *__restrict__ x, float *__restrict__ y)
 {
@@ -169,28 +169,28 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R, uint32
     const int total4 = M * K / 4;
     const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
     float4 xv[XPT];
-    x_load<XPT>(xr, 0, xv);
+    x_load<XPT, NT>(xr, 0, xv);
 
     v4i hdr[UPL], qs[UPL];
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int u = min(w * 8 + (lane >> 3) + 32 * c, U - 1);   // clamped: see k_q4_0
+        const int u = min(w * 8 + (lane >> 3) + (NT / 8) * c, U - 1);   // clamped: see k_q4_0
         const uint8_t *blk = W + ((size_t)row0 * nsb + u) * 144;
         hdr[c] = *(const v4i *)blk;
         qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
     }
 
     __builtin_amdgcn_sched_barrier(0);   // keep every load above ahead of the quantizer's math
-    q8_K_from_regs<XPT>(xv, 0, total4, xq, xbs, xd);
-    for (int c0 = 256 * XPT; c0 < total4; c0 += 256 * XPT) {
-        x_load<XPT>(xr, c0, xv);
-        q8_K_from_regs<XPT>(xv, c0, total4, xq, xbs, xd);
+    q8_K_from_regs<XPT, NT>(xv, 0, total4, xq, xbs, xd);
+    for (int c0 = NT * XPT; c0 < total4; c0 += NT * XPT) {
+        x_load<XPT, NT>(xr, c0, xv);
+        q8_K_from_regs<XPT, NT>(xv, c0, total4, xq, xbs, xd);
     }
     __syncthreads();
 
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int u = w * 8 + (lane >> 3) + 32 * c;
+        const int u = w * 8 + (lane >> 3) + (NT / 8) * c;
         const bool valid = u < U;  // uniform over the 8 lanes of a unit
         const int sb = valid ? u - fast_div(u, nsb_mg) * nsb : 0;
         const uint32_t h0 = (uint32_t)hdr[c][0];
@@ -244,9 +244,9 @@ __global__ __launch_bounds__(256) void k_q4_K(int M, int N, int K, int R, uint32
 // Work unit = (row, super-block), 4 lanes per unit: lane i (hh = i/2, lh = i%2) loads qs bytes
 // [32hh + 16lh, +16) and hmask bytes [16lh, +16) and decodes the 64 elements
 // 128hh + 32j + 16lh + (0..15), j = 0..3 (shift 2j, hmask bit 4hh+j, scale index 8hh+2j+lh),
-// as in dequantize_q3_K_block (qwen_moe_q3k.c:565-575).  Wave w takes units w*16 + lane/4 + 64*c.
-template <int MR, int UPL, int XPT>
-__global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R, uint32_t nsb_mg,
+// as in dequantize_q3_K_block (qwen_moe_q3k.c:565-575).  Wave w takes units w*16 + lane/4 + (NT/4)*c.
+template <int MR, int UPL, int XPT, int NT>
+__global__ __launch_bounds__(NT) void k_q3_K(int M, int N, int K, int R, uint32_t nsb_mg,
                                               const uint8_t *__restrict__ hq,
                                               const uint8_t *__restrict__ scl,
                                               const uint16_t *__restrict__ wdd,
@@ -269,14 +269,14 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R, uint32
     const int total4 = M * K / 4;
     const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
     float4 xv[XPT];
-    x_load<XPT>(xr, 0, xv);
+    x_load<XPT, NT>(xr, 0, xv);
 
     v4i qv[UPL], hv[UPL];
     uint32_t s0[UPL], s1[UPL], s2[UPL];
     uint32_t dv[UPL];
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int u = min(w * 16 + (lane >> 2) + 64 * c, U - 1);  // clamped: see k_q4_0
+        const int u = min(w * 16 + (lane >> 2) + (NT / 4) * c, U - 1);  // clamped: see k_q4_0
         const size_t rec = (size_t)row0 * nsb + u;
         qv[c] = __builtin_nontemporal_load((const v4i *)(hq + rec * 96 + 32 + 32 * hh + 16 * lh));
         hv[c] = *(const v4i *)(hq + rec * 96 + 16 * lh);
@@ -288,16 +288,16 @@ __global__ __launch_bounds__(256) void k_q3_K(int M, int N, int K, int R, uint32
     }
 
     __builtin_amdgcn_sched_barrier(0);   // keep every load above ahead of the quantizer's math
-    q8_K_from_regs<XPT>(xv, 0, total4, xq, xbs, xd);
-    for (int c0 = 256 * XPT; c0 < total4; c0 += 256 * XPT) {
-        x_load<XPT>(xr, c0, xv);
-        q8_K_from_regs<XPT>(xv, c0, total4, xq, xbs, xd);
+    q8_K_from_regs<XPT, NT>(xv, 0, total4, xq, xbs, xd);
+    for (int c0 = NT * XPT; c0 < total4; c0 += NT * XPT) {
+        x_load<XPT, NT>(xr, c0, xv);
+        q8_K_from_regs<XPT, NT>(xv, c0, total4, xq, xbs, xd);
     }
     __syncthreads();
 
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int u = w * 16 + (lane >> 2) + 64 * c;
+        const int u = w * 16 + (lane >> 2) + (NT / 4) * c;
         const bool valid = u < U;
         const int sb = valid ? u - fast_div(u, nsb_mg) * nsb : 0;
         int scl_j[4];
@@ -463,58 +463,76 @@ hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float
     }
 }
 
-// One K-quant launch with a compile-time number of work units per lane.
-template <int MR, int UPL, int XPT>
-hipError_t launch_kq_upl_x(int qtype, dim3 grid, size_t lds, int M, int N, int K, int R, const void *w,
-                           const float *x, float *y, hipStream_t s)
+// Threads per block of the K-quant kernels (one block per CU).  With several token rows the dot
+// products and the activation quantizer are spread over more waves (Q4_K: 8, Q3_K: 16), so each
+// SIMD has other waves to issue while one waits on a DPP or LDS result; one row is fastest with
+// 4 waves.  LPU = lanes per work unit (Q4_K 8, Q3_K 4).
+template <int MR, int LPU> constexpr int kq_nt() { return MR == 1 ? 256 : (LPU == 8 ? 512 : 1024); }
+
+// Activation float4 per thread per load pass for NT threads: enough for M*K <= 4*NT*XPT.
+inline int xpt_kq(int M, int K, int nt)
 {
-    if (qtype == X100_Q4_K) {
-        hipLaunchKernelGGL((k_q4_K<MR, UPL, XPT>), grid, dim3(256), lds, s, M, N, K, R, div_magic(K / 256),
+    const int need = (M * K + 4 * nt - 1) / (4 * nt);
+    return need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+}
+
+// One K-quant launch with a compile-time number of work units per lane.
+template <int MR, int LPU, int UPL, int XPT>
+hipError_t launch_kq_upl_x(dim3 grid, size_t lds, int M, int N, int K, int R, const void *w, const float *x,
+                           float *y, hipStream_t s)
+{
+    constexpr int NT = kq_nt<MR, LPU>();
+    if constexpr (LPU == 8) {
+        hipLaunchKernelGGL((k_q4_K<MR, UPL, XPT, NT>), grid, dim3(NT), lds, s, M, N, K, R, div_magic(K / 256),
                            (const uint8_t *)w, x, y);
     } else {
         const size_t nblk = (size_t)N * (K / 256);
         const uint8_t *hq = (const uint8_t *)w;
         const uint8_t *scl = hq + nblk * 96;
         const uint16_t *dd = (const uint16_t *)(scl + nblk * 12);
-        hipLaunchKernelGGL((k_q3_K<MR, UPL, XPT>), grid, dim3(256), lds, s, M, N, K, R, div_magic(K / 256), hq, scl, dd, x, y);
+        hipLaunchKernelGGL((k_q3_K<MR, UPL, XPT, NT>), grid, dim3(NT), lds, s, M, N, K, R, div_magic(K / 256), hq,
+                           scl, dd, x, y);
     }
     return hipGetLastError();
 }
 
-template <int MR, int UPL>
-hipError_t launch_kq_upl(int qtype, dim3 grid, size_t lds, int M, int N, int K, int R, const void *w,
-                         const float *x, float *y, hipStream_t s)
+template <int MR, int LPU, int UPL>
+hipError_t launch_kq_upl(dim3 grid, size_t lds, int M, int N, int K, int R, const void *w, const float *x,
+                         float *y, hipStream_t s)
 {
-    switch (xpt_for(M, K)) {
-    case 2: return launch_kq_upl_x<MR, UPL, 2>(qtype, grid, lds, M, N, K, R, w, x, y, s);
-    case 4: return launch_kq_upl_x<MR, UPL, 4>(qtype, grid, lds, M, N, K, R, w, x, y, s);
-    case 8: return launch_kq_upl_x<MR, UPL, 8>(qtype, grid, lds, M, N, K, R, w, x, y, s);
-    default: return launch_kq_upl_x<MR, UPL, 16>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    switch (xpt_kq(M, K, kq_nt<MR, LPU>())) {
+    case 1: return launch_kq_upl_x<MR, LPU, UPL, 1>(grid, lds, M, N, K, R, w, x, y, s);
+    case 2: return launch_kq_upl_x<MR, LPU, UPL, 2>(grid, lds, M, N, K, R, w, x, y, s);
+    case 4: return launch_kq_upl_x<MR, LPU, UPL, 4>(grid, lds, M, N, K, R, w, x, y, s);
+    default: return launch_kq_upl_x<MR, LPU, UPL, 8>(grid, lds, M, N, K, R, w, x, y, s);
     }
 }
 
-// Rows per block R for the K-quant kernels: about 256 blocks, each lane holding UPL <= 8 units
-// (Q4_K: 8 lanes per unit, Q3_K: 4 lanes per unit).
-template <int MR, int LANES_PER_UNIT>
-hipError_t launch_kq(int qtype, int M, int N, int K, const void *w, const float *x, float *y,
-                     hipStream_t s)
+// Rows per block R for the K-quant kernels: about 256 blocks, each lane holding at most UPL_MAX
+// units (1024-thread blocks have 128 VGPRs per lane, which 8 units of Q3_K would exceed).
+template <int MR, int LPU>
+hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
 {
     const int nsb = K / 256;
-    constexpr int UNITS_PER_PASS = 256 / LANES_PER_UNIT;
+    constexpr int UNITS_PER_PASS = kq_nt<MR, LPU>() / LPU;
+    constexpr int UPL_MAX = kq_nt<MR, LPU>() >= 1024 ? 4 : 8;
     int R = (N + 255) / 256;
     if (R < 1) R = 1;
-    if (R * nsb > 8 * UNITS_PER_PASS) R = (8 * UNITS_PER_PASS) / nsb;
+    if (R * nsb > UPL_MAX * UNITS_PER_PASS) R = (UPL_MAX * UNITS_PER_PASS) / nsb;
     if (R < 1) return hipErrorInvalidValue;  // a single row does not fit in one pass
     int upl = (R * nsb + UNITS_PER_PASS - 1) / UNITS_PER_PASS;
     const dim3 grid((N + R - 1) / R);
     const size_t lds = ((size_t)MR * nsb + 1) * (256 + 64 + 4) + ((size_t)MR * R * nsb + 1) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    if (upl <= 1) return launch_kq_upl<MR, 1>(qtype, grid, lds, M, N, K, R, w, x, y, s);
-    if (upl <= 2) return launch_kq_upl<MR, 2>(qtype, grid, lds, M, N, K, R, w, x, y, s);
-    if (upl <= 3) return launch_kq_upl<MR, 3>(qtype, grid, lds, M, N, K, R, w, x, y, s);
-    if (upl <= 4) return launch_kq_upl<MR, 4>(qtype, grid, lds, M, N, K, R, w, x, y, s);
-    if (upl <= 6) return launch_kq_upl<MR, 6>(qtype, grid, lds, M, N, K, R, w, x, y, s);
-    return launch_kq_upl<MR, 8>(qtype, grid, lds, M, N, K, R, w, x, y, s);
+    if (upl <= 1) return launch_kq_upl<MR, LPU, 1>(grid, lds, M, N, K, R, w, x, y, s);
+    if (upl <= 2) return launch_kq_upl<MR, LPU, 2>(grid, lds, M, N, K, R, w, x, y, s);
+    if (upl <= 3) return launch_kq_upl<MR, LPU, 3>(grid, lds, M, N, K, R, w, x, y, s);
+    if (upl <= 4 || UPL_MAX == 4) return launch_kq_upl<MR, LPU, 4>(grid, lds, M, N, K, R, w, x, y, s);
+    if constexpr (UPL_MAX == 8) {
+        if (upl <= 6) return launch_kq_upl<MR, LPU, 6>(grid, lds, M, N, K, R, w, x, y, s);
+        return launch_kq_upl<MR, LPU, 8>(grid, lds, M, N, K, R, w, x, y, s);
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -533,13 +551,13 @@ hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, cons
     if (qtype == X100_Q4_K || qtype == X100_Q3_K) {
         if (K % 256) return hipErrorInvalidValue;
         if (qtype == X100_Q4_K) {
-            if (M == 1) return launch_kq<1, 8>(qtype, M, N, K, w, x, y, s);
-            if (M <= 4) return launch_kq<4, 8>(qtype, M, N, K, w, x, y, s);
-            return launch_kq<8, 8>(qtype, M, N, K, w, x, y, s);
+            if (M == 1) return launch_kq<1, 8>(M, N, K, w, x, y, s);
+            if (M <= 4) return launch_kq<4, 8>(M, N, K, w, x, y, s);
+            return launch_kq<8, 8>(M, N, K, w, x, y, s);
         }
-        if (M == 1) return launch_kq<1, 4>(qtype, M, N, K, w, x, y, s);
-        if (M <= 4) return launch_kq<4, 4>(qtype, M, N, K, w, x, y, s);
-        return launch_kq<8, 4>(qtype, M, N, K, w, x, y, s);
+        if (M == 1) return launch_kq<1, 4>(M, N, K, w, x, y, s);
+        if (M <= 4) return launch_kq<4, 4>(M, N, K, w, x, y, s);
+        return launch_kq<8, 4>(M, N, K, w, x, y, s);
     }
     return hipErrorInvalidValue;
 }

@@ -197,18 +197,18 @@ X100_DEV void dma_1k(const void *src, void *lds_base)
 // ------------------------------------------------------------------------------------------------
 // Activation quantizers for a 256-thread block.  The M x K fp32 rows are read as float4 (float4
 // f = c0 + tid + 256*i holds elements 4f .. 4f+3 of the flattened rows) in chunks of XPT float4
-// per thread: x_load issues a chunk's loads (through a buffer resource of M*K*4 bytes, so
+// per thread (NT threads per block): x_load issues a chunk's loads (through a buffer resource of M*K*4 bytes, so
 // elements past the end read as 0), the *_from_regs functions quantize the chunk into LDS.
 // Kernels issue chunk 0 before their weight loads so that it arrives while the weights are still
 // in flight.
 //   Q8_0 (quantize_q8_0_native rounding): a 32-element block is 8 consecutive threads.
 //   Q8_K (pack_A_q3k rounding): a 256-element block is one wave (64 threads).
 // ------------------------------------------------------------------------------------------------
-template <int XPT>
+template <int XPT, int NT = 256>
 X100_DEV void x_load(rsrc_t xr, int c0, float4 (&v)[XPT])
 {
 #pragma unroll
-    for (int i = 0; i < XPT; i++) v[i] = buf_load_f4(xr, (uint32_t)(c0 + threadIdx.x + 256 * i) * 16u);
+    for (int i = 0; i < XPT; i++) v[i] = buf_load_f4(xr, (uint32_t)(c0 + threadIdx.x + NT * i) * 16u);
 }
 
 // Branch-free stores (so the unrolled iterations can be interleaved by the scheduler): blocks past
@@ -241,13 +241,13 @@ X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, 
     }
 }
 
-template <int XPT>
+template <int XPT, int NT = 256>
 X100_DEV void q8_K_from_regs(const float4 (&v)[XPT], int c0, int total4, int8_t *xq, int *xbs, float *xd)
 {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
-        const int f = c0 + threadIdx.x + 256 * i;
+        const int f = c0 + threadIdx.x + NT * i;
         const float a = fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
         const float amax = wave_max_u(a);
         const float d = amax / 127.0f;
