@@ -54,6 +54,7 @@ def test_kquant_6144x2048(dev, qtype, M):
 
 @pytest.mark.parametrize("qtype,N,K,M", [
     (synth.Q4_0, 1, 32, 1), (synth.Q4_0, 7, 96, 2), (synth.Q4_0, 300, 2048, 3), (synth.Q4_0, 64, 8192, 8),
+    (synth.Q4_0, 130, 1024, 6),
     (synth.Q4_0, 33, 16384, 1), (synth.Q4_K, 1, 256, 1), (synth.Q4_K, 5, 768, 2), (synth.Q4_K, 2048, 768, 8),
     (synth.Q4_K, 100, 4096, 3), (synth.Q4_K, 9, 8192, 1), (synth.Q3_K, 1, 256, 1), (synth.Q3_K, 13, 768, 5),
     (synth.Q3_K, 700, 4096, 8), (synth.Q3_K, 3, 16384, 2)])

@@ -49,10 +49,10 @@ inline uint32_t div_magic(uint32_t d) { return (uint32_t)((0x100000000ull + d - 
 // ------------------------------------------------------------------------------------------------
 // Q4_0 x Q8_0
 // ------------------------------------------------------------------------------------------------
-// Block = 4 waves; wave w owns rows row0 + w*RPW .. +RPW-1; lane l owns blocks l, l+64, ...
+// Block = NT/64 waves; wave w owns rows row0 + w*RPW .. +RPW-1; lane l owns blocks l, l+64, ...
 // (BPL per row).  All RPW*BPL nibble loads (16 B) and scale loads are issued first.
-template <int MR, int RPW, int BPL, int XPT>
-__global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_t *__restrict__ wd,
+template <int MR, int RPW, int BPL, int XPT, int NT>
+__global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t *__restrict__ wd,
                                               const uint8_t *__restrict__ wq,
                                               const float *__restrict__ x, float *__restrict__ y)
 {
@@ -65,12 +65,12 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
     int *xs = (int *)(xd + nb1);
 
     const int lane = threadIdx.x & 63, w = wave_id();
-    const int rowb = blockIdx.x * 4 * RPW + w * RPW;
+    const int rowb = blockIdx.x * (NT / 64) * RPW + w * RPW;
 
     const int total4 = M * K / 4;
     const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
     float4 xv[XPT];
-    x_load<XPT>(xr, 0, xv);
+    x_load<XPT, NT>(xr, 0, xv);
 
     // Unconditional loads (indices clamped into the matrix; out-of-range results are discarded),
     // so every load of the lane is in flight before the first one is waited for.
@@ -87,10 +87,10 @@ __global__ __launch_bounds__(256) void k_q4_0(int M, int N, int K, const uint16_
         }
 
     __builtin_amdgcn_sched_barrier(0);   // keep every load above ahead of the quantizer's math
-    q8_0_from_regs<XPT>(xv, 0, total4, K, xlo, xhi, xd, xs);
-    for (int c0 = 256 * XPT; c0 < total4; c0 += 256 * XPT) {
-        x_load<XPT>(xr, c0, xv);
-        q8_0_from_regs<XPT>(xv, c0, total4, K, xlo, xhi, xd, xs);
+    q8_0_from_regs<XPT, NT>(xv, 0, total4, K, xlo, xhi, xd, xs);
+    for (int c0 = NT * XPT; c0 < total4; c0 += NT * XPT) {
+        x_load<XPT, NT>(xr, c0, xv);
+        q8_0_from_regs<XPT, NT>(xv, c0, total4, K, xlo, xhi, xd, xs);
     }
     __syncthreads();
 
@@ -428,8 +428,23 @@ hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *ds
 
 namespace {
 
-// Activation float4 per thread per load pass: enough for M*K <= 1024*XPT in one pass.
-inline int xpt_for(int M, int K) { const int need = (M * K + 1023) / 1024; return need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16; }
+
+// Q4_0 block shape: one token row takes 4 waves of 4 rows each; several token rows take 16 waves
+// of one row each (the same 16 rows per block, with the activation quantizer and the per-row dot
+// products spread over four times as many waves) where the lane's blocks fit the 128 VGPRs of a
+// 1024-thread block (BPL * MR <= 8).  BPL = 32-element blocks per lane per row.
+inline int q40_bpl(int nb) { return nb <= 64 ? 1 : nb <= 128 ? 2 : nb <= 256 ? 4 : 8; }
+constexpr bool q40_wide(int mr, int bpl) { return mr > 1 && bpl * mr <= 8; }
+
+template <int MR, int BPL, int XPT>
+void launch_q4_0_b(int M, int N, int K, const uint16_t *wd, const uint8_t *wq, size_t lds, const float *x,
+                   float *y, hipStream_t s)
+{
+    constexpr int NT = q40_wide(MR, BPL) ? 1024 : 256, RPW = q40_wide(MR, BPL) ? 1 : 4;
+    const int rows = (NT / 64) * RPW;
+    const dim3 grid((N + rows - 1) / rows);
+    hipLaunchKernelGGL((k_q4_0<MR, RPW, BPL, XPT, NT>), grid, dim3(NT), lds, s, M, N, K, wd, wq, x, y);
+}
 
 template <int MR, int XPT>
 hipError_t launch_q4_0_x(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
@@ -439,28 +454,25 @@ hipError_t launch_q4_0_x(int M, int N, int K, const void *w, const float *x, flo
     const uint16_t *wd = (const uint16_t *)w;
     const uint8_t *wq = (const uint8_t *)w + align256(nblk * 2);
     const size_t lds = ((size_t)MR * nb + 1) * 40;
-    constexpr int RPW = 4;
-    const dim3 grid((N + 4 * RPW - 1) / (4 * RPW));
-    if (nb <= 64)
-        hipLaunchKernelGGL((k_q4_0<MR, RPW, 1, XPT>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
-    else if (nb <= 128)
-        hipLaunchKernelGGL((k_q4_0<MR, RPW, 2, XPT>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
-    else if (nb <= 256)
-        hipLaunchKernelGGL((k_q4_0<MR, RPW, 4, XPT>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
-    else
-        hipLaunchKernelGGL((k_q4_0<MR, RPW, 8, XPT>), grid, dim3(256), lds, s, M, N, K, wd, wq, x, y);
+    switch (q40_bpl(nb)) {
+    case 1: launch_q4_0_b<MR, 1, XPT>(M, N, K, wd, wq, lds, x, y, s); break;
+    case 2: launch_q4_0_b<MR, 2, XPT>(M, N, K, wd, wq, lds, x, y, s); break;
+    case 4: launch_q4_0_b<MR, 4, XPT>(M, N, K, wd, wq, lds, x, y, s); break;
+    default: launch_q4_0_b<MR, 8, XPT>(M, N, K, wd, wq, lds, x, y, s); break;
+    }
     return hipGetLastError();
 }
 
 template <int MR>
 hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
 {
-    switch (xpt_for(M, K)) {
-    case 2: return launch_q4_0_x<MR, 2>(M, N, K, w, x, y, s);
-    case 4: return launch_q4_0_x<MR, 4>(M, N, K, w, x, y, s);
-    case 8: return launch_q4_0_x<MR, 8>(M, N, K, w, x, y, s);
-    default: return launch_q4_0_x<MR, 16>(M, N, K, w, x, y, s);
-    }
+    // activation float4 per thread per pass, for the block's thread count
+    const int nt = q40_wide(MR, q40_bpl(K / 32)) ? 1024 : 256;
+    const int need = (M * K + 4 * nt - 1) / (4 * nt);
+    if (need <= 2) return launch_q4_0_x<MR, 2>(M, N, K, w, x, y, s);
+    if (need <= 4) return launch_q4_0_x<MR, 4>(M, N, K, w, x, y, s);
+    if (need <= 8) return launch_q4_0_x<MR, 8>(M, N, K, w, x, y, s);
+    return launch_q4_0_x<MR, 16>(M, N, K, w, x, y, s);
 }
 
 // Threads per block of the K-quant kernels (one block per CU).  With several token rows the dot

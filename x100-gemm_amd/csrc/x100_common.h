@@ -214,14 +214,14 @@ X100_DEV void x_load(rsrc_t xr, int c0, float4 (&v)[XPT])
 // Branch-free stores (so the unrolled iterations can be interleaved by the scheduler): blocks past
 // the end go to the spare slot (index M*nb / M*nsb) that the LDS layout provides, and values that
 // several lanes hold (d, sum) are stored by all of them.
-template <int XPT>
+template <int XPT, int NT = 256>
 X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, int8_t *xlo,
                              int8_t *xhi, float *xd, int *xs)
 {
     const int nb = K / 32;
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
-        const int f = c0 + threadIdx.x + 256 * i;
+        const int f = c0 + threadIdx.x + NT * i;
         const float a = max8_f(fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
         const float amax = fmaxf(a, 1e-6f);
         const float d = amax / 127.0f;
