@@ -94,7 +94,7 @@ def gpu_gemv(int4, W, x, dev):
 @pytest.mark.parametrize("int4", [True, False])
 @pytest.mark.parametrize("N,K,M", [(4864, 896, 1), (4864, 896, 4), (4864, 896, 8), (8, 32, 1), (8, 32, 8),
                                    (40, 96, 3), (2048, 768, 2), (768, 2048, 5), (136, 4096, 1),
-                                   (16, 6144, 8)])
+                                   (16, 6144, 8), (8192, 512, 3)])
 def test_gemv_tile_gpu(dev, int4, N, K, M):
     if int4:
         W, x = q4_gemv_inputs(N, K, M, seed=N + K + M)

@@ -52,19 +52,25 @@ X100_DEV int sum_stride8(int v)
 
 constexpr int CH = 4;   // 1 KiB chunks per load pass
 
-// grid = ceil(N/8 / 4) blocks of 4 waves; wave = N-block.
-template <int MR, bool INT4>
+// grid = ceil(N/8 * S / 4) blocks of 4 waves.  S waves share an N-block, each taking a contiguous
+// share of its chunks (S = 2 or 4 when there are too few N-blocks to give every CU several waves);
+// their int32 partial sums are added through LDS, which is exact in any order.
+template <int MR, bool INT4, int S>
 __global__ __launch_bounds__(256) void k_gemv_tile(int M, int N, int K, const uint8_t *__restrict__ W,
                                                    const int8_t *__restrict__ x, int32_t *__restrict__ y)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int red[4][MR][8];                     // partial sums of the S waves of an N-block
     int8_t *xs = (int8_t *)smem;                      // [M][K] + one spare 16-byte slot
     int *xsum = (int *)(smem + (size_t)M * K + 16);   // [M][K/16] + one spare
     const int lane = threadIdx.x & 63, w = wave_id();
     const int Nb = N / 8;
-    const int nb = min((int)blockIdx.x * 4 + w, Nb - 1);   // clamped: the store below is skipped
-    const int tiles = INT4 ? K / 32 : K / 16;               // 128-byte tiles per N-block
-    const int nch = (tiles + 7) / 8;                        // 1 KiB chunks (8 tiles)
+    const int nbk = (int)blockIdx.x * (4 / S) + w / S;   // this wave's N-block
+    const int ks = w % S;                                // its share of the N-block's chunks
+    const int nb = min(nbk, Nb - 1);                     // clamped: the store below is skipped
+    const int tiles = INT4 ? K / 32 : K / 16;            // 128-byte tiles per N-block
+    const int nch = (tiles + 7) / 8;                     // 1 KiB chunks (8 tiles)
+    const int cb = ks * nch / S, ce = (ks + 1) * nch / S;
     const rsrc_t wr = buf_rsrc(W + (size_t)nb * tiles * 128, (uint32_t)tiles * 128u);
     const int n = lane & 7;
 
@@ -75,7 +81,8 @@ __global__ __launch_bounds__(256) void k_gemv_tile(int M, int N, int K, const ui
     xload(xr, 0, xt);
     v4u wv[CH];
 #pragma unroll
-    for (int c = 0; c < CH; c++) wv[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, (c * 64 + lane) * 16, 0, 0);
+    for (int c = 0; c < CH; c++)
+        wv[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, ((cb + c) * 64 + lane) * 16, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     xstore(xt, 0, nv, xs, xsum);
     for (int v0 = 1024; v0 < nv; v0 += 1024) {
@@ -87,8 +94,8 @@ __global__ __launch_bounds__(256) void k_gemv_tile(int M, int N, int K, const ui
     int acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) acc[m] = 0;
-    for (int c0 = 0; c0 < nch; c0 += CH) {
-        if (c0 > 0) {
+    for (int c0 = cb; c0 < ce; c0 += CH) {
+        if (c0 > cb) {
 #pragma unroll
             for (int c = 0; c < CH; c++)
                 wv[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, ((c0 + c) * 64 + lane) * 16, 0, 0);
@@ -96,7 +103,7 @@ __global__ __launch_bounds__(256) void k_gemv_tile(int M, int N, int K, const ui
 #pragma unroll
         for (int c = 0; c < CH; c++) {
             const int t = (c0 + c) * 8 + (lane >> 3);   // tile of this lane
-            if (t < tiles) {
+            if (t < tiles && c0 + c < ce) {
                 if (INT4) {
                     int lo[4], hi[4];
 #pragma unroll
@@ -133,26 +140,68 @@ __global__ __launch_bounds__(256) void k_gemv_tile(int M, int N, int K, const ui
             }
         }
     }
-    const bool store = (int)blockIdx.x * 4 + w < Nb && lane < 8;
+    const bool store = nbk < Nb && lane < 8;
+    if constexpr (S == 1) {
 #pragma unroll
-    for (int m = 0; m < MR; m++) {
-        if (m < M) {
+        for (int m = 0; m < MR; m++) {
+            if (m < M) {
+                const int v = sum_stride8(acc[m]);
+                if (store) y[(size_t)m * N + nb * 8 + n] = v;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
             const int v = sum_stride8(acc[m]);
-            if (store) y[(size_t)m * N + nb * 8 + n] = v;
+            if (lane < 8) red[w][m][n] = v;
+        }
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                if (m < M) {
+                    int v = 0;
+#pragma unroll
+                    for (int k = 0; k < S; k++) v += red[w + k][m][n & 7];
+                    if (store) y[(size_t)m * N + nb * 8 + n] = v;
+                }
+            }
         }
     }
+}
+
+// Waves per N-block: enough to give the chip ~1024 waves when the matrix has few N-blocks, as long
+// as every wave keeps at least 3 chunks (2 with several token rows, whose dot products dominate).
+inline int tile_split(int M, int N, int nch)
+{
+    const int nblk = N / 8;
+    const int by_waves = nblk >= 1024 ? 1 : nblk >= 512 ? 2 : 4;
+    const int minch = M >= 4 ? 2 : 3;
+    const int by_chunks = nch / 4 >= minch ? 4 : nch / 2 >= minch ? 2 : 1;
+    return min(by_waves, by_chunks);
+}
+
+template <int MR, int S>
+hipError_t launch_tile_s(bool int4, int M, int N, int K, const void *W, const int8_t *x, int32_t *y, hipStream_t s)
+{
+    const dim3 grid((N / 8 * S + 3) / 4);
+    const size_t lds = (size_t)M * K + 16 + ((size_t)M * (K / 16) + 1) * 4;
+    if (int4)
+        hipLaunchKernelGGL((k_gemv_tile<MR, true, S>), grid, dim3(256), lds, s, M, N, K, (const uint8_t *)W, x, y);
+    else
+        hipLaunchKernelGGL((k_gemv_tile<MR, false, S>), grid, dim3(256), lds, s, M, N, K, (const uint8_t *)W, x, y);
+    return hipGetLastError();
 }
 
 template <int MR>
 hipError_t launch_tile(bool int4, int M, int N, int K, const void *W, const int8_t *x, int32_t *y, hipStream_t s)
 {
-    const dim3 grid((N / 8 + 3) / 4);
-    const size_t lds = (size_t)M * K + 16 + ((size_t)M * (K / 16) + 1) * 4;
-    if (int4)
-        hipLaunchKernelGGL((k_gemv_tile<MR, true>), grid, dim3(256), lds, s, M, N, K, (const uint8_t *)W, x, y);
-    else
-        hipLaunchKernelGGL((k_gemv_tile<MR, false>), grid, dim3(256), lds, s, M, N, K, (const uint8_t *)W, x, y);
-    return hipGetLastError();
+    const int tiles = int4 ? K / 32 : K / 16;
+    switch (tile_split(M, N, (tiles + 7) / 8)) {
+    case 1: return launch_tile_s<MR, 1>(int4, M, N, K, W, x, y, s);
+    case 2: return launch_tile_s<MR, 2>(int4, M, N, K, W, x, y, s);
+    default: return launch_tile_s<MR, 4>(int4, M, N, K, W, x, y, s);
+    }
 }
 
 }  // namespace
