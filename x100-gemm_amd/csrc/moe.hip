@@ -299,7 +299,44 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
 // ------------------------------------------------------------------------------------------------
 // grid (U_max, ff / GU_ROWS).  Units (matrix g/u, row, super-block) = 2*GU_ROWS*nsb, 8 lanes each.
 // ------------------------------------------------------------------------------------------------
-template <int UPL, int NWV>
+// Routing of the rows (computed by route_block into rl) -> workspace: sel, sw (and the caller's
+// copies), the union (ascending expert id), its pair lists (token row ascending) and size.
+X100_DEV void publish_routing(int M, int n_act, const RouteLds &rl, MoeWs ws, int *__restrict__ sel_out,
+                              float *__restrict__ sw_out)
+{
+    const int t = threadIdx.x;
+    const int U = rl.U;
+    if (t < M * n_act) {
+        ws.sel[t] = rl.sel[t];
+        ws.sw[t] = rl.w[t];
+        if (sel_out) sel_out[t] = rl.sel[t];
+        if (sw_out) sw_out[t] = rl.w[t];
+    }
+    if (t < U) {
+        const int ex = rl.uniq[t];
+        int c = 0;
+        for (int m = 0; m < M; m++)
+            for (int a = 0; a < n_act; a++)
+                if (rl.sel[m * n_act + a] == ex) ws.upairs[t * 8 + c++] = m * n_act + a;
+        ws.uniq[t] = ex;
+        ws.ucnt[t] = c;
+    }
+    if (t == 0) *ws.nuniq = U;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Routing of M > 1 token rows, once, in one block (one wave per row): the gate/up blocks then read
+// it from the workspace instead of each re-deriving it.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(512) void k_moe_topk(int M, int n_exp, int n_act, MoeWs ws,
+                                                  int *__restrict__ sel_out, float *__restrict__ sw_out)
+{
+    __shared__ RouteLds rl;
+    route_block<8>(M, n_exp, n_act, ws.logits, rl);
+    publish_routing(M, n_act, rl, ws, sel_out, sw_out);
+}
+
+template <int UPL, int NWV, bool ROUTED>
 __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
                                                      const uint8_t *__restrict__ Wg,
                                                      const uint8_t *__restrict__ Wu, MoeWs ws,
@@ -317,32 +354,24 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     for (int ch = wave_id(); ch * 64 < totv; ch += NWV)
         dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
 
-    route_block<NWV>(M, n_exp, n_act, ws.logits, rl);
     const int u = blockIdx.x;
-    const int U = rl.U;
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
-        const int t = threadIdx.x;
-        if (t < M * n_act) {
-            ws.sel[t] = rl.sel[t];
-            ws.sw[t] = rl.w[t];
-            if (sel_out) sel_out[t] = rl.sel[t];
-            if (sw_out) sw_out[t] = rl.w[t];
-        }
-        if (t < U) {
-            const int ex = rl.uniq[t];
-            int c = 0;
-            for (int m = 0; m < M; m++)
-                for (int a = 0; a < n_act; a++)
-                    if (rl.sel[m * n_act + a] == ex) ws.upairs[t * 8 + c++] = m * n_act + a;
-            ws.uniq[t] = ex;
-            ws.ucnt[t] = c;
-        }
-        if (t == 0) *ws.nuniq = U;
+    int U, ex, pr = 0, cnt_r = 0;
+    if constexpr (ROUTED) {
+        // routing from k_moe_topk: union entry, its pairs and the union size in one round trip
+        // (u < gridDim.x = M * n_act, so every index is inside the workspace arrays)
+        ex = ws.uniq[u];
+        pr = ws.upairs[u * 8 + min((int)(threadIdx.x & 63), 7)];
+        cnt_r = ws.ucnt[u];
+        U = *ws.nuniq;
+    } else {
+        route_block<NWV>(M, n_exp, n_act, ws.logits, rl);
+        if (blockIdx.x == 0 && blockIdx.y == 0) publish_routing(M, n_act, rl, ws, sel_out, sw_out);
+        U = rl.U;
+        ex = rl.uniq[min(u, U - 1)];
     }
     if (u >= U) return;
 
     const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
-    const int ex = rl.uniq[u];
     const int r0 = blockIdx.y * GU_ROWS;
     const int nunits = 2 * GU_ROWS * nsb;
     const size_t erow = (size_t)nsb * 144;               // bytes per row
@@ -363,7 +392,10 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
 
     // Pairs (token row m, slot a) of this expert, m ascending (distinct experts per row, so at
     // most one slot per row).
-    if (threadIdx.x == 0) {
+    if constexpr (ROUTED) {
+        if (threadIdx.x < 8) s_pairs[threadIdx.x] = pr;
+        if (threadIdx.x == 0) s_cnt = cnt_r;
+    } else if (threadIdx.x == 0) {
         int c = 0;
         for (int m = 0; m < M; m++)
             for (int a = 0; a < n_act; a++)
@@ -676,7 +708,22 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     const int upl_gu = (2 * GU_ROWS * nsb + 8 * GU_NWV - 1) / (8 * GU_NWV);
     const dim3 g_gu(Umax, ff / GU_ROWS);
     const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
-#define X100_GU(U) hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV>), g_gu, dim3(64 * GU_NWV), lds_gu, s, M, d, ff, n_exp, n_act, wg, wu, ws, sel, sw)
+    // One row routes inside the gate/up blocks (a separate launch costs more than it saves);
+    // several rows route once in k_moe_topk.
+    if (M > 1) {
+        hipLaunchKernelGGL(k_moe_topk, dim3(1), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
+        err = hipGetLastError();
+        if (err != hipSuccess) return err;
+    }
+#define X100_GU(U)                                                                                       \
+    do {                                                                                                 \
+        if (M > 1)                                                                                       \
+            hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, true>), g_gu, dim3(64 * GU_NWV), lds_gu, s, M, d, ff, \
+                               n_exp, n_act, wg, wu, ws, sel, sw);                                       \
+        else                                                                                             \
+            hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, false>), g_gu, dim3(64 * GU_NWV), lds_gu, s, M, d,  \
+                               ff, n_exp, n_act, wg, wu, ws, sel, sw);                                   \
+    } while (0)
     switch (upl_gu) {
     case 1: X100_GU(1); break;
     case 2: X100_GU(2); break;
