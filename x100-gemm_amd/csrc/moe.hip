@@ -523,83 +523,81 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
 }
 
 // ------------------------------------------------------------------------------------------------
-// M = 1: down projection and slot combine in one launch.  Block = DN1 rows of d for every union
-// slot (units (slot, row, super-block) = U*DN1*nsf, 8 lanes each), so each block has all the y
-// values its rows need and combines them in slot order; with one token row the union is the n_act
-// selected experts and each slot's activation row is act[a] of its slot a.
+// Down projection and weighted combine in one launch.  grid = d / DN blocks of NWV waves; a block
+// owns DN output rows for every (token row m, slot a) pair p = m*n_act + a.  Units (pair p, row r,
+// super-block sb) = P*DN*nsf, 8 lanes each: the unit's expert is sel[p] and its activation row is
+// act[p] (an expert chosen by several token rows is read once per pair, the repeats mostly from
+// cache), so the activation loads depend on nothing and the weight loads only on sel.  Every block
+// quantizes the P activation rows to Q8_K in LDS; y(p, r) sums the super-blocks in order and
+// out[m][r] (+)= sum over slots a = 0..n_act-1 of w_a * y (qwen_moe.c:310-311), as k_moe_down and
+// k_moe_combine do.
 // ------------------------------------------------------------------------------------------------
-constexpr int DN1 = 8;
-constexpr int DN1_NWV = 16;   // waves per block of k_moe_down_m1
+constexpr int FD_NWV = 16;   // waves per block of k_moe_down_fused
+constexpr int FD_DN = 8;     // output rows per block
 
-template <int UPL, int NWV>
-__global__ __launch_bounds__(64 * NWV) void k_moe_down_m1(int d, int ff, int n_exp, int n_act, const uint8_t *__restrict__ Wd,
-                                                     MoeWs ws, float *__restrict__ out, int residual)
+template <int UPL, int QJ>   // QJ: activation blocks per wave per load pass
+__global__ __launch_bounds__(64 * FD_NWV) void k_moe_down_fused(int M, int d, int ff, int n_exp, int n_act,
+                                                                const uint8_t *__restrict__ Wd, MoeWs ws,
+                                                                float *__restrict__ out, int residual)
 {
+    constexpr int NWV = FD_NWV, DN = FD_DN;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ float s_y[8][DN1];
-    __shared__ int s_slot_u[8];
-    __shared__ float s_w[8];
+    __shared__ float s_y[32][FD_DN];
+    __shared__ float s_w[32];
     const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
-    const int U = *ws.nuniq;
+    const int P = M * n_act;
     const int nsf = ff / 256;
-    const int r0 = blockIdx.x * DN1;
-    const int nunits = U * DN1 * nsf;
+    const int r0 = blockIdx.x * DN;
+    const int nunits = P * DN * nsf;
     const size_t erow = (size_t)nsf * 144;
     const size_t emat = erow * d;
-    // Lane l (< 8) holds slot a of union entry l, and the expert of each unit is read per lane.
-    // No address depends on U: entries past U are clamped to a valid slot / expert (their results
-    // are discarded), so U, the union and the pairs are fetched in one round trip.
-    const int pu = (int)min((unsigned)ws.upairs[min(lane, 7) * 8], (unsigned)(n_act - 1));
-    const int umax = n_act * DN1 * nsf;   // units of a full union (U <= n_act at M = 1)
 
-    // Q8_K of the U activation rows (one wave per 256-element block) -> LDS; slot 8*nsf is a
-    // spare that blocks past nq write, so the quantizations run unrolled and branch-free.
-    int8_t *aq = (int8_t *)smem;                    // [8*nsf + 1][256]
-    int *abs_ = (int *)(aq + (8 * nsf + 1) * 256);  // [8*nsf + 1][16]
-    float *ad = (float *)(abs_ + (8 * nsf + 1) * 16);   // [8*nsf + 1]
-    float *tv = ad + 8 * nsf + 1;                   // [8][DN1][nsf] + one spare
-    const int nq = U * nsf, qspare = 8 * nsf;
-    // All activation loads of the first pass (32 blocks: nsf <= 4 takes one pass), then all weight
-    // loads, then the quantizations: the quantizer waits only for the activations.
-    constexpr int QJ = 32 / NWV;   // activation blocks per wave per pass
+    // LDS: Q8_K blocks of the P activation rows + one spare (blocks past nq write it, so the
+    // quantizations run unrolled and branch-free), then the unit results + one spare.
+    const int nq = P * nsf;
+    int8_t *aq = (int8_t *)smem;                       // [nq + 1][256]
+    int *abs_ = (int *)(aq + (nq + 1) * 256);          // [nq + 1][16]
+    float *ad = (float *)(abs_ + (nq + 1) * 16);       // [nq + 1]
+    float *tv = ad + nq + 1;                           // [P][DN][nsf] + one spare
     auto act_loads = [&](int q0, float4 (&v)[QJ]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < QJ; j++) {
-            const int q = min(q0 + NWV * j + w, n_act * nsf - 1);   // clamped; only q < nq is kept
-            const int u = q / nsf, sb = q - u * nsf;
-            v[j] = *(const float4 *)(ws.act + (size_t)__builtin_amdgcn_readlane(pu, u) * ff + sb * 256 + 4 * lane);
+            const int q = min(q0 + NWV * j + w, nq - 1);   // clamped; only q < nq is kept
+            const int p = q / nsf, sb = q - p * nsf;
+            v[j] = *(const float4 *)(ws.act + (size_t)p * ff + sb * 256 + 4 * lane);
         }
     };
     auto act_quant = [&](int q0, const float4 (&v)[QJ]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < QJ; j++) {
             const int q = q0 + NWV * j + w;
-            const int qd = q < nq ? q : qspare;
+            const int qd = q < nq ? q : nq;
             q8k_wave(v[j], aq + qd * 256, abs_ + qd * 16, ad + qd);
         }
     };
+    // The first pass's activation loads, then every weight load, then the quantizer (which waits
+    // only for the activations).
     float4 av[QJ];
     act_loads(0, av);
 
     v4i hdr[UPL], qs[UPL];
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int un = min(c * 8 * NWV + w * 8 + (lane >> 3), umax - 1);   // clamped: see k_moe_gate_up
-        const int u = un / (DN1 * nsf), rem = un - u * DN1 * nsf;
+        const int un = min(c * 8 * NWV + w * 8 + (lane >> 3), nunits - 1);   // clamped: see k_moe_gate_up
+        const int p = un / (DN * nsf), rem = un - p * DN * nsf;
         const int r = rem / nsf, sb = rem - r * nsf;
-        const int ex = min((unsigned)ws.uniq[u], (unsigned)(n_exp - 1));
+        const int ex = min((unsigned)ws.sel[p], (unsigned)(n_exp - 1));
         const uint8_t *blk = Wd + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
         hdr[c] = *(const v4i *)blk;
         qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
     }
     __builtin_amdgcn_sched_barrier(0);
     act_quant(0, av);
-    for (int q0 = 32; q0 < nq; q0 += 32) {
+    for (int q0 = QJ * NWV; q0 < nq; q0 += QJ * NWV) {
         act_loads(q0, av);
         act_quant(q0, av);
     }
-    if (threadIdx.x < U) s_slot_u[pu] = threadIdx.x;   // thread u < 8 is lane u of wave 0
-    if (threadIdx.x < n_act) s_w[threadIdx.x] = ws.sw[threadIdx.x];
+    if (threadIdx.x < P) s_w[threadIdx.x] = ws.sw[threadIdx.x];
     __syncthreads();
 
 #pragma unroll
@@ -607,27 +605,28 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_down_m1(int d, int ff, int n_e
         const int un = c * 8 * NWV + w * 8 + (lane >> 3);
         const bool valid = un < nunits;
         const int unc = valid ? un : 0;
-        const int u = unc / (DN1 * nsf), rem = unc - u * DN1 * nsf;
+        const int p = unc / (DN * nsf), rem = unc - p * DN * nsf;
         const int sb = rem - (rem / nsf) * nsf;
         int isc, imn;
-        q4k_unit_dot(hdr[c], qs[c], aq + (u * nsf + sb) * 256, abs_ + (u * nsf + sb) * 16, i, isc, imn);
-        tv[valid ? un : 8 * DN1 * nsf] = q4k_combine(hdr[c], ad[u * nsf + sb], isc, imn);
+        q4k_unit_dot(hdr[c], qs[c], aq + (p * nsf + sb) * 256, abs_ + (p * nsf + sb) * 16, i, isc, imn);
+        tv[valid ? un : nunits] = q4k_combine(hdr[c], ad[p * nsf + sb], isc, imn);
     }
     __syncthreads();
-    // y of each (slot, row): sequential over super-blocks (the oracle's order)
-    for (int t = threadIdx.x; t < U * DN1; t += 64 * NWV) {
-        const int u = t / DN1, r = t - u * DN1;
+    // y of each (pair, row): sequential over super-blocks (the oracle's order)
+    for (int t = threadIdx.x; t < P * DN; t += 64 * NWV) {
+        const int p = t / DN, r = t - p * DN;
         float y = 0.0f;
-        for (int sb = 0; sb < nsf; sb++) y = y + tv[(u * DN1 + r) * nsf + sb];
-        s_y[u][r] = y;
+        for (int sb = 0; sb < nsf; sb++) y = y + tv[(p * DN + r) * nsf + sb];
+        s_y[p][r] = y;
     }
     __syncthreads();
-    // out (+)= sum over slots a = 0..n_act-1 of w_a * y_a (qwen_moe.c:310-311)
-    if (threadIdx.x < DN1) {
-        const int row = r0 + threadIdx.x;
+    // out[m][row] (+)= sum over slots a of w_a * y_a, a ascending (qwen_moe.c:310-311)
+    for (int t = threadIdx.x; t < M * DN; t += 64 * NWV) {
+        const int m = t / DN, r = t - m * DN;
         float eo = 0.0f;
-        for (int a = 0; a < n_act; a++) eo = eo + s_w[a] * s_y[s_slot_u[a]][threadIdx.x];
-        out[row] = residual ? out[row] + eo : eo;
+        for (int a = 0; a < n_act; a++) eo = eo + s_w[m * n_act + a] * s_y[m * n_act + a][r];
+        float *o = out + (size_t)m * d + r0 + r;
+        *o = residual ? *o + eo : eo;
     }
 }
 
@@ -734,22 +733,36 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
-    if (M == 1 && d % DN1 == 0 && n_act * DN1 * nsf <= 8 * 8 * DN1_NWV) {
-        // down + combine in one launch (see k_moe_down_m1)
-        const size_t lds1 = ((size_t)8 * nsf + 1) * (256 + 64 + 4) + ((size_t)8 * DN1 * nsf + 1) * 4;
-        const int upl1 = (n_act * DN1 * nsf + 8 * DN1_NWV - 1) / (8 * DN1_NWV);
-        const dim3 g1(d / DN1), b1(64 * DN1_NWV);
-        const uint8_t *wd1 = (const uint8_t *)Wd;
-#define X100_DN1(U) hipLaunchKernelGGL((k_moe_down_m1<U, DN1_NWV>), g1, b1, lds1, s, d, ff, n_exp, n_act, wd1, ws, out, residual)
-        switch (upl1) {
-        case 1: X100_DN1(1); break;
-        case 2: X100_DN1(2); break;
-        case 3: case 4: X100_DN1(4); break;
-        case 5: case 6: X100_DN1(6); break;
-        default: X100_DN1(8); break;
+    {
+        // down + combine in one launch (k_moe_down_fused) up to 4 token rows, when the units fit 8
+        // per lane and the quantized activations fit LDS (every block quantizes all P rows, which
+        // at 8 token rows costs more than the separate combine); otherwise k_moe_down, then
+        // k_moe_combine
+        const int dn = FD_DN;
+        const int P = M * n_act, nq = P * nsf, nun = P * dn * nsf;
+        const int upl = (nun + 8 * FD_NWV - 1) / (8 * FD_NWV);
+        const size_t ldsf = ((size_t)nq + 1) * (256 + 64 + 4) + ((size_t)nun + 1) * 4;
+        if (M <= 4 && d % dn == 0 && upl <= 8 && ldsf <= 96 * 1024) {
+            const dim3 gf(d / dn), bf(64 * FD_NWV);
+            const uint8_t *wdf = (const uint8_t *)Wd;
+#define X100_FD(U, QJ) hipLaunchKernelGGL((k_moe_down_fused<U, QJ>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, wdf, ws, out, residual)
+#define X100_FD_SW(QJ)                          \
+    switch (upl) {                              \
+    case 1: X100_FD(1, QJ); break;              \
+    case 2: X100_FD(2, QJ); break;              \
+    case 3: case 4: X100_FD(4, QJ); break;      \
+    case 5: case 6: X100_FD(6, QJ); break;      \
+    default: X100_FD(8, QJ); break;             \
+    }
+            if (nq <= 2 * FD_NWV) {   // activation blocks per wave: 2 when they fit, else 4 per pass
+                X100_FD_SW(2)
+            } else {
+                X100_FD_SW(4)
+            }
+#undef X100_FD_SW
+#undef X100_FD
+            return hipGetLastError();
         }
-#undef X100_DN1
-        return hipGetLastError();
     }
     const size_t lds_dn = (size_t)8 * nsf * (256 + 64 + 4) + ((size_t)8 * DN_ROWS * nsf + 1) * 4;
     const int upl_dn = (DN_ROWS * nsf + 31) / 32;
