@@ -1,17 +1,20 @@
 // Qwen3-MoE decode layer (the FFN block of qwen_moe.c:294-311) for M <= 8 token rows.
 //
-// Four launches on one stream; each kernel only reads what an earlier launch wrote, so no block
-// ever waits for, or signals, another block (no fences, no atomics):
-//   k_moe_route    router logits R.hn (one wave per expert) and the Q8_K form of every hn row.
-//   k_moe_gate_up  grid (union slot, GU_ROWS rows of ff).  Every block re-derives softmax, top-k
-//                  and the expert union from the logits (a few hundred flops per row, cheaper
-//                  than another launch), then streams its GU_ROWS rows of the expert's gate and
-//                  up matrices once for all token rows that chose the expert (Q4_K x Q8_K, the
-//                  MUL_MAT_ID grouping of ime.cpp:667-697) and writes SwiGLU(g, u) per pair.
-//                  Block (0, 0) also publishes the routing (sel, sw, union) for the next launches.
-//   k_moe_down     grid (union slot, DN_ROWS rows of d).  Quantizes the expert's activation rows
-//                  (Q8_K, in LDS), down projection, writes y per (token row, slot) pair.
-//   k_moe_combine  out[m] (+)= sum over slots a = 0..n_act-1 of w_a * y_a, in slot order.
+// Three to five launches on one stream; each kernel only reads what an earlier launch wrote, so
+// no block ever waits for, or signals, another block (no fences, no atomics):
+//   k_moe_route       router logits R.hn (one wave per expert) and the Q8_K form of every hn row.
+//   k_moe_topk        (M > 1) softmax, top-k and the expert union of all rows, once, in one block.
+//   k_moe_gate_up     grid (union slot, GU_ROWS rows of ff).  With one token row every block
+//                     derives the routing itself (cheaper than another launch; block (0, 0)
+//                     publishes it), with several it reads k_moe_topk's.  It streams its GU_ROWS
+//                     rows of the expert's gate and up matrices once for all token rows that chose
+//                     the expert (Q4_K x Q8_K, the MUL_MAT_ID grouping of ime.cpp:667-697) and
+//                     writes SwiGLU(g, u) per (token row, slot) pair.
+//   k_moe_down_fused  (M <= 4) grid (FD_DN rows of d): every pair's activation row quantized to
+//                     Q8_K in LDS, the down projection of those rows for all pairs, and the
+//                     weighted combine in slot order, written to out.
+//   k_moe_down        (M > 4) grid (union slot, DN_ROWS rows of d): the expert's activation rows
+//   + k_moe_combine   in Q8_K, down projection, y per pair; then out[m] (+)= sum_a w_a * y_a.
 #include "x100_common.h"
 #include "x100_internal.h"
 
