@@ -173,7 +173,8 @@ struct RouteLds {
     __attribute__((aligned(16))) int sel[8 * 8];
     float w[8 * 8];
     int uniq[64];
-    int wcnt[4];
+    uint64_t mask[8][4];   // experts chosen by row m: bit l of mask[m][c] = expert 64c + l
+    uint64_t umask[4];     // their union
     int U;
 };
 
@@ -183,10 +184,13 @@ template <int NWV, int KC>
 X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
 {
     const int lane = threadIdx.x & 63, w = wave_id();
-    bool picked[KC];   // experts lane + 64c chosen for row w (used when M == 1)
+    uint64_t rowmask[KC];   // ballots of the chosen experts of this wave's last row
 #pragma unroll
-    for (int c = 0; c < KC; c++) picked[c] = false;
+    for (int c = 0; c < KC; c++) rowmask[c] = 0;
     for (int m = w; m < M; m += NWV) {
+        bool picked[KC];   // experts lane + 64c chosen for row m
+#pragma unroll
+        for (int c = 0; c < KC; c++) picked[c] = false;
         float p[KC];
         float mx = -1e30f;
 #pragma unroll
@@ -253,18 +257,25 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
 #pragma unroll
         for (int a = 1; a < 8; a++) mine = lane == a ? wsel[a] : mine;
         if (lane < n_act) rl.w[m * n_act + lane] = mine / ssum;
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            rowmask[c] = __ballot(picked[c]);
+            if (lane == 0) rl.mask[m][c] = rowmask[c];
+        }
     }
-    // Union slots in ascending expert id: slot of expert e = number of selected experts below e.
+    // Union slots in ascending expert id: slot of expert e = number of chosen experts below e;
+    // the union is the OR of the rows' masks, slots are prefix counts of its bits.
     if (M == 1) {
-        // One row: its wave holds the chosen experts as flags; prefix counts of the ballots.
+        // one row: wave 0 holds its masks in registers
         if (w == 0) {
             const uint64_t below = (1ull << lane) - 1ull;
             int base = 0;
 #pragma unroll
-            for (int c = 0; c < KC; c++) {
-                const uint64_t bal = __ballot(picked[c]);
-                if (picked[c]) rl.uniq[base + __popcll(bal & below)] = lane + 64 * c;
-                base += __popcll(bal);
+            for (int c = 0; c < 4; c++) {
+                const uint64_t um = c < KC ? rowmask[c < KC ? c : 0] : 0;
+                if ((um >> lane) & 1ull) rl.uniq[base + __popcll(um & below)] = lane + 64 * c;
+                base += __popcll(um);
+                if (lane == 0) rl.umask[c] = um;
             }
             if (lane == 0) rl.U = base;
         }
@@ -272,22 +283,22 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
         return;
     }
     __syncthreads();
-    bool chosen = false;
-    const int P = M * n_act;
-    for (int t0 = 0; t0 < P; t0 += 4) {
-        const v4i q = *(const v4i *)(rl.sel + t0);   // rl.sel is padded to a multiple of 4
+    if (w == 0) {
+        const uint64_t below = (1ull << lane) - 1ull;
+        int base = 0;
 #pragma unroll
-        for (int k = 0; k < 4; k++) chosen |= (t0 + k < P) && q[k] == (int)threadIdx.x;
+        for (int c = 0; c < KC; c++) {
+            uint64_t um = 0;
+            for (int m = 0; m < M; m++) um |= rl.mask[m][c];
+            if ((um >> lane) & 1ull) rl.uniq[base + __popcll(um & below)] = lane + 64 * c;
+            base += __popcll(um);
+            if (lane == 0) rl.umask[c] = um;
+        }
+#pragma unroll
+        for (int c = KC; c < 4; c++)
+            if (lane == 0) rl.umask[c] = 0;
+        if (lane == 0) rl.U = base;
     }
-    const uint64_t bal = __ballot(chosen);
-    if (lane == 0 && w < 4) rl.wcnt[w] = __popcll(bal);   // threads >= 256 >= n_exp are never chosen
-    __syncthreads();
-    if (chosen) {
-        int slot = __popcll(bal & ((1ull << lane) - 1ull));
-        for (int v = 0; v < w; v++) slot += rl.wcnt[v];
-        rl.uniq[slot] = threadIdx.x;
-    }
-    if (threadIdx.x == 0) rl.U = rl.wcnt[0] + rl.wcnt[1] + rl.wcnt[2] + rl.wcnt[3];
     __syncthreads();
 }
 template <int NWV>
@@ -310,19 +321,27 @@ X100_DEV void publish_routing(int M, int n_act, const RouteLds &rl, MoeWs ws, in
     const int t = threadIdx.x;
     const int U = rl.U;
     if (t < M * n_act) {
-        ws.sel[t] = rl.sel[t];
+        const int e = rl.sel[t], m = t / n_act, c = e >> 6;
+        const uint64_t bit = 1ull << (e & 63);
+        ws.sel[t] = e;
         ws.sw[t] = rl.w[t];
-        if (sel_out) sel_out[t] = rl.sel[t];
+        if (sel_out) sel_out[t] = e;
         if (sw_out) sw_out[t] = rl.w[t];
-    }
-    if (t < U) {
-        const int ex = rl.uniq[t];
-        int c = 0;
-        for (int m = 0; m < M; m++)
-            for (int a = 0; a < n_act; a++)
-                if (rl.sel[m * n_act + a] == ex) ws.upairs[t * 8 + c++] = m * n_act + a;
-        ws.uniq[t] = ex;
-        ws.ucnt[t] = c;
+        // union slot of e, the pair's place in the slot's list (earlier rows that chose e come
+        // first: token rows ascending) and the list length
+        int slot = __popcll(rl.umask[c] & (bit - 1ull));
+        for (int k = 0; k < c; k++) slot += __popcll(rl.umask[k]);
+        int pos = 0, cnt = 0;
+        for (int r = 0; r < M; r++) {
+            const int has = (rl.mask[r][c] & bit) != 0;
+            pos += r < m ? has : 0;
+            cnt += has;
+        }
+        ws.upairs[slot * 8 + pos] = t;
+        if (pos == 0) {
+            ws.uniq[slot] = e;
+            ws.ucnt[slot] = cnt;
+        }
     }
     if (t == 0) *ws.nuniq = U;
 }
@@ -757,10 +776,14 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     case 5: case 6: X100_FD(6, QJ); break;      \
     default: X100_FD(8, QJ); break;             \
     }
-            if (nq <= 2 * FD_NWV) {   // activation blocks per wave: 2 when they fit, else 4 per pass
+            // activation blocks per wave per pass: as many as nq needs, up to 8 (one pass up to
+            // 128 blocks, so no pass's loads wait behind another pass's quantization)
+            if (nq <= 2 * FD_NWV) {
                 X100_FD_SW(2)
-            } else {
+            } else if (nq <= 4 * FD_NWV) {
                 X100_FD_SW(4)
+            } else {
+                X100_FD_SW(8)
             }
 #undef X100_FD_SW
 #undef X100_FD
