@@ -634,56 +634,70 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     }
 }
 
-// Skinny GEMM, M <= MR rows.  Block = 4 waves over columns [n0, n0+256) and k rows
-// [k0, k0+256); wave w owns rows k0+64w .. +63.  Each lane streams 16 x 16 bytes of B (one
-// 256-byte row slice per 16 lanes, fully coalesced), the wave stages its 16 KB slice in LDS, then
-// each lane owns 4 columns: it reads 4 rows' dwords, transposes them to k-quads and runs dot4
-// against the A k-quads (wave-uniform LDS broadcast).  The 4 waves' partial sums are reduced in
-// LDS and added to C with int32 atomics.
-template <int MR>
-__global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K,
-                                                    const int8_t *__restrict__ A,
-                                                    const int8_t *__restrict__ B,
-                                                    int32_t *__restrict__ C)
+// Skinny GEMM, M <= MR rows.  Block = W waves over columns [n0, n0+256) and k rows
+// [k0, k0+256); wave w owns rows k0 + RW*w .. +RW-1 (RW = 256/W).  Each lane streams RW/4 x 16
+// bytes of B (one 256-byte row slice per 16 lanes, fully coalesced), the wave stages its slice in
+// LDS group by group as it arrives, and each lane owns 4 columns: it reads 4 rows' dwords,
+// transposes them to k-quads and runs dot4 against the A k-quads (wave-uniform LDS broadcast).
+// All loads are unconditional buffer loads issued before the first wait (A's first, since the
+// barrier waits for A and loads complete in order).  The W waves' partial sums are reduced in LDS
+// and added to C with int32 atomics.  B must fit one buffer resource (K*N < 2^32 bytes).  (W = 8, two waves per SIMD, measured slower: 11.3 vs
+// 8.9 us at 8 x 4096 x 4096.)
+template <int MR, int W>
+__global__ __launch_bounds__(64 * W) void k_gemm_skinny(int M, int N, int K,
+                                                       const int8_t *__restrict__ A,
+                                                       const int8_t *__restrict__ B,
+                                                       int32_t *__restrict__ C)
 {
-    __shared__ __attribute__((aligned(16))) uint32_t Bs[4][64 * 64];  // 64 KB: 4 x (64 rows x 256 B)
+    constexpr int RW = 256 / W;      // k rows per wave
+    constexpr int LPL = RW / 4;      // 16-byte loads per lane
+    static_assert(W * MR * 256 <= 4 * 64 * 64, "the reduction must fit the B staging area");
+    __shared__ __attribute__((aligned(16))) uint32_t Bs[W][RW * 64];  // 64 KB: W x (RW rows x 256 B)
     __shared__ __attribute__((aligned(16))) uint32_t As[MR][64];      // A[m][k0..k0+256) as dwords
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n0 = blockIdx.x * 256, k0 = blockIdx.y * 256;
-    const bool full = (n0 + 256 <= N) && (k0 + 256 <= K);
-
-    // Issue all B loads first (16 per lane) so the whole slice is in flight.
-    v4i rb[16];
+    // A slice (zero padded) first: the barrier below waits for these loads, and loads complete in
+    // order, so A must not queue behind the B slice.
+    // Unconditional byte loads through a buffer resource of M*K bytes (rows m >= M read 0); the
+    // K tail is zeroed by a select, so every load is issued before any is waited for.
+    const rsrc_t ar = buf_rsrc(A, (uint32_t)(M * K));
+    static_assert((MR * 64) % (64 * W) == 0, "the A slice is split evenly over the threads");
+    constexpr int AJ = MR * 64 / (64 * W);   // A dwords per thread
+    uint32_t av[AJ];
+#pragma unroll
+    for (int j = 0; j < AJ; j++) {
+        const int idx = tid + 64 * W * j;
+        const int m = idx >> 6, kq = idx & 63;
+        const int gk = k0 + 4 * kq;
+        uint32_t v = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int k = gk + e;
+            const uint32_t byte = __builtin_amdgcn_raw_buffer_load_b8(ar, (uint32_t)(m * K + min(k, K - 1)), 0, 0);
+            v |= (k < K ? byte : 0u) << (8 * e);
+        }
+        av[j] = v;
+    }
+    // Then all B loads, so the whole slice is in flight.
+    // Unconditional buffer loads: rows past K read 0 (past the resource's K*N bytes); columns past
+    // N read the next row's bytes, but those columns are never stored.
+    const rsrc_t br = buf_rsrc(B, (uint32_t)((size_t)K * N));
+    v4i rb[LPL];
     const int nc = lane & 15;
     const int gn = n0 + 16 * nc;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int gk = k0 + 64 * w + 4 * i + (lane >> 4);
-        if (full || (gk < K && gn < N))
-            rb[i] = *(const v4i *)(B + (size_t)gk * N + gn);
-        else
-            rb[i] = v4i{0, 0, 0, 0};
+    for (int i = 0; i < LPL; i++) {
+        const int gk = k0 + RW * w + 4 * i + (lane >> 4);
+        rb[i] = (v4i)__builtin_amdgcn_raw_buffer_load_b128(br, (uint32_t)min((size_t)gk * N + gn, (size_t)K * N), 0, 0);
     }
-    // A slice (zero padded) into LDS.
-    for (int idx = tid; idx < MR * 64; idx += 256) {
-        const int m = idx >> 6, kq = idx & 63;
-        uint32_t v = 0;
-        if (m < M) {
-            const int gk = k0 + 4 * kq;
-            const int8_t *ap = A + (size_t)m * K + gk;
+    __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the first store
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (gk + e < K) v |= (uint32_t)(uint8_t)ap[e] << (8 * e);
-        }
-        As[m][kq] = v;
+    for (int j = 0; j < AJ; j++) {
+        const int idx = tid + 64 * W * j;
+        As[idx >> 6][idx & 63] = av[j];
     }
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int row = 4 * i + (lane >> 4);
-        *(v4i *)(&Bs[w][row * 64 + 4 * nc]) = rb[i];
-    }
-    __syncthreads();
+    __syncthreads();   // A is in LDS; each wave's B slice is its own, written and read below
 
     int acc[MR][4];
 #pragma unroll
@@ -691,38 +705,48 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K,
 #pragma unroll
         for (int e = 0; e < 4; e++) acc[m][e] = 0;
 
+    // Groups of 16 k-rows: a group goes to LDS as soon as its 4 loads arrive and is consumed at
+    // once, so early groups' dot products overlap later groups' loads.  (LDS operations of one
+    // wave complete in order, so the wave reads its own rows back without a barrier.)
     const uint32_t *bw = Bs[w];
-#pragma unroll 4
-    for (int kq = 0; kq < 16; kq++) {
-        uint32_t o0, o1, o2, o3;
-        transpose4x4(bw[(4 * kq + 0) * 64 + lane], bw[(4 * kq + 1) * 64 + lane],
-                     bw[(4 * kq + 2) * 64 + lane], bw[(4 * kq + 3) * 64 + lane], o0, o1, o2, o3);
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            const int a = (int)As[m][16 * w + kq];
-            acc[m][0] = dot4((int)o0, a, acc[m][0]);
-            acc[m][1] = dot4((int)o1, a, acc[m][1]);
-            acc[m][2] = dot4((int)o2, a, acc[m][2]);
-            acc[m][3] = dot4((int)o3, a, acc[m][3]);
+    for (int g = 0; g < LPL / 4; g++) {
+#pragma unroll
+        for (int i = 4 * g; i < 4 * g + 4; i++) {
+            const int row = 4 * i + (lane >> 4);
+            *(v4i *)(&Bs[w][row * 64 + 4 * nc]) = rb[i];
+        }
+#pragma unroll
+        for (int kq = 4 * g; kq < 4 * g + 4; kq++) {
+            uint32_t o0, o1, o2, o3;
+            transpose4x4(bw[(4 * kq + 0) * 64 + lane], bw[(4 * kq + 1) * 64 + lane],
+                         bw[(4 * kq + 2) * 64 + lane], bw[(4 * kq + 3) * 64 + lane], o0, o1, o2, o3);
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const int a = (int)As[m][(RW / 4) * w + kq];
+                acc[m][0] = dot4((int)o0, a, acc[m][0]);
+                acc[m][1] = dot4((int)o1, a, acc[m][1]);
+                acc[m][2] = dot4((int)o2, a, acc[m][2]);
+                acc[m][3] = dot4((int)o3, a, acc[m][3]);
+            }
         }
     }
     __syncthreads();
 
     // Cross-wave reduction through LDS (reuses the B staging area).
-    int *red = (int *)&Bs[0][0];  // [4 waves][MR][256 columns]
+    int *red = (int *)&Bs[0][0];  // [W waves][MR][256 columns]
 #pragma unroll
     for (int m = 0; m < MR; m++)
         *(v4i *)(&red[(w * MR + m) * 256 + 4 * lane]) = v4i{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
     __syncthreads();
-    const int col = n0 + tid;
-    if (col < N) {
+    for (int t = tid; t < MR * 256; t += 64 * W) {
+        const int m = t >> 8, c = t & 255;
+        const int col = n0 + c;
+        if (m < M && col < N) {
+            int sum = 0;
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            if (m < M) {
-                int s = red[(0 * MR + m) * 256 + tid] + red[(1 * MR + m) * 256 + tid] +
-                        red[(2 * MR + m) * 256 + tid] + red[(3 * MR + m) * 256 + tid];
-                atomicAdd(&C[(size_t)m * N + col], s);
-            }
+            for (int v = 0; v < W; v++) sum += red[(v * MR + m) * 256 + c];
+            atomicAdd(&C[(size_t)m * N + col], sum);
         }
     }
 }
@@ -790,7 +814,7 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
     if (variant == X100_GEMM_AUTO) {
         if (!aligned)
             variant = X100_GEMM_GENERIC;
-        else if (M <= 16)
+        else if (M <= 16 && (size_t)K * N < ((size_t)1 << 32))   // B must fit one buffer resource
             variant = X100_GEMM_SKINNY;
         else if ((long)M * N >= 1024L * 1024L)
             variant = X100_GEMM_TILE256;
@@ -820,12 +844,12 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
     }
     case X100_GEMM_TILE128: return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
     case X100_GEMM_SKINNY: {
-        if (M > 16) return hipErrorInvalidValue;
+        if (M > 16 || (size_t)K * N >= ((size_t)1 << 32)) return hipErrorInvalidValue;
         dim3 grid((N + 255) / 256, (K + 255) / 256);
         if (M <= 8)
-            hipLaunchKernelGGL(k_gemm_skinny<8>, grid, dim3(256), 0, s, M, N, K, A, B, C);
+            hipLaunchKernelGGL((k_gemm_skinny<8, 4>), grid, dim3(256), 0, s, M, N, K, A, B, C);
         else
-            hipLaunchKernelGGL(k_gemm_skinny<16>, grid, dim3(256), 0, s, M, N, K, A, B, C);
+            hipLaunchKernelGGL((k_gemm_skinny<16, 4>), grid, dim3(256), 0, s, M, N, K, A, B, C);
         return hipGetLastError();
     }
     case X100_GEMM_GENERIC: {
