@@ -18,6 +18,8 @@ timed with HIP events on the launch stream.  The same JSON line carries:
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
        python bench.py --probe     (for rocprofv3 --pmc: `--steps` GEMM 4096^3 launches, then one
                                     256 MiB device-to-device copy as the byte-count calibration)
+       python bench.py --probe-all (the same with every other kernel family in between, 3 launches
+                                    each at its benchmark shape)
 """
 import argparse
 import json
@@ -321,8 +323,63 @@ def bench_extra(torch, timer, dev, args):
     return extra
 
 
+def probe_paths(torch, dev, s, reps=3):
+    """Launches of every other kernel family at its benchmark shape, for hardware counters:
+    skinny GEMM, the Q4_0 / Q4_K / Q3_K GEMVs at M = 1 and 4, the int4 / int8 tile GEMV at M = 1,
+    and the MoE layer at M = 1 and 4, each `reps` times on distinct weight copies."""
+    M, N, K = 8, 4096, 4096
+    A, B = synth.gemm_inputs(M, N, K, seed=2027)
+    dA = torch.from_numpy(A).to(dev)
+    dBs = [torch.from_numpy(B).to(dev).roll(i, 0) for i in range(reps)]
+    dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    for i in range(reps):
+        x100hip.gemm_dev(M, N, K, dA.data_ptr(), dBs[i].data_ptr(), dC.data_ptr(), s)
+    torch.cuda.synchronize()
+    del dBs
+    for qt, N, K in [(synth.Q4_0, 4096, 4096), (synth.Q4_K, 6144, 2048), (synth.Q3_K, 6144, 2048)]:
+        W = synth.quant_weight(qt, N, K, seed=100 + qt)
+        raw = torch.from_numpy(W.view(np.uint8).reshape(-1)).to(dev)
+        pb = x100hip.packed_bytes(qt, N, K)
+        packs = torch.empty((reps, (pb + 255) // 256 * 256), dtype=torch.uint8, device=dev)
+        for i in range(reps):
+            x100hip.pack(qt, N, K, raw.data_ptr(), packs[i].data_ptr(), s)
+        for M in (1, 4):
+            dx = torch.from_numpy(synth.normal_f32(7 + M, (M, K))).to(dev)
+            dy = torch.empty((M, N), dtype=torch.float32, device=dev)
+            for i in range(reps):
+                x100hip.qgemv(qt, M, N, K, packs[i].data_ptr(), dx.data_ptr(), dy.data_ptr(), s)
+        torch.cuda.synchronize()
+        del packs, raw
+    N, K = 4864, 896
+    Wt = (synth.rand_bytes(77, N * K).astype(np.int32) % 15 - 7).astype(np.int8).reshape(N, K)
+    for int4 in (True, False):
+        packed = x100hip.pack_w(int4, Wt)
+        dws = torch.from_numpy(packed.view(np.uint8)).to(dev).repeat(reps, 1)
+        dx = torch.from_numpy(synth.rand_int8(79, (1, K))).to(dev)
+        dy = torch.empty((1, N), dtype=torch.int32, device=dev)
+        for i in range(reps):
+            x100hip.gemv_tile(int4, 1, N, K, dws[i].data_ptr(), dx.data_ptr(), dy.data_ptr(), s)
+        torch.cuda.synchronize()
+        del dws
+    n_exp, d, ff, n_act = 128, 2048, 768, 8
+    Wg, Wu, Wd = synth.moe_weights(n_exp, d, ff, seed=500)
+    dR = torch.from_numpy(synth.moe_router(n_exp, d, seed=501)).to(dev)
+    base = [torch.from_numpy(np.ascontiguousarray(w).view(np.uint8).reshape(-1)).to(dev) for w in (Wg, Wu, Wd)]
+    layers = [base] + [[b.clone() for b in base] for _ in range(reps - 1)]
+    for M in (1, 4):
+        dh = torch.from_numpy(synth.normal_f32(900 + M, (reps, M, d))).to(dev)
+        out = torch.empty((M, d), dtype=torch.float32, device=dev)
+        for i in range(reps):
+            L = layers[i]
+            x100hip.moe_layer(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
+                              L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False, None, None, s)
+        torch.cuda.synchronize()
+
+
 def probe(torch, dev, args):
-    """Launches to read hardware counters from: GEMM 4096^3 x steps, then a 256 MiB copy."""
+    """Launches to read hardware counters from: GEMM 4096^3 x steps (with --probe-all, then every
+    other kernel family at its benchmark shape), then a 256 MiB copy that calibrates the byte
+    counters."""
     M = N = K = 4096
     A, B = synth.gemm_inputs(M, N, K, seed=2026)
     dA, dB = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
@@ -331,6 +388,9 @@ def probe(torch, dev, args):
     for _ in range(args.steps):
         x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
     torch.cuda.synchronize()
+    if args.probe_all:
+        del dA, dB, dC
+        probe_paths(torch, dev, s)
     src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
@@ -346,6 +406,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--probe", action="store_true")
+    ap.add_argument("--probe-all", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this backend has no multi-GPU path "
@@ -360,7 +421,7 @@ def main():
     if not caps.is_gfx950:
         raise SystemExit("not a gfx950 device: %s" % caps.arch.decode())
     timer = Timer(torch)
-    if args.probe:
+    if args.probe or args.probe_all:
         probe(torch, dev, args)
         return
     ms, tops, roof = bench_gemm(torch, timer, dev, args)
