@@ -421,14 +421,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     auto read_frags = [&](int slot, int kk, v4i (&af)[4], v4i (&bf)[FN]) __attribute__((always_inline)) {
         const uint8_t *As = SUPER == 2 ? smem + (slot >> 1) * 2 * STAGE : smem + slot * STAGE;
         const uint8_t *Bs = SUPER == 2 ? As + STAGE + (slot & 1) * BOFF : As + BOFF;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
+        auto read_a = [&](int i) __attribute__((always_inline)) {
             const int r = wm * 128 + 32 * i + lcol;
             if constexpr (SUPER == 2)
                 af[i] = *(const v4i *)(As + r * 128 + 16 * big_a2_chunk(r, 4 * (slot & 1) + 2 * kk + lgrp));
             else
                 af[i] = *(const v4i *)(As + r * 64 + 16 * big_a_chunk(r, 2 * kk + lgrp));
-        }
+        };
+        // In the order of first use by mma (row fragment outer): A0, every B fragment, A1..A3.
+        read_a(0);
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int c = 2 * FN * wn + 2 * j + ch;
@@ -438,6 +439,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
             const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(const lds_u8 *)(p0 + 8 * 256));
             bf[j] = v4i{lo.x, lo.y, hi.x, hi.y};
         }
+#pragma unroll
+        for (int i = 1; i < 4; i++) read_a(i);
     };
     auto mma = [&](const v4i (&af)[4], const v4i (&bf)[FN]) __attribute__((always_inline)) {
 #pragma unroll
