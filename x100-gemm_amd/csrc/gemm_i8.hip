@@ -227,16 +227,16 @@ X100_DEV int big_b_chunk(int k, int c) { return c ^ (2 * (k & 7)); }
 //   chunk c -> granule 8*(r&1) + (c ^ ((r>>1)&7)).
 X100_DEV int big_a2_chunk(int r, int c) { return c ^ ((r >> 1) & 7); }
 
+// The LDS destination (wave-uniform) is passed in M0 through the "{m0}" operand, so the compiler
+// knows the register is written.
 X100_DEV void dma16(const void *gsrc, uint32_t lds_base)
 {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(gsrc)
-                 : "memory", "m0");
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(lds_base) : "memory");
 }
 // Same with a wave-uniform 64-bit base address and a 32-bit per-lane byte offset.
 X100_DEV void dma16s(uint32_t voff, const void *sbase, uint32_t lds_base)
 {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_base), "v"(voff), "s"(sbase)
-                 : "memory", "m0");
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
 }
 
 template <int N> X100_DEV void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
