@@ -830,7 +830,7 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
         // Full 256x256 tiles only; other shapes use the 128x128 tile with edge guards.
         if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
         const int tiles_m = M / 256, tiles_n = N / 256;
-        if ((K / BK) % 8 == 0)   // whole superstages in each of the 4 C parts
+        if ((K / BK) % 8 == 0)   // superstages (the K shapes the superstage path is tested on)
             hipLaunchKernelGGL((k_gemm_big<8, 2>), dim3(tiles_m * tiles_n), dim3(512), 0, s, M, N, K, A, B, C,
                                tiles_m, tiles_n);
         else
@@ -841,8 +841,12 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
     case X100_GEMM_TILE256_W4: {
         if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
         const int tiles_m = M / 256, tiles_n = N / 256;
-        hipLaunchKernelGGL((k_gemm_big<4, 1>), dim3(tiles_m * tiles_n), dim3(256), 0, s, M, N, K, A, B, C,
-                           tiles_m, tiles_n);
+        if ((K / BK) % 8 == 0)
+            hipLaunchKernelGGL((k_gemm_big<4, 2>), dim3(tiles_m * tiles_n), dim3(256), 0, s, M, N, K, A, B, C,
+                               tiles_m, tiles_n);
+        else
+            hipLaunchKernelGGL((k_gemm_big<4, 1>), dim3(tiles_m * tiles_n), dim3(256), 0, s, M, N, K, A, B, C,
+                               tiles_m, tiles_n);
         return hipGetLastError();
     }
     case X100_GEMM_TILE128: return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
