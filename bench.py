@@ -191,6 +191,22 @@ def bench_extra(torch, timer, dev, args):
     extra = {}
     s = torch.cuda.current_stream().cuda_stream
 
+    # ---- 256^3 GEMM (the reference's own gemm_bench case; launch-bound) ------------------------
+    M = N = K = 256
+    A, B = synth.gemm_inputs(M, N, K, seed=2026)
+    dA, dB = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    fns = [lambda: x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream) for _ in range(32)]
+    us = timer.graph(fns)
+    lat = timer.single(fns[0])
+    Cc = np.zeros((M, N), np.int32)
+    cpu_us = cpu_time(lambda: ol.oracle().gemm_ref_i8(M, N, K, A.ctypes.data, B.ctypes.data, Cc.ctypes.data))
+    extra["gemm_i8_256"] = {"us": us, "TOPS": 2.0 * M * N * K / us / 1e6, "single_launch_us": lat,
+                            "cpu_us_1core": cpu_us, "cpu_GOPS_1core": 2.0 * M * N * K / cpu_us / 1e3}
+    log("gemm 256^3: %.2f us  %.1f TOPS (single %.2f us)  cpu %.0f us = %.2f GOP/s" % (
+        us, 2.0 * M * N * K / us / 1e6, lat, cpu_us, 2.0 * M * N * K / cpu_us / 1e3))
+
     # ---- skinny speculative-verify GEMM -------------------------------------------------------
     M, N, K = 8, 4096, 4096
     A, B = synth.gemm_inputs(M, N, K, seed=2027)

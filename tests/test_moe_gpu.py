@@ -96,3 +96,17 @@ def test_moe_repeat_calls_stable(dev):
     a = gpu_moe(hn, L, 4, dev)[0]
     for _ in range(3):
         assert np.array_equal(gpu_moe(hn, L, 4, dev)[0], a)
+
+
+@pytest.mark.parametrize("M", [2, 4, 8])
+def test_moe_batched_rows_equal_single_rows(dev, M):
+    # Several token rows (union grouping, one-block top-k, fused or separate down + combine) must
+    # give every row exactly what a one-row call gives it (per-row routing and Q8_K quantization)
+    L = layer(128, 2048, 768, 500, dev)
+    hn = synth.normal_f32(800 + M, (M, 2048))
+    out, sel, sw = gpu_moe(hn, L, 8, dev)
+    for m in range(M):
+        o1, s1, w1 = gpu_moe(hn[m:m + 1], L, 8, dev)
+        assert np.array_equal(sel[m], s1[0])
+        assert np.array_equal(sw[m].view(np.uint32), w1[0].view(np.uint32))
+        assert np.array_equal(out[m].view(np.uint32), o1[0].view(np.uint32)), "row %d differs" % m

@@ -74,3 +74,17 @@ def test_qgemv_rejects_bad_shapes(dev):
         x100hip.qgemv(synth.Q4_K, 1, 16, 100, 1 << 20, 1 << 20, 1 << 20)
     with pytest.raises(x100hip.X100Error):
         x100hip.qgemv(synth.Q4_0, 9, 16, 64, 1 << 20, 1 << 20, 1 << 20)
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q4_K, synth.Q3_K])
+@pytest.mark.parametrize("M", [4, 8])
+def test_qgemv_batched_rows_equal_single_rows(dev, qtype, M):
+    # the multi-row block shapes (more waves, one row per wave for Q4_0) compute each row exactly
+    # as the one-row kernels do: per-row quantization, same per-block order
+    N, K = 1024, 2048
+    W = synth.quant_weight(qtype, N, K, seed=900 + qtype)
+    x = synth.normal_f32(901 + M, (M, K))
+    y = gpu_qgemv(qtype, W, x, dev)
+    for m in range(M):
+        y1 = gpu_qgemv(qtype, W, x[m:m + 1], dev)
+        assert np.array_equal(y[m].view(np.uint32), y1[0].view(np.uint32)), "row %d differs" % m
