@@ -16,7 +16,9 @@ MI355X version (same matmul shapes, same bytes):
   * a token is 5 launches per layer + the lm_head, captured once in a HIP graph and replayed.
 Weights are random bytes written on the device (any byte is a valid int4 pair / int8 value).
 
-Usage: python x100-gemm_amd/moe_decode.py [--layers 48] [--reps 3] [--us 8,16,24,64]
+Usage: python x100-gemm_amd/moe_decode.py [nt] [--layers 48] [--reps 3] [--us 8,16,24,64]
+(`nt`, the reference's host thread count, has no meaning here and is accepted for argument
+compatibility.)
 """
 import argparse
 import os
@@ -133,6 +135,7 @@ def run(torch, L=48, reps=3, us=(8, 16, 24, 64), verbose=True):
 
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("nt", type=int, nargs="?", default=None, help="ignored (host threads of the reference)")
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--us", default="8,16,24,64")
