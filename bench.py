@@ -9,7 +9,8 @@ timed with HIP events on the launch stream.  The same JSON line carries:
   cpu_baseline  the reference's scalar gemm_ref_i8 (built from its sources into oracle/_ref, or the
                 oracle's restatement when that is absent) on a bounded row sample, 1 core;
   extra         the other measured shapes: skinny 8x4096x4096 GEMM, Q4_0 / Q4_K / Q3_K GEMV at
-                M = 1 and 4, the int4 / int8 tile GEMV of bench/q4_gemv.c, the Qwen3-30B-A3B MoE
+                M = 1 and 4, the int8 path (Q6_K lm_head, Q5_K attn_output, Q8_0 attn_k of
+                Qwen3-30B-A3B, requantized to Q8_0 at load), the int4 / int8 tile GEMV of bench/q4_gemv.c, the Qwen3-30B-A3B MoE
                 decode layer at M = 1 and 4, each beside its scalar CPU time, and the per-token
                 decode weight stream of bench/moe_decode.c (x100-gemm_amd/moe_decode.py).  GEMV and MoE run back-to-back in a captured graph over weight
                 copies totalling more than 256 MB (so the 256 MB Infinity Cache cannot hold them);
@@ -255,6 +256,41 @@ def bench_extra(torch, timer, dev, args):
                 key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
         del packs, raw
 
+    # ---- int8 path: Q6_K / Q5_K / Q8_0 weights requantized to Q8_0 at load (lin_new_i8) ----------
+    # Qwen3-30B-A3B's mixed checkpoint: lm_head (output.weight) Q6_K 151936 x 2048, attn_output
+    # Q5_K 2048 x 4096, attn_k Q8_0 512 x 2048.  The GEMV streams the requantized weight (34 B per
+    # 32 elements, the reference's BREC_I8 records), so that is the algorithmic byte count.
+    for qt, name, N, K, Ms in [(synth.Q6_K, "lm_head_q6_K", 151936, 2048, (1, 4, 8)),
+                               (synth.Q5_K, "attn_output_q5_K", 2048, 4096, (1, 4)),
+                               (synth.Q8_0, "attn_k_q8_0", 512, 2048, (1,))]:
+        W = synth.quant_weight(qt, N, K, seed=120 + qt)
+        raw = torch.from_numpy(W.view(np.uint8).reshape(-1)).to(dev)
+        pb = x100hip.packed_bytes(qt, N, K)
+        copies = int(300e6 // pb) + 1
+        packs = torch.empty((copies, (pb + 255) // 256 * 256), dtype=torch.uint8, device=dev)
+        for i in range(copies):
+            x100hip.pack(qt, N, K, raw.data_ptr(), packs[i].data_ptr(), s)
+        del raw
+        Wq8 = ol.requant_q8_0(qt, W)
+        wbytes = N * (K // 32) * 34
+        for M in Ms:
+            x = synth.normal_f32(9 + M, (M, K))
+            dx = torch.from_numpy(x).to(dev)
+            dy = torch.empty((M, N), dtype=torch.float32, device=dev)
+            fns = [lambda i=i: x100hip.qgemv(qt, M, N, K, packs[i].data_ptr(), dx.data_ptr(), dy.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream) for i in range(copies)]
+            us = timer.graph(fns)
+            lat = timer.single(fns[0])
+            byts = wbytes + M * K * 4 + M * N * 4
+            cpu_us = cpu_time(lambda: ol.qgemv_q8w(Wq8, x), min_s=0.3)
+            key = "%s_gemv_%dx%d_m%d" % (name, N, K, M)
+            extra[key] = {"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                          "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
+                          "cpu_us_1core": cpu_us}
+            log("%s: %.2f us  %.0f GB/s  (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
+                key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
+        del packs, W, Wq8
+
     # ---- integer tile GEMV (bench/q4_gemv.c defaults: N = 4864, K = 896) ----------------------
     N, K = 4864, 896
     r = synth.rand_bytes(77, N * K)
@@ -341,8 +377,9 @@ def bench_extra(torch, timer, dev, args):
 
 def probe_paths(torch, dev, s, reps=3):
     """Launches of every other kernel family at its benchmark shape, for hardware counters:
-    skinny GEMM, the Q4_0 / Q4_K / Q3_K GEMVs at M = 1 and 4, the int4 / int8 tile GEMV at M = 1,
-    and the MoE layer at M = 1 and 4, each `reps` times on distinct weight copies."""
+    skinny GEMM, the Q4_0 / Q4_K / Q3_K GEMVs and the int8-path GEMV of the Q6_K lm_head at M = 1
+    and 4, the int4 / int8 tile GEMV at M = 1, and the MoE layer at M = 1 and 4, each `reps` times
+    on distinct weight copies."""
     M, N, K = 8, 4096, 4096
     A, B = synth.gemm_inputs(M, N, K, seed=2027)
     dA = torch.from_numpy(A).to(dev)
@@ -352,7 +389,8 @@ def probe_paths(torch, dev, s, reps=3):
         x100hip.gemm_dev(M, N, K, dA.data_ptr(), dBs[i].data_ptr(), dC.data_ptr(), s)
     torch.cuda.synchronize()
     del dBs
-    for qt, N, K in [(synth.Q4_0, 4096, 4096), (synth.Q4_K, 6144, 2048), (synth.Q3_K, 6144, 2048)]:
+    for qt, N, K in [(synth.Q4_0, 4096, 4096), (synth.Q4_K, 6144, 2048), (synth.Q3_K, 6144, 2048),
+                     (synth.Q6_K, 151936, 2048)]:
         W = synth.quant_weight(qt, N, K, seed=100 + qt)
         raw = torch.from_numpy(W.view(np.uint8).reshape(-1)).to(dev)
         pb = x100hip.packed_bytes(qt, N, K)

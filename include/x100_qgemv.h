@@ -7,6 +7,12 @@
  * qwen_moe_q3k.c:612-624), each block's dot product is exact integer arithmetic, and the result
  * is scaled in fp32.
  *
+ * Q8_0, Q5_K and Q6_K weights take the reference's int8 path (attn_k, attn_output and lm_head of
+ * the mixed checkpoint, qwen_moe_q3k.c:1747-1768): x100q_pack dequantizes them and re-encodes
+ * every 32 elements as Q8_0 (lin_new_i8, qwen_moe_q3k.c:872-886), and qgemv_hip quantizes x per
+ * 32 with an fp32 scale (pack_A_i8, :420-427) and accumulates fma(dw * scale, isum, acc) per
+ * block (run_i8_m1, :428-510; lin_mm_i8_x, :1075-1081).
+ *
  * Replaces the reference's per-linear matmul `lin_mm(const Lin*, const float *x, float *y, ...)`
  * (qwen_moe.c:101-107, qwen_moe_hp.c:712-718) and the vendor kernel family
  * `gemm_kernel_i8i4* / i8i3k*` (reference/spacemit-backend/ime2_kernels.cpp:127-436): weights are
@@ -27,11 +33,15 @@ extern "C" {
 
 /* ggml type ids (reference bench/gguf_dump.c:12-13). */
 #define X100_Q4_0  2
+#define X100_Q8_0  8
 #define X100_Q3_K 11
 #define X100_Q4_K 12
+#define X100_Q5_K 13
+#define X100_Q6_K 14
 
-/* Bytes of N rows x K columns in GGUF-native blocks (Q4_0 18 B / 32, Q4_K 144 B / 256,
- * Q3_K 110 B / 256); 0 for an unsupported type or K not a multiple of the block size. */
+/* Bytes of N rows x K columns in GGUF-native blocks (Q4_0 18 B / 32, Q8_0 34 B / 32, Q4_K
+ * 144 B / 256, Q3_K 110 B / 256, Q5_K 176 B / 256, Q6_K 210 B / 256); 0 for an unsupported type
+ * or K not a multiple of the block size. */
 size_t x100q_gguf_bytes(int qtype, int N, int K);
 
 /* Bytes of the device layout produced by x100q_pack. */
@@ -39,11 +49,12 @@ size_t x100q_packed_bytes(int qtype, int N, int K);
 
 /* Repack GGUF-native blocks (device pointer w_gguf, row n at n*row_bytes) into the device
  * layout used by qgemv_hip (w_packed, x100q_packed_bytes bytes).  Done once per weight, like the
- * reference's load-time repack (repack.cpp:292, 452, 928). */
+ * reference's load-time repack (repack.cpp:292, 452, 928) and requantization (lin_new_i8,
+ * qwen_moe_q3k.c:872-886, for Q8_0 / Q5_K / Q6_K). */
 int x100q_pack(int qtype, int N, int K, const void *w_gguf, void *w_packed, void *stream);
 
-/* y[M][N] = W . x^T.  1 <= M <= 8; K % 32 == 0 (Q4_0) or K % 256 == 0 (K-quants); x 16-byte
- * aligned.  Asynchronous on stream. */
+/* y[M][N] = W . x^T.  1 <= M <= 8; K % 32 == 0 (Q4_0, Q8_0) or K % 256 == 0 (K-quants);
+ * K <= 16384 for Q4_0 and the int8 path; x 16-byte aligned.  Asynchronous on stream. */
 int qgemv_hip(int qtype, int M, int N, int K, const void *w_packed, const float *x, float *y,
               void *stream);
 

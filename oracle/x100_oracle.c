@@ -151,6 +151,10 @@ typedef struct { uint16_t d; int8_t qs[32]; } orc_q8_0;                        /
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } orc_q4_K; /* 144 B */
 typedef struct { uint8_t hmask[32]; uint8_t qs[64]; uint8_t scales[12]; uint16_t d; } orc_q3_K; /* 110 B */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } orc_q8_K;        /* 292 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } orc_q5_K; /* 176 B */
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } orc_q6_K;  /* 210 B */
+/* pack_A_i8 record (qwen_moe_q3k.c:420-427): fp32 scale, int16 sum, 32 int8, 38 B unpadded. */
+typedef struct __attribute__((packed)) { float s; int16_t asum; int8_t qs[32]; } orc_a_i8;
 
 size_t orc_block_bytes(int qtype)
 {
@@ -160,6 +164,8 @@ size_t orc_block_bytes(int qtype)
     case ORC_Q4_K: return sizeof(orc_q4_K);
     case ORC_Q3_K: return sizeof(orc_q3_K);
     case ORC_Q8_K: return sizeof(orc_q8_K);
+    case ORC_Q5_K: return sizeof(orc_q5_K);
+    case ORC_Q6_K: return sizeof(orc_q6_K);
     default: return 0;
     }
 }
@@ -168,7 +174,7 @@ int orc_block_elems(int qtype)
 {
     switch (qtype) {
     case ORC_Q4_0: case ORC_Q8_0: return 32;
-    case ORC_Q4_K: case ORC_Q3_K: case ORC_Q8_K: return 256;
+    case ORC_Q4_K: case ORC_Q3_K: case ORC_Q8_K: case ORC_Q5_K: case ORC_Q6_K: return 256;
     default: return 0;
     }
 }
@@ -274,6 +280,50 @@ int orc_dequant_row(int qtype, const void *blocks, int K, float *out)
         }
         return 0;
     }
+    case ORC_Q5_K: {                                   /* qwen_moe_q3k.c:540-551 */
+        const orc_q5_K *b = (const orc_q5_K *)blocks;
+        for (int ib = 0; ib < nb; ib++) {
+            float d = orc_f16_to_f32(b[ib].d), dmin = orc_f16_to_f32(b[ib].dmin);
+            /* 64-element chunk c: sub-blocks 2c (low nibbles, qh bit 2c) and 2c+1 (high
+             * nibbles, qh bit 2c+1) of qs[32c .. 32c+31] */
+            for (int c = 0; c < 4; c++) {
+                for (int hi = 0; hi < 2; hi++) {
+                    int sc, m;
+                    scale_min_k4(2 * c + hi, b[ib].scales, &sc, &m);
+                    float d1 = d * (float)sc, m1 = dmin * (float)m;
+                    for (int l = 0; l < 32; l++) {
+                        int q = hi ? (b[ib].qs[32 * c + l] >> 4) : (b[ib].qs[32 * c + l] & 0xf);
+                        if ((b[ib].qh[l] >> (2 * c + hi)) & 1) q += 16;
+                        out[ib * 256 + 64 * c + 32 * hi + l] = d1 * (float)q - m1;
+                    }
+                }
+            }
+        }
+        return 0;
+    }
+    case ORC_Q6_K: {                                   /* qwen_moe.c:168-177 */
+        const orc_q6_K *b = (const orc_q6_K *)blocks;
+        for (int ib = 0; ib < nb; ib++) {
+            float d = orc_f16_to_f32(b[ib].d);
+            for (int h = 0; h < 2; h++) {
+                const uint8_t *ql = b[ib].ql + 64 * h, *qh = b[ib].qh + 32 * h;
+                const int8_t *sc = b[ib].scales + 8 * h;
+                float *o = out + ib * 256 + 128 * h;
+                for (int l = 0; l < 32; l++) {
+                    int is = l / 16;
+                    int q1 = ((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                    int q2 = ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                    int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                    int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                    o[l] = d * (float)sc[is] * (float)q1;
+                    o[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                    o[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                    o[l + 96] = d * (float)sc[is + 6] * (float)q4;
+                }
+            }
+        }
+        return 0;
+    }
     case ORC_Q8_K: {
         const orc_q8_K *b = (const orc_q8_K *)blocks;
         for (int ib = 0; ib < nb; ib++)
@@ -338,6 +388,55 @@ void orc_quantize_q8_K(const float *x, int K, void *out)
             b[ib].bsums[g] = (int16_t)sum;
         }
     }
+}
+
+/* pack_A_i8, qwen_moe_q3k.c:420-427, over K/32 groups (pack_act_i8, :887-889): per 32 elements
+ * amax floored at 1e-6, fp32 scale amax/127, q = rint(x * (1/scale)) clamped to [-128,127], and
+ * the int16 sum of the 32 q values. */
+void orc_quantize_i8(const float *x, int K, void *out)
+{
+    orc_a_i8 *b = (orc_a_i8 *)out;
+    for (int ib = 0; ib < K / 32; ib++) {
+        const float *a = x + (size_t)ib * 32;
+        float amax = 1e-6f;
+        for (int i = 0; i < 32; i++) {
+            float v = fabsf(a[i]);
+            if (v > amax) amax = v;
+        }
+        float scale = amax / 127.0f;
+        float inv = scale ? 1.0f / scale : 0.0f;
+        int sum = 0;
+        orc_a_i8 r;
+        for (int i = 0; i < 32; i++) {
+            int q = (int)rintf(a[i] * inv);
+            if (q > 127) q = 127;
+            if (q < -128) q = -128;
+            r.qs[i] = (int8_t)q;
+            sum += q;
+        }
+        r.s = scale;
+        r.asum = (int16_t)sum;
+        memcpy(&b[ib], &r, sizeof r);
+    }
+}
+
+/* lin_new_i8 (qwen_moe_q3k.c:872-886) without its 32-row panel interleave: every row of a Q8_0,
+ * Q5_K or Q6_K weight is dequantized to fp32 (gguf_dequant_into, qwen_moe_q3k.c:1129-1158) and
+ * re-encoded per 32 elements by quantize_q8_0_native (:409-414), as the loader does for attn_k,
+ * attn_output and lm_head (:1747-1768).  Wq8 receives N rows of K/32 Q8_0 blocks. */
+int orc_requant_q8_0(int qtype, int N, int K, const void *W, void *Wq8)
+{
+    if (qtype != ORC_Q8_0 && qtype != ORC_Q5_K && qtype != ORC_Q6_K) return -1;
+    size_t rb = orc_row_bytes(qtype, K);
+    if (!rb || N < 0) return -1;
+    float *row = (float *)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
+    if (!row) return -1;
+    for (int n = 0; n < N; n++) {
+        orc_dequant_row(qtype, (const uint8_t *)W + (size_t)n * rb, K, row);
+        orc_quantize_q8_0(row, K, (uint8_t *)Wq8 + (size_t)n * (K / 32) * sizeof(orc_q8_0));
+    }
+    free(row);
+    return 0;
 }
 
 /* quantize_q4_0_native, qwen_moe_hp.c:100-109 (fp16 d rounded to nearest even). */
@@ -435,8 +534,57 @@ static float dot_q3_K_q8_K(const orc_q3_K *w, const orc_q8_K *x, int nb)
     return acc;
 }
 
+/* Q8_0 weight x pack_A_i8 activation row dot, run_i8_m1 (qwen_moe_q3k.c:428-510): per K32
+ * group the exact int32 dot, then acc += (dw * scale) * float(dot) as one fused multiply-add
+ * (vfmul.vf then vfmacc.vv), groups in K order. */
+static float dot_q8_0_i8(const orc_q8_0 *w, const orc_a_i8 *x, int nb)
+{
+    float acc = 0.0f;
+    for (int ib = 0; ib < nb; ib++) {
+        orc_a_i8 a;
+        memcpy(&a, &x[ib], sizeof a);
+        int isum = 0;
+        for (int j = 0; j < 32; j++) isum += w[ib].qs[j] * a.qs[j];
+        float v1 = orc_f16_to_f32(w[ib].d) * a.s;
+        acc = fmaf(v1, (float)isum, acc);
+    }
+    return acc;
+}
+
+static int is_i8_path(int qtype) { return qtype == ORC_Q8_0 || qtype == ORC_Q5_K || qtype == ORC_Q6_K; }
+
+/* The per-call part of the int8 path: y[M][N] = Wq8 . x^T for a weight already requantized to
+ * N rows of K/32 Q8_0 blocks (orc_requant_q8_0): pack_act_i8 of each x row, then run_i8_m1 per
+ * row (lin_mm_i8_x, qwen_moe_q3k.c:1075-1081). */
+int orc_qgemv_q8w(int M, int N, int K, const void *Wq8, const float *x, float *y)
+{
+    if (K <= 0 || K % 32 || M < 0 || N < 0) return -1;
+    const int nb = K / 32;
+    orc_a_i8 *xa = (orc_a_i8 *)malloc(sizeof(orc_a_i8) * (size_t)nb * (size_t)(M > 0 ? M : 1));
+    if (!xa) return -1;
+    for (int m = 0; m < M; m++) orc_quantize_i8(x + (size_t)m * K, K, xa + (size_t)m * nb);
+    const orc_q8_0 *wq = (const orc_q8_0 *)Wq8;
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++)
+            y[(size_t)m * N + n] = dot_q8_0_i8(wq + (size_t)n * nb, xa + (size_t)m * nb, nb);
+    free(xa);
+    return 0;
+}
+
 int orc_qgemv_q(int qtype, int M, int N, int K, const void *W, const void *xq, float *y)
 {
+    if (is_i8_path(qtype)) {
+        if (!orc_row_bytes(qtype, K) || K % 32 || M < 0 || N < 0) return -1;
+        const int nb = K / 32;
+        orc_q8_0 *wq = (orc_q8_0 *)malloc(sizeof(orc_q8_0) * (size_t)nb * (size_t)(N > 0 ? N : 1));
+        if (!wq) return -1;
+        orc_requant_q8_0(qtype, N, K, W, wq);
+        for (int m = 0; m < M; m++)
+            for (int n = 0; n < N; n++)
+                y[(size_t)m * N + n] = dot_q8_0_i8(wq + (size_t)n * nb, (const orc_a_i8 *)xq + (size_t)m * nb, nb);
+        free(wq);
+        return 0;
+    }
     size_t rb = orc_row_bytes(qtype, K);
     if (!rb || M < 0 || N < 0) return -1;
     int nb = K / orc_block_elems(qtype);
@@ -463,6 +611,15 @@ int orc_qgemv_q(int qtype, int M, int N, int K, const void *W, const void *xq, f
 
 int orc_qgemv(int qtype, int M, int N, int K, const void *W, const float *x, float *y)
 {
+    if (is_i8_path(qtype)) {
+        if (!orc_row_bytes(qtype, K) || M < 0) return -1;
+        orc_a_i8 *xa = (orc_a_i8 *)malloc(sizeof(orc_a_i8) * (size_t)(K / 32) * (size_t)(M > 0 ? M : 1));
+        if (!xa) return -1;
+        for (int m = 0; m < M; m++) orc_quantize_i8(x + (size_t)m * K, K, xa + (size_t)m * (K / 32));
+        int rc = orc_qgemv_q(qtype, M, N, K, W, xa, y);
+        free(xa);
+        return rc;
+    }
     if (qtype != ORC_Q4_0 && qtype != ORC_Q4_K && qtype != ORC_Q3_K) return -1;
     if (!orc_row_bytes(qtype, K)) return -1;
     int xtype = (qtype == ORC_Q4_0) ? ORC_Q8_0 : ORC_Q8_K;

@@ -42,6 +42,8 @@ extern "C" {
 #define ORC_Q8_0 8
 #define ORC_Q3_K 11
 #define ORC_Q4_K 12
+#define ORC_Q5_K 13
+#define ORC_Q6_K 14
 #define ORC_Q8_K 15
 
 /* fp16 <-> fp32.  f16_to_f32 follows qwen_moe_hp.c:80-86 (exact); f32_to_f16 rounds to nearest
@@ -65,34 +67,49 @@ int orc_pack_w_int4(int N, int K, const int8_t *W, uint8_t *Wq);
 int orc_pack_w_int8(int N, int K, const int8_t *W, int8_t *Wp);
 
 /* ---- block formats ------------------------------------------------------------------------- */
-size_t orc_block_bytes(int qtype);   /* 18, 34, 110, 144, 292 */
+size_t orc_block_bytes(int qtype);   /* 18, 34, 110, 144, 176, 210, 292 */
 int    orc_block_elems(int qtype);   /* 32 or 256 */
 size_t orc_row_bytes(int qtype, int K);
 
 /* Dequantize one row of K elements (GGUF-native blocks) to fp32.
  * Q4_0: qwen_moe.c:164-165.  Q4_K: repack.cpp:222-233 + 950-970.  Q3_K: qwen_moe_q3k.c:557-577.
- * Q8_0: qwen_moe.c:162-163.  Q8_K: value q*d. */
+ * Q8_0: qwen_moe.c:162-163.  Q5_K: qwen_moe_q3k.c:540-551.  Q6_K: qwen_moe.c:168-177.
+ * Q8_K: value q*d. */
 int orc_dequant_row(int qtype, const void *blocks, int K, float *out);
 
 /* Activation quantizers (see header note).  x has K elements; K % 32 (Q8_0) or K % 256 (Q8_K). */
 void orc_quantize_q8_0(const float *x, int K, void *out);
 void orc_quantize_q8_K(const float *x, int K, void *out);
 
+/* int8-path activation quantizer pack_A_i8 (qwen_moe_q3k.c:420-427): per 32 elements a 38-byte
+ * record {f32 scale; i16 sum; i8 qs[32]}, scale = max(amax, 1e-6)/127 kept in fp32, rint. */
+void orc_quantize_i8(const float *x, int K, void *out);
+/* Load-time requantization of a Q8_0 / Q5_K / Q6_K weight to Q8_0 (lin_new_i8,
+ * qwen_moe_q3k.c:872-886): dequantize each row, re-encode per 32 with orc_quantize_q8_0.
+ * Wq8 gets N rows of K/32 Q8_0 blocks.  Returns 0, or -1 for another type / shape. */
+int orc_requant_q8_0(int qtype, int N, int K, const void *W, void *Wq8);
 /* Weight-side Q4_0 encoder (qwen_moe_hp.c:100-109, fp16 rounding per header note). Used by
  * tests to build weights from float matrices. */
 void orc_quantize_q4_0(const float *w, int K, void *out);
 
 /* ---- quantized GEMV -------------------------------------------------------------------------
  * y[M][N] = W[N][K] . x[M][K]^T.  W is GGUF-native blocks, row n at n*row_bytes.  Each x row
- * is quantized on its own (Q8_0 for Q4_0 weights, Q8_K for Q4_K/Q3_K).  Per block the integer
- * dot is exact; the row result is the sequential fp32 sum over blocks of
+ * is quantized on its own (Q8_0 for Q4_0 weights, Q8_K for Q4_K/Q3_K, pack_A_i8 records for
+ * the int8 path).  Per block the integer dot is exact; the row result is the sequential fp32 sum
+ * over blocks of
  *   Q4_0: (dw*dx) * isum                                (ggml vec_dot_q4_0_q8_0 formula)
  *   Q4_K: dx * (d*isum_sc - dmin*isum_m)                (ggml vec_dot_q4_K_q8_K formula)
  *   Q3_K: dx * (d*isum_sc)                              (ggml vec_dot_q3_K_q8_K formula)
+ *   Q8_0 / Q5_K / Q6_K: the weight is first requantized to Q8_0 (orc_requant_q8_0), then per
+ *     K32 group acc = fma(dw*scale, isum, acc)        (run_i8_m1, qwen_moe_q3k.c:428-510)
  * Returns 0, or -1 for an unsupported type / shape. */
 int orc_qgemv(int qtype, int M, int N, int K, const void *W, const float *x, float *y);
 
-/* Same result from already-quantized activations (xq = M rows of Q8 blocks). */
+/* The per-call part of the int8 path: y = Wq8 . x^T for a weight already requantized by
+ * orc_requant_q8_0 (N rows of K/32 Q8_0 blocks); x rows are quantized with orc_quantize_i8. */
+int orc_qgemv_q8w(int M, int N, int K, const void *Wq8, const float *x, float *y);
+/* Same result from already-quantized activations (xq = M rows of Q8_0 / Q8_K blocks or
+ * pack_A_i8 records). */
 int orc_qgemv_q(int qtype, int M, int N, int K, const void *W, const void *xq, float *y);
 
 /* ---- MoE decode layer -----------------------------------------------------------------------

@@ -12,10 +12,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_PATH = os.path.join(ROOT, "oracle", "_ref", "libx100ref.so")
 
-Q4_0, Q8_0, Q3_K, Q4_K, Q8_K = 2, 8, 11, 12, 15
+Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 2, 8, 11, 12, 13, 14, 15
 DT_Q8_0 = np.dtype([("d", "<u2"), ("qs", "i1", (32,))])
 DT_Q8_K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
-assert DT_Q8_0.itemsize == 34 and DT_Q8_K.itemsize == 292
+DT_A_I8 = np.dtype([("s", "<f4"), ("asum", "<i2"), ("qs", "i1", (32,))])   # pack_A_i8 record
+assert DT_Q8_0.itemsize == 34 and DT_Q8_K.itemsize == 292 and DT_A_I8.itemsize == 38
 
 _o = None
 _r = None
@@ -47,6 +48,10 @@ def oracle():
         L.orc_quantize_q8_K.restype = None
         L.orc_quantize_q4_0.argtypes = [p, i, p]
         L.orc_quantize_q4_0.restype = None
+        L.orc_quantize_i8.argtypes = [p, i, p]
+        L.orc_quantize_i8.restype = None
+        L.orc_requant_q8_0.argtypes = [i, i, i, p, p]
+        L.orc_qgemv_q8w.argtypes = [i, i, i, p, p, p]
         L.orc_qgemv.argtypes = [i, i, i, i, p, p, p]
         L.orc_qgemv_q.argtypes = [i, i, i, i, p, p, p]
         L.orc_moe_layer.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p]
@@ -107,6 +112,37 @@ def quantize_q8_K(x):
     out = np.zeros(x.size // 256, dtype=DT_Q8_K)
     oracle().orc_quantize_q8_K(_p(x), x.size, _p(out))
     return out
+
+
+def quantize_i8(x):
+    """pack_A_i8 records (fp32 scale, int16 sum, 32 int8) of one fp32 row."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 32, dtype=DT_A_I8)
+    oracle().orc_quantize_i8(_p(x), x.size, _p(out))
+    return out
+
+
+def requant_q8_0(qtype, W):
+    """Load-time requantization of a Q8_0 / Q5_K / Q6_K weight (N rows of GGUF blocks) to
+    N x K/32 Q8_0 blocks."""
+    Wc = np.ascontiguousarray(W)
+    N = Wc.shape[0]
+    K = Wc.shape[1] * (32 if qtype == Q8_0 else 256)
+    out = np.zeros((N, K // 32), dtype=DT_Q8_0)
+    rc = oracle().orc_requant_q8_0(qtype, N, K, _p(Wc), _p(out))
+    assert rc == 0
+    return out
+
+
+def qgemv_q8w(Wq8, x):
+    """Per-call part of the int8 path for a weight already requantized by requant_q8_0."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    N = Wq8.shape[0]
+    y = np.empty((M, N), dtype=np.float32)
+    rc = oracle().orc_qgemv_q8w(M, N, K, _p(np.ascontiguousarray(Wq8)), _p(x), _p(y))
+    assert rc == 0
+    return y
 
 
 def quantize_q4_0(w, dtype):

@@ -265,6 +265,73 @@ def test_q3_K_known_block():
     assert np.array_equal(got, expect)
 
 
+def np_q6_K_encode(q):
+    """256 values q in [-32, 31] -> (ql[128], qh[64]) written from the Q6_K layout: in half h
+    (elements 128h + p, p < 128) the low 4 bits of q + 32 go to ql[64h + p % 64] (low nibble for
+    p < 64, high nibble otherwise) and its top 2 bits to qh[32h + p % 32] at bit 2 * (p // 32)."""
+    u = np.asarray(q) + 32
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for e in range(256):
+        h, p = e // 128, e % 128
+        ql[64 * h + p % 64] |= (u[e] & 15) << (4 * (p // 64))
+        qh[32 * h + p % 32] |= (u[e] >> 4) << (2 * (p // 32))
+    return ql, qh
+
+
+def test_q6_K_known_block():
+    rng = np.random.default_rng(5)
+    q = rng.integers(-32, 32, 256)
+    sc = rng.integers(-128, 128, 16)
+    blk = np.zeros(1, synth.DT_Q6_K)
+    blk["ql"][0], blk["qh"][0] = np_q6_K_encode(q)
+    blk["scales"][0] = sc
+    blk["d"] = F16_HALF
+    got = ol.dequant_row(ol.Q6_K, blk, 256)
+    expect = np.array([0.5 * sc[e // 16] * q[e] for e in range(256)], np.float32)   # 16-element sub-blocks
+    assert np.array_equal(got, expect)
+
+
+def np_q5_K_encode(q):
+    """256 values q in [0, 31] -> (qh[32], qs[128]) written from the Q5_K layout: element
+    e = 64c + 32hi + l keeps its low 4 bits in qs[32c + l] (low nibble hi = 0, high nibble hi = 1)
+    and its fifth bit in qh[l] at bit e // 32."""
+    q = np.asarray(q)
+    qh = np.zeros(32, np.uint8)
+    qs = np.zeros(128, np.uint8)
+    for e in range(256):
+        c, hi, l = e // 64, (e // 32) % 2, e % 32
+        qs[32 * c + l] |= (q[e] & 15) << (4 * hi)
+        qh[l] |= (q[e] >> 4) << (e // 32)
+    return qh, qs
+
+
+def test_q5_K_known_block():
+    rng = np.random.default_rng(6)
+    sc = rng.integers(0, 64, 8)
+    m = rng.integers(0, 64, 8)
+    q = rng.integers(0, 32, 256)
+    blk = np.zeros(1, synth.DT_Q5_K)
+    blk["d"] = F16_ONE
+    blk["dmin"] = F16_HALF
+    blk["scales"][0] = np_q4_K_encode_scales(sc, m)   # same 6-bit packing as Q4_K
+    blk["qh"][0], blk["qs"][0] = np_q5_K_encode(q)
+    got = ol.dequant_row(ol.Q5_K, blk, 256)
+    expect = np.array([1.0 * sc[e // 32] * q[e] - 0.5 * m[e // 32] for e in range(256)], np.float32)
+    assert np.array_equal(got, expect)
+
+
+def np_k_scale_min(s):
+    """6-bit (sc, m) of the 8 sub-blocks from the 12 scale bytes (Q4_K / Q5_K packing)."""
+    s = s.astype(np.int64)
+    sh = s.shape[:-1] + (8,)
+    sc, mn = np.zeros(sh, np.int64), np.zeros(sh, np.int64)
+    sc[..., :4], mn[..., :4] = s[..., 0:4] & 63, s[..., 4:8] & 63
+    sc[..., 4:] = (s[..., 8:12] & 15) | ((s[..., 0:4] >> 6) << 4)
+    mn[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
+    return sc, mn
+
+
 def np_dequant(qtype, W):
     """Vectorised numpy decoders of the three layouts (float64)."""
     N, nb = W.shape
@@ -297,10 +364,32 @@ def np_dequant(qtype, W):
         q = low - 4 * (1 - hb)
         sub = 8 * h + 2 * j + l // 16
         return (d[..., None] * (s6[..., sub] - 32) * q).reshape(N, nb * 256)
+    if qtype == synth.Q8_0:
+        d = W["d"].view(np.float16).astype(np.float64)
+        return (W["qs"].astype(np.float64) * d[..., None]).reshape(N, nb * 32)
+    e = np.arange(256)
+    if qtype == synth.Q5_K:
+        d = W["d"].view(np.float16).astype(np.float64)
+        dmin = W["dmin"].view(np.float16).astype(np.float64)
+        sc, mn = np_k_scale_min(W["scales"])
+        c, hi, l = e // 64, (e // 32) % 2, e % 32
+        nib = (W["qs"][..., 32 * c + l].astype(np.int64) >> (4 * hi)) & 15
+        hb = (W["qh"][..., l].astype(np.int64) >> (e // 32)) & 1
+        sub = e // 32
+        val = d[..., None] * sc[..., sub] * (nib + 16 * hb) - dmin[..., None] * mn[..., sub]
+        return val.reshape(N, nb * 256)
+    if qtype == synth.Q6_K:
+        d = W["d"].view(np.float16).astype(np.float64)
+        h, p = e // 128, e % 128
+        low = (W["ql"][..., 64 * h + p % 64].astype(np.int64) >> (4 * (p // 64))) & 15
+        top = (W["qh"][..., 32 * h + p % 32].astype(np.int64) >> (2 * (p // 32))) & 3
+        q = (low | (top << 4)) - 32
+        return (d[..., None] * W["scales"][..., e // 16].astype(np.int64) * q).reshape(N, nb * 256)
     raise ValueError(qtype)
 
 
-@pytest.mark.parametrize("qtype,K", [(synth.Q4_0, 512), (synth.Q4_K, 1024), (synth.Q3_K, 1024)])
+@pytest.mark.parametrize("qtype,K", [(synth.Q4_0, 512), (synth.Q4_K, 1024), (synth.Q3_K, 1024),
+                                     (synth.Q8_0, 512), (synth.Q5_K, 1024), (synth.Q6_K, 1024)])
 def test_dequant_random_blocks_vs_numpy(qtype, K):
     W = synth.quant_weight(qtype, 6, K, seed=21)
     ref = np_dequant(qtype, W)
@@ -312,11 +401,25 @@ def test_dequant_random_blocks_vs_numpy(qtype, K):
 # ------------------------------------------------------------------------------------------------
 # quantized GEMV
 # ------------------------------------------------------------------------------------------------
+I8_PATH = (synth.Q8_0, synth.Q5_K, synth.Q6_K)
+
+
+def w_dequant(qtype, W):
+    """float64 values of the weight the GEMV multiplies (after the load-time requantization
+    of the int8 path)."""
+    if qtype in I8_PATH:
+        return np_dequant(synth.Q8_0, ol.requant_q8_0(qtype, W))
+    return np_dequant(qtype, W)
+
+
 def q8_dequant(qtype, x):
     """Quantize x rows with the oracle, return the float64 values actually multiplied."""
     rows = []
     for r in x:
-        if qtype == synth.Q4_0:
+        if qtype in I8_PATH:
+            b = ol.quantize_i8(r)
+            rows.append((b["qs"].astype(np.float64) * b["s"].astype(np.float64)[:, None]).ravel())
+        elif qtype == synth.Q4_0:
             b = ol.quantize_q8_0(r)
             rows.append((b["qs"].astype(np.float64) * b["d"].view(np.float16).astype(np.float64)[:, None]).ravel())
         else:
@@ -327,12 +430,15 @@ def q8_dequant(qtype, x):
 
 @pytest.mark.parametrize("qtype,N,K,M", [(synth.Q4_0, 64, 1024, 1), (synth.Q4_0, 33, 256, 3),
                                          (synth.Q4_K, 48, 2048, 1), (synth.Q4_K, 20, 768, 4),
-                                         (synth.Q3_K, 48, 2048, 1), (synth.Q3_K, 17, 512, 4)])
+                                         (synth.Q3_K, 48, 2048, 1), (synth.Q3_K, 17, 512, 4),
+                                         (synth.Q8_0, 40, 1024, 1), (synth.Q8_0, 9, 96, 3),
+                                         (synth.Q5_K, 24, 1024, 2), (synth.Q6_K, 30, 2048, 1),
+                                         (synth.Q6_K, 11, 512, 4)])
 def test_qgemv_closed_form(qtype, N, K, M):
     W = synth.quant_weight(qtype, N, K, seed=N + K)
     x = synth.normal_f32(M * 7 + K, (M, K))
     y = ol.qgemv(qtype, W, x)
-    ref = q8_dequant(qtype, x) @ np_dequant(qtype, W).T
+    ref = q8_dequant(qtype, x) @ w_dequant(qtype, W).T
     err = np.abs(y - ref)
     assert np.all(err <= 1e-5 * np.abs(ref) + 1e-4 * np.abs(ref).max() * 1e-3 + 1e-6), err.max()
 
@@ -360,7 +466,85 @@ def test_qgemv_special_cases():
     np.testing.assert_allclose(y[0], expect, rtol=1e-6)
 
 
-@pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q4_K, synth.Q3_K])
+@pytest.mark.parametrize("qtype,K", [(synth.Q8_0, 256), (synth.Q5_K, 512), (synth.Q6_K, 512)])
+def test_requant_q8_0_bound_and_idempotence(qtype, K):
+    """Load-time requantization to Q8_0: every 32-group's largest element maps to +-127, every
+    element is within half a step (plus the fp16 rounding of the step) of the fp32 dequantized
+    value, and requantizing the result again changes nothing (the loader's lossless claim for
+    well-formed Q8_0 data, qwen_moe_q3k.c:520-524)."""
+    N = 5
+    W = synth.quant_weight(qtype, N, K, seed=31)
+    R = ol.requant_q8_0(qtype, W)
+    assert R.shape == (N, K // 32)
+    w = np.stack([ol.dequant_row(qtype, W[n], K) for n in range(N)]).reshape(N, K // 32, 32).astype(np.float64)
+    amax = np.maximum(np.abs(w).max(axis=2), 1e-6)
+    step = amax / 127.0
+    d16 = R["d"].view(np.float16).astype(np.float64)
+    assert np.all(np.abs(d16 - step) <= step * 2.0 ** -11)
+    assert np.all(np.abs(R["qs"]).max(axis=2) == 127)
+    err = np.abs(R["qs"].astype(np.float64) * d16[..., None] - w)
+    assert np.all(err <= 0.5 * step[..., None] * (1 + 1e-6) + 127 * np.abs(d16 - step)[..., None])
+    R2 = ol.requant_q8_0(synth.Q8_0, R)
+    assert np.array_equal(R2["d"], R["d"]) and np.array_equal(R2["qs"], R["qs"])
+
+
+def test_requant_q8_0_rescales_narrow_blocks():
+    # a Q8_0 block whose largest |q| is 64 (not 127) is re-encoded with d' = 64*d/127
+    W = np.zeros((1, 1), synth.DT_Q8_0)
+    W["d"] = F16_ONE
+    W["qs"][0, 0] = np.arange(-16, 16)
+    W["qs"][0, 0, 0] = 64
+    R = ol.requant_q8_0(synth.Q8_0, W)
+    assert R["d"][0, 0] == np.float16(np.float32(64.0) / np.float32(127.0)).view(np.uint16)
+    inv = np.float32(1.0) / np.float32(np.float32(64.0) / np.float32(127.0))
+    expect = np.clip(np.rint(W["qs"][0, 0].astype(np.float32) * inv), -128, 127)
+    assert np.array_equal(R["qs"][0, 0], expect.astype(np.int8))
+
+
+def test_quantize_i8_conventions():
+    # fp32 scale = max(amax, 1e-6)/127 (not fp16), ties to even, int16 sum of the 32 values
+    x = np.zeros(96, np.float32)
+    x[:32] = np.linspace(-3, 3, 32, dtype=np.float32)
+    x[0] = 127.0                      # scale 1.0 -> q = rint(x)
+    x[1:5] = [2.5, 3.5, -2.5, -0.5]   # ties -> 2, 4, -2, -0
+    x[32:64] = synth.normal_f32(3, (32,)) * np.float32(1e-3)
+    b = ol.quantize_i8(x)
+    assert b["s"][0] == np.float32(1.0)
+    assert b["qs"][0][:5].tolist() == [127, 2, 4, -2, 0]
+    assert np.array_equal(b["qs"][0].astype(np.float32), np.clip(np.rint(x[:32]), -128, 127))
+    amax = np.float32(np.abs(x[32:64]).max())
+    assert b["s"][1] == amax / np.float32(127.0) and np.abs(b["qs"][1]).max() == 127
+    assert b["s"][2] == np.float32(1e-6) / np.float32(127.0) and not b["qs"][2].any()
+    assert all(int(b["asum"][i]) == int(b["qs"][i].astype(np.int32).sum()) for i in range(3))
+
+
+def test_qgemv_q8w_is_the_per_call_part():
+    # the requantize-at-load + per-call split gives exactly the one-call result
+    W = synth.quant_weight(synth.Q6_K, 12, 512, seed=14)
+    x = synth.normal_f32(15, (3, 512))
+    y1 = ol.qgemv(synth.Q6_K, W, x)
+    y2 = ol.qgemv_q8w(ol.requant_q8_0(synth.Q6_K, W), x)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+def test_qgemv_i8_path_special_cases():
+    x = synth.normal_f32(11, (2, 512))
+    # Q6_K with every scale 0 -> weights 0 -> requantized d rounds to fp16 0 -> y == 0
+    W = synth.quant_weight(synth.Q6_K, 4, 512, seed=7)
+    W["scales"] = 0
+    assert not ol.qgemv(synth.Q6_K, W, x).any()
+    # Q5_K with sc = 0 and m = 1 -> every element -dmin -> y = -dmin * sum over the activation
+    W = synth.quant_weight(synth.Q5_K, 3, 512, seed=8)
+    W["scales"] = np_q4_K_encode_scales(np.zeros(8, int), np.ones(8, int))
+    W["dmin"] = F16_HALF
+    y = ol.qgemv(synth.Q5_K, W, x)
+    xa = np.stack([(lambda b: (b["qs"].astype(np.float64) * b["s"].astype(np.float64)[:, None]).sum())(ol.quantize_i8(r)) for r in x])
+    # requantized weight: every element -0.5 -> d' = fp16(0.5/127), q = -127
+    dq = float(np.float16(np.float32(0.5) / np.float32(127.0))) * -127
+    np.testing.assert_allclose(y, np.repeat((dq * xa)[:, None], 3, axis=1), rtol=1e-5)
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q4_K, synth.Q3_K, synth.Q8_0, synth.Q6_K])
 def test_qgemv_linear_in_scale(qtype):
     K = 512
     W = synth.quant_weight(qtype, 8, K, seed=6)

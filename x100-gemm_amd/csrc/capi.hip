@@ -204,17 +204,34 @@ const char *x100_hip_strerror(int code)
 // ---------------------------------------------------------------------------------------------
 // quantized GEMV
 // ---------------------------------------------------------------------------------------------
+// Elements and bytes per GGUF block (bench/gguf_dump.c:12-13 type ids; block sizes of ggml).
 static int qk_of(int qtype)
 {
-    return qtype == X100_Q4_0 ? 32 : (qtype == X100_Q4_K || qtype == X100_Q3_K) ? 256 : 0;
+    switch (qtype) {
+    case X100_Q4_0: case X100_Q8_0: return 32;
+    case X100_Q3_K: case X100_Q4_K: case X100_Q5_K: case X100_Q6_K: return 256;
+    }
+    return 0;
+}
+
+static size_t block_bytes_of(int qtype)
+{
+    switch (qtype) {
+    case X100_Q4_0: return 18;
+    case X100_Q8_0: return 34;
+    case X100_Q3_K: return 110;
+    case X100_Q4_K: return 144;
+    case X100_Q5_K: return 176;
+    case X100_Q6_K: return 210;
+    }
+    return 0;
 }
 
 size_t x100q_gguf_bytes(int qtype, int N, int K)
 {
     const int qk = qk_of(qtype);
     if (!qk || N < 0 || K <= 0 || K % qk) return 0;
-    const size_t bb = qtype == X100_Q4_0 ? 18 : qtype == X100_Q4_K ? 144 : 110;
-    return (size_t)N * (K / qk) * bb;
+    return (size_t)N * (K / qk) * block_bytes_of(qtype);
 }
 
 size_t x100q_packed_bytes(int qtype, int N, int K)
@@ -225,7 +242,7 @@ size_t x100q_packed_bytes(int qtype, int N, int K)
 
 int x100q_pack(int qtype, int N, int K, const void *w_gguf, void *w_packed, void *stream)
 {
-    if (!x100q_gguf_bytes(qtype, N, K) || !w_gguf || !w_packed) return X100_EINVAL;
+    if (!x100q_gguf_bytes(qtype, N, K) || !w_gguf || !w_packed || ((uintptr_t)w_packed & 255)) return X100_EINVAL;
     int rc = check_device();
     if (rc) return rc;
     hipError_t e = x100_q_pack_launch(qtype, N, K, w_gguf, w_packed, (hipStream_t)stream);

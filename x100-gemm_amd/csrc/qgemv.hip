@@ -1,9 +1,11 @@
 // Block-quantized dequant-GEMV for gfx950:  y[M][N] = W[N][K] . x[M][K]^T,  M <= 8.
 //
-// Weights are block-quantized (Q4_0, Q4_K, Q3_K); each x row is quantized inside the kernel
-// (Q8_0 for Q4_0, Q8_K for the K-quants) with the same fp32 operations as the scalar path
-// (quantize_q8_0_native, qwen_moe_hp.c:408-414; pack_A_q3k, qwen_moe_q3k.c:612-624), then every
-// block's dot product is done in exact integer arithmetic with v_dot4 and scaled in fp32.
+// Weights are block-quantized (Q4_0, Q4_K, Q3_K, and Q8_0 / Q5_K / Q6_K through the int8 path);
+// each x row is quantized inside the kernel (Q8_0 for Q4_0, Q8_K for the K-quants, Q8_0 with an
+// fp32 scale for the int8 path) with the same fp32 operations as the scalar path
+// (quantize_q8_0_native, qwen_moe_hp.c:408-414; pack_A_q3k, qwen_moe_q3k.c:612-624; pack_A_i8,
+// qwen_moe_q3k.c:420-427), then every block's dot product is done in exact integer arithmetic
+// with v_dot4 and scaled in fp32.
 //
 // At M <= 8 the work is bandwidth bound: every lane issues all of its 16-byte weight loads before
 // it quantizes x, so a block's whole weight slice is in flight at once; no MFMA.
@@ -12,7 +14,10 @@
 //   Q4_K  GGUF-native 144-byte blocks (16-byte aligned fields, consumed as is).
 //   Q4_0  split into d[N*K/32] (fp16) and qs[N*K/32][16], so nibble rows are 16-byte aligned.
 //   Q3_K  split into hq[N*K/256][96] (hmask 32 + qs 64), sc[N*K/256][12], d[N*K/256] (fp16).
-// Same byte count as the GGUF blocks (plus alignment padding between the arrays).
+//   Q8_0, Q5_K, Q6_K  requantized to Q8_0 (the reference loader's lin_new_i8) and split into
+//         d[N*K/32] (fp16) and qs[N*K/32][32].
+// Q4_0 / Q4_K / Q3_K keep the GGUF blocks' byte count (plus alignment padding between the
+// arrays); the int8 path stores 34 bytes per 32 elements.
 //
 // The K-quant kernels reduce each row in the same order as the scalar oracle (sequential over
 // super-blocks, no fused multiply-add), so their fp32 outputs are bit-identical to it; Q4_0 sums
@@ -352,6 +357,148 @@ __global__ __launch_bounds__(NT) void k_q3_K(int M, int N, int K, int R, uint32_
 }
 
 // ------------------------------------------------------------------------------------------------
+// Q8_0 x int8 activation: the int8 path of Q8_0 / Q5_K / Q6_K weights
+// ------------------------------------------------------------------------------------------------
+// The weight was requantized to Q8_0 at load (k_requant_q8_0): d[N*nb] fp16 and qs[N*nb][32].
+// x is quantized per 32 with an fp32 scale (pack_A_i8) and every 32-block contributes
+// acc = fma(dw * scale, isum, acc), as run_i8_m1 does (qwen_moe_q3k.c:428-510).
+//
+// A row is owned by LPR = 16, 32 or 64 lanes (a wave holds 64/LPR row slots): lane j of a slot
+// takes the 32-blocks j, j+LPR, ... (BPL per row), and the slot's sum is an in-row DPP prefix
+// sum (plus row broadcasts for LPR > 16) that ends in the slot's last lane.  A row group is NT/64
+// waves x RPW x 64/LPR rows.  Each block quantizes x once into LDS and then walks the row groups
+// blockIdx.x, +gridDim.x, ...: the loads of the next group are issued before the current group's
+// dot products, so a group's weights are always in flight while the previous one is reduced.
+// Weight loads go through buffer resources: a row past N or a block past nb reads 0 without
+// touching memory.  A row's arithmetic depends only on LPR and BPL (chosen from K), so a batch
+// of M rows gives each row exactly what a one-row call gives.
+template <int RPW, int BPL>
+struct I8Group {
+    v4i q[RPW][BPL][2];
+    uint32_t d[RPW][BPL];
+};
+
+template <int LPR, int RPW, int NT>
+X100_DEV int i8_row(int g, int w, int r, int lane)
+{
+    constexpr int SL = 64 / LPR;
+    return g * ((NT / 64) * RPW * SL) + (w * RPW + r) * SL + lane / LPR;
+}
+
+template <int LPR, int RPW, int BPL, int NT>
+X100_DEV void i8_load_group(I8Group<RPW, BPL> &t, int g, int N, int nb, rsrc_t qr, rsrc_t dr, uint32_t end)
+{
+    const int lane = threadIdx.x & 63, w = wave_id();
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+#pragma unroll
+        for (int c = 0; c < BPL; c++) {
+            const int row = i8_row<LPR, RPW, NT>(g, w, r, lane), b = (lane % LPR) + LPR * c;
+            const uint32_t blk = (row < N && b < nb) ? (uint32_t)row * (uint32_t)nb + (uint32_t)b : end;
+            t.q[r][c][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(blk * 32u), 0, 0));
+            t.q[r][c][1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(blk * 32u + 16u), 0, 0));
+            t.d[r][c] = __builtin_amdgcn_raw_buffer_load_b16(dr, (int)(blk * 2u), 0, 0);
+        }
+}
+
+// Sum over the LPR lanes of each row slot into the slot's last lane (inclusive prefix sum within
+// rows of 16, then row broadcasts 15 and 31, the steps of wave_sum_uf).
+template <int LPR>
+X100_DEV float slot_sum(float v)
+{
+    v += dpp_f<0x111>(0.0f, v);
+    v += dpp_f<0x112>(0.0f, v);
+    v += dpp_f<0x114>(0.0f, v);
+    v += dpp_f<0x118>(0.0f, v);
+    if constexpr (LPR >= 32) v += dpp_f<0x142, 0xa>(0.0f, v);
+    if constexpr (LPR >= 64) v += dpp_f<0x143, 0xc>(0.0f, v);
+    return v;
+}
+
+template <int MR, int LPR, int RPW, int BPL, int XPT, int NT>
+__global__ __launch_bounds__(NT) void k_q8_0(int M, int N, int K, int ngroups, const uint16_t *__restrict__ wd,
+                                              const int8_t *__restrict__ wq, const float *__restrict__ x,
+                                              float *__restrict__ y)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nb = K / 32;
+    const int nb1 = MR * nb + 1;                 // + the quantizer's spare block
+    int8_t *xlo = (int8_t *)smem;
+    int8_t *xhi = xlo + nb1 * 16;
+    float *xd = (float *)(xhi + nb1 * 16);
+    int *xs = (int *)(xd + nb1);
+
+    const int lane = threadIdx.x & 63, w = wave_id(), j = lane % LPR;
+    const uint32_t nblk = (uint32_t)N * (uint32_t)nb;   // < 2^27 (checked by the launcher)
+    const rsrc_t qr = buf_rsrc(wq, nblk * 32u);
+    const rsrc_t dr = buf_rsrc(wd, nblk * 2u);
+
+    const int total4 = M * K / 4;
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
+    float4 xv[XPT];
+    x_load<XPT, NT>(xr, 0, xv);
+
+    int g = blockIdx.x;
+    I8Group<RPW, BPL> cur;
+    i8_load_group<LPR, RPW, BPL, NT>(cur, g, N, nb, qr, dr, nblk);
+
+    __builtin_amdgcn_sched_barrier(0);   // keep the first group's loads ahead of the quantizer
+    q8_0_from_regs<XPT, NT, false>(xv, 0, total4, K, xlo, xhi, xd, xs);
+    for (int c0 = NT * XPT; c0 < total4; c0 += NT * XPT) {
+        x_load<XPT, NT>(xr, c0, xv);
+        q8_0_from_regs<XPT, NT, false>(xv, c0, total4, K, xlo, xhi, xd, xs);
+    }
+    __syncthreads();
+
+    for (; g < ngroups; g += gridDim.x) {
+        I8Group<RPW, BPL> nxt;
+        i8_load_group<LPR, RPW, BPL, NT>(nxt, g + (int)gridDim.x, N, nb, qr, dr, nblk);
+
+        float acc[RPW][MR];
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int m = 0; m < MR; m++) acc[r][m] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < BPL; c++) {
+            // A lane past the last block holds zero weights and a zero scale (its loads were out of
+            // range), so fma(0, 0, acc) leaves its sum as it is: no branch, the LDS reads of all
+            // blocks can be issued together.  Rows m >= M compute on unused LDS and are not stored.
+            const int b = min(j + LPR * c, nb - 1);
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const v4i xl = *(const v4i *)(xlo + (m * nb + b) * 16);
+                const v4i xh = *(const v4i *)(xhi + (m * nb + b) * 16);
+                const float sx = xd[m * nb + b];
+#pragma unroll
+                for (int r = 0; r < RPW; r++) {
+                    int s = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        s = dot4(cur.q[r][c][0][t], xl[t], s);
+                        s = dot4(cur.q[r][c][1][t], xh[t], s);
+                    }
+                    const float v1 = h2f((uint16_t)cur.d[r][c]) * sx;
+                    acc[r][m] = __builtin_fmaf(v1, (float)s, acc[r][m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            const int row = i8_row<LPR, RPW, NT>(g, w, r, lane);
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                if (m < M) {
+                    const float v = slot_sum<LPR>(acc[r][m]);
+                    if (j == LPR - 1 && row < N) y[(size_t)m * N + row] = v;
+                }
+            }
+        }
+        cur = nxt;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Weight packing (GGUF-native blocks -> device layout)
 // ------------------------------------------------------------------------------------------------
 __global__ void k_pack_q4_0(size_t nblk, const uint8_t *__restrict__ src, uint16_t *__restrict__ d,
@@ -377,6 +524,81 @@ __global__ void k_pack_q3_K(size_t nblk, const uint8_t *__restrict__ src, uint8_
     d[b] = (uint16_t)(s[108] | (s[109] << 8));
 }
 
+// Load-time requantization to Q8_0 (lin_new_i8, qwen_moe_q3k.c:872-886): thread g dequantizes
+// the 32-element group g from its GGUF block in fp32 with the operation order of
+// gguf_dequant_into (qwen_moe_q3k.c:1129-1158; Q6_K qwen_moe.c:168-177) and re-encodes it with
+// quantize_q8_0_native's rounding (amax floor 1e-6, d = amax/127, q = rint(w * (1/d)), d stored
+// as fp16 rounded to nearest even).
+template <int QT>
+__global__ void k_requant_q8_0(size_t ngrp, const uint8_t *__restrict__ src, uint16_t *__restrict__ dq,
+                               int8_t *__restrict__ qs)
+{
+    const size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= ngrp) return;
+    float v[32];
+    if constexpr (QT == X100_Q8_0) {
+        const uint8_t *b = src + g * 34;
+        const float d = h2f((uint16_t)(b[0] | (b[1] << 8)));
+#pragma unroll
+        for (int j = 0; j < 32; j++) v[j] = (float)(int8_t)b[2 + j] * d;
+    } else if constexpr (QT == X100_Q6_K) {
+        // group gi of the super-block: half h = gi/4, quarter gg = gi%4 of the half.  Element l
+        // takes the low (gg < 2) or high nibble of ql[64h + 32(gg%2) + l], bits 2gg, 2gg+1 of
+        // qh[32h + l] and the int8 scale 8h + 2gg + l/16.
+        const size_t sb = g >> 3;
+        const int gi = (int)(g & 7), h = gi >> 2, gg = gi & 3;
+        const uint8_t *b = src + sb * 210;
+        const uint8_t *ql = b + 64 * h + 32 * (gg & 1), *qh = b + 128 + 32 * h;
+        const int8_t *sc = (const int8_t *)(b + 192) + 8 * h + 2 * gg;
+        const float d = h2f((uint16_t)(b[208] | (b[209] << 8)));
+        const int nsh = 4 * (gg >> 1), hsh = 2 * gg;
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const int q = (((ql[l] >> nsh) & 15) | (((qh[l] >> hsh) & 3) << 4)) - 32;
+            v[l] = d * (float)sc[l >> 4] * (float)q;
+        }
+    } else {
+        static_assert(QT == X100_Q5_K, "requant source type");
+        // group gi = 2c + hi: low (hi = 0) or high nibbles of qs[32c + l], fifth bit = bit gi of
+        // qh[l], (scale, min) pair gi.
+        const size_t sb = g >> 3;
+        const int gi = (int)(g & 7), c = gi >> 1, hi = gi & 1;
+        const uint8_t *b = src + sb * 176;
+        const float d = h2f((uint16_t)(b[0] | (b[1] << 8))), dmin = h2f((uint16_t)(b[2] | (b[3] << 8)));
+        uint32_t s3[3];
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            s3[i] = (uint32_t)b[4 + 4 * i] | ((uint32_t)b[5 + 4 * i] << 8) | ((uint32_t)b[6 + 4 * i] << 16) |
+                    ((uint32_t)b[7 + 4 * i] << 24);
+        int sc, m;
+        scale_min_k4(gi, s3[0], s3[1], s3[2], sc, m);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        const uint8_t *ql = b + 48 + 32 * c, *qh = b + 16;
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const int q = ((ql[l] >> (4 * hi)) & 15) + (((qh[l] >> gi) & 1) << 4);
+            v[l] = d1 * (float)q - m1;
+        }
+    }
+    float amax = 1e-6f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / 127.0f;
+    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    dq[g] = f2h(d);
+    uint32_t pk[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) wv |= (uint32_t)(clamp_i8((int)rintf(v[4 * j + i] * inv)) & 0xff) << (8 * i);
+        pk[j] = wv;
+    }
+    uint4 *o = (uint4 *)(qs + g * 32);
+    o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+}
+
 constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 }  // namespace
@@ -392,6 +614,10 @@ size_t x100_q_packed_bytes(int qtype, int N, int K)
         return align256(nblk * 2) + nblk * 16;
     }
     case X100_Q4_K: return (size_t)N * (K / 256) * 144;
+    case X100_Q8_0: case X100_Q5_K: case X100_Q6_K: {
+        const size_t ngrp = (size_t)N * (K / 32);
+        return align256(ngrp * 2) + ngrp * 32;
+    }
     case X100_Q3_K: {
         const size_t nblk = (size_t)N * (K / 256);
         return nblk * 96 + nblk * 12 + nblk * 2;
@@ -413,6 +639,17 @@ hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *ds
     }
     case X100_Q4_K:
         return hipMemcpyAsync(dst, src, (size_t)N * (K / 256) * 144, hipMemcpyDeviceToDevice, s);
+    case X100_Q8_0: case X100_Q5_K: case X100_Q6_K: {
+        const size_t ngrp = (size_t)N * (K / 32);
+        uint16_t *d = (uint16_t *)dst;
+        int8_t *qs = (int8_t *)dst + align256(ngrp * 2);
+        const dim3 grid((unsigned)((ngrp + 255) / 256)), blk(256);
+        const uint8_t *sp = (const uint8_t *)src;
+        if (qtype == X100_Q8_0) hipLaunchKernelGGL(k_requant_q8_0<X100_Q8_0>, grid, blk, 0, s, ngrp, sp, d, qs);
+        else if (qtype == X100_Q5_K) hipLaunchKernelGGL(k_requant_q8_0<X100_Q5_K>, grid, blk, 0, s, ngrp, sp, d, qs);
+        else hipLaunchKernelGGL(k_requant_q8_0<X100_Q6_K>, grid, blk, 0, s, ngrp, sp, d, qs);
+        return hipGetLastError();
+    }
     case X100_Q3_K: {
         const size_t nblk = (size_t)N * (K / 256);
         uint8_t *hq = (uint8_t *)dst;
@@ -473,6 +710,73 @@ hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float
     if (need <= 4) return launch_q4_0_x<MR, 4>(M, N, K, w, x, y, s);
     if (need <= 8) return launch_q4_0_x<MR, 8>(M, N, K, w, x, y, s);
     return launch_q4_0_x<MR, 16>(M, N, K, w, x, y, s);
+}
+
+// Blocks of kernel k that are resident on the whole device at once with lds bytes of dynamic LDS
+// (the runtime's occupancy for the kernel times the CU count): the grid of a persistent launch.
+// Cached per kernel for the last (device, lds) pair of the calling thread.
+template <typename Kern>
+int resident_blocks(Kern k, int nt, size_t lds)
+{
+    static thread_local int c_dev = -1, c_blocks = 0;
+    static thread_local size_t c_lds = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    if (dev != c_dev || lds != c_lds) {
+        int occ = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, nt, lds) != hipSuccess || occ < 1) occ = 1;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        c_dev = dev;
+        c_lds = lds;
+        c_blocks = occ * cus;
+    }
+    return c_blocks;
+}
+
+// int8 path: 256 threads.  Lanes per row LPR and blocks per lane BPL from nb = K/32 (a slot covers
+// the row with at most 4 blocks per lane up to K = 8192); RPW row slots per wave so that a
+// group's loads (RPW * BPL blocks of 34 B per lane, twice for the prefetch) stay within about 64
+// VGPRs.  The grid is the number of blocks resident on the device at once, or one per row group
+// if there are fewer groups.
+template <int MR, int LPR, int BPL, int XPT>
+hipError_t launch_q8_0_b(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
+{
+    constexpr int NT = 256, RPW = BPL >= 4 ? 1 : 4 / BPL;
+    const int nb = K / 32;
+    const size_t ngrp = (size_t)N * nb;
+    const uint16_t *wd = (const uint16_t *)w;
+    const int8_t *wq = (const int8_t *)w + align256(ngrp * 2);
+    const size_t lds = ((size_t)MR * nb + 1) * 40;
+    const int rows = (NT / 64) * RPW * (64 / LPR);
+    const int ngroups = (N + rows - 1) / rows;
+    const int res = resident_blocks(k_q8_0<MR, LPR, RPW, BPL, XPT, NT>, NT, lds);
+    const int grid = ngroups < res ? ngroups : res;
+    hipLaunchKernelGGL((k_q8_0<MR, LPR, RPW, BPL, XPT, NT>), dim3(grid), dim3(NT), lds, s, M, N, K, ngroups, wd,
+                       wq, x, y);
+    return hipGetLastError();
+}
+
+template <int MR, int LPR, int BPL>
+hipError_t launch_q8_0_x(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
+{
+    const int need = (M * K + 4 * 256 - 1) / (4 * 256);
+    if (need <= 2) return launch_q8_0_b<MR, LPR, BPL, 2>(M, N, K, w, x, y, s);
+    if (need <= 4) return launch_q8_0_b<MR, LPR, BPL, 4>(M, N, K, w, x, y, s);
+    if (need <= 8) return launch_q8_0_b<MR, LPR, BPL, 8>(M, N, K, w, x, y, s);
+    return launch_q8_0_b<MR, LPR, BPL, 16>(M, N, K, w, x, y, s);
+}
+
+template <int MR>
+hipError_t launch_q8_0(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
+{
+    const int nb = K / 32;
+    if (nb <= 16) return launch_q8_0_x<MR, 16, 1>(M, N, K, w, x, y, s);
+    if (nb <= 32) return launch_q8_0_x<MR, 16, 2>(M, N, K, w, x, y, s);
+    if (nb <= 64) return launch_q8_0_x<MR, 16, 4>(M, N, K, w, x, y, s);
+    if (nb <= 128) return launch_q8_0_x<MR, 32, 4>(M, N, K, w, x, y, s);
+    if (nb <= 256) return launch_q8_0_x<MR, 64, 4>(M, N, K, w, x, y, s);
+    return launch_q8_0_x<MR, 64, 8>(M, N, K, w, x, y, s);
 }
 
 // Threads per block of the K-quant kernels (one block per CU).  With several token rows the dot
@@ -559,6 +863,14 @@ hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, cons
         if (M == 1) return launch_q4_0<1>(M, N, K, w, x, y, s);
         if (M <= 4) return launch_q4_0<4>(M, N, K, w, x, y, s);
         return launch_q4_0<8>(M, N, K, w, x, y, s);
+    }
+    if (qtype == X100_Q8_0 || qtype == X100_Q5_K || qtype == X100_Q6_K) {
+        if (K % (qtype == X100_Q8_0 ? 32 : 256) || K / 32 > 512) return hipErrorInvalidValue;
+        if (((size_t)(M <= 1 ? 1 : (M <= 4 ? 4 : 8)) * (K / 32) + 1) * 40 > 160 * 1024) return hipErrorInvalidValue;
+        if ((size_t)N * (K / 32) >= ((size_t)1 << 27)) return hipErrorInvalidValue;   // 32-bit buffer offsets
+        if (M == 1) return launch_q8_0<1>(M, N, K, w, x, y, s);
+        if (M <= 4) return launch_q8_0<4>(M, N, K, w, x, y, s);
+        return launch_q8_0<8>(M, N, K, w, x, y, s);
     }
     if (qtype == X100_Q4_K || qtype == X100_Q3_K) {
         if (K % 256) return hipErrorInvalidValue;

@@ -16,7 +16,7 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 #define X100_DEV __device__ __forceinline__
 
 // GGUF type ids (bench/gguf_dump.c:12-13 of the reference).
-enum { X100_Q4_0 = 2, X100_Q3_K = 11, X100_Q4_K = 12 };
+enum { X100_Q4_0 = 2, X100_Q8_0 = 8, X100_Q3_K = 11, X100_Q4_K = 12, X100_Q5_K = 13, X100_Q6_K = 14 };
 
 // fp16 bits -> fp32 (exact).
 X100_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -214,7 +214,9 @@ X100_DEV void x_load(rsrc_t xr, int c0, float4 (&v)[XPT])
 // Branch-free stores (so the unrolled iterations can be interleaved by the scheduler): blocks past
 // the end go to the spare slot (index M*nb / M*nsb) that the LDS layout provides, and values that
 // several lanes hold (d, sum) are stored by all of them.
-template <int XPT, int NT = 256>
+// F16D: the block scale is rounded to fp16 (quantize_q8_0_native, qwen_moe_hp.c:408-414) or kept
+// in fp32 (pack_A_i8, qwen_moe_q3k.c:420-427); the q values are the same either way.
+template <int XPT, int NT = 256, bool F16D = true>
 X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, int8_t *xlo,
                              int8_t *xhi, float *xd, int *xs)
 {
@@ -236,7 +238,7 @@ X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, 
                                 ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
         int8_t *dst = pos < 16 ? xlo + b * 16 + pos : xhi + b * 16 + (pos - 16);
         *(uint32_t *)dst = packed;
-        xd[b] = h2f(f2h(d));   // the 8 lanes of a block hold the same d and sum
+        xd[b] = F16D ? h2f(f2h(d)) : d;   // the 8 lanes of a block hold the same d and sum
         xs[b] = s;
     }
 }

@@ -7,7 +7,8 @@ torch.cuda.current_stream().cuda_stream).
 
 Entry points and what they replace in the reference:
   gemm_ime_i8 / gemm_hip_i8 / gemm_hip_i8_dev   include/x100_gemm.h:60-61 (C += A*B, int8->int32)
-  qgemv_hip (+ x100q_pack)                      lin_mm of qwen_moe.c:101-107 on Q4_0/Q4_K/Q3_K
+  qgemv_hip (+ x100q_pack)                      lin_mm of qwen_moe.c:101-107 on Q4_0/Q4_K/Q3_K;
+                                                lin_mm_i8_x of qwen_moe_q3k.c:1075 on Q8_0/Q5_K/Q6_K
   moe_layer_hip                                 the MoE block of qwen_moe.c:294-311
   gemv_int4_hip / gemv_int8_hip (+ packers)     gemv_nb_int4 / gemv_nb_int8 of bench/q4_gemv.c:67-99
 """
