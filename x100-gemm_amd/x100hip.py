@@ -20,7 +20,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libx100hip.so")
 
-Q4_0, Q3_K, Q4_K = 2, 11, 12
+Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K = 2, 8, 11, 12, 13, 14
 
 X100_OK, X100_EINVAL, X100_ENODEV, X100_EHIP, X100_ENOMEM = 0, -1, -2, -3, -4
 
