@@ -11,6 +11,7 @@
 #pragma GCC visibility push(default)
 #include "x100_gemm.h"
 #include "x100_gemv_tile.h"
+#include "x100_gguf.h"
 #include "x100_moe.h"
 #include "x100_qgemv.h"
 #pragma GCC visibility pop
@@ -197,6 +198,9 @@ const char *x100_hip_strerror(int code)
                                                       : "no gfx950 device";
     case X100_ENOMEM: return "device allocation failed";
     case X100_EHIP: return hipGetErrorString(g_last_hip);
+    case X100_EIO: return "file could not be opened or mapped";
+    case X100_EFORMAT: return "not a GGUF v2/v3 file, or a field lies outside the file";
+    case X100_ENOTFOUND: return "no tensor or key of that name (or of that type)";
     }
     return "unknown error";
 }

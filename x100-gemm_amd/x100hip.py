@@ -23,14 +23,21 @@ LIB_PATH = os.path.join(HERE, "lib", "libx100hip.so")
 Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K = 2, 8, 11, 12, 13, 14
 
 X100_OK, X100_EINVAL, X100_ENODEV, X100_EHIP, X100_ENOMEM = 0, -1, -2, -3, -4
+X100_EIO, X100_EFORMAT, X100_ENOTFOUND = -5, -6, -7
 
-# Every symbol declared in include/x100_gemm.h, x100_gemv_tile.h, x100_qgemv.h, x100_moe.h.
+# Every symbol declared in include/x100_gemm.h, x100_gemv_tile.h, x100_qgemv.h, x100_moe.h,
+# x100_gguf.h.
 EXPORTS = (
     "gemm_ime_i8", "gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant",
     "x100_hip_detect", "x100_hip_caps_print", "x100_hip_strerror",
     "x100_tile_bytes", "x100_pack_w_int4", "x100_pack_w_int8", "gemv_int4_hip", "gemv_int8_hip",
     "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip",
     "moe_layer_hip",
+    "x100_gguf_open", "x100_gguf_close", "x100_gguf_version", "x100_gguf_n_tensors", "x100_gguf_n_kv",
+    "x100_gguf_alignment", "x100_gguf_data_offset", "x100_gguf_tensor_at", "x100_gguf_find",
+    "x100_gguf_kv_at", "x100_gguf_get_int", "x100_gguf_get_float", "x100_gguf_get_str",
+    "x100_gguf_get_arr_str", "x100_gguf_qwen3moe_params", "x100_gguf_type_name", "x100_gguf_block_bytes",
+    "x100_gguf_block_elems", "x100_gguf_upload", "x100_gguf_pack_rows",
 )
 
 GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC, GEMM_TILE256_W4 = 0, 1, 2, 3, 4, 5
@@ -86,6 +93,36 @@ def lib():
     L.x100_pack_w_int8.argtypes = [i, i, p, p]
     L.gemv_int4_hip.argtypes = [i, i, i, p, p, p, p]
     L.gemv_int8_hip.argtypes = [i, i, i, p, p, p, p]
+    # GGUF reader (x100_gguf.h); the structures are declared in gguf.py
+    u32, u64, i64, cp = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int64, ctypes.c_char_p
+    L.x100_gguf_open.argtypes = [cp, ctypes.POINTER(p)]
+    L.x100_gguf_close.argtypes = [p]
+    L.x100_gguf_close.restype = None
+    for name, rt in (("x100_gguf_version", u32), ("x100_gguf_n_tensors", i64), ("x100_gguf_n_kv", i64),
+                     ("x100_gguf_alignment", u32), ("x100_gguf_data_offset", u64)):
+        getattr(L, name).argtypes = [p]
+        getattr(L, name).restype = rt
+    L.x100_gguf_tensor_at.argtypes = [p, i64, p]
+    L.x100_gguf_find.argtypes = [p, cp, p]
+    L.x100_gguf_kv_at.argtypes = [p, i64, ctypes.POINTER(cp), ctypes.POINTER(u32), ctypes.POINTER(u32),
+                                  ctypes.POINTER(u64)]
+    L.x100_gguf_get_int.argtypes = [p, cp, ctypes.POINTER(i64)]
+    L.x100_gguf_get_float.argtypes = [p, cp, ctypes.POINTER(ctypes.c_double)]
+    L.x100_gguf_get_str.argtypes = [p, cp, ctypes.POINTER(p), ctypes.POINTER(u64)]
+    L.x100_gguf_get_arr_str.argtypes = [p, cp, u64, ctypes.POINTER(p), ctypes.POINTER(u64)]
+    L.x100_gguf_qwen3moe_params.argtypes = [p, p]
+    L.x100_gguf_type_name.argtypes = [u32]
+    L.x100_gguf_type_name.restype = cp
+    L.x100_gguf_block_bytes.argtypes = [u32]
+    L.x100_gguf_block_bytes.restype = sz
+    L.x100_gguf_block_elems.argtypes = [u32]
+    L.x100_gguf_upload.argtypes = [p, p, u64, u64, p, p]
+    L.x100_gguf_pack_rows.argtypes = [p, p, u64, u64, p, p]
+    for name in ("x100_gguf_open", "x100_gguf_tensor_at", "x100_gguf_find", "x100_gguf_kv_at",
+                 "x100_gguf_get_int", "x100_gguf_get_float", "x100_gguf_get_str", "x100_gguf_get_arr_str",
+                 "x100_gguf_qwen3moe_params", "x100_gguf_block_elems", "x100_gguf_upload",
+                 "x100_gguf_pack_rows"):
+        getattr(L, name).restype = i
     for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant", "x100_hip_detect",
                  "x100q_pack", "qgemv_hip", "moe_layer_hip", "x100_pack_w_int4", "x100_pack_w_int8",
                  "gemv_int4_hip", "gemv_int8_hip"):
