@@ -6,6 +6,7 @@
  */
 #include "x100_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -471,10 +472,38 @@ void orc_quantize_q4_0(const float *w, int K, void *out)
  * Quantized GEMV (integer dot per block, sequential fp32 combine per row)
  * ------------------------------------------------------------------------------------------- */
 
-/* Q4_0 x Q8_0 row dot: ggml vec_dot_q4_0_q8_0 formula; nibble order of qwen_moe.c:165. */
+/* The kernels' reduction of lpr per-lane partial sums p[0..lpr-1] of one row: an inclusive prefix
+ * sum in each row of 16 lanes (row_shr 1, 2, 4, 8, with 0 shifted in), then row_bcast 15 into rows
+ * 1 and 3 and row_bcast 31 into rows 2 and 3; the row's value is the one left in the last lane.
+ * With row sums s0..s3 that is s0 (lpr 16), s1 + s0 (lpr 32), (s3 + s2) + (s1 + s0) (lpr 64). */
+static float row_scan16(const float *v)
+{
+    float a[16], b[16];
+    memcpy(a, v, sizeof a);
+    for (int k = 1; k < 16; k <<= 1) {
+        for (int i = 0; i < 16; i++) b[i] = a[i] + (i >= k ? a[i - k] : 0.0f);
+        memcpy(a, b, sizeof a);
+    }
+    return a[15];
+}
+
+static float lane_reduce(const float *p, int lpr)
+{
+    const float s0 = row_scan16(p);
+    if (lpr == 16) return s0;
+    const float s1 = row_scan16(p + 16);
+    if (lpr == 32) return s1 + s0;
+    const float s2 = row_scan16(p + 32) + 0.0f, s3 = row_scan16(p + 48);
+    return (s3 + s2) + (s1 + s0);
+}
+
+/* Q4_0 x Q8_0 row dot: ggml vec_dot_q4_0_q8_0 formula; nibble order of qwen_moe.c:165.  The float
+ * combine follows the kernel: block b goes to lane b % 64, which adds (float)isum * (dw*dx) in
+ * block order, and the 64 lane sums are reduced by lane_reduce. */
 static float dot_q4_0_q8_0(const orc_q4_0 *w, const orc_q8_0 *x, int nb)
 {
-    float acc = 0.0f;
+    float acc[64];
+    for (int l = 0; l < 64; l++) acc[l] = 0.0f;
     for (int ib = 0; ib < nb; ib++) {
         int isum = 0;
         for (int j = 0; j < 16; j++) {
@@ -482,9 +511,9 @@ static float dot_q4_0_q8_0(const orc_q4_0 *w, const orc_q8_0 *x, int nb)
             isum += ((w[ib].qs[j] >> 4) - 8) * x[ib].qs[j + 16];
         }
         float dd = orc_f16_to_f32(w[ib].d) * orc_f16_to_f32(x[ib].d);
-        acc = acc + (float)isum * dd;
+        acc[ib % 64] = acc[ib % 64] + (float)isum * dd;
     }
-    return acc;
+    return lane_reduce(acc, 64);
 }
 
 /* Q4_K x Q8_K row dot: y = sum_sb dx*d*sum_j sc_j*sum_l q*a - dx*dmin*sum_j m_j*(a-sum of j). */
@@ -536,19 +565,31 @@ static float dot_q3_K_q8_K(const orc_q3_K *w, const orc_q8_K *x, int nb)
 
 /* Q8_0 weight x pack_A_i8 activation row dot, run_i8_m1 (qwen_moe_q3k.c:428-510): per K32
  * group the exact int32 dot, then acc += (dw * scale) * float(dot) as one fused multiply-add
- * (vfmul.vf then vfmacc.vv), groups in K order. */
+ * (vfmul.vf then vfmacc.vv).  The groups are combined in the kernel's order: lpr lanes per row
+ * (16 up to K = 2048, 32 up to 4096, 64 beyond), lane j takes groups j, j + lpr, ... in order
+ * (bpl of them; a lane past the last group adds fma(0, 0, acc)), and lane_reduce combines them. */
 static float dot_q8_0_i8(const orc_q8_0 *w, const orc_a_i8 *x, int nb)
 {
-    float acc = 0.0f;
-    for (int ib = 0; ib < nb; ib++) {
-        orc_a_i8 a;
-        memcpy(&a, &x[ib], sizeof a);
-        int isum = 0;
-        for (int j = 0; j < 32; j++) isum += w[ib].qs[j] * a.qs[j];
-        float v1 = orc_f16_to_f32(w[ib].d) * a.s;
-        acc = fmaf(v1, (float)isum, acc);
+    const int lpr = nb <= 64 ? 16 : nb <= 128 ? 32 : 64;
+    const int bpl = nb <= 16 ? 1 : nb <= 32 ? 2 : nb <= 256 ? 4 : 8;
+    float acc[64];
+    for (int l = 0; l < lpr; l++) {
+        acc[l] = 0.0f;
+        for (int c = 0; c < bpl; c++) {
+            const int ib = l + lpr * c;
+            if (ib >= nb) {
+                acc[l] = fmaf(0.0f, 0.0f, acc[l]);
+                continue;
+            }
+            orc_a_i8 a;
+            memcpy(&a, &x[ib], sizeof a);
+            int isum = 0;
+            for (int j = 0; j < 32; j++) isum += w[ib].qs[j] * a.qs[j];
+            float v1 = orc_f16_to_f32(w[ib].d) * a.s;
+            acc[l] = fmaf(v1, (float)isum, acc[l]);
+        }
     }
-    return acc;
+    return lane_reduce(acc, lpr);
 }
 
 static int is_i8_path(int qtype) { return qtype == ORC_Q8_0 || qtype == ORC_Q5_K || qtype == ORC_Q6_K; }
@@ -781,3 +822,224 @@ done:
     free(sel_l); free(sw_l); free(g); free(u); free(y); free(eout); free(xq); free(aq);
     return rc;
 }
+
+/* ---------------------------------------------------------------------------------------------
+ * Decode step around the MoE block (qwen_moe.c:278-311 with the helpers of :187-189 and the
+ * rope table of qwen_moe_hp.c:799-804)
+ * ------------------------------------------------------------------------------------------- */
+
+/* rmsnorm, qwen_moe.c:187: s = 1/sqrtf(sum(x^2)/n + eps), o = (x*s)*w.  The sum of squares is
+ * taken in the kernel's order: thread t of 1024 sums x_i^2 for i = t, t + 1024, ... in order, each
+ * wave of 64 threads combines its sums by the xor butterfly (butterfly64), and the 16 wave sums are
+ * added in wave order.  (The reference sums in index order; the two differ by rounding only.) */
+void orc_rmsnorm(float *o, const float *x, const float *w, int n, float eps)
+{
+    float tot = 0.0f;
+    for (int wv = 0; wv < 16; wv++) {
+        float p[64];
+        for (int l = 0; l < 64; l++) {
+            float ss = 0.0f;
+            for (int i = 64 * wv + l; i < n; i += 1024) ss += x[i] * x[i];
+            p[l] = ss;
+        }
+        tot += butterfly64(p);
+    }
+    const float s = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int i = 0; i < n; i++) o[i] = x[i] * s * w[i];
+}
+
+/* The per-head rmsnorm of q and k (qwen_moe.c:284-285) for head_dim 128, in the kernel's order:
+ * lane i of 64 holds x_i^2 + x_{i+64}^2, combined by the xor butterfly. */
+static void rmsnorm_head128(float *v, const float *w, float eps)
+{
+    float p[64];
+    for (int i = 0; i < 64; i++) p[i] = v[i] * v[i] + v[i + 64] * v[i + 64];
+    const float s = 1.0f / sqrtf(butterfly64(p) / 128.0f + eps);
+    for (int i = 0; i < 128; i++) v[i] = v[i] * s * w[i];
+}
+
+/* rope_table, qwen_moe_hp.c:799-801 (the per-head rope of qwen_moe.c:188 computes the same):
+ * fr = base^(-2i/hd) with the exponent in fp32, a = pos*fr in fp32, cos a and sin a.  pow, cos
+ * and sin are evaluated in binary64 and rounded once (libm's powf/cosf/sinf differ by an ulp). */
+void orc_rope_table(float *cosb, float *sinb, int hd, int pos, float base)
+{
+    for (int i = 0; i < hd / 2; i++) {
+        float e = -2.0f * (float)i / (float)hd;
+        float fr = (float)pow((double)base, (double)e);
+        float a = (float)pos * fr;
+        cosb[i] = (float)cos((double)a);
+        sinb[i] = (float)sin((double)a);
+    }
+}
+
+/* rope_apply, qwen_moe_hp.c:802-804: rotate the pairs (i, i + hd/2). */
+void orc_rope_apply(float *v, int hd, const float *cosb, const float *sinb)
+{
+    for (int i = 0; i < hd / 2; i++) {
+        float c = cosb[i], sn = sinb[i], x = v[i], y = v[i + hd / 2];
+        v[i] = x * c - y * sn;
+        v[i + hd / 2] = x * sn + y * c;
+    }
+}
+
+static int layer_ok(const orc_layer_cfg *c)
+{
+    return c && c->d > 0 && c->n_head > 0 && c->n_head_kv > 0 && c->n_head % c->n_head_kv == 0 &&
+           c->head_dim == 128 && c->ctx > 0;
+}
+
+/* Attention of one query head over positions 0..n_pos-1 of its KV head (K, V: [pos][128]), in the
+ * kernels' order (softmax over the scores q.K_j * scale, then o = sum_j p_j V_j):
+ *   positions are cut into chunks of CH (attn_chunks); in a chunk, position j belongs to group
+ *   (j - j0) % 8, and each group keeps a running maximum m, sum l and output o, updated position by
+ *   position (online softmax: corr = e^(m - m'), p = e^(s - m'), l = l*corr + p,
+ *   o = fma(o, corr, p*v));
+ *   a score is the dot product split in 8 slices of 16 (an fma chain each) summed as
+ *   ((d0+d1) + (d2+d3)) + ((d4+d5) + (d6+d7)), times scale;
+ *   the 8 groups are merged by the xor butterfly (strides 1, 2, 4), chunk results in chunk order:
+ *   att = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+ * exp is evaluated in binary64 and rounded once.  Equal to the sequential softmax of
+ * qwen_moe.c:289-292 up to rounding. */
+static void attn_chunks(int n_pos, int n_kv, int *CH, int *nch)
+{
+    const int target = n_kv >= 512 ? 1 : 512 / n_kv;
+    int ch = (n_pos + target - 1) / target;
+    ch = (ch + 7) / 8 * 8;
+    if (ch < 8) ch = 8;
+    *CH = ch;
+    *nch = (n_pos + ch - 1) / ch;
+}
+
+typedef struct { float m, l, o[128]; } attn_state;
+
+static void attn_merge(attn_state *a, const attn_state *b)
+{
+    const float mn = fmaxf(a->m, b->m), ea = exp_f32(a->m - mn), eb = exp_f32(b->m - mn);
+    a->l = a->l * ea + b->l * eb;
+    for (int t = 0; t < 128; t++) a->o[t] = a->o[t] * ea + b->o[t] * eb;
+    a->m = mn;
+}
+
+static void attn_head(const float *qh, const float *K, const float *V, int n_pos, int n_kv, float scale,
+                      float *out)
+{
+    int CH, nch;
+    attn_chunks(n_pos, n_kv, &CH, &nch);
+    attn_state *part = (attn_state *)malloc(sizeof(attn_state) * (size_t)nch);
+    attn_state g[8], tmp[8];
+    for (int c = 0; c < nch; c++) {
+        const int j0 = c * CH, j1 = j0 + CH < n_pos ? j0 + CH : n_pos;
+        for (int k = 0; k < 8; k++) {
+            g[k].m = -FLT_MAX;
+            g[k].l = 0.0f;
+            for (int t = 0; t < 128; t++) g[k].o[t] = 0.0f;
+        }
+        for (int jb = j0; jb < j1; jb += 8)
+            for (int k = 0; k < 8; k++) {
+                const int j = jb + k, ok = j < j1;
+                const float *kr = K + (size_t)(ok ? j : j0) * 128, *vr = V + (size_t)(ok ? j : j0) * 128;
+                float dl[8];
+                for (int sl = 0; sl < 8; sl++) {
+                    float dd = 0.0f;
+                    for (int t = 0; t < 16; t++) dd = fmaf(qh[16 * sl + t], kr[16 * sl + t], dd);
+                    dl[sl] = dd;
+                }
+                const float sc = (((dl[0] + dl[1]) + (dl[2] + dl[3])) + ((dl[4] + dl[5]) + (dl[6] + dl[7]))) * scale;
+                const float mn = ok ? fmaxf(g[k].m, sc) : g[k].m;
+                const float corr = exp_f32(g[k].m - mn);
+                const float p = ok ? exp_f32(sc - mn) : 0.0f;
+                g[k].l = g[k].l * corr + p;
+                for (int t = 0; t < 128; t++) g[k].o[t] = fmaf(g[k].o[t], corr, p * vr[t]);
+                g[k].m = mn;
+            }
+        for (int off = 1; off < 8; off <<= 1) {
+            for (int k = 0; k < 8; k++) {
+                tmp[k] = g[k];
+                attn_merge(&tmp[k], &g[k ^ off]);
+            }
+            memcpy(g, tmp, sizeof g);
+        }
+        part[c] = g[0];
+    }
+    float M = -FLT_MAX;
+    for (int c = 0; c < nch; c++) M = fmaxf(M, part[c].m);
+    float L = 0.0f, O[128];
+    for (int t = 0; t < 128; t++) O[t] = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        const float e = exp_f32(part[c].m - M);
+        L += part[c].l * e;
+        for (int t = 0; t < 128; t++) O[t] += part[c].o[t] * e;
+    }
+    for (int t = 0; t < 128; t++) out[t] = O[t] / L;
+    free(part);
+}
+
+/* Attention half of one decoder layer for one token at position pos (qwen_moe.c:279-293):
+ *   hn = rmsnorm(h, attn_norm); q, k, v = Wq.hn, Wk.hn, Wv.hn (quantized GEMVs, orc_qgemv);
+ *   per head rmsnorm(q_norm / k_norm) then rope; k, v stored at pos of the head-major caches
+ *   kc, vc [n_head_kv][ctx][head_dim] (the layout of qwen_moe_hp.c:1469-1474);
+ *   per query head (kv head hh / (n_head / n_head_kv)): scores q.K_j * (1/sqrtf(hd)) for
+ *   j = 0..pos, softmax, o = sum_j p_j V_j (attn_head);
+ *   h += Wo.att.
+ * head_dim 128.  Sums are taken in the kernels' orders (orc_rmsnorm, rmsnorm_head128, attn_head). */
+int orc_attn_decode(const orc_layer_cfg *c, const float *attn_norm, const float *q_norm, const float *k_norm,
+                    const void *wq, const void *wk, const void *wv, const void *wo, float *kc, float *vc, int pos,
+                    float *h)
+{
+    if (!layer_ok(c) || pos < 0 || pos >= c->ctx) return -1;
+    const int d = c->d, nh = c->n_head, nkv = c->n_head_kv, hd = c->head_dim, gpr = nh / nkv;
+    const int qd = nh * hd, kvd = nkv * hd;
+    float *hn = (float *)malloc(sizeof(float) * (size_t)d), *q = (float *)malloc(sizeof(float) * (size_t)qd);
+    float *k = (float *)malloc(sizeof(float) * (size_t)kvd), *v = (float *)malloc(sizeof(float) * (size_t)kvd);
+    float *att = (float *)malloc(sizeof(float) * (size_t)qd), *tmp = (float *)malloc(sizeof(float) * (size_t)d);
+    float *sc = (float *)malloc(sizeof(float) * (size_t)(pos + 1));
+    float *cosb = (float *)malloc(sizeof(float) * (size_t)(hd / 2)), *sinb = (float *)malloc(sizeof(float) * (size_t)(hd / 2));
+    int rc = -1;
+    if (!hn || !q || !k || !v || !att || !tmp || !sc || !cosb || !sinb) goto done;
+    orc_rmsnorm(hn, h, attn_norm, d, c->eps);
+    if (orc_qgemv(c->wq_type, 1, qd, d, wq, hn, q) || orc_qgemv(c->wk_type, 1, kvd, d, wk, hn, k) ||
+        orc_qgemv(c->wv_type, 1, kvd, d, wv, hn, v))
+        goto done;
+    orc_rope_table(cosb, sinb, hd, pos, c->rope_base);
+    for (int hh = 0; hh < nh; hh++) {
+        rmsnorm_head128(q + hh * hd, q_norm, c->eps);
+        orc_rope_apply(q + hh * hd, hd, cosb, sinb);
+    }
+    for (int hh = 0; hh < nkv; hh++) {
+        rmsnorm_head128(k + hh * hd, k_norm, c->eps);
+        orc_rope_apply(k + hh * hd, hd, cosb, sinb);
+        memcpy(kc + ((size_t)hh * c->ctx + pos) * hd, k + hh * hd, sizeof(float) * (size_t)hd);
+        memcpy(vc + ((size_t)hh * c->ctx + pos) * hd, v + hh * hd, sizeof(float) * (size_t)hd);
+    }
+    {
+        const float scale = 1.0f / sqrtf((float)hd);
+        for (int hh = 0; hh < nh; hh++) {
+            const int kvh = hh / gpr;
+            attn_head(q + hh * hd, kc + (size_t)kvh * c->ctx * hd, vc + (size_t)kvh * c->ctx * hd, pos + 1, nkv,
+                      scale, att + hh * hd);
+        }
+    }
+    if (orc_qgemv(c->wo_type, 1, d, qd, wo, att, tmp)) goto done;
+    for (int i = 0; i < d; i++) h[i] += tmp[i];
+    rc = 0;
+done:
+    free(hn); free(q); free(k); free(v); free(att); free(tmp); free(sc); free(cosb); free(sinb);
+    return rc;
+}
+
+/* One whole decoder layer (qwen_moe.c:278-311): the attention half, then
+ * hn = rmsnorm(h, ffn_norm) and h += MoE(hn) (orc_moe_layer with the residual flag). */
+int orc_decode_layer(const orc_layer_cfg *c, const float *attn_norm, const float *q_norm, const float *k_norm,
+                     const void *wq, const void *wk, const void *wv, const void *wo, const float *ffn_norm,
+                     const float *router, const void *wg, const void *wu, const void *wd, float *kc, float *vc,
+                     int pos, float *h, int *sel, float *sw)
+{
+    if (orc_attn_decode(c, attn_norm, q_norm, k_norm, wq, wk, wv, wo, kc, vc, pos, h)) return -1;
+    float *hn = (float *)malloc(sizeof(float) * (size_t)c->d);
+    if (!hn) return -1;
+    orc_rmsnorm(hn, h, ffn_norm, c->d, c->eps);
+    int rc = orc_moe_layer(1, c->d, c->ff, c->n_exp, c->n_act, hn, router, wg, wu, wd, h, 1, sel, sw);
+    free(hn);
+    return rc;
+}
+

@@ -21,8 +21,10 @@
  *   - the router dot products and the softmax sum use one fixed order (64 lane-strided partial
  *     sums, then a butterfly over the partials), the order the HIP kernel uses, so expert choice
  *     and weights match it bit for bit;
- *   - the float combine of a row's per-block integer dots is sequential in block order with
- *     no fused multiply-add (build with -ffp-contract=off).
+ *   - the float combine of a row's per-block integer dots: K-quants sequential in block order
+ *     with no fused multiply-add (build with -ffp-contract=off); Q4_0 and the int8 path in the
+ *     kernels' lane order (lane-strided partial sums and their DPP prefix-sum reduction), which
+ *     differs from the reference's sequential order by rounding only.
  *
  * Parity pinning (what checks each function beyond itself) is listed in the test files
  * tests/test_oracle.py and tests/golden/.
@@ -132,6 +134,32 @@ int orc_moe_route(int M, int d, int n_exp, int n_act, const float *hn, const flo
 
 /* SiLU-gated product used by the MoE block (qwen_moe.c:309 / qwen_moe_hp.c:1307-1309). */
 float orc_swiglu(float g, float u);
+
+/* ---- decode step around the MoE block -------------------------------------------------------- */
+/* rmsnorm (qwen_moe.c:187), rope table and rotation (qwen_moe_hp.c:799-804; pow/cos/sin in
+ * binary64, rounded once). */
+void orc_rmsnorm(float *o, const float *x, const float *w, int n, float eps);
+void orc_rope_table(float *cosb, float *sinb, int hd, int pos, float base);
+void orc_rope_apply(float *v, int hd, const float *cosb, const float *sinb);
+
+typedef struct {
+    int d, n_head, n_head_kv, head_dim, ff, n_exp, n_act, ctx;
+    float eps, rope_base;
+    int wq_type, wk_type, wv_type, wo_type;   /* ggml type ids of the attention weights */
+} orc_layer_cfg;
+
+/* Attention half of a decoder layer for one token (qwen_moe.c:279-293): h += Wo.attn(...), and
+ * k, v written at pos of the head-major caches kc, vc [n_head_kv][ctx][head_dim].  Weights are
+ * GGUF-native blocks, row-major (Wq: n_head*head_dim rows of d; Wk, Wv: n_head_kv*head_dim rows
+ * of d; Wo: d rows of n_head*head_dim).  Returns 0 or -1. */
+int orc_attn_decode(const orc_layer_cfg *c, const float *attn_norm, const float *q_norm, const float *k_norm,
+                    const void *wq, const void *wk, const void *wv, const void *wo, float *kc, float *vc, int pos,
+                    float *h);
+/* Whole layer (qwen_moe.c:278-311): attention half, rmsnorm(ffn_norm), h += MoE (orc_moe_layer). */
+int orc_decode_layer(const orc_layer_cfg *c, const float *attn_norm, const float *q_norm, const float *k_norm,
+                     const void *wq, const void *wk, const void *wv, const void *wo, const float *ffn_norm,
+                     const float *router, const void *wg, const void *wu, const void *wd, float *kc, float *vc,
+                     int pos, float *h, int *sel, float *sw);
 
 #ifdef __cplusplus
 }

@@ -18,6 +18,13 @@ DT_Q8_K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))]
 DT_A_I8 = np.dtype([("s", "<f4"), ("asum", "<i2"), ("qs", "i1", (32,))])   # pack_A_i8 record
 assert DT_Q8_0.itemsize == 34 and DT_Q8_K.itemsize == 292 and DT_A_I8.itemsize == 38
 
+class LayerCfg(ctypes.Structure):
+    """orc_layer_cfg."""
+    _fields_ = [(n, ctypes.c_int) for n in ("d", "n_head", "n_head_kv", "head_dim", "ff", "n_exp", "n_act", "ctx")] + \
+               [("eps", ctypes.c_float), ("rope_base", ctypes.c_float)] + \
+               [(n, ctypes.c_int) for n in ("wq_type", "wk_type", "wv_type", "wo_type")]
+
+
 _o = None
 _r = None
 
@@ -60,6 +67,14 @@ def oracle():
         L.orc_gemv_int.restype = None
         L.orc_pack_w_int4.argtypes = [i, i, p, p]
         L.orc_pack_w_int8.argtypes = [i, i, p, p]
+        L.orc_rmsnorm.argtypes = [p, p, p, i, f]
+        L.orc_rmsnorm.restype = None
+        L.orc_rope_table.argtypes = [p, p, i, i, f]
+        L.orc_rope_table.restype = None
+        L.orc_rope_apply.argtypes = [p, i, p, p]
+        L.orc_rope_apply.restype = None
+        L.orc_attn_decode.argtypes = [ctypes.POINTER(LayerCfg)] + [p] * 9 + [i, p]
+        L.orc_decode_layer.argtypes = [ctypes.POINTER(LayerCfg)] + [p] * 14 + [i, p, p, p]
         L.orc_swiglu.argtypes = [f, f]
         L.orc_swiglu.restype = f
         _o = L
@@ -217,3 +232,44 @@ def pack_w(int4, W):
         rc = oracle().orc_pack_w_int8(N, K, _p(W), _p(out))
     assert rc == 0
     return out
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    oracle().orc_rmsnorm(_p(out), _p(x), _p(w), x.size, eps)
+    return out
+
+
+def rope_table(hd, pos, base):
+    c = np.empty(hd // 2, np.float32)
+    s_ = np.empty(hd // 2, np.float32)
+    oracle().orc_rope_table(_p(c), _p(s_), hd, pos, base)
+    return c, s_
+
+
+def _a(x):
+    return None if x is None else _p(np.ascontiguousarray(x))
+
+
+def attn_decode(cfg, L, kc, vc, pos, h):
+    """h (modified in place) += attention; kc / vc (modified in place) get k, v at pos.  L: dict of
+    numpy weights (GGUF blocks for wq / wk / wv / wo)."""
+    assert h.dtype == np.float32 and h.flags.c_contiguous and kc.flags.c_contiguous and vc.flags.c_contiguous
+    rc = oracle().orc_attn_decode(ctypes.byref(cfg), _a(L["attn_norm"]), _a(L["q_norm"]), _a(L["k_norm"]),
+                                  _a(L["wq"]), _a(L["wk"]), _a(L["wv"]), _a(L["wo"]), _p(kc), _p(vc), pos, _p(h))
+    assert rc == 0
+
+
+def decode_layer(cfg, L, kc, vc, pos, h):
+    assert h.dtype == np.float32 and h.flags.c_contiguous
+    sel = np.zeros(cfg.n_act, np.int32)
+    sw = np.zeros(cfg.n_act, np.float32)
+    rc = oracle().orc_decode_layer(ctypes.byref(cfg), _a(L["attn_norm"]), _a(L["q_norm"]), _a(L["k_norm"]),
+                                   _a(L["wq"]), _a(L["wk"]), _a(L["wv"]), _a(L["wo"]), _a(L["ffn_norm"]),
+                                   _a(L["router"]), _a(L["wg"]), _a(L["wu"]), _a(L["wd"]), _p(kc), _p(vc), pos, _p(h),
+                                   _p(sel), _p(sw))
+    assert rc == 0
+    return sel, sw
+

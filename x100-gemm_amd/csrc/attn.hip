@@ -1,0 +1,255 @@
+// The decode step around the MoE block, for one token (qwen_moe.c:278-293): RMSNorm, the q / k / v
+// GEMVs (qgemv.hip), per-head RMSNorm + RoPE with the KV-cache write, grouped-query attention split
+// over position chunks (flash-decoding) and merged, the output GEMV and the residual add.
+//
+// Launches for the attention half: rmsnorm, 3 GEMVs, qk_rope, attn_part, attn_combine, 1 GEMV,
+// residual (+ the next rmsnorm, fused).  The work between the GEMVs is small (a few KB per head);
+// the attention reads each KV-cache row once per block (K and V: 1 KiB per position and KV head).
+#include <float.h>
+
+#include <algorithm>
+
+#include "x100_common.h"
+#include "x100_internal.h"
+
+namespace {
+
+constexpr int HD = 128;   // head_dim of the kernels below (Qwen3)
+
+// RMSNorm of one row (qwen_moe.c:187): s = 1/sqrt(mean(x^2) + eps), out = (x*s)*w.  One block.  With
+// add != NULL the residual x += add is done first and written back (qwen_moe.c:293, fused with the
+// norm that follows it); with w == NULL only the residual is done.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_rmsnorm(float *__restrict__ x, const float *__restrict__ add,
+                                                const float *__restrict__ w, float eps, int n,
+                                                float *__restrict__ out)
+{
+    __shared__ float red[NT / 64];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += NT) {
+        float v = x[i];
+        if (add) {
+            v += add[i];
+            x[i] = v;
+        }
+        ss += v * v;
+    }
+    if (!w) return;
+    ss = wave_sum_bfly_f(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NT / 64; k++) tot += red[k];
+    const float s = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += NT) out[i] = x[i] * s * w[i];
+}
+
+// Per-head RMSNorm and RoPE (qwen_moe.c:284-285; rope table qwen_moe_hp.c:799-804) and the KV-cache
+// write.  Block b < n_head: query head b, in place.  Block n_head + j: key head j, written to
+// kc[j][pos]; value head j copied to vc[j][pos].  Lane i rotates the pair (i, i + HD/2).
+// fr = base^(-2i/hd) with the exponent in fp32 and a = pos*fr in fp32, as the reference; pow, cos
+// and sin are evaluated in double and rounded once.
+__global__ __launch_bounds__(64) void k_qk_rope(float *__restrict__ q, const float *__restrict__ k,
+                                                const float *__restrict__ v, const float *__restrict__ q_norm,
+                                                const float *__restrict__ k_norm, int n_head, int ctx, int pos,
+                                                float eps, float base, float *__restrict__ kc,
+                                                float *__restrict__ vc)
+{
+    const int b = blockIdx.x, i = threadIdx.x;
+    const bool is_q = b < n_head;
+    const int j = b - n_head;
+    const float *src = is_q ? q + (size_t)b * HD : k + (size_t)j * HD;
+    float *dst = is_q ? q + (size_t)b * HD : kc + ((size_t)j * ctx + pos) * HD;
+    const float *w = is_q ? q_norm : k_norm;
+    const float x = src[i], y = src[i + HD / 2];
+    const float ss = wave_sum_bfly_f(x * x + y * y);
+    const float s = 1.0f / sqrtf(ss / (float)HD + eps);
+    const float a0 = x * s * w[i], a1 = y * s * w[i + HD / 2];
+    const float e = -2.0f * (float)i / (float)HD;
+    const float fr = (float)pow((double)base, (double)e);
+    const float ang = (float)pos * fr;
+    const float c = (float)cos((double)ang), sn = (float)sin((double)ang);
+    dst[i] = a0 * c - a1 * sn;
+    dst[i + HD / 2] = a0 * sn + a1 * c;
+    if (!is_q) {
+        float *vd = vc + ((size_t)j * ctx + pos) * HD;
+        vd[i] = v[(size_t)j * HD + i];
+        vd[i + HD / 2] = v[(size_t)j * HD + i + HD / 2];
+    }
+}
+
+// e^x evaluated in double and rounded once (the oracle does the same; libm's expf differs by at most
+// one ulp).
+X100_DEV float exp_r(float x) { return (float)exp((double)x); }
+
+// 8-lane all-reduce (lanes 8g .. 8g+7): xor 1, xor 2 within quads, then the half-row mirror pairs
+// each lane with one of the other quad.
+X100_DEV float sum8_all(float v)
+{
+    v += dpp_f<0xB1>(0.0f, v);
+    v += dpp_f<0x4E>(0.0f, v);
+    v += dpp_f<0x141>(0.0f, v);
+    return v;
+}
+
+// Attention over one chunk of positions for one KV head (qwen_moe.c:289-292: scores q.K_j/sqrt(hd),
+// softmax over j, o = sum_j p_j V_j).  Block (kvh, c) covers positions [c*CH, min((c+1)*CH, n_pos))
+// for the gpr query heads of KV head kvh; wave w takes the heads w, w+4, ... (QPW of them).  A wave
+// steps through the chunk 8 positions at a time: 8 lanes per position, each with 16 of the 128
+// dimensions of K_j and V_j, keeping a running maximum m, sum l and output o per position group and
+// head (online softmax).  The 8 groups are then merged, and lanes 0-7 write (m, l, o[128]) of each
+// head to part[head][c].
+template <int QPW>
+__global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, const float *__restrict__ kc,
+                                                   const float *__restrict__ vc, int gpr, int ctx, int n_pos, int CH,
+                                                   float scale, float *__restrict__ part)
+{
+    constexpr int DL = HD / 8;
+    const int kvh = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
+    const int lane = threadIdx.x & 63, w = wave_id(), grp = lane >> 3, sl = lane & 7;
+    const int j0 = c * CH, j1 = min(j0 + CH, n_pos);
+    const float *K = kc + (size_t)kvh * ctx * HD + sl * DL, *V = vc + (size_t)kvh * ctx * HD + sl * DL;
+
+    float qr[QPW][DL], m[QPW], l[QPW], o[QPW][DL];
+#pragma unroll
+    for (int g = 0; g < QPW; g++) {
+        const int hq = w + 4 * g;
+        const float *qh = q + ((size_t)kvh * gpr + min(hq, gpr - 1)) * HD + sl * DL;
+#pragma unroll
+        for (int t = 0; t < DL; t += 4) {
+            const float4 v4 = *(const float4 *)(qh + t);
+            qr[g][t] = v4.x; qr[g][t + 1] = v4.y; qr[g][t + 2] = v4.z; qr[g][t + 3] = v4.w;
+        }
+        m[g] = -FLT_MAX;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < DL; t++) o[g][t] = 0.0f;
+    }
+
+    for (int jb = j0; jb < j1; jb += 8) {
+        const int j = jb + grp;
+        const bool ok = j < j1;
+        const size_t row = (size_t)(ok ? j : j0) * HD;
+        float kr[DL], vr[DL];
+#pragma unroll
+        for (int t = 0; t < DL; t += 4) {
+            const float4 a = *(const float4 *)(K + row + t), b4 = *(const float4 *)(V + row + t);
+            kr[t] = a.x; kr[t + 1] = a.y; kr[t + 2] = a.z; kr[t + 3] = a.w;
+            vr[t] = b4.x; vr[t + 1] = b4.y; vr[t + 2] = b4.z; vr[t + 3] = b4.w;
+        }
+#pragma unroll
+        for (int g = 0; g < QPW; g++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int t = 0; t < DL; t++) d = __builtin_fmaf(qr[g][t], kr[t], d);
+            const float sc = sum8_all(d) * scale;
+            const float mn = ok ? fmaxf(m[g], sc) : m[g];
+            const float corr = exp_r(m[g] - mn);
+            const float p = ok ? exp_r(sc - mn) : 0.0f;
+            l[g] = l[g] * corr + p;
+#pragma unroll
+            for (int t = 0; t < DL; t++) o[g][t] = __builtin_fmaf(o[g][t], corr, p * vr[t]);
+            m[g] = mn;
+        }
+    }
+
+    // merge the 8 position groups (lanes l, l^8, l^16, l^32 hold the same dimensions)
+#pragma unroll
+    for (int g = 0; g < QPW; g++) {
+#pragma unroll
+        for (int off = 8; off < 64; off <<= 1) {
+            const float m2 = __shfl_xor(m[g], off, 64), l2 = __shfl_xor(l[g], off, 64);
+            const float mn = fmaxf(m[g], m2), a = exp_r(m[g] - mn), b = exp_r(m2 - mn);
+            l[g] = l[g] * a + l2 * b;
+#pragma unroll
+            for (int t = 0; t < DL; t++) o[g][t] = o[g][t] * a + __shfl_xor(o[g][t], off, 64) * b;
+            m[g] = mn;
+        }
+        const int hq = w + 4 * g;
+        if (hq < gpr && grp == 0) {
+            float *P = part + ((size_t)(kvh * gpr + hq) * nch + c) * (HD + 2);
+            if (sl == 0) {
+                P[0] = m[g];
+                P[1] = l[g];
+            }
+#pragma unroll
+            for (int t = 0; t < DL; t++) P[2 + sl * DL + t] = o[g][t];
+        }
+    }
+}
+
+// Merge the chunks of one query head: att = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+__global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ part, int nch, float *__restrict__ att)
+{
+    const int h = blockIdx.x, t = threadIdx.x;
+    const float *P = part + (size_t)h * nch * (HD + 2);
+    float M = -FLT_MAX;
+    for (int c = 0; c < nch; c++) M = fmaxf(M, P[(size_t)c * (HD + 2)]);
+    float L = 0.0f, O = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        const float e = exp_r(P[(size_t)c * (HD + 2)] - M);
+        L += P[(size_t)c * (HD + 2) + 1] * e;
+        O += P[(size_t)c * (HD + 2) + 2 + t] * e;
+    }
+    att[(size_t)h * HD + t] = O / L;
+}
+
+// Chunking of 0..pos: about 512 blocks over the KV heads, at least 8 positions per chunk.  Since
+// CH >= n_pos / target and CH >= 8, nch <= min(target, ceil(n_pos / 8)) for every n_pos.
+int chunk_target(int n_kv) { return n_kv >= 512 ? 1 : 512 / n_kv; }
+void chunks(int n_pos, int n_kv, int &CH, int &nch)
+{
+    const int target = chunk_target(n_kv);
+    CH = (n_pos + target - 1) / target;
+    CH = (CH + 7) / 8 * 8;
+    if (CH < 8) CH = 8;
+    nch = (n_pos + CH - 1) / CH;
+}
+
+constexpr size_t seg(size_t floats) { return (floats + 63) / 64 * 64; }   // 256-byte segments
+
+}  // namespace
+
+// Workspace floats: hn[d] q[qd] k[kvd] v[kvd] att[qd] o[d] part[n_head][nch_max][HD + 2].
+size_t x100_attn_workspace_bytes(const x100_layer_cfg *c)
+{
+    const int nch = std::min(chunk_target(c->n_head_kv), (c->ctx + 7) / 8);   // bound for every pos < ctx
+    const size_t qd = (size_t)c->n_head * HD, kvd = (size_t)c->n_head_kv * HD;
+    return 4 * (seg(c->d) * 2 + seg(qd) * 2 + seg(kvd) * 2 + seg((size_t)c->n_head * nch * (HD + 2)));
+}
+
+hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h,
+                            float *ws, float **hn_out, hipStream_t s)
+{
+    const int d = c->d, nh = c->n_head, nkv = c->n_head_kv, gpr = nh / nkv, qd = nh * HD, kvd = nkv * HD;
+    float *hn = ws, *q = hn + seg(d), *k = q + seg(qd), *v = k + seg(kvd), *att = v + seg(kvd),
+          *o = att + seg(qd), *part = o + seg(d);
+    hipLaunchKernelGGL(k_rmsnorm<1024>, dim3(1), dim3(1024), 0, s, h, (const float *)nullptr, w->attn_norm, c->eps,
+                       d, hn);
+    hipError_t e;
+    if ((e = x100_qgemv_launch(c->wq_type, 1, qd, d, w->wq, hn, q, s)) != hipSuccess) return e;
+    if ((e = x100_qgemv_launch(c->wk_type, 1, kvd, d, w->wk, hn, k, s)) != hipSuccess) return e;
+    if ((e = x100_qgemv_launch(c->wv_type, 1, kvd, d, w->wv, hn, v, s)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_qk_rope, dim3(nh + nkv), dim3(64), 0, s, q, k, v, w->q_norm, w->k_norm, nh, c->ctx, pos,
+                       c->eps, c->rope_base, w->k_cache, w->v_cache);
+    int CH, nch;
+    chunks(pos + 1, nkv, CH, nch);
+    const float scale = 1.0f / sqrtf((float)HD);
+    const dim3 grid(nkv, nch);
+    if (gpr <= 4)
+        hipLaunchKernelGGL(k_attn_part<1>, grid, dim3(256), 0, s, q, w->k_cache, w->v_cache, gpr, c->ctx, pos + 1,
+                           CH, scale, part);
+    else if (gpr <= 8)
+        hipLaunchKernelGGL(k_attn_part<2>, grid, dim3(256), 0, s, q, w->k_cache, w->v_cache, gpr, c->ctx, pos + 1,
+                           CH, scale, part);
+    else
+        hipLaunchKernelGGL(k_attn_part<4>, grid, dim3(256), 0, s, q, w->k_cache, w->v_cache, gpr, c->ctx, pos + 1,
+                           CH, scale, part);
+    hipLaunchKernelGGL(k_attn_combine, dim3(nh), dim3(HD), 0, s, part, nch, att);
+    if ((e = x100_qgemv_launch(c->wo_type, 1, d, qd, w->wo, att, o, s)) != hipSuccess) return e;
+    // h += o, and hn = rmsnorm(h, ffn_norm) for the MoE block that follows (skipped without ffn_norm)
+    hipLaunchKernelGGL(k_rmsnorm<1024>, dim3(1), dim3(1024), 0, s, h, (const float *)o, w->ffn_norm, c->eps, d, hn);
+    if (hn_out) *hn_out = hn;
+    return hipGetLastError();
+}

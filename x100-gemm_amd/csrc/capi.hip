@@ -9,6 +9,7 @@
 
 // Only the extern "C" entry points are exported (the library is built with -fvisibility=hidden).
 #pragma GCC visibility push(default)
+#include "x100_decode.h"
 #include "x100_gemm.h"
 #include "x100_gemv_tile.h"
 #include "x100_gguf.h"
@@ -53,21 +54,22 @@ int check_device()
     return X100_OK;
 }
 
-// Per-device MoE workspace (grown on demand, zero-filled so completion counters start at 0).
+// Per-device workspaces (grown on demand, zero-filled so completion counters start at 0): slot 0
+// for the MoE block, slot 1 for the attention half of the decode layer.
 struct Workspace {
     void *ptr = nullptr;
     size_t bytes = 0;
 };
 std::mutex g_ws_mu;
-Workspace g_moe_ws[64];
+Workspace g_ws[64][2];
 
-int moe_workspace(size_t need, void **out)
+int dev_workspace(int slot, size_t need, void **out)
 {
     int dev = 0;
     X100_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= 64) return X100_ENODEV;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace &w = g_moe_ws[dev];
+    Workspace &w = g_ws[dev][slot];
     if (w.bytes < need) {
         if (w.ptr) {
             X100_TRY(hipDeviceSynchronize());
@@ -344,13 +346,74 @@ int moe_layer_hip(int M, int d, int ff, int n_exp, int n_act, const float *hn, c
     int rc = check_device();
     if (rc) return rc;
     void *ws = nullptr;
-    rc = moe_workspace(x100_moe_workspace_bytes(M, d, ff, n_exp, n_act), &ws);
+    rc = dev_workspace(0, x100_moe_workspace_bytes(M, d, ff, n_exp, n_act), &ws);
     if (rc) return rc;
     hipError_t e = x100_moe_launch(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw,
                                    ws, (hipStream_t)stream);
     if (e == hipErrorInvalidValue) return X100_EINVAL;
     if (e != hipSuccess) return hip_fail(e);
     return X100_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// decode layer
+// ---------------------------------------------------------------------------------------------
+static int check_layer(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, const float *h, bool moe)
+{
+    if (!c || !w || !h) return X100_EINVAL;
+    if (c->d <= 0 || c->head_dim != 128 || c->n_head < 1 || c->n_head_kv < 1 || c->n_head % c->n_head_kv ||
+        c->n_head / c->n_head_kv > 16 || c->ctx < 1 || pos < 0 || pos >= c->ctx)
+        return X100_EINVAL;
+    if ((size_t)c->n_head_kv * c->ctx * 128 >= ((size_t)1 << 40)) return X100_EINVAL;
+    if (!w->attn_norm || !w->q_norm || !w->k_norm || !w->wq || !w->wk || !w->wv || !w->wo || !w->k_cache ||
+        !w->v_cache)
+        return X100_EINVAL;
+    if (((uintptr_t)w->k_cache & 15) || ((uintptr_t)w->v_cache & 15)) return X100_EINVAL;
+    const int qd = c->n_head * 128, kvd = c->n_head_kv * 128;
+    if (!x100q_gguf_bytes(c->wq_type, qd, c->d) || !x100q_gguf_bytes(c->wk_type, kvd, c->d) ||
+        !x100q_gguf_bytes(c->wv_type, kvd, c->d) || !x100q_gguf_bytes(c->wo_type, c->d, qd))
+        return X100_EINVAL;
+    if (((uintptr_t)w->wq | (uintptr_t)w->wk | (uintptr_t)w->wv | (uintptr_t)w->wo) & 255) return X100_EINVAL;
+    if (moe && (!w->ffn_norm || !w->router || !w->wg || !w->wu || !w->wd)) return X100_EINVAL;
+    return X100_OK;
+}
+
+static int attn_half(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, float **hn,
+                     void *stream)
+{
+    int rc = check_device();
+    if (rc) return rc;
+    void *ws = nullptr;
+    rc = dev_workspace(1, x100_attn_workspace_bytes(c), &ws);
+    if (rc) return rc;
+    hipError_t e = x100_attn_launch(c, w, pos, h, (float *)ws, hn, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return X100_EINVAL;
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
+int x100_attn_decode_hip(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, void *stream)
+{
+    int rc = check_layer(c, w, pos, h, false);
+    if (rc) return rc;
+    x100_layer_weights w2 = *w;
+    w2.ffn_norm = nullptr;   // the residual add only, no norm for a following block
+    return attn_half(c, &w2, pos, h, nullptr, stream);
+}
+
+int x100_decode_layer_hip(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, int *sel,
+                          float *sw, void *stream)
+{
+    int rc = check_layer(c, w, pos, h, true);
+    if (rc) return rc;
+    if (c->n_act < 1 || c->n_act > 8 || c->n_exp < c->n_act || c->n_exp > 256 || c->d % 256 || c->ff % 256 ||
+        c->d > 4096 || c->ff > 4096 || c->ff <= 0)
+        return X100_EINVAL;
+    float *hn = nullptr;
+    rc = attn_half(c, w, pos, h, &hn, stream);
+    if (rc) return rc;
+    return moe_layer_hip(1, c->d, c->ff, c->n_exp, c->n_act, hn, w->router, w->wg, w->wu, w->wd, h, 1, sel, sw,
+                         stream);
 }
 
 }  // extern "C"

@@ -441,7 +441,7 @@ int x100_gguf_pack_rows(const x100_gguf *g, const x100_gguf_tensor *t, uint64_t 
         e = hipStreamSynchronize((hipStream_t)stream);
         if (e != hipSuccess) rc = map_err(e);
     }
-    hipFree(tmp);
+    (void)hipFree(tmp);
     return rc;
 }
 

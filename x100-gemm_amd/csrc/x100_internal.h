@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "x100_decode.h"
+
 enum {
     X100_GEMM_AUTO = 0,
     X100_GEMM_TILE256 = 1,
@@ -27,3 +29,10 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
 
 hipError_t x100_gemv_tile_launch(int int4, int M, int N, int K, const void *W, const int8_t *x, int32_t *y,
                                  hipStream_t s);
+
+// Attention half of a decoder layer (attn.hip).  ws holds x100_attn_workspace_bytes(c) bytes; with
+// w->ffn_norm set, *hn_out receives rmsnorm(h, ffn_norm) (inside ws) for the MoE block.
+size_t x100_attn_workspace_bytes(const x100_layer_cfg *c);
+hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h,
+                            float *ws, float **hn_out, hipStream_t s);
+

@@ -143,3 +143,24 @@ def moe_weights(n_exp, d, ff, seed):
 
 def moe_router(n_exp, d, seed):
     return normal_f32(seed, (n_exp, d), std=0.02)
+
+
+def decode_layer_weights(d, n_head, n_head_kv, head_dim, ff, n_exp, types, seed):
+    """One Qwen3-MoE decoder layer: norms (fp32, around 1), attention weights in the given ggml
+    types (types = (q, k, v, o); Wq n_head*head_dim x d, Wk / Wv n_head_kv*head_dim x d, Wo
+    d x n_head*head_dim, GGUF blocks), router fp32 N(0, 0.02) [n_exp][d], Q4_K experts."""
+    qd, kvd = n_head * head_dim, n_head_kv * head_dim
+    L = {
+        "attn_norm": (1.0 + 0.1 * normal_f32(seed, (d,))).astype(np.float32),
+        "q_norm": (1.0 + 0.1 * normal_f32(seed + 1, (head_dim,))).astype(np.float32),
+        "k_norm": (1.0 + 0.1 * normal_f32(seed + 2, (head_dim,))).astype(np.float32),
+        "ffn_norm": (1.0 + 0.1 * normal_f32(seed + 3, (d,))).astype(np.float32),
+        "wq": quant_weight(types[0], qd, d, seed + 10),
+        "wk": quant_weight(types[1], kvd, d, seed + 20),
+        "wv": quant_weight(types[2], kvd, d, seed + 30),
+        "wo": quant_weight(types[3], d, qd, seed + 40),
+        "router": moe_router(n_exp, d, seed + 50),
+    }
+    L["wg"], L["wu"], L["wd"] = moe_weights(n_exp, d, ff, seed + 60)
+    return L
+

@@ -26,7 +26,7 @@ X100_OK, X100_EINVAL, X100_ENODEV, X100_EHIP, X100_ENOMEM = 0, -1, -2, -3, -4
 X100_EIO, X100_EFORMAT, X100_ENOTFOUND = -5, -6, -7
 
 # Every symbol declared in include/x100_gemm.h, x100_gemv_tile.h, x100_qgemv.h, x100_moe.h,
-# x100_gguf.h.
+# x100_gguf.h, x100_decode.h.
 EXPORTS = (
     "gemm_ime_i8", "gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant",
     "x100_hip_detect", "x100_hip_caps_print", "x100_hip_strerror",
@@ -38,6 +38,7 @@ EXPORTS = (
     "x100_gguf_kv_at", "x100_gguf_get_int", "x100_gguf_get_float", "x100_gguf_get_str",
     "x100_gguf_get_arr_str", "x100_gguf_qwen3moe_params", "x100_gguf_type_name", "x100_gguf_block_bytes",
     "x100_gguf_block_elems", "x100_gguf_upload", "x100_gguf_pack_rows",
+    "x100_attn_decode_hip", "x100_decode_layer_hip",
 )
 
 GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC, GEMM_TILE256_W4 = 0, 1, 2, 3, 4, 5
@@ -55,6 +56,19 @@ class Caps(ctypes.Structure):
         ("cu_count", ctypes.c_int), ("clock_khz", ctypes.c_int), ("hbm_bytes", ctypes.c_size_t),
         ("lds_bytes", ctypes.c_int), ("l2_bytes", ctypes.c_int), ("is_gfx950", ctypes.c_int),
     ]
+
+
+class LayerCfg(ctypes.Structure):
+    """x100_layer_cfg (x100_decode.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("d", "n_head", "n_head_kv", "head_dim", "ff", "n_exp", "n_act", "ctx")] + \
+               [("eps", ctypes.c_float), ("rope_base", ctypes.c_float)] + \
+               [(n, ctypes.c_int) for n in ("wq_type", "wk_type", "wv_type", "wo_type")]
+
+
+class LayerWeights(ctypes.Structure):
+    """x100_layer_weights (x100_decode.h): device pointers."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("attn_norm", "q_norm", "k_norm", "ffn_norm", "wq", "wk", "wv", "wo",
+                                               "router", "wg", "wu", "wd", "k_cache", "v_cache")]
 
 
 _lib = None
@@ -123,6 +137,10 @@ def lib():
                  "x100_gguf_qwen3moe_params", "x100_gguf_block_elems", "x100_gguf_upload",
                  "x100_gguf_pack_rows"):
         getattr(L, name).restype = i
+    L.x100_attn_decode_hip.argtypes = [ctypes.POINTER(LayerCfg), ctypes.POINTER(LayerWeights), i, p, p]
+    L.x100_decode_layer_hip.argtypes = [ctypes.POINTER(LayerCfg), ctypes.POINTER(LayerWeights), i, p, p, p, p]
+    L.x100_attn_decode_hip.restype = i
+    L.x100_decode_layer_hip.restype = i
     for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant", "x100_hip_detect",
                  "x100q_pack", "qgemv_hip", "moe_layer_hip", "x100_pack_w_int4", "x100_pack_w_int8",
                  "gemv_int4_hip", "gemv_int8_hip"):
@@ -213,3 +231,17 @@ def gemv_tile(int4, M, N, K, d_w, d_x, d_y, stream=None):
     if int4:
         return _check("gemv_int4_hip", lib().gemv_int4_hip(M, N, K, d_w, d_x, d_y, stream))
     return _check("gemv_int8_hip", lib().gemv_int8_hip(M, N, K, d_w, d_x, d_y, stream))
+
+
+# ---- decode layer (x100_decode.h) -----------------------------------------------------------------
+def attn_decode(cfg, weights, pos, d_h, stream=None):
+    """h += Wo.attention(...) for one token at pos; k, v written into the caches."""
+    return _check("x100_attn_decode_hip", lib().x100_attn_decode_hip(ctypes.byref(cfg), ctypes.byref(weights), pos,
+                                                                     d_h, stream))
+
+
+def decode_layer(cfg, weights, pos, d_h, d_sel=None, d_sw=None, stream=None):
+    """One whole decoder layer (attention half, then h += MoE(rmsnorm(h)))."""
+    return _check("x100_decode_layer_hip", lib().x100_decode_layer_hip(ctypes.byref(cfg), ctypes.byref(weights), pos,
+                                                                       d_h, d_sel, d_sw, stream))
+
