@@ -10,7 +10,8 @@ timed with HIP events on the launch stream.  The same JSON line carries:
                 oracle's restatement when that is absent) on a bounded row sample, 1 core;
   extra         the other measured shapes: skinny 8x4096x4096 GEMM, Q4_0 / Q4_K / Q3_K GEMV at
                 M = 1 and 4, the int8 path (Q6_K lm_head, Q5_K attn_output, Q8_0 attn_k of
-                Qwen3-30B-A3B, requantized to Q8_0 at load), the int4 / int8 tile GEMV of bench/q4_gemv.c, the Qwen3-30B-A3B MoE
+                Qwen3-30B-A3B, requantized to Q8_0 at load), the whole decoder layer (attention +
+                MoE, 1024 and 4096 cached positions), the int4 / int8 tile GEMV of bench/q4_gemv.c, the Qwen3-30B-A3B MoE
                 decode layer at M = 1 and 4, each beside its scalar CPU time, and the per-token
                 decode weight stream of bench/moe_decode.c (x100-gemm_amd/moe_decode.py).  GEMV and MoE run back-to-back in a captured graph over weight
                 copies totalling more than 256 MB (so the 256 MB Infinity Cache cannot hold them);
@@ -376,6 +377,69 @@ def bench_extra(torch, timer, dev, args):
                       "bytes_per_layer": byts, "cpu_us_1core": cpu_us}
         log("%s: %.2f us/layer  U=%.1f  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
             key, us, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
+    del layers, base
+
+    # ---- whole decoder layer (x100_decode_layer_hip), one token --------------------------------
+    # Qwen3-30B-A3B: d 2048, 32 query / 4 KV heads of 128, attention weights as in the mixed
+    # checkpoint (q, v Q3_K; k Q8_0; o Q5_K), Q4_K experts; KV cache [4][ctx][128] fp32.  Four
+    # device copies of the layer (1.4 GB) rotate so the Infinity Cache cannot serve them.
+    types = (synth.Q3_K, synth.Q8_0, synth.Q3_K, synth.Q5_K)
+    nh, nkv, hd, ctx = 32, 4, 128, 4096
+    Ld = synth.decode_layer_weights(d, nh, nkv, hd, ff, n_exp, types, seed=520)
+    cfg = x100hip.LayerCfg(d, nh, nkv, hd, ff, n_exp, n_act, ctx, 1e-6, 1e6, *types)
+    host_cfg = ol.LayerCfg(d, nh, nkv, hd, ff, n_exp, n_act, ctx, 1e-6, 1e6, *types)
+    keep = []
+
+    def dev_layer():
+        def f32(a):
+            t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+            keep.append(t)
+            return t.data_ptr()
+
+        def packed(qt, W):
+            N, K = W.shape[0], W.shape[1] * synth.BLOCK_ELEMS[qt]
+            raw = torch.from_numpy(np.ascontiguousarray(W).view(np.uint8).reshape(-1)).to(dev)
+            pk = torch.empty(x100hip.packed_bytes(qt, N, K), dtype=torch.uint8, device=dev)
+            x100hip.pack(qt, N, K, raw.data_ptr(), pk.data_ptr(), s)
+            keep.append(pk)
+            return pk.data_ptr()
+
+        def raw(W):
+            t = torch.from_numpy(np.ascontiguousarray(W).view(np.uint8).reshape(-1)).to(dev)
+            keep.append(t)
+            return t.data_ptr()
+
+        kc = torch.from_numpy(synth.normal_f32(530, (nkv, ctx, hd))).to(dev)
+        vc = torch.from_numpy(synth.normal_f32(531, (nkv, ctx, hd))).to(dev)
+        keep.extend([kc, vc])
+        return x100hip.LayerWeights(f32(Ld["attn_norm"]), f32(Ld["q_norm"]), f32(Ld["k_norm"]), f32(Ld["ffn_norm"]),
+                                    packed(types[0], Ld["wq"]), packed(types[1], Ld["wk"]), packed(types[2], Ld["wv"]),
+                                    packed(types[3], Ld["wo"]), f32(Ld["router"]), raw(Ld["wg"]), raw(Ld["wu"]),
+                                    raw(Ld["wd"]), kc.data_ptr(), vc.data_ptr())
+
+    lw = [dev_layer() for _ in range(4)]
+    attn_bytes = sum(x100hip.packed_bytes(t, n, k) for t, n, k in
+                     ((types[0], nh * hd, d), (types[1], nkv * hd, d), (types[2], nkv * hd, d), (types[3], d, nh * hd)))
+    h0 = synth.normal_f32(532, (d,))
+    dh = torch.from_numpy(h0).to(dev)
+    for pos in (1023, 4095):
+        fns = [lambda i=i: x100hip.decode_layer(cfg, lw[i % 4], pos, dh.data_ptr(), None, None,
+                                                torch.cuda.current_stream().cuda_stream) for i in range(16)]
+        us = timer.graph(fns)
+        lat = timer.single(fns[0])
+        kv_bytes = 2 * nkv * (pos + 1) * hd * 4
+        byts = float(attn_bytes + kv_bytes + n_exp * d * 4 + n_act * 3 * (ff * d // 256 * 144) + 6 * d * 4)
+        hk = synth.normal_f32(533, (nkv, ctx, hd))
+        hv = synth.normal_f32(534, (nkv, ctx, hd))
+        hh = h0.copy()
+        cpu_us = cpu_time(lambda: ol.decode_layer(host_cfg, Ld, hk, hv, pos, hh), min_s=0.3)
+        key = "decode_layer_qwen3_30b_a3b_pos%d" % (pos + 1)
+        extra[key] = {"us_per_layer": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                      "single_launch_us": lat, "bytes_per_layer": byts, "kv_positions": pos + 1,
+                      "cpu_us_1core": cpu_us}
+        log("%s: %.2f us/layer  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us  (x48 layers: %.2f ms/token)" % (
+            key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us, 48 * us / 1e3))
+    del lw, keep
     return extra
 
 

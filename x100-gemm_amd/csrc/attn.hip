@@ -127,70 +127,114 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, 
         for (int t = 0; t < DL; t++) o[g][t] = 0.0f;
     }
 
-    for (int jb = j0; jb < j1; jb += 8) {
+    // The K / V rows of the next step are loaded before the current step is computed.
+    float kr[DL], vr[DL], kn[DL], vn[DL];
+    auto load_rows = [&](int jb, float (&kk)[DL], float (&vv)[DL]) {
         const int j = jb + grp;
-        const bool ok = j < j1;
-        const size_t row = (size_t)(ok ? j : j0) * HD;
-        float kr[DL], vr[DL];
+        const size_t row = (size_t)(j < j1 ? j : j0) * HD;
 #pragma unroll
         for (int t = 0; t < DL; t += 4) {
             const float4 a = *(const float4 *)(K + row + t), b4 = *(const float4 *)(V + row + t);
-            kr[t] = a.x; kr[t + 1] = a.y; kr[t + 2] = a.z; kr[t + 3] = a.w;
-            vr[t] = b4.x; vr[t + 1] = b4.y; vr[t + 2] = b4.z; vr[t + 3] = b4.w;
+            kk[t] = a.x; kk[t + 1] = a.y; kk[t + 2] = a.z; kk[t + 3] = a.w;
+            vv[t] = b4.x; vv[t + 1] = b4.y; vv[t + 2] = b4.z; vv[t + 3] = b4.w;
         }
+    };
+    load_rows(j0, kr, vr);
+    for (int jb = j0; jb < j1; jb += 8) {
+        const bool more = jb + 8 < j1;
+        if (more) load_rows(jb + 8, kn, vn);
+        const bool ok = jb + grp < j1;
 #pragma unroll
         for (int g = 0; g < QPW; g++) {
             float d = 0.0f;
 #pragma unroll
             for (int t = 0; t < DL; t++) d = __builtin_fmaf(qr[g][t], kr[t], d);
             const float sc = sum8_all(d) * scale;
-            const float mn = ok ? fmaxf(m[g], sc) : m[g];
-            const float corr = exp_r(m[g] - mn);
-            const float p = ok ? exp_r(sc - mn) : 0.0f;
+            // m' = max(m, sc): one of e^(m - m') and e^(sc - m') is e^0 = 1, so one exp suffices
+            const bool up = ok && sc > m[g];
+            const float ex = exp_r(up ? m[g] - sc : sc - m[g]);
+            const float corr = up ? ex : 1.0f;
+            const float p = ok ? (up ? 1.0f : ex) : 0.0f;
             l[g] = l[g] * corr + p;
 #pragma unroll
             for (int t = 0; t < DL; t++) o[g][t] = __builtin_fmaf(o[g][t], corr, p * vr[t]);
-            m[g] = mn;
+            m[g] = up ? sc : m[g];
+        }
+        if (more) {
+#pragma unroll
+            for (int t = 0; t < DL; t++) {
+                kr[t] = kn[t];
+                vr[t] = vn[t];
+            }
         }
     }
 
-    // merge the 8 position groups (lanes l, l^8, l^16, l^32 hold the same dimensions)
+    // merge the 8 position groups (lanes l, l^8, l^16, l^32 hold the same dimensions): xor 8 is a
+    // rotation by 8 within a row of 16 (DPP), xor 16 and xor 32 go through ds_bpermute
 #pragma unroll
     for (int g = 0; g < QPW; g++) {
 #pragma unroll
-        for (int off = 8; off < 64; off <<= 1) {
-            const float m2 = __shfl_xor(m[g], off, 64), l2 = __shfl_xor(l[g], off, 64);
-            const float mn = fmaxf(m[g], m2), a = exp_r(m[g] - mn), b = exp_r(m2 - mn);
+        for (int lvl = 0; lvl < 3; lvl++) {
+            const int off = 8 << lvl;
+            auto xch = [&](float v) { return lvl == 0 ? dpp_f<0x128>(v, v) : __shfl_xor(v, off, 64); };
+            const float m2 = xch(m[g]), l2 = xch(l[g]);
+            // a = e^(m - max), b = e^(m2 - max): one of them is 1
+            const bool mine = m[g] >= m2;
+            const float ex = exp_r(mine ? m2 - m[g] : m[g] - m2);
+            const float a = mine ? 1.0f : ex, b = mine ? ex : 1.0f;
             l[g] = l[g] * a + l2 * b;
 #pragma unroll
-            for (int t = 0; t < DL; t++) o[g][t] = o[g][t] * a + __shfl_xor(o[g][t], off, 64) * b;
-            m[g] = mn;
+            for (int t = 0; t < DL; t++) o[g][t] = o[g][t] * a + xch(o[g][t]) * b;
+            m[g] = mine ? m[g] : m2;
         }
         const int hq = w + 4 * g;
         if (hq < gpr && grp == 0) {
-            float *P = part + ((size_t)(kvh * gpr + hq) * nch + c) * (HD + 2);
+            // per head: m[nch], l[nch], then o[dim][nch] (a dimension's chunks contiguous)
+            float *P = part + (size_t)(kvh * gpr + hq) * nch * (HD + 2);
             if (sl == 0) {
-                P[0] = m[g];
-                P[1] = l[g];
+                P[c] = m[g];
+                P[nch + c] = l[g];
             }
 #pragma unroll
-            for (int t = 0; t < DL; t++) P[2 + sl * DL + t] = o[g][t];
+            for (int t = 0; t < DL; t++) P[(size_t)(2 + sl * DL + t) * nch + c] = o[g][t];
         }
     }
 }
 
-// Merge the chunks of one query head: att = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+// Merge the chunks of one query head: att = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).  The
+// maximum M (exact in any order) and the weights e_c are computed once per chunk, spread over the
+// threads, into LDS; the two sums then run in chunk order in every thread (the order the oracle
+// uses), reading a dimension's chunks contiguously.  nch <= 512.
 __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ part, int nch, float *__restrict__ att)
 {
+    __shared__ float se[512], red[HD / 64];
     const int h = blockIdx.x, t = threadIdx.x;
     const float *P = part + (size_t)h * nch * (HD + 2);
-    float M = -FLT_MAX;
-    for (int c = 0; c < nch; c++) M = fmaxf(M, P[(size_t)c * (HD + 2)]);
+    float mx = -FLT_MAX;
+    for (int c = t; c < nch; c += HD) {
+        se[c] = P[c];
+        mx = fmaxf(mx, se[c]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, dpp_f<0x128>(mx, mx));
+    mx = fmaxf(mx, dpp_f<0x124>(mx, mx));
+    mx = fmaxf(mx, dpp_f<0x4E>(mx, mx));
+    mx = fmaxf(mx, dpp_f<0xB1>(mx, mx));
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int k = 1; k < HD / 64; k++) M = fmaxf(M, red[k]);
+    for (int c = t; c < nch; c += HD) se[c] = exp_r(se[c] - M);
+    __syncthreads();
+    const float *Lc = P + nch, *Oc = P + (size_t)(2 + t) * nch;
     float L = 0.0f, O = 0.0f;
+#pragma unroll 16
     for (int c = 0; c < nch; c++) {
-        const float e = exp_r(P[(size_t)c * (HD + 2)] - M);
-        L += P[(size_t)c * (HD + 2) + 1] * e;
-        O += P[(size_t)c * (HD + 2) + 2 + t] * e;
+        const float e = se[c];
+        L += Lc[c] * e;
+        O += Oc[c] * e;
     }
     att[(size_t)h * HD + t] = O / L;
 }
