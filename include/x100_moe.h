@@ -2,17 +2,20 @@
  * x100_moe.h -- Qwen3-MoE decode layer entry point of libx100hip (gfx950).
  *
  * The FFN block of the reference's forward() (qwen_moe.c:294-311; qwen_moe_hp.c:1512-1570) for
- * M <= 8 token rows (decode or speculative verify), one call per layer:
+ * M token rows (decode, speculative verify or prefill), one call per layer:
  *   logits = R . hn (fp32), softmax over all n_exp experts, top-n_act (ties -> lower expert id),
  *   renormalised weights; for each selected expert: g = Wg[e].hn, u = Wu[e].hn, act = silu(g)*u,
  *   y = Wd[e].act; out = sum_a w_a * y_a  (plus out's old value when residual != 0).
  * Experts are Q4_K blocks in the ggml 3-D layout, experts outermost (qwen_moe.c:220-222):
  *   Wg, Wu: [n_exp][ff][d/256] blocks, Wd: [n_exp][d][ff/256] blocks.
  * Activations are quantized to Q8_K per row (hn before gate/up, act before down) with the
- * scalar path's rounding; rows that pick the same expert share one pass over its weights.
+ * scalar path's rounding; rows that pick the same expert share one pass over its weights (up to
+ * 8 rows per pass: beyond 8 token rows the (row, slot) pairs are grouped by expert into chunks
+ * of 8, the MUL_MAT_ID grouping of ime.cpp:667-697).  Each row's result is the same as a
+ * one-row call's.
  *
  * All pointers are device pointers.  sel / sw (may be NULL) receive [M][n_act] expert ids and
- * renormalised weights.  Limits: 1 <= M <= 8, 1 <= n_act <= 8, n_act <= n_exp <= 256,
+ * renormalised weights.  Limits: 1 <= M <= X100_MOE_MAX_ROWS, 1 <= n_act <= 8, n_act <= n_exp <= 256,
  * d % 256 == 0, ff % 256 == 0, d <= 4096, ff <= 4096.  The library keeps a device workspace per
  * GPU (allocated on the first call with a given shape); calls that overlap on one GPU must use
  * the same stream.
@@ -22,6 +25,8 @@
 
 #include <stddef.h>
 #include <stdint.h>
+
+#define X100_MOE_MAX_ROWS 512
 
 #ifdef __cplusplus
 extern "C" {

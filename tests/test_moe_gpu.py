@@ -110,3 +110,40 @@ def test_moe_batched_rows_equal_single_rows(dev, M):
         assert np.array_equal(sel[m], s1[0])
         assert np.array_equal(sw[m].view(np.uint32), w1[0].view(np.uint32))
         assert np.array_equal(out[m].view(np.uint32), o1[0].view(np.uint32)), "row %d differs" % m
+
+
+# ---- more than 8 token rows: routing per 8-row chunk, pairs grouped by expert in chunks of 8 ----
+@pytest.mark.parametrize("M", [9, 16, 64, 512])
+def test_moe_many_rows_qwen3_shape(dev, M):
+    check(M, 128, 2048, 768, 8, seed=510 + M, dev=dev)
+
+
+@pytest.mark.parametrize("M,n_exp,d,ff,n_act", [(100, 8, 256, 256, 8),     # every expert in every row: 13 chunks each
+                                                (40, 16, 512, 256, 4), (17, 64, 1024, 512, 2),
+                                                (33, 200, 256, 256, 6)])
+def test_moe_many_rows_small_shapes(dev, M, n_exp, d, ff, n_act):
+    check(M, n_exp, d, ff, n_act, seed=620 + M + n_exp, dev=dev)
+
+
+def test_moe_many_rows_residual(dev):
+    check(33, 128, 2048, 768, 8, seed=530, dev=dev, residual=True)
+
+
+def test_moe_many_rows_equal_single_rows(dev):
+    L = layer(128, 2048, 768, 500, dev)
+    hn = synth.normal_f32(840, (24, 2048))
+    out, sel, sw = gpu_moe(hn, L, 8, dev)
+    for m in (0, 7, 8, 15, 23):
+        o1, s1, w1 = gpu_moe(hn[m:m + 1], L, 8, dev)
+        assert np.array_equal(sel[m], s1[0])
+        assert np.array_equal(out[m].view(np.uint32), o1[0].view(np.uint32)), "row %d differs" % m
+
+
+def test_moe_rejects_too_many_rows(dev):
+    L = layer(16, 512, 256, 700, dev)
+    import torch
+    hn = torch.zeros((513, 512), device=dev)
+    out = torch.zeros((513, 512), device=dev)
+    with pytest.raises(x100hip.X100Error):
+        x100hip.moe_layer(513, 512, 256, 16, 4, hn.data_ptr(), L[5].data_ptr(), L[4][0].data_ptr(),
+                          L[4][1].data_ptr(), L[4][2].data_ptr(), out.data_ptr(), False, None, None)

@@ -337,7 +337,7 @@ int moe_layer_hip(int M, int d, int ff, int n_exp, int n_act, const float *hn, c
                   const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
                   int *sel, float *sw, void *stream)
 {
-    if (M < 1 || M > 8 || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return X100_EINVAL;
+    if (M < 1 || M > X100_MOE_MAX_ROWS || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return X100_EINVAL;
     if (d <= 0 || ff <= 0 || d % 256 || ff % 256 || d > 4096 || ff > 4096) return X100_EINVAL;
     if (!hn || !R || !Wg || !Wu || !Wd || !out) return X100_EINVAL;
     if (((uintptr_t)hn & 15) || ((uintptr_t)R & 15) || ((uintptr_t)Wg & 15) ||

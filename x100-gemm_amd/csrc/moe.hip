@@ -1,4 +1,6 @@
-// Qwen3-MoE decode layer (the FFN block of qwen_moe.c:294-311) for M <= 8 token rows.
+// Qwen3-MoE decode layer (the FFN block of qwen_moe.c:294-311) for M token rows: the kernels below
+// for M <= 8, and (moe_launch_rows) the same gate/up and down kernels over expert-grouped chunks of
+// 8 (row, slot) pairs for more rows.
 //
 // Three to five launches on one stream; each kernel only reads what an earlier launch wrote, so
 // no block ever waits for, or signals, another block (no fences, no atomics):
@@ -121,10 +123,14 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
                                                    const float *__restrict__ R, MoeWs ws)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    float4 *s_hn = (float4 *)smem;   // [M][d/4]
+    float4 *s_hn = (float4 *)smem;   // [Mloc][d/4]
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + wave_id();
     const int nsb = d / 256;
+    // grid row y covers token rows row0 .. row0 + Mloc - 1 (8 per grid row)
+    const int row0 = blockIdx.y * 8;
+    M = min(8, M - row0);
+    hn += (size_t)row0 * d;
 
     // The wave's router row (clamped expert; elements past d read as 0 and are not used).
     const int e = min(wave, n_exp - 1);
@@ -152,11 +158,11 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
                     s += rv[j].w * hv.w;
                 }
             s = wave_sum_bfly_f(s);
-            if (lane == 0) ws.logits[m * n_exp + wave] = s;
+            if (lane == 0) ws.logits[(row0 + m) * n_exp + wave] = s;
         }
     } else if (wave < n_exp + M * nsb) {
         const int q = wave - n_exp, m = q / nsb, sb = q - m * nsb;
-        uint8_t *rec = ws.xrec + (size_t)m * q8k_rec_bytes(nsb);
+        uint8_t *rec = ws.xrec + (size_t)(row0 + m) * q8k_rec_bytes(nsb);
         q8k_wave(s_hn[q * 64 + lane], (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16,
                  (float *)(rec + nsb * 320) + sb);
     }
@@ -358,7 +364,66 @@ __global__ __launch_bounds__(512) void k_moe_topk(int M, int n_exp, int n_act, M
     publish_routing(M, n_act, rl, ws, sel_out, sw_out);
 }
 
-template <int UPL, int NWV, bool ROUTED>
+// ------------------------------------------------------------------------------------------------
+// More than 8 token rows (verify / prefill).  Routing per 8-row chunk of the grid (the same
+// route_block as above), written per row; then the pairs (row, slot) are grouped by expert (the
+// MUL_MAT_ID grouping of ime.cpp:667-697, qwen_moe_hp.c:1674-1700) into chunks of at most 8 pairs
+// per expert ("virtual" union slots), in the union-slot format the gate/up and down kernels read.
+// Each pair is computed exactly as with one token row, so the order of pairs inside an expert's
+// chunks (set by atomics here) does not change any result.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(512) void k_moe_topk_rows(int M, int n_exp, int n_act, MoeWs ws,
+                                                       int *__restrict__ sel_out, float *__restrict__ sw_out)
+{
+    __shared__ RouteLds rl;
+    const int row0 = blockIdx.x * 8, Mloc = min(8, M - row0);
+    route_block<8>(Mloc, n_exp, n_act, ws.logits + (size_t)row0 * n_exp, rl);
+    const int t = threadIdx.x;
+    if (t < Mloc * n_act) {
+        const int p = row0 * n_act + t;
+        ws.sel[p] = rl.sel[t];
+        ws.sw[p] = rl.w[t];
+        if (sel_out) sel_out[p] = rl.sel[t];
+        if (sw_out) sw_out[p] = rl.w[t];
+    }
+}
+
+// One block of 256 threads (n_exp <= 256): per-expert pair counts, the virtual-slot base of each
+// expert (exclusive scan of ceil(count / 8)), then each pair placed by an atomic cursor.
+__global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
+{
+    __shared__ int s_cnt[256], s_cur[256], s_vbase[257];
+    const int t = threadIdx.x;
+    s_cnt[t] = 0;
+    s_cur[t] = 0;
+    __syncthreads();
+    for (int p = t; p < P; p += 256) atomicAdd(&s_cnt[ws.sel[p]], 1);
+    __syncthreads();
+    if (t == 0) {
+        int v = 0;
+        for (int e = 0; e < n_exp; e++) {
+            s_vbase[e] = v;
+            v += (s_cnt[e] + 7) / 8;
+        }
+        s_vbase[n_exp] = v;
+        *ws.nuniq = v;
+    }
+    __syncthreads();
+    if (t < n_exp) {
+        const int c = s_cnt[t], v0 = s_vbase[t];
+        for (int k = 0; k * 8 < c; k++) {
+            ws.uniq[v0 + k] = t;
+            ws.ucnt[v0 + k] = min(8, c - 8 * k);
+        }
+    }
+    for (int p = t; p < P; p += 256) {
+        const int e = ws.sel[p];
+        const int k = atomicAdd(&s_cur[e], 1);
+        ws.upairs[(s_vbase[e] + k / 8) * 8 + (k & 7)] = p;
+    }
+}
+
+template <int UPL, int NWV, bool ROUTED, bool GATHER = false>
 __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
                                                      const uint8_t *__restrict__ Wg,
                                                      const uint8_t *__restrict__ Wu, MoeWs ws,
@@ -371,20 +436,35 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     const int rec = q8k_rec_bytes(nsb);
 
     // Q8_K records of all M hn rows -> LDS [M][rec], asynchronous (1 KiB chunks, one wave each;
-    // sources clamped to the records, the LDS area is padded to whole chunks).
+    // sources clamped to the records, the LDS area is padded to whole chunks).  With GATHER (more
+    // than 8 token rows) only the rows of this block's pairs are staged, row k of the pair list at
+    // k * cpr KiB, once the pair list has been read.
     const int totv = M * rec / 16;
-    for (int ch = wave_id(); ch * 64 < totv; ch += NWV)
-        dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
+    const int cpr = (rec + 1023) / 1024;   // KiB chunks per record
+    if constexpr (!GATHER)
+        for (int ch = wave_id(); ch * 64 < totv; ch += NWV)
+            dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
 
     const int u = blockIdx.x;
     int U, ex, pr = 0, cnt_r = 0;
     if constexpr (ROUTED) {
-        // routing from k_moe_topk: union entry, its pairs and the union size in one round trip
-        // (u < gridDim.x = M * n_act, so every index is inside the workspace arrays)
+        // routing from k_moe_topk / k_moe_group: union entry, its pairs and the union size in one
+        // round trip (u < gridDim.x <= M * n_act, so every index is inside the workspace arrays)
         ex = ws.uniq[u];
         pr = ws.upairs[u * 8 + min((int)(threadIdx.x & 63), 7)];
         cnt_r = ws.ucnt[u];
         U = *ws.nuniq;
+        if constexpr (GATHER) {
+            if (u < U) {
+                const int lane = threadIdx.x & 63;
+                for (int ch = wave_id(); ch < cnt_r * cpr; ch += NWV) {
+                    const int k = ch / cpr, part = ch - k * cpr;
+                    const int row = __shfl(pr, k, 64) / n_act;   // pair k's token row
+                    const int v = min(row * rec / 16 + part * 64 + lane, totv - 1);
+                    dma_1k((const v4i *)ws.xrec + v, smem + ch * 1024);
+                }
+            }
+        }
     } else {
         route_block<NWV>(M, n_exp, n_act, ws.logits, rl);
         if (blockIdx.x == 0 && blockIdx.y == 0) publish_routing(M, n_act, rl, ws, sel_out, sw_out);
@@ -426,13 +506,13 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     }
     __syncthreads();
     const int cnt = s_cnt;
-    float *tv = (float *)(smem + ((size_t)M * rec + 1023) / 1024 * 1024);   // [8][2][GU_ROWS][nsb]
+    float *tv = (float *)(smem + (GATHER ? (size_t)8 * cpr * 1024 : ((size_t)M * rec + 1023) / 1024 * 1024));
 
     // Token rows outer, units inner (unrolled and branch-free so the scheduler interleaves them):
     // the 8 lanes of a unit store the same value; invalid units write the spare slot.
     const int tv_spare = 8 * 2 * GU_ROWS * nsb;
     for (int k = 0; k < cnt; k++) {
-        const uint8_t *xr = smem + (size_t)(s_pairs[k] / n_act) * rec;
+        const uint8_t *xr = smem + (GATHER ? (size_t)k * cpr * 1024 : (size_t)(s_pairs[k] / n_act) * rec);
 #pragma unroll
         for (int c = 0; c < UPL; c++) {
             const int un = c * 8 * NWV + w * 8 + (lane >> 3);
@@ -700,6 +780,47 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     return ws;
 }
 
+// More than 8 token rows: route per 8-row chunk, group the pairs by expert into chunks of at
+// most 8, then the routed gate/up (gathering each chunk's rows), the down projection and the
+// combine of the M <= 8 path.
+hipError_t moe_launch_rows(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
+                           float *sw, MoeWs ws, hipStream_t s)
+{
+    const int nsb = d / 256, nsf = ff / 256, P = M * n_act, nrc = (M + 7) / 8;
+    const int Vmax = min(P, (P + 7) / 8 + n_exp);   // chunks of <= 8 pairs over the experts
+    hipLaunchKernelGGL(k_moe_route, dim3((n_exp + 8 * nsb + 3) / 4, nrc), dim3(256), (size_t)8 * d * 4, s, M, d,
+                       n_exp, hn, R, ws);
+    hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
+    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(256), 0, s, P, n_exp, ws);
+    const int rec = q8k_rec_bytes(nsb), cpr = (rec + 1023) / 1024;
+    const size_t lds_gu = (size_t)8 * cpr * 1024 + ((size_t)8 * 2 * GU_ROWS * nsb + 1) * 4;
+    const int upl_gu = (2 * GU_ROWS * nsb + 8 * GU_NWV - 1) / (8 * GU_NWV);
+    const dim3 g_gu(Vmax, ff / GU_ROWS), b_gu(64 * GU_NWV);
+    const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
+#define X100_GUR(U) hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, true, true>), g_gu, b_gu, lds_gu, s, M, d, ff, \
+                                       n_exp, n_act, wg, wu, ws, sel, sw)
+    switch (upl_gu) {
+    case 1: X100_GUR(1); break;
+    case 2: X100_GUR(2); break;
+    case 3: case 4: X100_GUR(4); break;
+    default: X100_GUR(8); break;
+    }
+#undef X100_GUR
+    const size_t lds_dn = (size_t)8 * nsf * (256 + 64 + 4) + ((size_t)8 * DN_ROWS * nsf + 1) * 4;
+    const int upl_dn = (DN_ROWS * nsf + 31) / 32;
+    const dim3 g_dn(Vmax, d / DN_ROWS);
+    const uint8_t *wd = (const uint8_t *)Wd;
+    switch (upl_dn) {
+    case 1: hipLaunchKernelGGL(k_moe_down<1>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 2: hipLaunchKernelGGL(k_moe_down<2>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 3: case 4: hipLaunchKernelGGL(k_moe_down<4>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    default: hipLaunchKernelGGL(k_moe_down<8>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    }
+    hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act)
@@ -713,12 +834,14 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
                            const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
                            int *sel, float *sw, void *workspace, hipStream_t s)
 {
-    if (M < 1 || M > 8 || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return hipErrorInvalidValue;
+    if (M < 1 || M > X100_MOE_MAX_ROWS || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256)
+        return hipErrorInvalidValue;
     if (d % 256 || ff % 256 || d > 4096 || ff > 4096 || d % DN_ROWS || ff % GU_ROWS) return hipErrorInvalidValue;
     const int nsb = d / 256, nsf = ff / 256;
     if (2 * GU_ROWS * nsb > 8 * 8 * GU_NWV || DN_ROWS * nsf > 8 * 32) return hipErrorInvalidValue;
     MoeWs ws = carve((uintptr_t)workspace, M, d, ff, n_exp, n_act, nullptr);
     const int Umax = min(M * n_act, n_exp);
+    if (M > 8) return moe_launch_rows(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
 
     const int nwaves = n_exp + M * nsb;
     hipLaunchKernelGGL(k_moe_route, dim3((nwaves + 3) / 4), dim3(256), (size_t)M * d * 4, s, M, d, n_exp, hn, R, ws);

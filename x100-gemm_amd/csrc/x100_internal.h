@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include "x100_decode.h"
+#include "x100_moe.h"
 
 enum {
     X100_GEMM_AUTO = 0,
