@@ -10,7 +10,8 @@ timed with HIP events on the launch stream.  The same JSON line carries:
                 oracle's restatement when that is absent) on a bounded row sample, 1 core;
   extra         the other measured shapes: skinny 8x4096x4096 GEMM, Q4_0 / Q4_K / Q3_K GEMV at
                 M = 1 and 4, the int8 path (Q6_K lm_head, Q5_K attn_output, Q8_0 attn_k of
-                Qwen3-30B-A3B, requantized to Q8_0 at load), the whole decoder layer (attention +
+                Qwen3-30B-A3B, requantized to Q8_0 at load), the MoE layer at 64 and 512 token rows
+                (verify / prefill), the whole decoder layer (attention +
                 MoE, 1024 and 4096 cached positions), the int4 / int8 tile GEMV of bench/q4_gemv.c, the Qwen3-30B-A3B MoE
                 decode layer at M = 1 and 4, each beside its scalar CPU time, and the per-token
                 decode weight stream of bench/moe_decode.c (x100-gemm_amd/moe_decode.py).  GEMV and MoE run back-to-back in a captured graph over weight
@@ -377,6 +378,35 @@ def bench_extra(torch, timer, dev, args):
                       "bytes_per_layer": byts, "cpu_us_1core": cpu_us}
         log("%s: %.2f us/layer  U=%.1f  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
             key, us, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
+    # many token rows (verify / prefill): pairs grouped by expert in chunks of 8
+    for M in (64, 512):
+        n_h = 6
+        hns = synth.normal_f32(950 + M, (n_h, M, d))
+        dh = torch.from_numpy(hns).to(dev)
+        out = torch.empty((M, d), dtype=torch.float32, device=dev)
+        sel = torch.empty((n_h, M, n_act), dtype=torch.int32, device=dev)
+
+        def callm(i, with_sel=False):
+            L = layers[i % 3]
+            x100hip.moe_layer(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
+                              L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False,
+                              sel[i].data_ptr() if with_sel else None, None,
+                              torch.cuda.current_stream().cuda_stream)
+
+        for i in range(n_h):
+            callm(i, True)
+        torch.cuda.synchronize()
+        U = np.array([len(set(r.ravel().tolist())) for r in sel.cpu().numpy()])
+        us = timer.graph([lambda i=i: callm(i) for i in range(n_h)])
+        byts = float(n_exp * d * 4 + U.mean() * 3 * (ff * d // 256 * 144) + M * d * 4 * 2)
+        cpu_us = cpu_time(lambda: ol.moe_layer(hns[0][:8], R, Wg, Wu, Wd, n_act), min_s=0.3) * M / 8
+        key = "moe_layer_qwen3_30b_a3b_m%d" % M
+        extra[key] = {"us_per_layer": us, "us_per_token": us / M, "tokens_per_s": M / us * 1e6,
+                      "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                      "experts_union_mean": float(U.mean()), "bytes_per_layer": byts,
+                      "cpu_us_1core": cpu_us, "cpu_note": "8-row sample scaled to M rows"}
+        log("%s: %.2f us/layer (%.3f us/token)  U=%.1f  %.0f GB/s (%.1f%% HBM)  cpu %.0f us" % (
+            key, us, us / M, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, cpu_us))
     del layers, base
 
     # ---- whole decoder layer (x100_decode_layer_hip), one token --------------------------------

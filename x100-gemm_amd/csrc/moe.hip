@@ -34,11 +34,13 @@ struct MoeWs {
     int *nuniq;           // [1]
     int *uniq;            // [P]          expert id of union slot u (P = M*n_act)
     int *ucnt;            // [P]          pairs in union slot u
-    int *upairs;          // [P][8]       pair ids (m*n_act + a) of union slot u, m ascending
+    int *upairs;          // [slot][8 or 16] pair ids (m*n_act + a) of union slot u (m ascending
+                          // for M <= 8; chunks of 16 per expert beyond)
     uint8_t *xrec;        // [M][rec]: Q8_K of hn row m = q[nsb][256] | bsum[nsb][16] (int) |
                           // d[nsb] (float), rec = that size rounded up to 16 bytes
     float *act;           // [P][ff]
     float *ydn;           // [P][d]
+    uint8_t *xact;        // [P][recf]: Q8_K of act row p (more than 8 token rows), layout of xrec
 };
 
 inline size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -390,6 +392,7 @@ __global__ __launch_bounds__(512) void k_moe_topk_rows(int M, int n_exp, int n_a
 
 // One block of 256 threads (n_exp <= 256): per-expert pair counts, the virtual-slot base of each
 // expert (exclusive scan of ceil(count / 8)), then each pair placed by an atomic cursor.
+template <int PCH>
 __global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
 {
     __shared__ int s_cnt[256], s_cur[256], s_vbase[257];
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
         int v = 0;
         for (int e = 0; e < n_exp; e++) {
             s_vbase[e] = v;
-            v += (s_cnt[e] + 7) / 8;
+            v += (s_cnt[e] + PCH - 1) / PCH;
         }
         s_vbase[n_exp] = v;
         *ws.nuniq = v;
@@ -411,19 +414,19 @@ __global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
     __syncthreads();
     if (t < n_exp) {
         const int c = s_cnt[t], v0 = s_vbase[t];
-        for (int k = 0; k * 8 < c; k++) {
+        for (int k = 0; k * PCH < c; k++) {
             ws.uniq[v0 + k] = t;
-            ws.ucnt[v0 + k] = min(8, c - 8 * k);
+            ws.ucnt[v0 + k] = min(PCH, c - PCH * k);
         }
     }
     for (int p = t; p < P; p += 256) {
         const int e = ws.sel[p];
         const int k = atomicAdd(&s_cur[e], 1);
-        ws.upairs[(s_vbase[e] + k / 8) * 8 + (k & 7)] = p;
+        ws.upairs[(s_vbase[e] + k / PCH) * PCH + (k % PCH)] = p;
     }
 }
 
-template <int UPL, int NWV, bool ROUTED, bool GATHER = false>
+template <int UPL, int NWV, bool ROUTED, bool GATHER = false, int PCH = 8>   // PCH: pairs per union slot
 __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
                                                      const uint8_t *__restrict__ Wg,
                                                      const uint8_t *__restrict__ Wu, MoeWs ws,
@@ -431,7 +434,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ RouteLds rl;
-    __shared__ int s_pairs[8], s_cnt;
+    __shared__ int s_pairs[PCH], s_cnt;
     const int nsb = d / 256;
     const int rec = q8k_rec_bytes(nsb);
 
@@ -451,7 +454,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
         // routing from k_moe_topk / k_moe_group: union entry, its pairs and the union size in one
         // round trip (u < gridDim.x <= M * n_act, so every index is inside the workspace arrays)
         ex = ws.uniq[u];
-        pr = ws.upairs[u * 8 + min((int)(threadIdx.x & 63), 7)];
+        pr = ws.upairs[u * PCH + min((int)(threadIdx.x & 63), PCH - 1)];
         cnt_r = ws.ucnt[u];
         U = *ws.nuniq;
         if constexpr (GATHER) {
@@ -495,7 +498,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     // Pairs (token row m, slot a) of this expert, m ascending (distinct experts per row, so at
     // most one slot per row).
     if constexpr (ROUTED) {
-        if (threadIdx.x < 8) s_pairs[threadIdx.x] = pr;
+        if (threadIdx.x < PCH) s_pairs[threadIdx.x] = pr;
         if (threadIdx.x == 0) s_cnt = cnt_r;
     } else if (threadIdx.x == 0) {
         int c = 0;
@@ -506,11 +509,11 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     }
     __syncthreads();
     const int cnt = s_cnt;
-    float *tv = (float *)(smem + (GATHER ? (size_t)8 * cpr * 1024 : ((size_t)M * rec + 1023) / 1024 * 1024));
+    float *tv = (float *)(smem + (GATHER ? (size_t)PCH * cpr * 1024 : ((size_t)M * rec + 1023) / 1024 * 1024));
 
     // Token rows outer, units inner (unrolled and branch-free so the scheduler interleaves them):
     // the 8 lanes of a unit store the same value; invalid units write the spare slot.
-    const int tv_spare = 8 * 2 * GU_ROWS * nsb;
+    const int tv_spare = PCH * 2 * GU_ROWS * nsb;
     for (int k = 0; k < cnt; k++) {
         const uint8_t *xr = smem + (GATHER ? (size_t)k * cpr * 1024 : (size_t)(s_pairs[k] / n_act) * rec);
 #pragma unroll
@@ -540,18 +543,32 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     __syncthreads();
 }
 
+// Q8_K of every pair's activation row, once (more than 8 token rows): wave q quantizes block
+// q % nsf of pair q / nsf with q8k_wave, into the pair's record of ws.xact.
+__global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
+{
+    const int nsf = ff / 256, q = blockIdx.x * 4 + wave_id(), lane = threadIdx.x & 63;
+    if (q >= P * nsf) return;
+    const int p = q / nsf, sb = q - p * nsf;
+    const float4 v = *(const float4 *)(ws.act + (size_t)p * ff + sb * 256 + 4 * lane);
+    uint8_t *rec = ws.xact + (size_t)p * q8k_rec_bytes(nsf);
+    q8k_wave(v, (int8_t *)rec + sb * 256, (int *)(rec + nsf * 256) + sb * 16, (float *)(rec + nsf * 320) + sb);
+}
+
 // ------------------------------------------------------------------------------------------------
 // grid (U_max, d / DN_ROWS).  Units (row, super-block) = DN_ROWS*nsf, 8 lanes each.
 // ------------------------------------------------------------------------------------------------
-template <int UPL>
-__global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *__restrict__ Wd, MoeWs ws)
+// PREQ (more than 8 token rows): the activation rows were quantized once by k_moe_act_q8k; the
+// block stages its pairs' records (row k at k * cprf KiB) instead of quantizing them again.
+template <int UPL, bool PREQ = false, int PCH = 8>   // PCH: pairs per union slot (16 only with PREQ)
+__global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *__restrict__ Wd, MoeWs ws, int P)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int u = blockIdx.x;
     // Union slot metadata in one round trip (entries of slots >= U are stale and unused).
     const int U = *ws.nuniq;
     const int ex = ws.uniq[u], cnt = ws.ucnt[u];
-    const int prl = ws.upairs[u * 8 + (threadIdx.x & 7)];   // lane l holds pair l % 8 of the slot
+    const int prl = ws.upairs[u * PCH + (threadIdx.x & (PCH - 1))];   // lane l holds pair l % PCH of the slot
     if (u >= U) return;
     const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
     const int nsf = ff / 256;
@@ -590,17 +607,28 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
         const int q = (q0) + 4 * j + w;                                                           \
         if (q < nq) q8k_wave(v[j], aq + q * 256, abs_ + q * 16, ad + q);                          \
     }
-    X100_ACT_LOADS(0)
-    __builtin_amdgcn_sched_barrier(0);
-    X100_ACT_QUANT(0)
-    for (int q0 = 16; q0 < nq; q0 += 16) {
-        X100_ACT_LOADS(q0)
-        X100_ACT_QUANT(q0)
+    const int recf = q8k_rec_bytes(nsf), cprf = (recf + 1023) / 1024;
+    if constexpr (PREQ) {
+        const int totv = P * recf / 16;
+        for (int ch = w; ch < cnt * cprf; ch += 4) {
+            const int k = ch / cprf, part = ch - k * cprf;
+            const int v = min(__builtin_amdgcn_readlane(prl, k) * recf / 16 + part * 64 + lane, totv - 1);
+            dma_1k((const v4i *)ws.xact + v, smem + ch * 1024);
+        }
+        tv = (float *)(smem + (size_t)PCH * cprf * 1024);
+    } else {
+        X100_ACT_LOADS(0)
+        __builtin_amdgcn_sched_barrier(0);
+        X100_ACT_QUANT(0)
+        for (int q0 = 16; q0 < nq; q0 += 16) {
+            X100_ACT_LOADS(q0)
+            X100_ACT_QUANT(q0)
+        }
     }
 #undef X100_ACT_LOADS
 #undef X100_ACT_QUANT
-    __shared__ int s_pr[8];
-    if (threadIdx.x < 8) s_pr[threadIdx.x] = prl;
+    __shared__ int s_pr[PCH];
+    if (threadIdx.x < PCH) s_pr[threadIdx.x] = prl;
     __syncthreads();
 
     // As in gate/up: pairs outer, units inner, branch-free (spare slot 8 * nunits).
@@ -611,8 +639,16 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
             const bool valid = un < nunits;
             const int sb = valid ? un % nsf : 0;
             int isc, imn;
-            q4k_unit_dot(hdr[c], qs[c], aq + (k * nsf + sb) * 256, abs_ + (k * nsf + sb) * 16, i, isc, imn);
-            tv[valid ? k * nunits + un : 8 * nunits] = q4k_combine(hdr[c], ad[k * nsf + sb], isc, imn);
+            if constexpr (PREQ) {
+                const uint8_t *xr = smem + (size_t)k * cprf * 1024;
+                q4k_unit_dot(hdr[c], qs[c], (const int8_t *)xr + sb * 256, (const int *)(xr + nsf * 256) + sb * 16, i,
+                             isc, imn);
+                tv[valid ? k * nunits + un : PCH * nunits] =
+                    q4k_combine(hdr[c], ((const float *)(xr + nsf * 320))[sb], isc, imn);
+            } else {
+                q4k_unit_dot(hdr[c], qs[c], aq + (k * nsf + sb) * 256, abs_ + (k * nsf + sb) * 16, i, isc, imn);
+                tv[valid ? k * nunits + un : 8 * nunits] = q4k_combine(hdr[c], ad[k * nsf + sb], isc, imn);
+            }
         }
     }
     __syncthreads();
@@ -772,10 +808,11 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     ws.nuniq = (int *)take(sizeof(int));
     ws.uniq = (int *)take(sizeof(int) * P);
     ws.ucnt = (int *)take(sizeof(int) * P);
-    ws.upairs = (int *)take(sizeof(int) * P * 8);
+    ws.upairs = (int *)take(sizeof(int) * ((size_t)P * 8 + 16 * (size_t)n_exp + 16));   // chunks of 8 or 16
     ws.xrec = (uint8_t *)take((size_t)M * q8k_rec_bytes(nsb));
     ws.act = (float *)take(sizeof(float) * (size_t)P * ff);
     ws.ydn = (float *)take(sizeof(float) * (size_t)P * d);
+    ws.xact = (uint8_t *)take((size_t)P * q8k_rec_bytes(ff / 256));
     if (total) *total = off;
     return ws;
 }
@@ -787,18 +824,19 @@ hipError_t moe_launch_rows(int M, int d, int ff, int n_exp, int n_act, const flo
                            const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
                            float *sw, MoeWs ws, hipStream_t s)
 {
+    constexpr int PCH = 8;                           // pairs per chunk (16 measured slower: fewer, longer blocks)
     const int nsb = d / 256, nsf = ff / 256, P = M * n_act, nrc = (M + 7) / 8;
-    const int Vmax = min(P, (P + 7) / 8 + n_exp);   // chunks of <= 8 pairs over the experts
+    const int Vmax = min(P, (P + PCH - 1) / PCH + n_exp);   // chunks of <= PCH pairs over the experts
     hipLaunchKernelGGL(k_moe_route, dim3((n_exp + 8 * nsb + 3) / 4, nrc), dim3(256), (size_t)8 * d * 4, s, M, d,
                        n_exp, hn, R, ws);
     hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
-    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(256), 0, s, P, n_exp, ws);
+    hipLaunchKernelGGL(k_moe_group<PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
     const int rec = q8k_rec_bytes(nsb), cpr = (rec + 1023) / 1024;
-    const size_t lds_gu = (size_t)8 * cpr * 1024 + ((size_t)8 * 2 * GU_ROWS * nsb + 1) * 4;
+    const size_t lds_gu = (size_t)PCH * cpr * 1024 + ((size_t)PCH * 2 * GU_ROWS * nsb + 1) * 4;
     const int upl_gu = (2 * GU_ROWS * nsb + 8 * GU_NWV - 1) / (8 * GU_NWV);
     const dim3 g_gu(Vmax, ff / GU_ROWS), b_gu(64 * GU_NWV);
     const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
-#define X100_GUR(U) hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, true, true>), g_gu, b_gu, lds_gu, s, M, d, ff, \
+#define X100_GUR(U) hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, true, true, PCH>), g_gu, b_gu, lds_gu, s, M, d, ff, \
                                        n_exp, n_act, wg, wu, ws, sel, sw)
     switch (upl_gu) {
     case 1: X100_GUR(1); break;
@@ -807,15 +845,17 @@ hipError_t moe_launch_rows(int M, int d, int ff, int n_exp, int n_act, const flo
     default: X100_GUR(8); break;
     }
 #undef X100_GUR
-    const size_t lds_dn = (size_t)8 * nsf * (256 + 64 + 4) + ((size_t)8 * DN_ROWS * nsf + 1) * 4;
+    hipLaunchKernelGGL(k_moe_act_q8k, dim3((P * nsf + 3) / 4), dim3(256), 0, s, P, ff, ws);
+    const int recf = q8k_rec_bytes(nsf), cprf = (recf + 1023) / 1024;
+    const size_t lds_dn = (size_t)PCH * cprf * 1024 + ((size_t)PCH * DN_ROWS * nsf + 1) * 4;
     const int upl_dn = (DN_ROWS * nsf + 31) / 32;
     const dim3 g_dn(Vmax, d / DN_ROWS);
     const uint8_t *wd = (const uint8_t *)Wd;
     switch (upl_dn) {
-    case 1: hipLaunchKernelGGL(k_moe_down<1>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    case 2: hipLaunchKernelGGL(k_moe_down<2>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    case 3: case 4: hipLaunchKernelGGL(k_moe_down<4>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    default: hipLaunchKernelGGL(k_moe_down<8>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 1: hipLaunchKernelGGL((k_moe_down<1, true, PCH>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, P); break;
+    case 2: hipLaunchKernelGGL((k_moe_down<2, true, PCH>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, P); break;
+    case 3: case 4: hipLaunchKernelGGL((k_moe_down<4, true, PCH>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, P); break;
+    default: hipLaunchKernelGGL((k_moe_down<8, true, PCH>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, P); break;
     }
     hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
     return hipGetLastError();
@@ -918,10 +958,10 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     const dim3 g_dn(Umax, d / DN_ROWS);
     const uint8_t *wd = (const uint8_t *)Wd;
     switch (upl_dn) {
-    case 1: hipLaunchKernelGGL(k_moe_down<1>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    case 2: hipLaunchKernelGGL(k_moe_down<2>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    case 3: case 4: hipLaunchKernelGGL(k_moe_down<4>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    default: hipLaunchKernelGGL(k_moe_down<8>, g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 1: hipLaunchKernelGGL((k_moe_down<1>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, M * n_act); break;
+    case 2: hipLaunchKernelGGL((k_moe_down<2>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, M * n_act); break;
+    case 3: case 4: hipLaunchKernelGGL((k_moe_down<4>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, M * n_act); break;
+    default: hipLaunchKernelGGL((k_moe_down<8>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, M * n_act); break;
     }
     err = hipGetLastError();
     if (err != hipSuccess) return err;
