@@ -25,6 +25,7 @@ namespace {
 constexpr int GU_ROWS = 8;    // gate/up rows of ff per block
 constexpr int GU_NWV = 4;     // waves per block of k_moe_gate_up (more waves: fewer blocks resident per CU, each re-deriving the routing)
 constexpr int DN_ROWS = 16;   // down rows of d per block
+constexpr int MF_MIN_ROWS = 16;   // token rows from which the expert products run on the matrix cores
 
 // Workspace layout (device memory owned by the library, sized by x100_moe_workspace_bytes).
 struct MoeWs {
@@ -556,6 +557,157 @@ __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 }
 
 // ------------------------------------------------------------------------------------------------
+// Expert-grouped Q4_K x Q8_K products on the matrix cores (many token rows).  The pairs of one
+// expert come in chunks of up to 32 (k_moe_group<32>); a wave computes a 32 x 32 tile (chunk pairs
+// x weight rows) with one v_mfma_i32_32x32x32_i8 per 32-element sub-block j:
+//   A = the pairs' Q8_K bytes of sub-block j (lane l: pair l % 32, elements 16 * (l / 32) .. +16),
+//   B = the weight rows' 4-bit values of sub-block j (lane l: row l % 32, the same elements),
+// so the accumulator holds dot_j(pair, row) exactly.  Lane l owns weight row l % 32 in every
+// accumulator register, so isc += sc_j(row) * dot_j is one multiply-add per register; the min term
+// sum_j m_j * (sum of the activation bytes of sub-block j) is a second MFMA chain whose B holds m_j in
+// every byte.  These integers equal those of the one-row kernels, and the fp32 combine per
+// super-block (q4k_combine) and the sum over super-blocks run in the same order, so every output
+// is bit-identical to theirs.
+//
+// GU: gate and up (A = the hn records, pair p reads row p / n_act); wave w computes matrix w & 1
+// (gate, up) for ff rows r0 + 32 * (w >> 1) .. +32, and SwiGLU pairs them through LDS.
+// !GU: down projection (A = the activation records of ws.xact, row p); wave w computes d rows
+// r0 + 32 * w .. +32.  grid (chunks, ff / 64 or d / 128).
+// ------------------------------------------------------------------------------------------------
+constexpr int MF_PCH = 32;   // pairs per chunk of the MFMA path
+
+template <bool GU>
+__global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, const uint8_t *__restrict__ Wa,
+                                                  const uint8_t *__restrict__ Wb, MoeWs ws)
+{
+    // The chunk's activation bytes, staged once per block: 1 KiB per sub-block c = 8 * sb + j,
+    // laid out [h][pair][16 B] so that the A operand of lane l is the 16 bytes at l * 16.
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int s_pairs[MF_PCH];
+    __shared__ float s_dx[16][MF_PCH];          // activation scale [super-block][chunk pair]
+    __shared__ float s_up[GU ? 2 : 1][MF_PCH][33];
+    const int u = blockIdx.x;
+    const int U = *ws.nuniq;
+    if (u >= U) return;
+    const int ex = ws.uniq[u], cnt = ws.ucnt[u];   // cnt >= 1 for a chunk that exists
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    if (t < MF_PCH) s_pairs[t] = ws.upairs[u * MF_PCH + min(t, cnt - 1)];   // past cnt: the last pair again
+    __syncthreads();
+
+    const int K = GU ? d : ff, nsb = K / 256, rec = q8k_rec_bytes(nsb);
+    const uint8_t *X = GU ? ws.xrec : ws.xact;
+    for (int i = t; i < nsb * MF_PCH; i += 256) {
+        const int sb = i / MF_PCH, k = i - sb * MF_PCH;
+        const int row = GU ? s_pairs[k] / n_act : s_pairs[k];
+        s_dx[sb][k] = ((const float *)(X + (size_t)row * rec + nsb * 320))[sb];
+    }
+
+    const int col = lane & 31, h = lane >> 5;
+    const int mat = GU ? (w & 1) : 0, nrows = GU ? ff : d;
+    const int r0 = GU ? blockIdx.y * 64 + 32 * (w >> 1) : blockIdx.y * 128 + 32 * w;
+    const size_t erow = (size_t)nsb * 144;
+    const uint8_t *wr = (mat ? Wb : Wa) + (size_t)ex * erow * nrows + (size_t)(r0 + col) * erow;
+
+    // Weight operands in a ring of NB register buffers: the loads run NB - 1 super-blocks ahead
+    // of the math (the last ones reload the final super-block, in bounds).
+    struct Wt {
+        v4i hdr, q[4];
+    };
+    constexpr int NB = 2;
+    Wt wb[NB];
+    auto wload = [&](int sb, Wt &o) {
+        o.hdr = *(const v4i *)(wr + sb * 144);
+#pragma unroll
+        for (int p = 0; p < 4; p++) o.q[p] = *(const v4i *)(wr + sb * 144 + 16 + 32 * p + 16 * h);
+    };
+#pragma unroll
+    for (int i = 0; i < NB - 1; i++) wload(min(i, nsb - 1), wb[i]);
+    {
+        // DMA lane l fetches pair l % 32, bytes 16 * (l / 32) .. +16 of each sub-block.
+        const int arow = GU ? s_pairs[col] / n_act : s_pairs[col];
+        const uint8_t *src = X + (size_t)arow * rec + 16 * h;
+        for (int c = w; c < nsb * 8; c += 4) dma_1k(src + 32 * c, smem + c * 1024);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();   // staged activations, s_dx
+
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    // Sub-block j's dot is issued before sub-block j-1's is scaled (two dot accumulators in
+    // flight) and its A operand is read from LDS one step earlier.  The empty asm statements fix
+    // each partial isc where it is computed and the scheduling barriers keep the steps in place:
+    // otherwise the compiler reassociates the sum and holds all eight dot accumulators at once,
+    // which halves the occupancy.
+    auto compute = [&](int sb, const Wt &o) {
+        const uint8_t *as = smem + sb * 8 * 1024 + lane * 16;
+        int isc[16], sc[8], mm[8];
+        v16i imn = {}, dot[2];
+        v4i a[9];
+#pragma unroll
+        for (int r = 0; r < 16; r++) isc[r] = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int m;
+            gsm(o.hdr, j, sc[j], m);
+            mm[j] = (int)__builtin_amdgcn_perm((uint32_t)m, (uint32_t)m, 0u);   // m in every byte
+        }
+        a[0] = *(const v4i *)as;
+#pragma unroll
+        for (int j = 0; j <= 8; j++) {
+            if (j < 7) a[j + 1] = *(const v4i *)(as + (j + 1) * 1024);
+            if (j < 8) {
+                const v4i b = (o.q[j >> 1] >> (4 * (j & 1))) & 0x0F0F0F0F;
+                dot[j & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], b, v16i{}, 0, 0, 0);
+                imn = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], v4i{mm[j], mm[j], mm[j], mm[j]}, imn, 0, 0, 0);
+            }
+            if (j > 0)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    isc[r] += __mul24(sc[j - 1], dot[(j - 1) & 1][r]);
+                    asm volatile("" : "+v"(isc[r]));
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int k = 8 * (r >> 2) + 4 * h + (r & 3);   // chunk pair of accumulator register r
+            acc[r] = acc[r] + q4k_combine(o.hdr, s_dx[sb][k], isc[r], imn[r]);
+        }
+    };
+    for (int sb0 = 0; sb0 < nsb; sb0 += NB) {
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int sb = sb0 + i;
+            if (sb < nsb) {
+                wload(min(sb + NB - 1, nsb - 1), wb[(i + NB - 1) % NB]);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(sb, wb[i]);
+            }
+        }
+    }
+
+    if constexpr (GU) {
+        if (mat == 1)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s_up[w >> 1][8 * (r >> 2) + 4 * h + (r & 3)][col] = acc[r];
+        __syncthreads();
+        if (mat == 0)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int k = 8 * (r >> 2) + 4 * h + (r & 3);
+                if (k < cnt) ws.act[(size_t)s_pairs[k] * ff + r0 + col] = swiglu(acc[r], s_up[w >> 1][k][col]);
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int k = 8 * (r >> 2) + 4 * h + (r & 3);
+            if (k < cnt) ws.ydn[(size_t)s_pairs[k] * d + r0 + col] = acc[r];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // grid (U_max, d / DN_ROWS).  Units (row, super-block) = DN_ROWS*nsf, 8 lanes each.
 // ------------------------------------------------------------------------------------------------
 // PREQ (more than 8 token rows): the activation rows were quantized once by k_moe_act_q8k; the
@@ -808,7 +960,9 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     ws.nuniq = (int *)take(sizeof(int));
     ws.uniq = (int *)take(sizeof(int) * P);
     ws.ucnt = (int *)take(sizeof(int) * P);
-    ws.upairs = (int *)take(sizeof(int) * ((size_t)P * 8 + 16 * (size_t)n_exp + 16));   // chunks of 8 or 16
+    // chunks of 8 (M <= 8: one per union slot; beyond, at most P/8 + n_exp + 1 of them) or of 32
+    // (at most P/32 + n_exp + 1, and at most P)
+    ws.upairs = (int *)take(sizeof(int) * ((size_t)P * 8 + 32 * (size_t)n_exp + 32));
     ws.xrec = (uint8_t *)take((size_t)M * q8k_rec_bytes(nsb));
     ws.act = (float *)take(sizeof(float) * (size_t)P * ff);
     ws.ydn = (float *)take(sizeof(float) * (size_t)P * d);
@@ -861,6 +1015,27 @@ hipError_t moe_launch_rows(int M, int d, int ff, int n_exp, int n_act, const flo
     return hipGetLastError();
 }
 
+// Many token rows on the matrix cores: routing and grouping as moe_launch_rows, in chunks of 32
+// pairs; gate/up + SwiGLU and the down projection by k_moe_mfma; the same combine.
+hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
+                           float *sw, MoeWs ws, hipStream_t s)
+{
+    const int nsb = d / 256, nsf = ff / 256, P = M * n_act, nrc = (M + 7) / 8;
+    const int Vmax = min(P, (P + MF_PCH - 1) / MF_PCH + n_exp);
+    hipLaunchKernelGGL(k_moe_route, dim3((n_exp + 8 * nsb + 3) / 4, nrc), dim3(256), (size_t)8 * d * 4, s, M, d,
+                       n_exp, hn, R, ws);
+    hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
+    hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
+    hipLaunchKernelGGL(k_moe_mfma<true>, dim3(Vmax, ff / 64), dim3(256), (size_t)nsb * 8192, s, d, ff, n_act,
+                       (const uint8_t *)Wg, (const uint8_t *)Wu, ws);
+    hipLaunchKernelGGL(k_moe_act_q8k, dim3((P * nsf + 3) / 4), dim3(256), 0, s, P, ff, ws);
+    hipLaunchKernelGGL(k_moe_mfma<false>, dim3(Vmax, d / 128), dim3(256), (size_t)nsf * 8192, s, d, ff, n_act,
+                       (const uint8_t *)Wd, (const uint8_t *)nullptr, ws);
+    hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act)
@@ -881,6 +1056,7 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     if (2 * GU_ROWS * nsb > 8 * 8 * GU_NWV || DN_ROWS * nsf > 8 * 32) return hipErrorInvalidValue;
     MoeWs ws = carve((uintptr_t)workspace, M, d, ff, n_exp, n_act, nullptr);
     const int Umax = min(M * n_act, n_exp);
+    if (M >= MF_MIN_ROWS) return moe_launch_mfma(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
     if (M > 8) return moe_launch_rows(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
 
     const int nwaves = n_exp + M * nsb;
