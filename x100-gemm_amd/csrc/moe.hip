@@ -172,6 +172,76 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
 }
 
 // ------------------------------------------------------------------------------------------------
+// Router of many token rows: the logits of k_moe_route (same per-lane order and butterfly, so the
+// same bits) from blocks of RR_ROWS token rows x 4 * epw experts, so that each staged hn row serves
+// up to 32 experts instead of 4 (epw grows with M: more experts per block, fewer blocks).  Wave w
+// computes experts 4 * epw * bx + epw * w .. +epw, the router rows of the next two experts loaded
+// while the current one's dots run.  Blocks bx >= ceil(n_exp / (4 * epw)) quantize the chunk's hn rows to
+// Q8_K (one wave per 256-element block, from global memory).
+// grid (ceil(n_exp / (4 * epw)) + ceil(RR_ROWS * d / 1024), ceil(M / RR_ROWS)).
+// ------------------------------------------------------------------------------------------------
+constexpr int RR_ROWS = 4;
+
+template <int NJ>   // 256-element blocks of d held per lane (d <= 256 * NJ)
+__global__ __launch_bounds__(256) void k_moe_route_rows(int M, int d, int n_exp, int epw, const float *__restrict__ hn,
+                                                        const float *__restrict__ R, MoeWs ws)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const float4 *s_hn = (const float4 *)smem;   // [RR_ROWS][d / 4]
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int nsb = d / 256;
+    const int row0 = blockIdx.y * RR_ROWS, nr = min(RR_ROWS, M - row0);
+    const int ngrp = (n_exp + 4 * epw - 1) / (4 * epw);
+    if ((int)blockIdx.x >= ngrp) {
+        const int q = ((int)blockIdx.x - ngrp) * 4 + w;
+        if (q >= nr * nsb) return;
+        const int m = q / nsb, sb = q - m * nsb;
+        const float4 v = *(const float4 *)(hn + (size_t)(row0 + m) * d + sb * 256 + 4 * lane);
+        uint8_t *rec = ws.xrec + (size_t)(row0 + m) * q8k_rec_bytes(nsb);
+        q8k_wave(v, (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16, (float *)(rec + nsb * 320) + sb);
+        return;
+    }
+
+    // The wave's first router row, then the chunk's hn rows -> LDS.
+    const int e0 = blockIdx.x * 4 * epw + epw * w;
+    auto rload = [&](int e, float4 *rv) {
+        const rsrc_t rr = buf_rsrc(R + (size_t)min(e, n_exp - 1) * d, (uint32_t)d * 4u);   // clamped expert
+#pragma unroll
+        for (int j = 0; j < NJ; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
+    };
+    float4 rv[3][NJ];   // ring: router rows of experts i, i + 1, i + 2
+    rload(e0, rv[0]);
+    if (epw > 1) rload(e0 + 1, rv[1]);
+    for (int ch = w; ch < nr * nsb; ch += 4)
+        dma_1k(hn + (size_t)row0 * d + (size_t)ch * 256 + 4 * lane, smem + ch * 1024);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int e = e0 + i;
+        if (i >= epw) break;
+        if (i + 2 < epw) rload(e + 2, rv[(i + 2) % 3]);
+        if (e < n_exp)
+            for (int m = 0; m < nr; m++) {
+                const float4 *hr = s_hn + m * (d / 4);
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    if (j < nsb) {
+                        const float4 hv = hr[lane + 64 * j];
+                        sum += rv[i % 3][j].x * hv.x;
+                        sum += rv[i % 3][j].y * hv.y;
+                        sum += rv[i % 3][j].z * hv.z;
+                        sum += rv[i % 3][j].w * hv.w;
+                    }
+                sum = wave_sum_bfly_f(sum);
+                if (lane == 0) ws.logits[(size_t)(row0 + m) * n_exp + e] = sum;
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Routing of all M rows from the logits, computed identically by every gate/up block.
 // Softmax over all experts (max-subtract, exp, times 1/sum; lane l of a wave holds experts
 // l, l+64, l+128, l+192 and the sum is lane-partial then butterfly), top-n_act by repeated
@@ -587,22 +657,24 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     __shared__ float s_dx[16][MF_PCH];          // activation scale [super-block][chunk pair]
     __shared__ float s_up[GU ? 2 : 1][MF_PCH][33];
     const int u = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, col = lane & 31, h = lane >> 5;
+    // One round trip for the chunk count, the chunk's expert and size, and its pair col (u <
+    // gridDim.x keeps every index inside the workspace arrays; entries at or past the size are
+    // stale and replaced by pair 0, which every chunk has).
     const int U = *ws.nuniq;
+    const int ex = ws.uniq[u], cnt = ws.ucnt[u];
+    int pc = ws.upairs[u * MF_PCH + col];
     if (u >= U) return;
-    const int ex = ws.uniq[u], cnt = ws.ucnt[u];   // cnt >= 1 for a chunk that exists
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    if (t < MF_PCH) s_pairs[t] = ws.upairs[u * MF_PCH + min(t, cnt - 1)];   // past cnt: the last pair again
-    __syncthreads();
+    pc = __shfl(pc, col < cnt ? lane : 0, 64);
+    if (t < MF_PCH) s_pairs[t] = pc;
 
+    // Second round trip (weights, staged activations, activation scales), then one barrier.
     const int K = GU ? d : ff, nsb = K / 256, rec = q8k_rec_bytes(nsb);
     const uint8_t *X = GU ? ws.xrec : ws.xact;
-    for (int i = t; i < nsb * MF_PCH; i += 256) {
-        const int sb = i / MF_PCH, k = i - sb * MF_PCH;
-        const int row = GU ? s_pairs[k] / n_act : s_pairs[k];
-        s_dx[sb][k] = ((const float *)(X + (size_t)row * rec + nsb * 320))[sb];
-    }
+    const int arow = GU ? pc / n_act : pc;          // activation row of pair col (the A row of lane l)
+    for (int sb = 2 * w + h; sb < nsb; sb += 8)
+        s_dx[sb][col] = ((const float *)(X + (size_t)arow * rec + nsb * 320))[sb];
 
-    const int col = lane & 31, h = lane >> 5;
     const int mat = GU ? (w & 1) : 0, nrows = GU ? ff : d;
     const int r0 = GU ? blockIdx.y * 64 + 32 * (w >> 1) : blockIdx.y * 128 + 32 * w;
     const size_t erow = (size_t)nsb * 144;
@@ -624,12 +696,11 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     for (int i = 0; i < NB - 1; i++) wload(min(i, nsb - 1), wb[i]);
     {
         // DMA lane l fetches pair l % 32, bytes 16 * (l / 32) .. +16 of each sub-block.
-        const int arow = GU ? s_pairs[col] / n_act : s_pairs[col];
         const uint8_t *src = X + (size_t)arow * rec + 16 * h;
         for (int c = w; c < nsb * 8; c += 4) dma_1k(src + 32 * c, smem + c * 1024);
     }
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();   // staged activations, s_dx
+    __syncthreads();   // staged activations, s_dx, s_pairs
 
     float acc[16];
 #pragma unroll
@@ -971,6 +1042,18 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     return ws;
 }
 
+void route_rows(int M, int d, int n_exp, const float *hn, const float *R, MoeWs ws, hipStream_t s)
+{
+    const int epw = max(1, min(8, M / 64));   // experts per wave
+    const int ngrp = (n_exp + 4 * epw - 1) / (4 * epw), nq = (RR_ROWS * (d / 256) + 3) / 4;
+    const dim3 g(ngrp + nq, (M + RR_ROWS - 1) / RR_ROWS);
+    if (d <= 2048)
+        hipLaunchKernelGGL(k_moe_route_rows<8>, g, dim3(256), (size_t)RR_ROWS * d * 4, s, M, d, n_exp, epw, hn, R, ws);
+    else
+        hipLaunchKernelGGL(k_moe_route_rows<16>, g, dim3(256), (size_t)RR_ROWS * d * 4, s, M, d, n_exp, epw, hn, R,
+                           ws);
+}
+
 // More than 8 token rows: route per 8-row chunk, group the pairs by expert into chunks of at
 // most 8, then the routed gate/up (gathering each chunk's rows), the down projection and the
 // combine of the M <= 8 path.
@@ -981,8 +1064,7 @@ hipError_t moe_launch_rows(int M, int d, int ff, int n_exp, int n_act, const flo
     constexpr int PCH = 8;                           // pairs per chunk (16 measured slower: fewer, longer blocks)
     const int nsb = d / 256, nsf = ff / 256, P = M * n_act, nrc = (M + 7) / 8;
     const int Vmax = min(P, (P + PCH - 1) / PCH + n_exp);   // chunks of <= PCH pairs over the experts
-    hipLaunchKernelGGL(k_moe_route, dim3((n_exp + 8 * nsb + 3) / 4, nrc), dim3(256), (size_t)8 * d * 4, s, M, d,
-                       n_exp, hn, R, ws);
+    route_rows(M, d, n_exp, hn, R, ws, s);
     hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
     hipLaunchKernelGGL(k_moe_group<PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
     const int rec = q8k_rec_bytes(nsb), cpr = (rec + 1023) / 1024;
@@ -1023,8 +1105,7 @@ hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const flo
 {
     const int nsb = d / 256, nsf = ff / 256, P = M * n_act, nrc = (M + 7) / 8;
     const int Vmax = min(P, (P + MF_PCH - 1) / MF_PCH + n_exp);
-    hipLaunchKernelGGL(k_moe_route, dim3((n_exp + 8 * nsb + 3) / 4, nrc), dim3(256), (size_t)8 * d * 4, s, M, d,
-                       n_exp, hn, R, ws);
+    route_rows(M, d, n_exp, hn, R, ws, s);
     hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
     hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
     hipLaunchKernelGGL(k_moe_mfma<true>, dim3(Vmax, ff / 64), dim3(256), (size_t)nsb * 8192, s, d, ff, n_act,
