@@ -1,6 +1,7 @@
 // Qwen3-MoE decode layer (the FFN block of qwen_moe.c:294-311) for M token rows: the kernels below
-// for M <= 8, and (moe_launch_rows) the same gate/up and down kernels over expert-grouped chunks of
-// 8 (row, slot) pairs for more rows.
+// for M <= 8; for 9..15 rows (moe_launch_rows) the same gate/up and down kernels over
+// expert-grouped chunks of 8 (row, slot) pairs; from 16 rows (moe_launch_mfma) chunks of 32 pairs
+// on the matrix cores (k_moe_mfma).  Every path gives each row the same bits as a one-row call.
 //
 // Three to five launches on one stream; each kernel only reads what an earlier launch wrote, so
 // no block ever waits for, or signals, another block (no fences, no atomics):
