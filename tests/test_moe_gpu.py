@@ -112,8 +112,8 @@ def test_moe_batched_rows_equal_single_rows(dev, M):
         assert np.array_equal(out[m].view(np.uint32), o1[0].view(np.uint32)), "row %d differs" % m
 
 
-# ---- more than 8 token rows: routing per 8-row chunk, pairs grouped by expert (chunks of 8 pairs
-# below 16 rows, of 32 pairs on the matrix cores from 16 rows) ----
+# ---- 8 or more token rows: routing per 8-row chunk, pairs grouped by expert into chunks of 32 on
+# the matrix cores ----
 @pytest.mark.parametrize("M", [9, 12, 15, 16, 64, 512])
 def test_moe_many_rows_qwen3_shape(dev, M):
     check(M, 128, 2048, 768, 8, seed=510 + M, dev=dev)

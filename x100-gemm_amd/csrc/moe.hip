@@ -1,10 +1,10 @@
 // Qwen3-MoE decode layer (the FFN block of qwen_moe.c:294-311) for M token rows: the kernels below
-// for M <= 8; for 9..15 rows (moe_launch_rows) the same gate/up and down kernels over
-// expert-grouped chunks of 8 (row, slot) pairs; from 16 rows (moe_launch_mfma) chunks of 32 pairs
-// on the matrix cores (k_moe_mfma).  Every path gives each row the same bits as a one-row call.
+// for M < 8, and from 8 rows (moe_launch_mfma) the (row, slot) pairs grouped by expert into
+// chunks of 32 on the matrix cores (k_moe_mfma).  Both give each row the same bits as a one-row
+// call.
 //
-// Three to five launches on one stream; each kernel only reads what an earlier launch wrote, so
-// no block ever waits for, or signals, another block (no fences, no atomics):
+// Below 8 rows, three to five launches on one stream; each kernel only reads what an earlier launch
+// wrote, so no block ever waits for, or signals, another block (no fences, no atomics):
 //   k_moe_route       router logits R.hn (one wave per expert) and the Q8_K form of every hn row.
 //   k_moe_topk        (M > 1) softmax, top-k and the expert union of all rows, once, in one block.
 //   k_moe_gate_up     grid (union slot, GU_ROWS rows of ff).  With one token row every block
@@ -26,7 +26,7 @@ namespace {
 constexpr int GU_ROWS = 8;    // gate/up rows of ff per block
 constexpr int GU_NWV = 4;     // waves per block of k_moe_gate_up (more waves: fewer blocks resident per CU, each re-deriving the routing)
 constexpr int DN_ROWS = 16;   // down rows of d per block
-constexpr int MF_MIN_ROWS = 16;   // token rows from which the expert products run on the matrix cores
+constexpr int MF_MIN_ROWS = 8;   // token rows from which the expert products run on the matrix cores
 
 // Workspace layout (device memory owned by the library, sized by x100_moe_workspace_bytes).
 struct MoeWs {
@@ -36,13 +36,13 @@ struct MoeWs {
     int *nuniq;           // [1]
     int *uniq;            // [P]          expert id of union slot u (P = M*n_act)
     int *ucnt;            // [P]          pairs in union slot u
-    int *upairs;          // [slot][8 or 16] pair ids (m*n_act + a) of union slot u (m ascending
-                          // for M <= 8; chunks of 16 per expert beyond)
+    int *upairs;          // [slot][8] pair ids (m*n_act + a) of union slot u, m ascending (M < 8);
+                          // [chunk][32] from 8 rows (chunks of up to 32 pairs per expert)
     uint8_t *xrec;        // [M][rec]: Q8_K of hn row m = q[nsb][256] | bsum[nsb][16] (int) |
                           // d[nsb] (float), rec = that size rounded up to 16 bytes
     float *act;           // [P][ff]
     float *ydn;           // [P][d]
-    uint8_t *xact;        // [P][recf]: Q8_K of act row p (more than 8 token rows), layout of xrec
+    uint8_t *xact;        // [P][recf]: Q8_K of act row p (8 or more token rows), layout of xrec
 };
 
 inline size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -127,14 +127,10 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
                                                    const float *__restrict__ R, MoeWs ws)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    float4 *s_hn = (float4 *)smem;   // [Mloc][d/4]
+    float4 *s_hn = (float4 *)smem;   // [M][d/4]
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + wave_id();
     const int nsb = d / 256;
-    // grid row y covers token rows row0 .. row0 + Mloc - 1 (8 per grid row)
-    const int row0 = blockIdx.y * 8;
-    M = min(8, M - row0);
-    hn += (size_t)row0 * d;
 
     // The wave's router row (clamped expert; elements past d read as 0 and are not used).
     const int e = min(wave, n_exp - 1);
@@ -162,11 +158,11 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
                     s += rv[j].w * hv.w;
                 }
             s = wave_sum_bfly_f(s);
-            if (lane == 0) ws.logits[(row0 + m) * n_exp + wave] = s;
+            if (lane == 0) ws.logits[m * n_exp + wave] = s;
         }
     } else if (wave < n_exp + M * nsb) {
         const int q = wave - n_exp, m = q / nsb, sb = q - m * nsb;
-        uint8_t *rec = ws.xrec + (size_t)(row0 + m) * q8k_rec_bytes(nsb);
+        uint8_t *rec = ws.xrec + (size_t)m * q8k_rec_bytes(nsb);
         q8k_wave(s_hn[q * 64 + lane], (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16,
                  (float *)(rec + nsb * 320) + sb);
     }
@@ -439,10 +435,10 @@ __global__ __launch_bounds__(512) void k_moe_topk(int M, int n_exp, int n_act, M
 }
 
 // ------------------------------------------------------------------------------------------------
-// More than 8 token rows (verify / prefill).  Routing per 8-row chunk of the grid (the same
+// 8 or more token rows (verify / prefill).  Routing per 8-row chunk of the grid (the same
 // route_block as above), written per row; then the pairs (row, slot) are grouped by expert (the
-// MUL_MAT_ID grouping of ime.cpp:667-697, qwen_moe_hp.c:1674-1700) into chunks of at most 8 pairs
-// per expert ("virtual" union slots), in the union-slot format the gate/up and down kernels read.
+// MUL_MAT_ID grouping of ime.cpp:667-697, qwen_moe_hp.c:1674-1700) into chunks of at most PCH
+// pairs per expert, in the union-slot format (uniq, ucnt, upairs) that k_moe_mfma reads.
 // Each pair is computed exactly as with one token row, so the order of pairs inside an expert's
 // chunks (set by atomics here) does not change any result.
 // ------------------------------------------------------------------------------------------------
@@ -462,8 +458,8 @@ __global__ __launch_bounds__(512) void k_moe_topk_rows(int M, int n_exp, int n_a
     }
 }
 
-// One block of 256 threads (n_exp <= 256): per-expert pair counts, the virtual-slot base of each
-// expert (exclusive scan of ceil(count / 8)), then each pair placed by an atomic cursor.
+// One block of 256 threads (n_exp <= 256): per-expert pair counts, the chunk base of each expert
+// (exclusive scan of ceil(count / PCH)), then each pair placed by an atomic cursor.
 template <int PCH>
 __global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
 {
@@ -498,7 +494,7 @@ __global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
     }
 }
 
-template <int UPL, int NWV, bool ROUTED, bool GATHER = false, int PCH = 8>   // PCH: pairs per union slot
+template <int UPL, int NWV, bool ROUTED>
 __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
                                                      const uint8_t *__restrict__ Wg,
                                                      const uint8_t *__restrict__ Wu, MoeWs ws,
@@ -506,40 +502,25 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ RouteLds rl;
-    __shared__ int s_pairs[PCH], s_cnt;
+    __shared__ int s_pairs[8], s_cnt;
     const int nsb = d / 256;
     const int rec = q8k_rec_bytes(nsb);
 
     // Q8_K records of all M hn rows -> LDS [M][rec], asynchronous (1 KiB chunks, one wave each;
-    // sources clamped to the records, the LDS area is padded to whole chunks).  With GATHER (more
-    // than 8 token rows) only the rows of this block's pairs are staged, row k of the pair list at
-    // k * cpr KiB, once the pair list has been read.
+    // sources clamped to the records, the LDS area is padded to whole chunks).
     const int totv = M * rec / 16;
-    const int cpr = (rec + 1023) / 1024;   // KiB chunks per record
-    if constexpr (!GATHER)
-        for (int ch = wave_id(); ch * 64 < totv; ch += NWV)
-            dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
+    for (int ch = wave_id(); ch * 64 < totv; ch += NWV)
+        dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
 
     const int u = blockIdx.x;
     int U, ex, pr = 0, cnt_r = 0;
     if constexpr (ROUTED) {
-        // routing from k_moe_topk / k_moe_group: union entry, its pairs and the union size in one
-        // round trip (u < gridDim.x <= M * n_act, so every index is inside the workspace arrays)
+        // routing from k_moe_topk: union entry, its pairs and the union size in one round trip
+        // (u < gridDim.x = M * n_act, so every index is inside the workspace arrays)
         ex = ws.uniq[u];
-        pr = ws.upairs[u * PCH + min((int)(threadIdx.x & 63), PCH - 1)];
+        pr = ws.upairs[u * 8 + min((int)(threadIdx.x & 63), 7)];
         cnt_r = ws.ucnt[u];
         U = *ws.nuniq;
-        if constexpr (GATHER) {
-            if (u < U) {
-                const int lane = threadIdx.x & 63;
-                for (int ch = wave_id(); ch < cnt_r * cpr; ch += NWV) {
-                    const int k = ch / cpr, part = ch - k * cpr;
-                    const int row = __shfl(pr, k, 64) / n_act;   // pair k's token row
-                    const int v = min(row * rec / 16 + part * 64 + lane, totv - 1);
-                    dma_1k((const v4i *)ws.xrec + v, smem + ch * 1024);
-                }
-            }
-        }
     } else {
         route_block<NWV>(M, n_exp, n_act, ws.logits, rl);
         if (blockIdx.x == 0 && blockIdx.y == 0) publish_routing(M, n_act, rl, ws, sel_out, sw_out);
@@ -570,7 +551,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     // Pairs (token row m, slot a) of this expert, m ascending (distinct experts per row, so at
     // most one slot per row).
     if constexpr (ROUTED) {
-        if (threadIdx.x < PCH) s_pairs[threadIdx.x] = pr;
+        if (threadIdx.x < 8) s_pairs[threadIdx.x] = pr;
         if (threadIdx.x == 0) s_cnt = cnt_r;
     } else if (threadIdx.x == 0) {
         int c = 0;
@@ -581,13 +562,13 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     }
     __syncthreads();
     const int cnt = s_cnt;
-    float *tv = (float *)(smem + (GATHER ? (size_t)PCH * cpr * 1024 : ((size_t)M * rec + 1023) / 1024 * 1024));
+    float *tv = (float *)(smem + ((size_t)M * rec + 1023) / 1024 * 1024);   // [8][2][GU_ROWS][nsb]
 
     // Token rows outer, units inner (unrolled and branch-free so the scheduler interleaves them):
     // the 8 lanes of a unit store the same value; invalid units write the spare slot.
-    const int tv_spare = PCH * 2 * GU_ROWS * nsb;
+    const int tv_spare = 8 * 2 * GU_ROWS * nsb;
     for (int k = 0; k < cnt; k++) {
-        const uint8_t *xr = smem + (GATHER ? (size_t)k * cpr * 1024 : (size_t)(s_pairs[k] / n_act) * rec);
+        const uint8_t *xr = smem + (size_t)(s_pairs[k] / n_act) * rec;
 #pragma unroll
         for (int c = 0; c < UPL; c++) {
             const int un = c * 8 * NWV + w * 8 + (lane >> 3);
@@ -615,7 +596,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     __syncthreads();
 }
 
-// Q8_K of every pair's activation row, once (more than 8 token rows): wave q quantizes block
+// Q8_K of every pair's activation row, once (8 or more token rows): wave q quantizes block
 // q % nsf of pair q / nsf with q8k_wave, into the pair's record of ws.xact.
 __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 {
@@ -782,17 +763,15 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
 // ------------------------------------------------------------------------------------------------
 // grid (U_max, d / DN_ROWS).  Units (row, super-block) = DN_ROWS*nsf, 8 lanes each.
 // ------------------------------------------------------------------------------------------------
-// PREQ (more than 8 token rows): the activation rows were quantized once by k_moe_act_q8k; the
-// block stages its pairs' records (row k at k * cprf KiB) instead of quantizing them again.
-template <int UPL, bool PREQ = false, int PCH = 8>   // PCH: pairs per union slot (16 only with PREQ)
-__global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *__restrict__ Wd, MoeWs ws, int P)
+template <int UPL>
+__global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *__restrict__ Wd, MoeWs ws)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int u = blockIdx.x;
     // Union slot metadata in one round trip (entries of slots >= U are stale and unused).
     const int U = *ws.nuniq;
     const int ex = ws.uniq[u], cnt = ws.ucnt[u];
-    const int prl = ws.upairs[u * PCH + (threadIdx.x & (PCH - 1))];   // lane l holds pair l % PCH of the slot
+    const int prl = ws.upairs[u * 8 + (threadIdx.x & 7)];   // lane l holds pair l % 8 of the slot
     if (u >= U) return;
     const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
     const int nsf = ff / 256;
@@ -831,28 +810,17 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
         const int q = (q0) + 4 * j + w;                                                           \
         if (q < nq) q8k_wave(v[j], aq + q * 256, abs_ + q * 16, ad + q);                          \
     }
-    const int recf = q8k_rec_bytes(nsf), cprf = (recf + 1023) / 1024;
-    if constexpr (PREQ) {
-        const int totv = P * recf / 16;
-        for (int ch = w; ch < cnt * cprf; ch += 4) {
-            const int k = ch / cprf, part = ch - k * cprf;
-            const int v = min(__builtin_amdgcn_readlane(prl, k) * recf / 16 + part * 64 + lane, totv - 1);
-            dma_1k((const v4i *)ws.xact + v, smem + ch * 1024);
-        }
-        tv = (float *)(smem + (size_t)PCH * cprf * 1024);
-    } else {
-        X100_ACT_LOADS(0)
-        __builtin_amdgcn_sched_barrier(0);
-        X100_ACT_QUANT(0)
-        for (int q0 = 16; q0 < nq; q0 += 16) {
-            X100_ACT_LOADS(q0)
-            X100_ACT_QUANT(q0)
-        }
+    X100_ACT_LOADS(0)
+    __builtin_amdgcn_sched_barrier(0);
+    X100_ACT_QUANT(0)
+    for (int q0 = 16; q0 < nq; q0 += 16) {
+        X100_ACT_LOADS(q0)
+        X100_ACT_QUANT(q0)
     }
 #undef X100_ACT_LOADS
 #undef X100_ACT_QUANT
-    __shared__ int s_pr[PCH];
-    if (threadIdx.x < PCH) s_pr[threadIdx.x] = prl;
+    __shared__ int s_pr[8];
+    if (threadIdx.x < 8) s_pr[threadIdx.x] = prl;
     __syncthreads();
 
     // As in gate/up: pairs outer, units inner, branch-free (spare slot 8 * nunits).
@@ -863,16 +831,8 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
             const bool valid = un < nunits;
             const int sb = valid ? un % nsf : 0;
             int isc, imn;
-            if constexpr (PREQ) {
-                const uint8_t *xr = smem + (size_t)k * cprf * 1024;
-                q4k_unit_dot(hdr[c], qs[c], (const int8_t *)xr + sb * 256, (const int *)(xr + nsf * 256) + sb * 16, i,
-                             isc, imn);
-                tv[valid ? k * nunits + un : PCH * nunits] =
-                    q4k_combine(hdr[c], ((const float *)(xr + nsf * 320))[sb], isc, imn);
-            } else {
-                q4k_unit_dot(hdr[c], qs[c], aq + (k * nsf + sb) * 256, abs_ + (k * nsf + sb) * 16, i, isc, imn);
-                tv[valid ? k * nunits + un : 8 * nunits] = q4k_combine(hdr[c], ad[k * nsf + sb], isc, imn);
-            }
+            q4k_unit_dot(hdr[c], qs[c], aq + (k * nsf + sb) * 256, abs_ + (k * nsf + sb) * 16, i, isc, imn);
+            tv[valid ? k * nunits + un : 8 * nunits] = q4k_combine(hdr[c], ad[k * nsf + sb], isc, imn);
         }
     }
     __syncthreads();
@@ -1032,8 +992,8 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     ws.nuniq = (int *)take(sizeof(int));
     ws.uniq = (int *)take(sizeof(int) * P);
     ws.ucnt = (int *)take(sizeof(int) * P);
-    // chunks of 8 (M <= 8: one per union slot; beyond, at most P/8 + n_exp + 1 of them) or of 32
-    // (at most P/32 + n_exp + 1, and at most P)
+    // union slots of 8 (M < 8: at most P of them) or chunks of 32 (at most P/32 + n_exp + 1, and
+    // at most P)
     ws.upairs = (int *)take(sizeof(int) * ((size_t)P * 8 + 32 * (size_t)n_exp + 32));
     ws.xrec = (uint8_t *)take((size_t)M * q8k_rec_bytes(nsb));
     ws.act = (float *)take(sizeof(float) * (size_t)P * ff);
@@ -1055,51 +1015,9 @@ void route_rows(int M, int d, int n_exp, const float *hn, const float *R, MoeWs 
                            ws);
 }
 
-// More than 8 token rows: route per 8-row chunk, group the pairs by expert into chunks of at
-// most 8, then the routed gate/up (gathering each chunk's rows), the down projection and the
-// combine of the M <= 8 path.
-hipError_t moe_launch_rows(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
-                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
-                           float *sw, MoeWs ws, hipStream_t s)
-{
-    constexpr int PCH = 8;                           // pairs per chunk (16 measured slower: fewer, longer blocks)
-    const int nsb = d / 256, nsf = ff / 256, P = M * n_act, nrc = (M + 7) / 8;
-    const int Vmax = min(P, (P + PCH - 1) / PCH + n_exp);   // chunks of <= PCH pairs over the experts
-    route_rows(M, d, n_exp, hn, R, ws, s);
-    hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
-    hipLaunchKernelGGL(k_moe_group<PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
-    const int rec = q8k_rec_bytes(nsb), cpr = (rec + 1023) / 1024;
-    const size_t lds_gu = (size_t)PCH * cpr * 1024 + ((size_t)PCH * 2 * GU_ROWS * nsb + 1) * 4;
-    const int upl_gu = (2 * GU_ROWS * nsb + 8 * GU_NWV - 1) / (8 * GU_NWV);
-    const dim3 g_gu(Vmax, ff / GU_ROWS), b_gu(64 * GU_NWV);
-    const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
-#define X100_GUR(U) hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, true, true, PCH>), g_gu, b_gu, lds_gu, s, M, d, ff, \
-                                       n_exp, n_act, wg, wu, ws, sel, sw)
-    switch (upl_gu) {
-    case 1: X100_GUR(1); break;
-    case 2: X100_GUR(2); break;
-    case 3: case 4: X100_GUR(4); break;
-    default: X100_GUR(8); break;
-    }
-#undef X100_GUR
-    hipLaunchKernelGGL(k_moe_act_q8k, dim3((P * nsf + 3) / 4), dim3(256), 0, s, P, ff, ws);
-    const int recf = q8k_rec_bytes(nsf), cprf = (recf + 1023) / 1024;
-    const size_t lds_dn = (size_t)PCH * cprf * 1024 + ((size_t)PCH * DN_ROWS * nsf + 1) * 4;
-    const int upl_dn = (DN_ROWS * nsf + 31) / 32;
-    const dim3 g_dn(Vmax, d / DN_ROWS);
-    const uint8_t *wd = (const uint8_t *)Wd;
-    switch (upl_dn) {
-    case 1: hipLaunchKernelGGL((k_moe_down<1, true, PCH>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, P); break;
-    case 2: hipLaunchKernelGGL((k_moe_down<2, true, PCH>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, P); break;
-    case 3: case 4: hipLaunchKernelGGL((k_moe_down<4, true, PCH>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, P); break;
-    default: hipLaunchKernelGGL((k_moe_down<8, true, PCH>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, P); break;
-    }
-    hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
-    return hipGetLastError();
-}
-
-// Many token rows on the matrix cores: routing and grouping as moe_launch_rows, in chunks of 32
-// pairs; gate/up + SwiGLU and the down projection by k_moe_mfma; the same combine.
+// Eight or more token rows, on the matrix cores: router logits and Q8_K records per 4-row chunk,
+// softmax / top-k per 8-row chunk, the pairs grouped by expert into chunks of 32, gate/up + SwiGLU
+// and the down projection by k_moe_mfma, then the weighted combine.
 hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                            const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
                            float *sw, MoeWs ws, hipStream_t s)
@@ -1139,7 +1057,6 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     MoeWs ws = carve((uintptr_t)workspace, M, d, ff, n_exp, n_act, nullptr);
     const int Umax = min(M * n_act, n_exp);
     if (M >= MF_MIN_ROWS) return moe_launch_mfma(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
-    if (M > 8) return moe_launch_rows(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
 
     const int nwaves = n_exp + M * nsb;
     hipLaunchKernelGGL(k_moe_route, dim3((nwaves + 3) / 4), dim3(256), (size_t)M * d * 4, s, M, d, n_exp, hn, R, ws);
@@ -1216,10 +1133,10 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     const dim3 g_dn(Umax, d / DN_ROWS);
     const uint8_t *wd = (const uint8_t *)Wd;
     switch (upl_dn) {
-    case 1: hipLaunchKernelGGL((k_moe_down<1>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, M * n_act); break;
-    case 2: hipLaunchKernelGGL((k_moe_down<2>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, M * n_act); break;
-    case 3: case 4: hipLaunchKernelGGL((k_moe_down<4>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, M * n_act); break;
-    default: hipLaunchKernelGGL((k_moe_down<8>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws, M * n_act); break;
+    case 1: hipLaunchKernelGGL((k_moe_down<1>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 2: hipLaunchKernelGGL((k_moe_down<2>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 3: case 4: hipLaunchKernelGGL((k_moe_down<4>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    default: hipLaunchKernelGGL((k_moe_down<8>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
     }
     err = hipGetLastError();
     if (err != hipSuccess) return err;
