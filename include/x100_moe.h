@@ -9,10 +9,10 @@
  * Experts are Q4_K blocks in the ggml 3-D layout, experts outermost (qwen_moe.c:220-222):
  *   Wg, Wu: [n_exp][ff][d/256] blocks, Wd: [n_exp][d][ff/256] blocks.
  * Activations are quantized to Q8_K per row (hn before gate/up, act before down) with the
- * scalar path's rounding; rows that pick the same expert share one pass over its weights (up to
- * 8 rows per pass: beyond 8 token rows the (row, slot) pairs are grouped by expert into chunks,
- * the MUL_MAT_ID grouping of ime.cpp:667-697; from 16 rows chunks of 32 pairs run on the matrix
- * cores).  Each row's result is the same as a one-row call's, bit for bit.
+ * scalar path's rounding; rows that pick the same expert share one pass over its weights (below
+ * 8 token rows all rows at once; from 8 rows the (row, slot) pairs are grouped by expert into
+ * chunks of 32 on the matrix cores, the MUL_MAT_ID grouping of ime.cpp:667-697).  Each row's
+ * result is the same as a one-row call's, bit for bit.
  *
  * All pointers are device pointers.  sel / sw (may be NULL) receive [M][n_act] expert ids and
  * renormalised weights.  Limits: 1 <= M <= X100_MOE_MAX_ROWS, 1 <= n_act <= 8, n_act <= n_exp <= 256,
