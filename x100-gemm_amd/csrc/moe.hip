@@ -687,6 +687,9 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     float acc[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    // Accumulator registers 4q .. 4q+3 hold chunk pairs 8q .. 8q+7: only the first nq quads hold
+    // pairs of the chunk, so the scaling and the combine skip the others (a block-uniform branch).
+    const int nq = (cnt + 7) / 8;
     // Sub-block j's dot is issued before sub-block j-1's is scaled (two dot accumulators in
     // flight) and its A operand is read from LDS one step earlier.  The empty asm statements fix
     // each partial isc where it is computed and the scheduling barriers keep the steps in place:
@@ -716,17 +719,23 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
             }
             if (j > 0)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    isc[r] += __mul24(sc[j - 1], dot[(j - 1) & 1][r]);
-                    asm volatile("" : "+v"(isc[r]));
-                }
+                for (int qd = 0; qd < 4; qd++)
+                    if (qd < nq)
+#pragma unroll
+                        for (int r = 4 * qd; r < 4 * qd + 4; r++) {
+                            isc[r] += __mul24(sc[j - 1], dot[(j - 1) & 1][r]);
+                            asm volatile("" : "+v"(isc[r]));
+                        }
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int k = 8 * (r >> 2) + 4 * h + (r & 3);   // chunk pair of accumulator register r
-            acc[r] = acc[r] + q4k_combine(o.hdr, s_dx[sb][k], isc[r], imn[r]);
-        }
+        for (int qd = 0; qd < 4; qd++)
+            if (qd < nq)
+#pragma unroll
+                for (int r = 4 * qd; r < 4 * qd + 4; r++) {
+                    const int k = 8 * (r >> 2) + 4 * h + (r & 3);   // chunk pair of accumulator register r
+                    acc[r] = acc[r] + q4k_combine(o.hdr, s_dx[sb][k], isc[r], imn[r]);
+                }
     };
     for (int sb0 = 0; sb0 < nsb; sb0 += NB) {
 #pragma unroll
