@@ -189,14 +189,16 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, 
         }
         const int hq = w + 4 * g;
         if (hq < gpr && grp == 0) {
-            // per head: m[nch], l[nch], then o[dim][nch] (a dimension's chunks contiguous)
+            // per head: m[nch], l[nch], then o[nch][HD] (a chunk's 128 dimensions contiguous, so the
+            // combine reads each chunk with whole-line loads)
             float *P = part + (size_t)(kvh * gpr + hq) * nch * (HD + 2);
             if (sl == 0) {
                 P[c] = m[g];
                 P[nch + c] = l[g];
             }
+            float *Pc = P + 2 * (size_t)nch + (size_t)c * HD + sl * DL;   // 4-byte aligned only
 #pragma unroll
-            for (int t = 0; t < DL; t++) P[(size_t)(2 + sl * DL + t) * nch + c] = o[g][t];
+            for (int t = 0; t < DL; t++) Pc[t] = o[g][t];
         }
     }
 }
@@ -204,7 +206,8 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, 
 // Merge the chunks of one query head: att = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).  The
 // maximum M (exact in any order) and the weights e_c are computed once per chunk, spread over the
 // threads, into LDS; the two sums then run in chunk order in every thread (the order the oracle
-// uses), reading a dimension's chunks contiguously.  nch <= 512.
+// uses), thread t reading dimension t of each chunk (one contiguous 512-byte row per chunk for
+// the block).  nch <= 512.
 __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ part, int nch, float *__restrict__ att)
 {
     __shared__ float se[512], red[HD / 64];
@@ -228,13 +231,13 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     for (int k = 1; k < HD / 64; k++) M = fmaxf(M, red[k]);
     for (int c = t; c < nch; c += HD) se[c] = exp_r(se[c] - M);
     __syncthreads();
-    const float *Lc = P + nch, *Oc = P + (size_t)(2 + t) * nch;
+    const float *Lc = P + nch, *Oc = P + 2 * (size_t)nch + t;
     float L = 0.0f, O = 0.0f;
 #pragma unroll 16
     for (int c = 0; c < nch; c++) {
         const float e = se[c];
         L += Lc[c] * e;
-        O += Oc[c] * e;
+        O += Oc[(size_t)c * HD] * e;
     }
     att[(size_t)h * HD + t] = O / L;
 }
