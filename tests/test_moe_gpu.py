@@ -126,6 +126,13 @@ def test_moe_many_rows_small_shapes(dev, M, n_exp, d, ff, n_act):
     check(M, n_exp, d, ff, n_act, seed=620 + M + n_exp, dev=dev)
 
 
+@pytest.mark.parametrize("M", [3, 16])
+def test_moe_largest_hidden_and_ff(dev, M):
+    # d = ff = 4096, the largest the kernels take: 16 super-blocks per row (router rows of 16
+    # blocks per lane, 128 KiB of staged activations per matrix-core block)
+    check(M, 4, 4096, 4096, 2, seed=760, dev=dev)
+
+
 def test_moe_many_rows_residual(dev):
     check(33, 128, 2048, 768, 8, seed=530, dev=dev, residual=True)
 
