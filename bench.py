@@ -10,13 +10,14 @@ timed with HIP events on the launch stream.  The same JSON line carries:
                 oracle's restatement when that is absent) on a bounded row sample, 1 core;
   extra         the other measured shapes: skinny 8x4096x4096 GEMM, Q4_0 / Q4_K / Q3_K GEMV at
                 M = 1 and 4, the int8 path (Q6_K lm_head, Q5_K attn_output, Q8_0 attn_k of
-                Qwen3-30B-A3B, requantized to Q8_0 at load), the MoE layer at 64 and 512 token rows
-                (verify / prefill), the whole decoder layer (attention +
-                MoE, 1024 and 4096 cached positions), the int4 / int8 tile GEMV of bench/q4_gemv.c, the Qwen3-30B-A3B MoE
-                decode layer at M = 1 and 4, each beside its scalar CPU time, and the per-token
-                decode weight stream of bench/moe_decode.c (x100-gemm_amd/moe_decode.py).  GEMV and MoE run back-to-back in a captured graph over weight
-                copies totalling more than 256 MB (so the 256 MB Infinity Cache cannot hold them);
-                single-launch latency is reported separately.
+                Qwen3-30B-A3B, requantized to Q8_0 at load), the int4 / int8 tile GEMV of
+                bench/q4_gemv.c, the Qwen3-30B-A3B MoE decode layer at M = 1, 4 and 8 (decode and
+                speculative verify) and at 64 and 512 token rows (verify / prefill), the whole
+                decoder layer (attention + MoE, 1024 and 4096 cached positions), each beside its
+                scalar CPU time, and the per-token decode weight stream of bench/moe_decode.c
+                (x100-gemm_amd/moe_decode.py).  GEMV and MoE run back-to-back in a captured graph
+                over weight copies totalling more than 256 MB (so the 256 MB Infinity Cache cannot
+                hold them); single-launch latency is reported separately.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
        python bench.py --probe     (for rocprofv3 --pmc: `--steps` GEMM 4096^3 launches, then one
@@ -351,7 +352,7 @@ def bench_extra(torch, timer, dev, args):
         layers.append([b.clone() for b in base] if li else base)
     dR = torch.from_numpy(R).to(dev)
     n_h = 48
-    for M in (1, 4):
+    for M in (1, 4, 8):   # decode, and speculative verify of 4 and 8 rows (8: on the matrix cores)
         hns = synth.normal_f32(900 + M, (n_h, M, d))
         dh = torch.from_numpy(hns).to(dev)
         out = torch.empty((M, d), dtype=torch.float32, device=dev)
@@ -378,7 +379,7 @@ def bench_extra(torch, timer, dev, args):
                       "bytes_per_layer": byts, "cpu_us_1core": cpu_us}
         log("%s: %.2f us/layer  U=%.1f  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
             key, us, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
-    # many token rows (verify / prefill): pairs grouped by expert in chunks of 8
+    # many token rows (verify / prefill): pairs grouped by expert in chunks of 32, matrix cores
     for M in (64, 512):
         n_h = 6
         hns = synth.normal_f32(950 + M, (n_h, M, d))
