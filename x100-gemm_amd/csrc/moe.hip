@@ -627,13 +627,17 @@ __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 // r0 + 32 * w .. +32.  grid (chunks, ff / 64 or d / 128).
 // ------------------------------------------------------------------------------------------------
 constexpr int MF_PCH = 32;   // pairs per chunk of the MFMA path
+// Super-blocks in the first staged half of k_moe_mfma's activations (even, at most nsb).
+__host__ __device__ inline int mf_half(int nsb) { return min(nsb, ((nsb + 1) / 2 + 1) & ~1); }
 
 template <bool GU>
 __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, const uint8_t *__restrict__ Wa,
                                                   const uint8_t *__restrict__ Wb, MoeWs ws)
 {
-    // The chunk's activation bytes, staged once per block: 1 KiB per sub-block c = 8 * sb + j,
-    // laid out [h][pair][16 B] so that the A operand of lane l is the 16 bytes at l * 16.
+    // The chunk's activation bytes, staged per block in two halves (super-blocks 0 .. nh1-1, then
+    // nh1 .. nsb-1, so that the LDS of a block is half the chunk's and more blocks fit a CU):
+    // 1 KiB per sub-block c = 8 * sb + j, laid out [h][pair][16 B] so that the A operand of lane l
+    // is the 16 bytes at l * 16.
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int s_pairs[MF_PCH];
     __shared__ float s_dx[16][MF_PCH];          // activation scale [super-block][chunk pair]
@@ -676,11 +680,13 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     };
 #pragma unroll
     for (int i = 0; i < NB - 1; i++) wload(min(i, nsb - 1), wb[i]);
-    {
-        // DMA lane l fetches pair l % 32, bytes 16 * (l / 32) .. +16 of each sub-block.
-        const uint8_t *src = X + (size_t)arow * rec + 16 * h;
-        for (int c = w; c < nsb * 8; c += 4) dma_1k(src + 32 * c, smem + c * 1024);
-    }
+    // DMA lane l fetches pair l % 32, bytes 16 * (l / 32) .. +16 of each sub-block.
+    const uint8_t *src = X + (size_t)arow * rec + 16 * h;
+    const int nh1 = mf_half(nsb);   // even, so the halves meet between two ring steps
+    auto stage = [&](int sb0, int sb1) {
+        for (int c = 8 * sb0 + w; c < 8 * sb1; c += 4) dma_1k(src + 32 * c, smem + (c - 8 * sb0) * 1024);
+    };
+    stage(0, nh1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // staged activations, s_dx, s_pairs
 
@@ -696,7 +702,7 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     // otherwise the compiler reassociates the sum and holds all eight dot accumulators at once,
     // which halves the occupancy.
     auto compute = [&](int sb, const Wt &o) {
-        const uint8_t *as = smem + sb * 8 * 1024 + lane * 16;
+        const uint8_t *as = smem + (sb < nh1 ? sb : sb - nh1) * 8 * 1024 + lane * 16;
         int isc[16], sc[8], mm[8];
         v16i imn = {}, dot[2];
         v4i a[9];
@@ -738,6 +744,12 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
                 }
     };
     for (int sb0 = 0; sb0 < nsb; sb0 += NB) {
+        if (sb0 == nh1) {   // second half of the activations into the same LDS
+            __syncthreads();
+            stage(nh1, nsb);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
             const int sb = sb0 + i;
@@ -1036,10 +1048,10 @@ hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const flo
     route_rows(M, d, n_exp, hn, R, ws, s);
     hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
     hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
-    hipLaunchKernelGGL(k_moe_mfma<true>, dim3(Vmax, ff / 64), dim3(256), (size_t)nsb * 8192, s, d, ff, n_act,
+    hipLaunchKernelGGL(k_moe_mfma<true>, dim3(Vmax, ff / 64), dim3(256), (size_t)mf_half(nsb) * 8192, s, d, ff, n_act,
                        (const uint8_t *)Wg, (const uint8_t *)Wu, ws);
     hipLaunchKernelGGL(k_moe_act_q8k, dim3((P * nsf + 3) / 4), dim3(256), 0, s, P, ff, ws);
-    hipLaunchKernelGGL(k_moe_mfma<false>, dim3(Vmax, d / 128), dim3(256), (size_t)nsf * 8192, s, d, ff, n_act,
+    hipLaunchKernelGGL(k_moe_mfma<false>, dim3(Vmax, d / 128), dim3(256), (size_t)mf_half(nsf) * 8192, s, d, ff, n_act,
                        (const uint8_t *)Wd, (const uint8_t *)nullptr, ws);
     hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
     return hipGetLastError();
