@@ -227,13 +227,9 @@ X100_DEV int big_b_chunk(int k, int c) { return c ^ (2 * (k & 7)); }
 //   chunk c -> granule 8*(r&1) + (c ^ ((r>>1)&7)).
 X100_DEV int big_a2_chunk(int r, int c) { return c ^ ((r >> 1) & 7); }
 
-// The LDS destination (wave-uniform) is passed in M0 through the "{m0}" operand, so the compiler
-// knows the register is written.
-X100_DEV void dma16(const void *gsrc, uint32_t lds_base)
-{
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(lds_base) : "memory");
-}
-// Same with a wave-uniform 64-bit base address and a 32-bit per-lane byte offset.
+// Global -> LDS DMA of 16 bytes per lane: a wave-uniform 64-bit base address plus a 32-bit per-lane
+// byte offset.  The LDS destination (wave-uniform) is passed in M0 through the "{m0}" operand, so
+// the compiler knows the register is written.
 X100_DEV void dma16s(uint32_t voff, const void *sbase, uint32_t lds_base)
 {
     asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");

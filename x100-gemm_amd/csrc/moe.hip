@@ -940,7 +940,7 @@ __global__ __launch_bounds__(64 * FD_NWV) void k_moe_down_fused(int M, int d, in
         act_loads(q0, av);
         act_quant(q0, av);
     }
-    if (threadIdx.x < P) s_w[threadIdx.x] = ws.sw[threadIdx.x];
+    if ((int)threadIdx.x < P) s_w[threadIdx.x] = ws.sw[threadIdx.x];
     __syncthreads();
 
 #pragma unroll
