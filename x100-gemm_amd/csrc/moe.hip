@@ -458,17 +458,22 @@ __global__ __launch_bounds__(512) void k_moe_topk_rows(int M, int n_exp, int n_a
     }
 }
 
-// One block of 256 threads (n_exp <= 256): per-expert pair counts, the chunk base of each expert
-// (exclusive scan of ceil(count / PCH)), then each pair placed by an atomic cursor.
-template <int PCH>
-__global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
+// Groups the P pairs (pair p chose expert sel(p)) by expert into chunks of at most PCH: per-expert
+// counts by LDS atomics, the chunk base of each expert (exclusive scan of ceil(count / PCH)), then
+// each pair placed by an atomic cursor.  Threads 0 .. 255 of the block take part (n_exp <= 256).
+template <int PCH, class Sel>
+X100_DEV void group_pairs(int P, int n_exp, Sel sel, MoeWs ws)
 {
     __shared__ int s_cnt[256], s_cur[256], s_vbase[257];
     const int t = threadIdx.x;
-    s_cnt[t] = 0;
-    s_cur[t] = 0;
+    const bool on = t < 256;
+    if (on) {
+        s_cnt[t] = 0;
+        s_cur[t] = 0;
+    }
     __syncthreads();
-    for (int p = t; p < P; p += 256) atomicAdd(&s_cnt[ws.sel[p]], 1);
+    if (on)
+        for (int p = t; p < P; p += 256) atomicAdd(&s_cnt[sel(p)], 1);
     __syncthreads();
     if (t == 0) {
         int v = 0;
@@ -487,11 +492,37 @@ __global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
             ws.ucnt[v0 + k] = min(PCH, c - PCH * k);
         }
     }
-    for (int p = t; p < P; p += 256) {
-        const int e = ws.sel[p];
-        const int k = atomicAdd(&s_cur[e], 1);
-        ws.upairs[(s_vbase[e] + k / PCH) * PCH + (k % PCH)] = p;
+    if (on)
+        for (int p = t; p < P; p += 256) {
+            const int e = sel(p);
+            const int k = atomicAdd(&s_cur[e], 1);
+            ws.upairs[(s_vbase[e] + k / PCH) * PCH + (k % PCH)] = p;
+        }
+}
+
+// One block of 256 threads: the grouping of all P pairs from ws.sel.
+template <int PCH>
+__global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
+{
+    group_pairs<PCH>(P, n_exp, [&](int p) { return ws.sel[p]; }, ws);
+}
+
+// Up to 8 token rows: k_moe_topk_rows and k_moe_group in one block (one launch fewer), the
+// grouping reading the selections from LDS.
+template <int PCH>
+__global__ __launch_bounds__(512) void k_moe_topk_group(int M, int n_exp, int n_act, MoeWs ws,
+                                                        int *__restrict__ sel_out, float *__restrict__ sw_out)
+{
+    __shared__ RouteLds rl;
+    route_block<8>(M, n_exp, n_act, ws.logits, rl);
+    const int t = threadIdx.x, P = M * n_act;
+    if (t < P) {
+        ws.sel[t] = rl.sel[t];
+        ws.sw[t] = rl.w[t];
+        if (sel_out) sel_out[t] = rl.sel[t];
+        if (sw_out) sw_out[t] = rl.w[t];
     }
+    group_pairs<PCH>(P, n_exp, [&](int p) { return rl.sel[p]; }, ws);
 }
 
 template <int UPL, int NWV, bool ROUTED>
@@ -1046,8 +1077,12 @@ hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const flo
     const int nsb = d / 256, nsf = ff / 256, P = M * n_act, nrc = (M + 7) / 8;
     const int Vmax = min(P, (P + MF_PCH - 1) / MF_PCH + n_exp);
     route_rows(M, d, n_exp, hn, R, ws, s);
-    hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
-    hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
+    if (M <= 8) {
+        hipLaunchKernelGGL(k_moe_topk_group<MF_PCH>, dim3(1), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
+    } else {
+        hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
+        hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
+    }
     hipLaunchKernelGGL(k_moe_mfma<true>, dim3(Vmax, ff / 64), dim3(256), (size_t)mf_half(nsb) * 8192, s, d, ff, n_act,
                        (const uint8_t *)Wg, (const uint8_t *)Wu, ws);
     hipLaunchKernelGGL(k_moe_act_q8k, dim3((P * nsf + 3) / 4), dim3(256), 0, s, P, ff, ws);
