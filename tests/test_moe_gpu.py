@@ -126,6 +126,13 @@ def test_moe_many_rows_small_shapes(dev, M, n_exp, d, ff, n_act):
     check(M, n_exp, d, ff, n_act, seed=620 + M + n_exp, dev=dev)
 
 
+@pytest.mark.parametrize("M,n_exp,d,ff,n_act", [(8, 16, 512, 4096, 4),    # 16 super-blocks of ff, two halves
+                                                (8, 200, 256, 256, 6)])
+def test_moe_eight_rows_small_shapes(dev, M, n_exp, d, ff, n_act):
+    # 8 rows on the matrix cores at small shapes (ff of 16 super-blocks: activations in two halves)
+    check(M, n_exp, d, ff, n_act, seed=780 + n_exp, dev=dev)
+
+
 @pytest.mark.parametrize("M", [3, 16])
 def test_moe_largest_hidden_and_ff(dev, M):
     # d = ff = 4096, the largest the kernels take: 16 super-blocks per row (router rows of 16
