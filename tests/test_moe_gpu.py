@@ -133,6 +133,12 @@ def test_moe_eight_rows_small_shapes(dev, M, n_exp, d, ff, n_act):
     check(M, n_exp, d, ff, n_act, seed=780 + n_exp, dev=dev)
 
 
+def test_moe_few_rows_large_ff(dev):
+    # 3 rows x 8 experts with ff = 4096: the fused down projection does not fit LDS, so the
+    # union-slot down kernel and the separate combine run
+    check(3, 16, 512, 4096, 8, seed=790, dev=dev)
+
+
 @pytest.mark.parametrize("M", [3, 16])
 def test_moe_largest_hidden_and_ff(dev, M):
     # d = ff = 4096, the largest the kernels take: 16 super-blocks per row (router rows of 16
