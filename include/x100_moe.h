@@ -10,7 +10,7 @@
  *   Wg, Wu: [n_exp][ff][d/256] blocks, Wd: [n_exp][d][ff/256] blocks.
  * Activations are quantized to Q8_K per row (hn before gate/up, act before down) with the
  * scalar path's rounding; rows that pick the same expert share one pass over its weights (below
- * 4 token rows all rows at once; from 4 rows the (row, slot) pairs are grouped by expert into
+ * 5 token rows all rows at once; from 5 rows the (row, slot) pairs are grouped by expert into
  * chunks of 32 on the matrix cores, the MUL_MAT_ID grouping of ime.cpp:667-697).  Each row's
  * result is the same as a one-row call's, bit for bit.
  *

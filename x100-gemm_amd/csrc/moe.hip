@@ -1,9 +1,9 @@
 // Qwen3-MoE decode layer (the FFN block of qwen_moe.c:294-311) for M token rows: the kernels below
-// for M < 4, and from 4 rows (moe_launch_mfma) the (row, slot) pairs grouped by expert into
+// for M < 5, and from 5 rows (moe_launch_mfma) the (row, slot) pairs grouped by expert into
 // chunks of 32 on the matrix cores (k_moe_mfma).  Both give each row the same bits as a one-row
 // call.
 //
-// Below 4 rows, three to five launches on one stream; each kernel only reads what an earlier launch
+// Below 5 rows, three to five launches on one stream; each kernel only reads what an earlier launch
 // wrote, so no block ever waits for, or signals, another block (no fences, no atomics):
 //   k_moe_route       router logits R.hn (one wave per expert) and the Q8_K form of every hn row.
 //   k_moe_topk        (M > 1) softmax, top-k and the expert union of all rows, once, in one block.
@@ -27,7 +27,7 @@ namespace {
 constexpr int GU_ROWS = 8;    // gate/up rows of ff per block
 constexpr int GU_NWV = 4;     // waves per block of k_moe_gate_up (more waves: fewer blocks resident per CU, each re-deriving the routing)
 constexpr int DN_ROWS = 16;   // down rows of d per block
-constexpr int MF_MIN_ROWS = 4;   // token rows from which the expert products run on the matrix cores
+constexpr int MF_MIN_ROWS = 5;   // token rows from which the expert products run on the matrix cores
 
 // Workspace layout (device memory owned by the library, sized by x100_moe_workspace_bytes).
 struct MoeWs {
@@ -37,13 +37,13 @@ struct MoeWs {
     int *nuniq;           // [1]
     int *uniq;            // [P]          expert id of union slot u (P = M*n_act)
     int *ucnt;            // [P]          pairs in union slot u
-    int *upairs;          // [slot][8] pair ids (m*n_act + a) of union slot u, m ascending (M < 4);
-                          // [chunk][32] from 4 rows (chunks of up to 32 pairs per expert)
+    int *upairs;          // [slot][8] pair ids (m*n_act + a) of union slot u, m ascending (M < 5);
+                          // [chunk][32] from 5 rows (chunks of up to 32 pairs per expert)
     uint8_t *xrec;        // [M][rec]: Q8_K of hn row m = q[nsb][256] | bsum[nsb][16] (int) |
                           // d[nsb] (float), rec = that size rounded up to 16 bytes
     float *act;           // [P][ff]
     float *ydn;           // [P][d]
-    uint8_t *xact;        // [P][recf]: Q8_K of act row p (4 or more token rows), layout of xrec
+    uint8_t *xact;        // [P][recf]: Q8_K of act row p (5 or more token rows), layout of xrec
 };
 
 inline size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -436,7 +436,7 @@ __global__ __launch_bounds__(512) void k_moe_topk(int M, int n_exp, int n_act, M
 }
 
 // ------------------------------------------------------------------------------------------------
-// 4 or more token rows (verify / prefill).  Routing per 8-row chunk of the grid (the same
+// 5 or more token rows (verify / prefill).  Routing per 8-row chunk of the grid (the same
 // route_block as above), written per row; then the pairs (row, slot) are grouped by expert (the
 // MUL_MAT_ID grouping of ime.cpp:667-697, qwen_moe_hp.c:1674-1700) into chunks of at most PCH
 // pairs per expert, in the union-slot format (uniq, ucnt, upairs) that k_moe_mfma reads.
@@ -628,7 +628,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     __syncthreads();
 }
 
-// Q8_K of every pair's activation row, once (4 or more token rows): wave q quantizes block
+// Q8_K of every pair's activation row, once (5 or more token rows): wave q quantizes block
 // q % nsf of pair q / nsf with q8k_wave, into the pair's record of ws.xact.
 __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 {
@@ -1045,7 +1045,7 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     ws.nuniq = (int *)take(sizeof(int));
     ws.uniq = (int *)take(sizeof(int) * P);
     ws.ucnt = (int *)take(sizeof(int) * P);
-    // union slots of 8 (M < 4: at most P of them) or chunks of 32 (at most P/32 + n_exp + 1, and
+    // union slots of 8 (M < 5: at most P of them) or chunks of 32 (at most P/32 + n_exp + 1, and
     // at most P)
     ws.upairs = (int *)take(sizeof(int) * ((size_t)P * 8 + 32 * (size_t)n_exp + 32));
     ws.xrec = (uint8_t *)take((size_t)M * q8k_rec_bytes(nsb));
@@ -1068,7 +1068,7 @@ void route_rows(int M, int d, int n_exp, const float *hn, const float *R, MoeWs 
                            ws);
 }
 
-// Four or more token rows, on the matrix cores: router logits and Q8_K records per 4-row chunk,
+// Five or more token rows, on the matrix cores: router logits and Q8_K records per 4-row chunk,
 // softmax / top-k per 8-row chunk, the pairs grouped by expert into chunks of 32, gate/up + SwiGLU
 // and the down projection by k_moe_mfma, then the weighted combine.
 hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
