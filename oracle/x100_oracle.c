@@ -15,34 +15,24 @@
  * fp16 helpers
  * ------------------------------------------------------------------------------------------- */
 
-/* Round-to-nearest-even fp32 -> fp16.  Replaces the truncating f32_to_f16 of
- * qwen_moe_hp.c:71-79 (see header).  Checked against numpy.float16 in tests/test_oracle.py. */
+/* fp32 -> fp16 as the reference's f32_to_f16 (qwen_moe_hp.c:71-79) converts: the fp16 exponent is
+ * the fp32 one rebiased; a normal result keeps the top 10 mantissa bits (the other 13 are
+ * dropped, never rounded up); below the fp16 normal range the mantissa with its leading one is
+ * shifted into the subnormal field (again dropping bits), and below 2^-24 the result is a signed
+ * zero; an exponent past the fp16 range (|f| >= 2^16, inf, NaN) gives a signed infinity.  For
+ * |f| < 2^16 this is round-toward-zero.  Checked in tests/test_oracle.py against an independent
+ * round-toward-zero restatement and hand-computed cases. */
 uint16_t orc_f32_to_f16(float f)
 {
     uint32_t x;
     memcpy(&x, &f, 4);
-    uint32_t sign = (x >> 16) & 0x8000u;
-    uint32_t ax = x & 0x7fffffffu;
-    if (ax >= 0x7f800000u) {                       /* inf / nan */
-        if (ax == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
-        return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
-    }
-    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   /* >= 65520 rounds to inf */
-    if (ax < 0x38800000u) {                        /* below 2^-14: fp16 subnormal or zero */
-        if (ax < 0x33000000u) return (uint16_t)sign;            /* <= 2^-25 rounds to 0 */
-        uint32_t e = ax >> 23;
-        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
-        uint32_t shift = 126u - e;                 /* value / 2^-24 = m >> shift */
-        uint32_t r = m >> shift;
-        uint32_t rem = m & ((1u << shift) - 1u);
-        uint32_t half = 1u << (shift - 1u);
-        if (rem > half || (rem == half && (r & 1u))) r++;
-        return (uint16_t)(sign | r);
-    }
-    uint32_t r = (ax >> 13) - ((127u - 15u) << 10);
-    uint32_t rem = ax & 0x1fffu;
-    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
-    return (uint16_t)(sign | r);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int e16 = (int)((x >> 23) & 0xffu) - 127 + 15;
+    const uint32_t frac = x & 0x7fffffu;
+    if (e16 >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e16 > 0) return (uint16_t)(sign | ((uint32_t)e16 << 10) | (frac >> 13));
+    if (e16 < -10) return (uint16_t)sign;
+    return (uint16_t)(sign | ((frac | 0x800000u) >> (14 - e16)));
 }
 
 /* Exact fp16 -> fp32; same decoding as f16_to_f32 in qwen_moe_hp.c:80-86 and f16f in
@@ -339,7 +329,7 @@ int orc_dequant_row(int qtype, const void *blocks, int K, float *out)
  * Quantizers
  * ------------------------------------------------------------------------------------------- */
 
-/* quantize_q8_0_native, qwen_moe_hp.c:408-414 (fp16 d rounded to nearest even). */
+/* quantize_q8_0_native, qwen_moe_hp.c:408-414 (fp16 d by the truncating f32_to_f16). */
 void orc_quantize_q8_0(const float *x, int K, void *out)
 {
     orc_q8_0 *b = (orc_q8_0 *)out;
@@ -440,7 +430,7 @@ int orc_requant_q8_0(int qtype, int N, int K, const void *W, void *Wq8)
     return 0;
 }
 
-/* quantize_q4_0_native, qwen_moe_hp.c:100-109 (fp16 d rounded to nearest even). */
+/* quantize_q4_0_native, qwen_moe_hp.c:100-109 (fp16 d by the truncating f32_to_f16). */
 void orc_quantize_q4_0(const float *w, int K, void *out)
 {
     orc_q4_0 *b = (orc_q4_0 *)out;

@@ -8,10 +8,12 @@
  * Every function cites the reference file:line whose algorithm it restates.  Numeric conventions
  * that the reference leaves open (or gets differently in different files) are fixed here and
  * implemented identically by the HIP kernels:
- *   - fp32 -> fp16 is round-to-nearest-even (the reference's f32_to_f16 at qwen_moe_hp.c:71-79
- *     truncates; hardware v_cvt_f16_f32 and ggml round to nearest even);
- *   - Q8_0 activations: amax floored at 1e-6, d = amax/127, q = rint(x * (1/d)) (half-even),
- *     clamp [-128,127], d stored as fp16 (qwen_moe_hp.c:408-414);
+ *   - fp32 -> fp16 is the reference's f32_to_f16 (qwen_moe_hp.c:71-79): the magnitude is
+ *     truncated (round toward zero, fp16 subnormals included), |f| >= 2^16 and NaN give a signed
+ *     infinity.  Every fp16 scale the reference writes goes through it (quantize_q8_0_native,
+ *     quantize_q4_0_native, and lin_new_i8's requantization via quantize_q8_0_native);
+ *   - Q8_0 activations: amax floored at 1e-6, d = amax/127, q = rint(x * (1/d)) (half-even,
+ *     with the fp32 d), clamp [-128,127], d stored as fp16 (qwen_moe_hp.c:408-414);
  *   - Q8_K activations: amax (no floor), d = amax/127 kept in fp32, q = roundf(x * (1/d))
  *     (half away from zero), clamp [-128,127], all-zero block -> d = 0, q = 0
  *     (qwen_moe_q3k.c:612-624; rvv_kernels.cpp:1820-1828); bsums are the plain (positive)
@@ -48,8 +50,8 @@ extern "C" {
 #define ORC_Q6_K 14
 #define ORC_Q8_K 15
 
-/* fp16 <-> fp32.  f16_to_f32 follows qwen_moe_hp.c:80-86 (exact); f32_to_f16 rounds to nearest
- * even (see header note). */
+/* fp16 <-> fp32.  f16_to_f32 follows qwen_moe_hp.c:80-86 (exact); f32_to_f16 follows
+ * qwen_moe_hp.c:71-79 (truncation, see header note). */
 uint16_t orc_f32_to_f16(float f);
 float    orc_f16_to_f32(uint16_t h);
 

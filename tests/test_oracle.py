@@ -3,7 +3,8 @@
 Each oracle function is checked against something other than itself:
   gemm_ref_i8         numpy int64 matmul (closed form), the reference's own gemm_ref_i8 built from
                       its sources (oracle/_ref), golden vectors from that build, invariants.
-  fp16 conversions    numpy.float16 (IEEE round-to-nearest-even), exhaustive over fp16.
+  fp16 conversions    f16->f32: numpy.float16, exhaustive; f32->f16: the reference's truncation,
+                      against a round-toward-zero restatement and hand-computed cases.
   Q8_0 / Q8_K         independent numpy restatements + hand-worked tie cases (rint vs roundf).
   Q4_0 / Q4_K / Q3_K  hand-built blocks with known values; numpy encoders written from the block
   dequant             layout (not from the C decoder); random blocks vs numpy decoders.
@@ -18,6 +19,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as ol
+import refseq
 import synth
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -101,24 +103,47 @@ def test_f16_to_f32_exhaustive():
     assert np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])
 
 
-def test_f32_to_f16_round_nearest_even():
+np_f16_trunc = refseq.f16_trunc   # round-toward-zero restated from its definition
+
+
+def test_f32_to_f16_truncates_like_reference():
+    """orc_f32_to_f16 is the reference's truncating f32_to_f16 (qwen_moe_hp.c:71-79)."""
     o = ol.oracle()
     rng = np.random.default_rng(1)
     bits = rng.integers(0, 2**32, size=200000, dtype=np.uint64).astype(np.uint32)
-    special = np.array([0x00000000, 0x80000000, 0x33000000, 0x33000001, 0x337fffff, 0x33800000,
-                        0x38800000, 0x387fffff, 0x387fe000, 0x387ff000, 0x477fe000, 0x477fefff,
-                        0x477ff000, 0x477ff001, 0x7f800000, 0xff800000, 0x3f800000, 0x3f801000,
-                        0x3f803000, 0x3f802000, 0x3f806000], dtype=np.uint32)
-    # every halfway case in one binade and around the subnormal range
-    ties = (np.arange(0x3f800000, 0x3f800000 + (1 << 23), 0x1000, dtype=np.uint64) | 0x1000).astype(np.uint32)
-    sub = np.arange(0x33000000, 0x38900000, 0x800, dtype=np.uint32)
-    allb = np.concatenate([bits, special, ties[:4000], sub])
-    f = allb.view(np.float32)
-    keep = ~np.isnan(f)
-    f = f[keep]
-    ref = f.astype(np.float16).view(np.uint16)
+    # every discarded-bit pattern of the top 3 dropped bits in one binade, the subnormal range
+    # and the edges of the fp16 range
+    binade = (np.arange(0x3f800000, 0x3f800000 + (1 << 23), 0x400, dtype=np.uint64)).astype(np.uint32)
+    sub = np.arange(0x32800000, 0x38900000, 0x800, dtype=np.uint32)
+    edges = np.array([0x477fe000, 0x477fefff, 0x477ff000, 0x477fffff, 0x47800000, 0x7f7fffff,
+                      0x7f800000, 0xff800000, 0x7fc00000, 0xffc00001], dtype=np.uint32)
+    f = np.concatenate([bits, binade, sub, edges]).view(np.float32)
+    ref = np_f16_trunc(f)
     got = np.array([o.orc_f32_to_f16(float(v)) for v in f], dtype=np.uint16)
     assert np.array_equal(got, ref)
+
+
+def test_f32_to_f16_hand_computed_truncation_cases():
+    """Values worked out by hand from the fp16 format (ulp 2^-10 at 1.0, subnormal step 2^-24)."""
+    o = ol.oracle()
+    cases = [
+        (1.0, 0x3C00),
+        (1.0 + 0.75 * 2.0**-10, 0x3C00),      # dropped part 0.75 ulp: truncated, RNE gives 0x3C01
+        (1.0 + 1.5 * 2.0**-10, 0x3C01),       # tie: RNE goes to the even 0x3C02
+        (-(1.0 + 0.999 * 2.0**-10), 0xBC00),  # sign kept, magnitude truncated
+        (127.0 / 127.0 * 0.0234375, 0x2600),  # 3 * 2^-7 exactly representable
+        (3.75 * 2.0**-24, 0x0003),            # subnormal d: 3 steps (RNE gives 4)
+        (2.0**-24, 0x0001),
+        (0.999 * 2.0**-24, 0x0000),           # below the smallest subnormal
+        (1e-6 / 127.0, 0x0000),               # the Q8_0 amax floor of 1e-6: d rounds to zero
+        (2.0**-14 * (1 - 2.0**-23), 0x03FF),  # just below the normal range: all subnormal bits
+        (65535.0, 0x7BFF),                    # 65504, the largest finite fp16
+        (65536.0, 0x7C00),                    # exponent past the fp16 range
+        (-0.0, 0x8000),
+        (float("nan"), 0x7C00),
+    ]
+    for v, want in cases:
+        assert o.orc_f32_to_f16(v) == want, (v, hex(o.orc_f32_to_f16(v)), hex(want))
 
 
 # ------------------------------------------------------------------------------------------------
@@ -130,7 +155,7 @@ def np_q8_0(x):
     d = (amax / np.float32(127.0)).astype(np.float32)
     inv = np.where(d != 0, np.float32(1.0) / d, np.float32(0)).astype(np.float32)
     q = np.clip(np.rint(b * inv[:, None]), -128, 127).astype(np.int8)
-    return d.astype(np.float16).view(np.uint16), q
+    return np_f16_trunc(d), q
 
 
 def np_q8_K(x):
@@ -469,7 +494,7 @@ def test_qgemv_special_cases():
 @pytest.mark.parametrize("qtype,K", [(synth.Q8_0, 256), (synth.Q5_K, 512), (synth.Q6_K, 512)])
 def test_requant_q8_0_bound_and_idempotence(qtype, K):
     """Load-time requantization to Q8_0: every 32-group's largest element maps to +-127, every
-    element is within half a step (plus the fp16 rounding of the step) of the fp32 dequantized
+    element is within half a step (plus the fp16 truncation of the step) of the fp32 dequantized
     value, and requantizing the result again changes nothing (the loader's lossless claim for
     well-formed Q8_0 data, qwen_moe_q3k.c:520-524)."""
     N = 5
@@ -480,7 +505,10 @@ def test_requant_q8_0_bound_and_idempotence(qtype, K):
     amax = np.maximum(np.abs(w).max(axis=2), 1e-6)
     step = amax / 127.0
     d16 = R["d"].view(np.float16).astype(np.float64)
-    assert np.all(np.abs(d16 - step) <= step * 2.0 ** -11)
+    # the stored step is the fp32 step truncated to fp16: never above it, less than one fp16 ulp
+    # (2^-10 relative) below it
+    assert np.all(d16 <= step * (1 + 2.0 ** -23))
+    assert np.all(d16 > step * (1 - 2.0 ** -10) * (1 - 2.0 ** -23))
     assert np.all(np.abs(R["qs"]).max(axis=2) == 127)
     err = np.abs(R["qs"].astype(np.float64) * d16[..., None] - w)
     assert np.all(err <= 0.5 * step[..., None] * (1 + 1e-6) + 127 * np.abs(d16 - step)[..., None])
@@ -495,7 +523,8 @@ def test_requant_q8_0_rescales_narrow_blocks():
     W["qs"][0, 0] = np.arange(-16, 16)
     W["qs"][0, 0, 0] = 64
     R = ol.requant_q8_0(synth.Q8_0, W)
-    assert R["d"][0, 0] == np.float16(np.float32(64.0) / np.float32(127.0)).view(np.uint16)
+    assert R["d"][0, 0] == np_f16_trunc(np.float32(64.0) / np.float32(127.0))
+    assert R["d"][0, 0] == 0x3808   # 64/127 = 2^-1 * 1.0078740: exponent field 14, mantissa 8.06 -> 8
     inv = np.float32(1.0) / np.float32(np.float32(64.0) / np.float32(127.0))
     expect = np.clip(np.rint(W["qs"][0, 0].astype(np.float32) * inv), -128, 127)
     assert np.array_equal(R["qs"][0, 0], expect.astype(np.int8))
@@ -539,8 +568,8 @@ def test_qgemv_i8_path_special_cases():
     W["dmin"] = F16_HALF
     y = ol.qgemv(synth.Q5_K, W, x)
     xa = np.stack([(lambda b: (b["qs"].astype(np.float64) * b["s"].astype(np.float64)[:, None]).sum())(ol.quantize_i8(r)) for r in x])
-    # requantized weight: every element -0.5 -> d' = fp16(0.5/127), q = -127
-    dq = float(np.float16(np.float32(0.5) / np.float32(127.0))) * -127
+    # requantized weight: every element -0.5 -> d' = fp16 truncation of 0.5/127, q = -127
+    dq = float(np_f16_trunc(np.float32(0.5) / np.float32(127.0)).view(np.float16)) * -127
     np.testing.assert_allclose(y, np.repeat((dq * xa)[:, None], 3, axis=1), rtol=1e-5)
 
 

@@ -41,15 +41,28 @@ def check(qtype, N, K, M, seed, dev, exact=None):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "not bit-identical"
 
 
+def check_reference_order(qtype, N, K, M, seed, dev):
+    """The benchmark configurations: bit-identical to the oracle, and within rel 1e-3 / abs 1e-4
+    of the reference's own checking arithmetic (tests/refseq.py) on every element."""
+    import refseq
+    check(qtype, N, K, M, seed, dev)
+    W = synth.quant_weight(qtype, N, K, seed)
+    x = synth.normal_f32(seed + 1, (M, K))
+    got = gpu_qgemv(qtype, W, x, dev)
+    ref = refseq.gemv(qtype, W, x)
+    bad = np.abs(got - ref) > ATOL + RTOL * np.abs(ref)
+    assert not bad.any(), "%d elements outside tolerance of the reference order" % int(bad.sum())
+
+
 @pytest.mark.parametrize("M", [1, 4])
 def test_q4_0_4096(dev, M):
-    check(synth.Q4_0, 4096, 4096, M, seed=300 + M, dev=dev)
+    check_reference_order(synth.Q4_0, 4096, 4096, M, seed=300 + M, dev=dev)
 
 
 @pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q3_K])
 @pytest.mark.parametrize("M", [1, 4])
 def test_kquant_6144x2048(dev, qtype, M):
-    check(qtype, 6144, 2048, M, seed=400 + M + qtype, dev=dev)
+    check_reference_order(qtype, 6144, 2048, M, seed=400 + M + qtype, dev=dev)
 
 
 @pytest.mark.parametrize("qtype,N,K,M", [

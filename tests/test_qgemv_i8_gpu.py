@@ -51,6 +51,44 @@ def test_requant_matches_oracle(dev, qtype, N, K):
     assert np.array_equal(qs, ref["qs"]), "values differ"
 
 
+def test_requant_scale_truncation_edges(dev):
+    """The device's fp16 truncation (the reference's f32_to_f16) over every branch: Q8_0 blocks
+    whose requantized step amax/127 is fp16-normal with dropped bits, fp16-subnormal, below the
+    smallest subnormal (the 1e-6 floor of an all-zero block) and at the top of the fp16 range;
+    checked against the oracle and against the truncation's closed form."""
+    import refseq
+    rng = np.random.default_rng(5)
+    nb = 64 * 8
+    W = np.zeros((64, 8), synth.DT_Q8_0)
+    q = rng.integers(-120, 121, size=(64, 8, 32)).astype(np.int8)
+    q[:, 4:, 0] = 127                                  # amax = 127 * d: the step is d itself
+    W["qs"] = q                                        # elsewhere the step drops bits
+    # input scales (fp16 bits): normal, subnormal, tiny subnormal, large
+    d_in = np.concatenate([rng.integers(0x0400, 0x7800, size=nb // 4),      # normal
+                           rng.integers(0x0001, 0x0400, size=nb // 4),      # subnormal
+                           rng.integers(0x0001, 0x0008, size=nb // 4),      # a few subnormal steps
+                           rng.integers(0x7800, 0x7BFF, size=nb // 4)]).astype(np.uint16)
+    W["d"] = d_in.reshape(64, 8)
+    W["qs"][5] = 0                                     # all-zero rows: amax floored at 1e-6
+    W["d"][6] = 0x7BFF                                 # 65504 * 127 / 127
+    packed = gpu_pack(synth.Q8_0, W, 256, dev)
+    ref = ol.requant_q8_0(synth.Q8_0, W).reshape(-1)
+    d = packed[:nb * 2].view(np.uint16)
+    assert np.array_equal(d, ref["d"]), "scales differ from the oracle"
+    assert np.array_equal(d, refseq.requant_q8_0(synth.Q8_0, W)[0].reshape(-1)), "scales differ from the truncation"
+    assert (d[5 * 8:6 * 8] == 0).all()                 # 1e-6 / 127 truncates to zero
+    qs_off = (nb * 2 + 255) // 256 * 256
+    assert np.array_equal(packed[qs_off:qs_off + nb * 32].view(np.int8).reshape(nb, 32), ref["qs"])
+    # a step of 2^16 or more (only reachable from a K-quant source) gives infinity
+    W6 = synth.quant_weight(synth.Q6_K, 1, 256, seed=3)
+    W6["d"] = 0x7BFF
+    W6["scales"] = 127
+    W6["ql"], W6["qh"] = 0xFF, 0xFF                    # q = 63 - 32 = 31 everywhere
+    d6 = gpu_pack(synth.Q6_K, W6, 256, dev)[:16].view(np.uint16)
+    assert np.array_equal(d6, ol.requant_q8_0(synth.Q6_K, W6)["d"].reshape(-1))
+    assert (d6 == 0x7C00).all()
+
+
 @pytest.mark.parametrize("qtype,N,K,M", [
     (synth.Q8_0, 512, 2048, 1),            # attn_k of Qwen3-30B-A3B
     (synth.Q5_K, 2048, 4096, 1),           # attn_output

@@ -585,7 +585,7 @@ __global__ void k_requant_q8_0(size_t ngrp, const uint8_t *__restrict__ src, uin
     for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
     const float d = amax / 127.0f;
     const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-    dq[g] = f2h(d);
+    dq[g] = f2h_trunc(d);   // quantize_q8_0_native's f32_to_f16 (qwen_moe_hp.c:71-79)
     uint32_t pk[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {

@@ -20,8 +20,23 @@ enum { X100_Q4_0 = 2, X100_Q8_0 = 8, X100_Q3_K = 11, X100_Q4_K = 12, X100_Q5_K =
 
 // fp16 bits -> fp32 (exact).
 X100_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32 in the default rounding mode).
-X100_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// fp32 -> fp16 bits as the reference's f32_to_f16 (qwen_moe_hp.c:71-79) converts, which every
+// fp16 scale of its Q8_0 quantizer goes through: the 13 low mantissa bits are dropped (a normal
+// result is the magnitude truncated, never rounded up), results below the normal range are
+// truncated into the subnormal field and below 2^-24 to a signed zero, and exponents past the
+// fp16 range (|f| >= 2^16, inf, NaN) give a signed infinity.  Selects only, no branches.
+X100_DEV uint16_t f2h_trunc(float f)
+{
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int e16 = (int)((x >> 23) & 0xffu) - 112;
+    const uint32_t frac = x & 0x7fffffu;
+    const uint32_t normal = sign | ((uint32_t)e16 << 10) | (frac >> 13);
+    const uint32_t sub = sign | ((frac | 0x800000u) >> min(max(14 - e16, 0), 31));
+    uint32_t r = e16 > 0 ? normal : (e16 < -10 ? sign : sub);
+    r = e16 >= 31 ? (sign | 0x7c00u) : r;
+    return (uint16_t)r;
+}
 
 // 4-way int8 dot product with int32 accumulate: acc + sum_i a.b[i]*b.b[i] (signed bytes).
 X100_DEV int dot4(int a, int b, int acc) { return __builtin_amdgcn_sdot4(a, b, acc, false); }
@@ -214,8 +229,9 @@ X100_DEV void x_load(rsrc_t xr, int c0, float4 (&v)[XPT])
 // Branch-free stores (so the unrolled iterations can be interleaved by the scheduler): blocks past
 // the end go to the spare slot (index M*nb / M*nsb) that the LDS layout provides, and values that
 // several lanes hold (d, sum) are stored by all of them.
-// F16D: the block scale is rounded to fp16 (quantize_q8_0_native, qwen_moe_hp.c:408-414) or kept
-// in fp32 (pack_A_i8, qwen_moe_q3k.c:420-427); the q values are the same either way.
+// F16D: the block scale is stored as fp16 by the reference's truncating conversion
+// (quantize_q8_0_native, qwen_moe_hp.c:408-414) or kept in fp32 (pack_A_i8,
+// qwen_moe_q3k.c:420-427); the q values are the same either way (they use the fp32 scale).
 template <int XPT, int NT = 256, bool F16D = true>
 X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, int8_t *xlo,
                              int8_t *xhi, float *xd, int *xs)
@@ -238,7 +254,7 @@ X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, 
                                 ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
         int8_t *dst = pos < 16 ? xlo + b * 16 + pos : xhi + b * 16 + (pos - 16);
         *(uint32_t *)dst = packed;
-        xd[b] = F16D ? h2f(f2h(d)) : d;   // the 8 lanes of a block hold the same d and sum
+        xd[b] = F16D ? h2f(f2h_trunc(d)) : d;   // the 8 lanes of a block hold the same d and sum
         xs[b] = s;
     }
 }
