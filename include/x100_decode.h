@@ -13,12 +13,19 @@
  * computed over position chunks and merged, equal to the sequential one within rounding).
  *
  * All pointers are device pointers; the caches are head-major [n_head_kv][ctx][head_dim] fp32
- * (the layout of qwen_moe_hp.c:1469-1474).  The library keeps a per-device workspace (grown on
- * demand), so calls on one device must not overlap.  Asynchronous on stream.
+ * (the layout of qwen_moe_hp.c:1469-1474).  Asynchronous on stream.  Every argument is checked
+ * before any work is enqueued: an error return leaves h and the caches as they were.
+ *
+ * Scratch: the _ws forms take a caller device buffer (256-byte aligned) of at least
+ * x100_decode_workspace_bytes(cfg) bytes (the reference's forward takes its scratch vectors hn, q,
+ * k, v, att, tmp, g, u, eout, xt from the caller, qwen_moe.c:272-273), allocate nothing and never
+ * synchronise, so a captured graph can hold them; overlapping calls need distinct buffers.  The plain forms use the
+ * library's per-(device, stream) workspace, as moe_layer_hip does (x100_moe.h).
  */
 #ifndef X100_HIP_DECODE_H
 #define X100_HIP_DECODE_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -56,6 +63,16 @@ int x100_attn_decode_hip(const x100_layer_cfg *cfg, const x100_layer_weights *w,
  * n_act entries each, may be NULL) receive the chosen experts and their weights. */
 int x100_decode_layer_hip(const x100_layer_cfg *cfg, const x100_layer_weights *w, int pos, float *h,
                           int *sel, float *sw, void *stream);
+
+/* Scratch bytes of the _ws forms for this configuration (the attention half's share, plus the
+ * MoE block's when cfg's n_exp / n_act / ff describe one); 0 for an invalid configuration. */
+size_t x100_decode_workspace_bytes(const x100_layer_cfg *cfg);
+
+/* x100_attn_decode_hip / x100_decode_layer_hip on caller scratch ws of ws_bytes bytes. */
+int x100_attn_decode_hip_ws(const x100_layer_cfg *cfg, const x100_layer_weights *w, int pos, float *h,
+                            void *ws, size_t ws_bytes, void *stream);
+int x100_decode_layer_hip_ws(const x100_layer_cfg *cfg, const x100_layer_weights *w, int pos, float *h,
+                             int *sel, float *sw, void *ws, size_t ws_bytes, void *stream);
 
 #ifdef __cplusplus
 }

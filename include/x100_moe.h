@@ -16,9 +16,17 @@
  *
  * All pointers are device pointers.  sel / sw (may be NULL) receive [M][n_act] expert ids and
  * renormalised weights.  Limits: 1 <= M <= X100_MOE_MAX_ROWS, 1 <= n_act <= 8, n_act <= n_exp <= 256,
- * d % 256 == 0, ff % 256 == 0, d <= 4096, ff <= 4096.  The library keeps a device workspace per
- * GPU (allocated on the first call with a given shape); calls that overlap on one GPU must use
- * the same stream.
+ * d % 256 == 0, ff % 256 == 0, d <= 4096, ff <= 4096; hn, R, Wg, Wu, Wd 16-byte aligned.
+ *
+ * Scratch: the reference's linears take caller scratch (the packed activation and partial sums,
+ * qwen_moe.c:90-101; per-thread buffers, qwen_moe_hp.c:712-718).  moe_layer_hip_ws does the same:
+ * the caller passes a device buffer of moe_layer_workspace_bytes(...) bytes; the call allocates
+ * nothing and never synchronises, so it can be captured into a HIP graph at any shape, and calls
+ * on different streams run concurrently when their buffers differ.  moe_layer_hip is the
+ * convenience form: the library keeps one workspace per (device, stream), grown by hipMalloc when
+ * a larger shape arrives (outgrown buffers are kept until the process ends, so graphs captured
+ * earlier stay valid); a call that would grow it while its stream is being captured returns
+ * X100_EINVAL.  Workspace contents never need initialising.
  */
 #ifndef X100_HIP_MOE_H
 #define X100_HIP_MOE_H
@@ -32,9 +40,20 @@
 extern "C" {
 #endif
 
+/* Replaces the MoE block of forward(), qwen_moe.c:294-311 (and qwen_moe_hp.c:1512-1570). */
 int moe_layer_hip(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                   const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
                   int *sel, float *sw, void *stream);
+
+/* Device scratch bytes moe_layer_hip_ws needs for this shape; 0 outside the limits above. */
+size_t moe_layer_workspace_bytes(int M, int d, int ff, int n_exp, int n_act);
+
+/* moe_layer_hip on caller scratch ws (device, 256-byte aligned, ws_bytes >=
+ * moe_layer_workspace_bytes(M, d, ff, n_exp, n_act)), in the way lin_mm takes xt
+ * (qwen_moe.c:101).  Calls whose executions overlap must use distinct buffers. */
+int moe_layer_hip_ws(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                     const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
+                     int *sel, float *sw, void *ws, size_t ws_bytes, void *stream);
 
 #ifdef __cplusplus
 }

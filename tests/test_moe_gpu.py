@@ -90,7 +90,7 @@ def test_moe_small_shapes(dev, M, n_exp, d, ff, n_act):
 
 
 def test_moe_repeat_calls_stable(dev):
-    # completion counters are reset by the kernels themselves: repeated calls give the same bits
+    # every kernel writes the scratch it reads within the call: repeated calls give the same bits
     L = layer(16, 512, 256, 700, dev)
     hn = synth.normal_f32(701, (2, 512))
     a = gpu_moe(hn, L, 4, dev)[0]

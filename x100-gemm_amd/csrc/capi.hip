@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <vector>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -54,37 +55,76 @@ int check_device()
     return X100_OK;
 }
 
-// Per-device workspaces (grown on demand, zero-filled so completion counters start at 0): slot 0
-// for the MoE block, slot 1 for the attention half of the decode layer.
-struct Workspace {
-    void *ptr = nullptr;
-    size_t bytes = 0;
+// Workspaces of the convenience entry points (moe_layer_hip, x100_attn_decode_hip,
+// x100_decode_layer_hip), one per (device, stream), so that calls on different streams never
+// share scratch.  A workspace only grows: the larger one is allocated with hipMalloc and the old
+// one is kept until the process ends (never freed, no synchronisation), because work already
+// queued on the stream, or a graph captured earlier at a smaller shape, may still use it.  The
+// kernels write every workspace byte they read within the same call, so the contents never
+// need clearing.  Growth is impossible while the stream is being captured: such a call returns
+// X100_EINVAL (callers that capture graphs use the _ws entry points with their own scratch).
+struct StreamWs {
+    int dev;
+    hipStream_t stream;
+    void *ptr;
+    size_t bytes;
 };
 std::mutex g_ws_mu;
-Workspace g_ws[64][2];
+std::vector<StreamWs> g_ws;       // live workspace per (device, stream)
+std::vector<void *> g_ws_retired;  // outgrown workspaces, kept alive
 
-int dev_workspace(int slot, size_t need, void **out)
+int stream_workspace(hipStream_t stream, size_t need, void **out)
 {
     int dev = 0;
     X100_TRY(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64) return X100_ENODEV;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace &w = g_ws[dev][slot];
-    if (w.bytes < need) {
-        if (w.ptr) {
-            X100_TRY(hipDeviceSynchronize());
-            X100_TRY(hipFree(w.ptr));
-            w.ptr = nullptr;
-            w.bytes = 0;
-        }
-        void *p = nullptr;
-        X100_TRY(hipMalloc(&p, need));
-        X100_TRY(hipMemset(p, 0, need));
-        X100_TRY(hipDeviceSynchronize());
-        w.ptr = p;
-        w.bytes = need;
+    StreamWs *w = nullptr;
+    for (StreamWs &e : g_ws)
+        if (e.dev == dev && e.stream == stream) w = &e;
+    if (w && w->bytes >= need) {
+        *out = w->ptr;
+        return X100_OK;
     }
-    *out = w.ptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (stream) X100_TRY(hipStreamIsCapturing(stream, &cs));
+    if (cs != hipStreamCaptureStatusNone) return X100_EINVAL;
+    size_t bytes = (size_t)1 << 20;
+    while (bytes < need) bytes <<= 1;
+    void *p = nullptr;
+    X100_TRY(hipMalloc(&p, bytes));
+    if (w) {
+        g_ws_retired.push_back(w->ptr);
+        w->ptr = p;
+        w->bytes = bytes;
+    } else {
+        g_ws.push_back(StreamWs{dev, stream, p, bytes});
+    }
+    *out = p;
+    return X100_OK;
+}
+
+inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Shape checks of the MoE block (moe_layer_hip's contract in x100_moe.h).
+bool moe_shape_ok(int M, int d, int ff, int n_exp, int n_act)
+{
+    if (M < 1 || M > X100_MOE_MAX_ROWS || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return false;
+    return d > 0 && ff > 0 && d % 256 == 0 && ff % 256 == 0 && d <= 4096 && ff <= 4096;
+}
+
+bool moe_ptrs_ok(const float *hn, const float *R, const void *Wg, const void *Wu, const void *Wd, const float *out)
+{
+    if (!hn || !R || !Wg || !Wu || !Wd || !out) return false;
+    return !(((uintptr_t)hn | (uintptr_t)R | (uintptr_t)Wg | (uintptr_t)Wu | (uintptr_t)Wd) & 15);
+}
+
+int moe_run(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R, const void *Wg,
+            const void *Wu, const void *Wd, float *out, int residual, int *sel, float *sw, void *ws, void *stream)
+{
+    hipError_t e = x100_moe_launch(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws,
+                                   (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return X100_EINVAL;
+    if (e != hipSuccess) return hip_fail(e);
     return X100_OK;
 }
 
@@ -333,36 +373,49 @@ int gemv_int8_hip(int M, int N, int K, const int8_t *Wp, const int8_t *x, int32_
 // ---------------------------------------------------------------------------------------------
 // MoE decode layer
 // ---------------------------------------------------------------------------------------------
+size_t moe_layer_workspace_bytes(int M, int d, int ff, int n_exp, int n_act)
+{
+    if (!moe_shape_ok(M, d, ff, n_exp, n_act)) return 0;
+    return al256(x100_moe_workspace_bytes(M, d, ff, n_exp, n_act));
+}
+
+int moe_layer_hip_ws(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R, const void *Wg,
+                     const void *Wu, const void *Wd, float *out, int residual, int *sel, float *sw, void *ws,
+                     size_t ws_bytes, void *stream)
+{
+    if (!moe_shape_ok(M, d, ff, n_exp, n_act) || !moe_ptrs_ok(hn, R, Wg, Wu, Wd, out)) return X100_EINVAL;
+    if (!ws || ((uintptr_t)ws & 255) || ws_bytes < moe_layer_workspace_bytes(M, d, ff, n_exp, n_act))
+        return X100_EINVAL;
+    int rc = check_device();
+    if (rc) return rc;
+    return moe_run(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, stream);
+}
+
 int moe_layer_hip(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                   const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
                   int *sel, float *sw, void *stream)
 {
-    if (M < 1 || M > X100_MOE_MAX_ROWS || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return X100_EINVAL;
-    if (d <= 0 || ff <= 0 || d % 256 || ff % 256 || d > 4096 || ff > 4096) return X100_EINVAL;
-    if (!hn || !R || !Wg || !Wu || !Wd || !out) return X100_EINVAL;
-    if (((uintptr_t)hn & 15) || ((uintptr_t)R & 15) || ((uintptr_t)Wg & 15) ||
-        ((uintptr_t)Wu & 15) || ((uintptr_t)Wd & 15))
-        return X100_EINVAL;
+    if (!moe_shape_ok(M, d, ff, n_exp, n_act) || !moe_ptrs_ok(hn, R, Wg, Wu, Wd, out)) return X100_EINVAL;
     int rc = check_device();
     if (rc) return rc;
+    const size_t need = moe_layer_workspace_bytes(M, d, ff, n_exp, n_act);
     void *ws = nullptr;
-    rc = dev_workspace(0, x100_moe_workspace_bytes(M, d, ff, n_exp, n_act), &ws);
+    rc = stream_workspace((hipStream_t)stream, need, &ws);
     if (rc) return rc;
-    hipError_t e = x100_moe_launch(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw,
-                                   ws, (hipStream_t)stream);
-    if (e == hipErrorInvalidValue) return X100_EINVAL;
-    if (e != hipSuccess) return hip_fail(e);
-    return X100_OK;
+    return moe_run(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, stream);
 }
 
 // ---------------------------------------------------------------------------------------------
 // decode layer
 // ---------------------------------------------------------------------------------------------
+// Every argument of the layer is checked here, before any kernel is enqueued, so that an error
+// return leaves h and the caches untouched.
 static int check_layer(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, const float *h, bool moe)
 {
     if (!c || !w || !h) return X100_EINVAL;
     if (c->d <= 0 || c->head_dim != 128 || c->n_head < 1 || c->n_head_kv < 1 || c->n_head % c->n_head_kv ||
-        c->n_head / c->n_head_kv > 16 || c->ctx < 1 || pos < 0 || pos >= c->ctx)
+        c->n_head / c->n_head_kv > 16 || c->ctx < 1 || pos < 0 || pos >= c->ctx || c->d > 65536 ||
+        c->n_head > 1024)
         return X100_EINVAL;
     if ((size_t)c->n_head_kv * c->ctx * 128 >= ((size_t)1 << 40)) return X100_EINVAL;
     if (!w->attn_norm || !w->q_norm || !w->k_norm || !w->wq || !w->wk || !w->wv || !w->wo || !w->k_cache ||
@@ -373,32 +426,86 @@ static int check_layer(const x100_layer_cfg *c, const x100_layer_weights *w, int
     if (!x100q_gguf_bytes(c->wq_type, qd, c->d) || !x100q_gguf_bytes(c->wk_type, kvd, c->d) ||
         !x100q_gguf_bytes(c->wv_type, kvd, c->d) || !x100q_gguf_bytes(c->wo_type, c->d, qd))
         return X100_EINVAL;
+    if (!x100_qgemv_supported(c->wq_type, 1, qd, c->d) || !x100_qgemv_supported(c->wk_type, 1, kvd, c->d) ||
+        !x100_qgemv_supported(c->wv_type, 1, kvd, c->d) || !x100_qgemv_supported(c->wo_type, 1, c->d, qd))
+        return X100_EINVAL;
     if (((uintptr_t)w->wq | (uintptr_t)w->wk | (uintptr_t)w->wv | (uintptr_t)w->wo) & 255) return X100_EINVAL;
-    if (moe && (!w->ffn_norm || !w->router || !w->wg || !w->wu || !w->wd)) return X100_EINVAL;
+    if (moe) {
+        if (!w->ffn_norm || !moe_shape_ok(1, c->d, c->ff, c->n_exp, c->n_act)) return X100_EINVAL;
+        if (!w->router || !w->wg || !w->wu || !w->wd) return X100_EINVAL;
+        if (((uintptr_t)w->router | (uintptr_t)w->wg | (uintptr_t)w->wu | (uintptr_t)w->wd) & 15) return X100_EINVAL;
+    }
     return X100_OK;
 }
 
-static int attn_half(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, float **hn,
+static size_t attn_ws_bytes(const x100_layer_cfg *c) { return al256(x100_attn_workspace_bytes(c)); }
+
+size_t x100_decode_workspace_bytes(const x100_layer_cfg *c)
+{
+    if (!c || c->d <= 0 || c->head_dim != 128 || c->n_head < 1 || c->n_head_kv < 1 || c->ctx < 1 || c->d > 65536 ||
+        c->n_head > 1024)
+        return 0;
+    const size_t attn = attn_ws_bytes(c);
+    // the MoE block's share when the configuration has one (the attention half alone needs less)
+    return attn + moe_layer_workspace_bytes(1, c->d, c->ff, c->n_exp, c->n_act);
+}
+
+// The attention half on workspace ws; with w->ffn_norm set, *hn receives rmsnorm(h, ffn_norm).
+static int attn_half(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, float **hn, void *ws,
                      void *stream)
 {
-    int rc = check_device();
-    if (rc) return rc;
-    void *ws = nullptr;
-    rc = dev_workspace(1, x100_attn_workspace_bytes(c), &ws);
-    if (rc) return rc;
     hipError_t e = x100_attn_launch(c, w, pos, h, (float *)ws, hn, (hipStream_t)stream);
     if (e == hipErrorInvalidValue) return X100_EINVAL;
     if (e != hipSuccess) return hip_fail(e);
     return X100_OK;
 }
 
+static int attn_decode(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, void *ws,
+                       void *stream)
+{
+    x100_layer_weights w2 = *w;
+    w2.ffn_norm = nullptr;   // the residual add only, no norm for a following block
+    return attn_half(c, &w2, pos, h, nullptr, ws, stream);
+}
+
+static int decode_layer(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, int *sel, float *sw,
+                        void *ws, void *stream)
+{
+    float *hn = nullptr;
+    int rc = attn_half(c, w, pos, h, &hn, ws, stream);
+    if (rc) return rc;
+    return moe_run(1, c->d, c->ff, c->n_exp, c->n_act, hn, w->router, w->wg, w->wu, w->wd, h, 1, sel, sw,
+                   (uint8_t *)ws + attn_ws_bytes(c), stream);
+}
+
+int x100_attn_decode_hip_ws(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, void *ws,
+                            size_t ws_bytes, void *stream)
+{
+    int rc = check_layer(c, w, pos, h, false);
+    if (rc) return rc;
+    if (!ws || ((uintptr_t)ws & 255) || ws_bytes < attn_ws_bytes(c)) return X100_EINVAL;
+    if ((rc = check_device())) return rc;
+    return attn_decode(c, w, pos, h, ws, stream);
+}
+
 int x100_attn_decode_hip(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, void *stream)
 {
     int rc = check_layer(c, w, pos, h, false);
     if (rc) return rc;
-    x100_layer_weights w2 = *w;
-    w2.ffn_norm = nullptr;   // the residual add only, no norm for a following block
-    return attn_half(c, &w2, pos, h, nullptr, stream);
+    if ((rc = check_device())) return rc;
+    void *ws = nullptr;
+    if ((rc = stream_workspace((hipStream_t)stream, attn_ws_bytes(c), &ws))) return rc;
+    return attn_decode(c, w, pos, h, ws, stream);
+}
+
+int x100_decode_layer_hip_ws(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, int *sel,
+                             float *sw, void *ws, size_t ws_bytes, void *stream)
+{
+    int rc = check_layer(c, w, pos, h, true);
+    if (rc) return rc;
+    if (!ws || ((uintptr_t)ws & 255) || ws_bytes < x100_decode_workspace_bytes(c)) return X100_EINVAL;
+    if ((rc = check_device())) return rc;
+    return decode_layer(c, w, pos, h, sel, sw, ws, stream);
 }
 
 int x100_decode_layer_hip(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, int *sel,
@@ -406,14 +513,10 @@ int x100_decode_layer_hip(const x100_layer_cfg *c, const x100_layer_weights *w, 
 {
     int rc = check_layer(c, w, pos, h, true);
     if (rc) return rc;
-    if (c->n_act < 1 || c->n_act > 8 || c->n_exp < c->n_act || c->n_exp > 256 || c->d % 256 || c->ff % 256 ||
-        c->d > 4096 || c->ff > 4096 || c->ff <= 0)
-        return X100_EINVAL;
-    float *hn = nullptr;
-    rc = attn_half(c, w, pos, h, &hn, stream);
-    if (rc) return rc;
-    return moe_layer_hip(1, c->d, c->ff, c->n_exp, c->n_act, hn, w->router, w->wg, w->wu, w->wd, h, 1, sel, sw,
-                         stream);
+    if ((rc = check_device())) return rc;
+    void *ws = nullptr;
+    if ((rc = stream_workspace((hipStream_t)stream, x100_decode_workspace_bytes(c), &ws))) return rc;
+    return decode_layer(c, w, pos, h, sel, sw, ws, stream);
 }
 
 }  // extern "C"

@@ -825,21 +825,32 @@ hipError_t launch_kq_upl(dim3 grid, size_t lds, int M, int N, int K, int R, cons
 }
 
 // Rows per block R for the K-quant kernels: about 256 blocks, each lane holding at most UPL_MAX
-// units (1024-thread blocks have 128 VGPRs per lane, which 8 units of Q3_K would exceed).
+// units (1024-thread blocks have 128 VGPRs per lane, which 8 units of Q3_K would exceed).  False
+// when K is too long for one row to fit in one pass or in LDS.
+template <int MR, int LPU>
+bool kq_plan(int N, int K, int &R, size_t &lds)
+{
+    const int nsb = K / 256;
+    constexpr int UNITS_PER_PASS = kq_nt<MR, LPU>() / LPU;
+    constexpr int UPL_MAX = kq_nt<MR, LPU>() >= 1024 ? 4 : 8;
+    R = (N + 255) / 256;
+    if (R < 1) R = 1;
+    if (R * nsb > UPL_MAX * UNITS_PER_PASS) R = (UPL_MAX * UNITS_PER_PASS) / nsb;
+    lds = ((size_t)MR * nsb + 1) * (256 + 64 + 4) + ((size_t)MR * R * nsb + 1) * 4;
+    return R >= 1 && lds <= 160 * 1024;
+}
+
 template <int MR, int LPU>
 hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
 {
     const int nsb = K / 256;
     constexpr int UNITS_PER_PASS = kq_nt<MR, LPU>() / LPU;
     constexpr int UPL_MAX = kq_nt<MR, LPU>() >= 1024 ? 4 : 8;
-    int R = (N + 255) / 256;
-    if (R < 1) R = 1;
-    if (R * nsb > UPL_MAX * UNITS_PER_PASS) R = (UPL_MAX * UNITS_PER_PASS) / nsb;
-    if (R < 1) return hipErrorInvalidValue;  // a single row does not fit in one pass
+    int R;
+    size_t lds;
+    if (!kq_plan<MR, LPU>(N, K, R, lds)) return hipErrorInvalidValue;
     int upl = (R * nsb + UNITS_PER_PASS - 1) / UNITS_PER_PASS;
     const dim3 grid((N + R - 1) / R);
-    const size_t lds = ((size_t)MR * nsb + 1) * (256 + 64 + 4) + ((size_t)MR * R * nsb + 1) * 4;
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
     if (upl <= 1) return launch_kq_upl<MR, LPU, 1>(grid, lds, M, N, K, R, w, x, y, s);
     if (upl <= 2) return launch_kq_upl<MR, LPU, 2>(grid, lds, M, N, K, R, w, x, y, s);
     if (upl <= 3) return launch_kq_upl<MR, LPU, 3>(grid, lds, M, N, K, R, w, x, y, s);
@@ -853,27 +864,41 @@ hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *
 
 }  // namespace
 
+bool x100_qgemv_supported(int qtype, int M, int N, int K)
+{
+    if (M < 1 || M > 8 || N < 0 || K <= 0) return false;
+    const size_t mr = M <= 1 ? 1 : (M <= 4 ? 4 : 8);
+    if (qtype == X100_Q4_0)
+        return K % 32 == 0 && K / 32 <= 512 && (mr * (K / 32) + 1) * 40 <= 160 * 1024;
+    if (qtype == X100_Q8_0 || qtype == X100_Q5_K || qtype == X100_Q6_K)
+        return K % (qtype == X100_Q8_0 ? 32 : 256) == 0 && K / 32 <= 512 && (mr * (K / 32) + 1) * 40 <= 160 * 1024 &&
+               (size_t)N * (K / 32) < ((size_t)1 << 27);   // 32-bit buffer offsets
+    if (qtype == X100_Q4_K || qtype == X100_Q3_K) {
+        if (K % 256) return false;
+        int R;
+        size_t lds;
+        if (qtype == X100_Q4_K)
+            return mr == 1 ? kq_plan<1, 8>(N, K, R, lds) : (mr == 4 ? kq_plan<4, 8>(N, K, R, lds) : kq_plan<8, 8>(N, K, R, lds));
+        return mr == 1 ? kq_plan<1, 4>(N, K, R, lds) : (mr == 4 ? kq_plan<4, 4>(N, K, R, lds) : kq_plan<8, 4>(N, K, R, lds));
+    }
+    return false;
+}
+
 hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, const float *x, float *y,
                              hipStream_t s)
 {
-    if (M < 1 || M > 8) return hipErrorInvalidValue;
+    if (!x100_qgemv_supported(qtype, M, N, K)) return hipErrorInvalidValue;
     if (qtype == X100_Q4_0) {
-        if (K % 32 || K / 32 > 512) return hipErrorInvalidValue;
-        if (((size_t)(M <= 1 ? 1 : (M <= 4 ? 4 : 8)) * (K / 32) + 1) * 40 > 160 * 1024) return hipErrorInvalidValue;
         if (M == 1) return launch_q4_0<1>(M, N, K, w, x, y, s);
         if (M <= 4) return launch_q4_0<4>(M, N, K, w, x, y, s);
         return launch_q4_0<8>(M, N, K, w, x, y, s);
     }
     if (qtype == X100_Q8_0 || qtype == X100_Q5_K || qtype == X100_Q6_K) {
-        if (K % (qtype == X100_Q8_0 ? 32 : 256) || K / 32 > 512) return hipErrorInvalidValue;
-        if (((size_t)(M <= 1 ? 1 : (M <= 4 ? 4 : 8)) * (K / 32) + 1) * 40 > 160 * 1024) return hipErrorInvalidValue;
-        if ((size_t)N * (K / 32) >= ((size_t)1 << 27)) return hipErrorInvalidValue;   // 32-bit buffer offsets
         if (M == 1) return launch_q8_0<1>(M, N, K, w, x, y, s);
         if (M <= 4) return launch_q8_0<4>(M, N, K, w, x, y, s);
         return launch_q8_0<8>(M, N, K, w, x, y, s);
     }
     if (qtype == X100_Q4_K || qtype == X100_Q3_K) {
-        if (K % 256) return hipErrorInvalidValue;
         if (qtype == X100_Q4_K) {
             if (M == 1) return launch_kq<1, 8>(M, N, K, w, x, y, s);
             if (M <= 4) return launch_kq<4, 8>(M, N, K, w, x, y, s);

@@ -22,6 +22,8 @@ size_t x100_q_packed_bytes(int qtype, int N, int K);
 hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *dst, hipStream_t s);
 hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, const float *x, float *y,
                              hipStream_t s);
+// True when x100_qgemv_launch accepts the shape (it then launches without further checks).
+bool x100_qgemv_supported(int qtype, int M, int N, int K);
 
 size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act);
 hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,

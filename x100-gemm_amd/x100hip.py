@@ -9,7 +9,8 @@ Entry points and what they replace in the reference:
   gemm_ime_i8 / gemm_hip_i8 / gemm_hip_i8_dev   include/x100_gemm.h:60-61 (C += A*B, int8->int32)
   qgemv_hip (+ x100q_pack)                      lin_mm of qwen_moe.c:101-107 on Q4_0/Q4_K/Q3_K;
                                                 lin_mm_i8_x of qwen_moe_q3k.c:1075 on Q8_0/Q5_K/Q6_K
-  moe_layer_hip                                 the MoE block of qwen_moe.c:294-311
+  moe_layer_hip / moe_layer_hip_ws              the MoE block of qwen_moe.c:294-311 (library or
+                                                caller scratch)
   gemv_int4_hip / gemv_int8_hip (+ packers)     gemv_nb_int4 / gemv_nb_int8 of bench/q4_gemv.c:67-99
 """
 import ctypes
@@ -32,13 +33,14 @@ EXPORTS = (
     "x100_hip_detect", "x100_hip_caps_print", "x100_hip_strerror",
     "x100_tile_bytes", "x100_pack_w_int4", "x100_pack_w_int8", "gemv_int4_hip", "gemv_int8_hip",
     "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip",
-    "moe_layer_hip",
+    "moe_layer_hip", "moe_layer_workspace_bytes", "moe_layer_hip_ws",
     "x100_gguf_open", "x100_gguf_close", "x100_gguf_version", "x100_gguf_n_tensors", "x100_gguf_n_kv",
     "x100_gguf_alignment", "x100_gguf_data_offset", "x100_gguf_tensor_at", "x100_gguf_find",
     "x100_gguf_kv_at", "x100_gguf_get_int", "x100_gguf_get_float", "x100_gguf_get_str",
     "x100_gguf_get_arr_str", "x100_gguf_qwen3moe_params", "x100_gguf_type_name", "x100_gguf_block_bytes",
     "x100_gguf_block_elems", "x100_gguf_upload", "x100_gguf_pack_rows",
-    "x100_attn_decode_hip", "x100_decode_layer_hip",
+    "x100_attn_decode_hip", "x100_decode_layer_hip", "x100_decode_workspace_bytes",
+    "x100_attn_decode_hip_ws", "x100_decode_layer_hip_ws",
 )
 
 GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC, GEMM_TILE256_W4 = 0, 1, 2, 3, 4, 5
@@ -101,6 +103,9 @@ def lib():
     L.x100q_pack.argtypes = [i, i, i, p, p, p]
     L.qgemv_hip.argtypes = [i, i, i, i, p, p, p, p]
     L.moe_layer_hip.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p]
+    L.moe_layer_workspace_bytes.argtypes = [i, i, i, i, i]
+    L.moe_layer_workspace_bytes.restype = sz
+    L.moe_layer_hip_ws.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p, sz, p]
     L.x100_tile_bytes.argtypes = [i, i, i]
     L.x100_tile_bytes.restype = sz
     L.x100_pack_w_int4.argtypes = [i, i, p, p]
@@ -141,8 +146,16 @@ def lib():
     L.x100_decode_layer_hip.argtypes = [ctypes.POINTER(LayerCfg), ctypes.POINTER(LayerWeights), i, p, p, p, p]
     L.x100_attn_decode_hip.restype = i
     L.x100_decode_layer_hip.restype = i
+    L.x100_decode_workspace_bytes.argtypes = [ctypes.POINTER(LayerCfg)]
+    L.x100_decode_workspace_bytes.restype = sz
+    L.x100_attn_decode_hip_ws.argtypes = [ctypes.POINTER(LayerCfg), ctypes.POINTER(LayerWeights), i, p, p, sz, p]
+    L.x100_decode_layer_hip_ws.argtypes = [ctypes.POINTER(LayerCfg), ctypes.POINTER(LayerWeights), i, p, p, p, p, sz,
+                                           p]
+    L.x100_attn_decode_hip_ws.restype = i
+    L.x100_decode_layer_hip_ws.restype = i
     for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant", "x100_hip_detect",
-                 "x100q_pack", "qgemv_hip", "moe_layer_hip", "x100_pack_w_int4", "x100_pack_w_int8",
+                 "x100q_pack", "qgemv_hip", "moe_layer_hip", "moe_layer_hip_ws", "x100_pack_w_int4",
+                 "x100_pack_w_int8",
                  "gemv_int4_hip", "gemv_int8_hip"):
         getattr(L, name).restype = i
     _lib = L
@@ -209,6 +222,18 @@ def moe_layer(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residu
                                       1 if residual else 0, d_sel, d_sw, stream))
 
 
+def moe_workspace_bytes(M, d, ff, n_exp, n_act):
+    return lib().moe_layer_workspace_bytes(M, d, ff, n_exp, n_act)
+
+
+def moe_layer_ws(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residual, d_sel, d_sw, d_ws, ws_bytes,
+                 stream=None):
+    """moe_layer on caller scratch (d_ws: device buffer of ws_bytes >= moe_workspace_bytes)."""
+    return _check("moe_layer_hip_ws",
+                  lib().moe_layer_hip_ws(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out,
+                                         1 if residual else 0, d_sel, d_sw, d_ws, ws_bytes, stream))
+
+
 # ---- integer tile GEMV (int4 / int8 weights) ---------------------------------------------------
 def tile_bytes(int4, N, K):
     return lib().x100_tile_bytes(1 if int4 else 0, N, K)
@@ -245,3 +270,17 @@ def decode_layer(cfg, weights, pos, d_h, d_sel=None, d_sw=None, stream=None):
     return _check("x100_decode_layer_hip", lib().x100_decode_layer_hip(ctypes.byref(cfg), ctypes.byref(weights), pos,
                                                                        d_h, d_sel, d_sw, stream))
 
+
+def decode_workspace_bytes(cfg):
+    return lib().x100_decode_workspace_bytes(ctypes.byref(cfg))
+
+
+def attn_decode_ws(cfg, weights, pos, d_h, d_ws, ws_bytes, stream=None):
+    return _check("x100_attn_decode_hip_ws", lib().x100_attn_decode_hip_ws(ctypes.byref(cfg), ctypes.byref(weights),
+                                                                           pos, d_h, d_ws, ws_bytes, stream))
+
+
+def decode_layer_ws(cfg, weights, pos, d_h, d_sel, d_sw, d_ws, ws_bytes, stream=None):
+    return _check("x100_decode_layer_hip_ws", lib().x100_decode_layer_hip_ws(ctypes.byref(cfg), ctypes.byref(weights),
+                                                                             pos, d_h, d_sel, d_sw, d_ws, ws_bytes,
+                                                                             stream))
