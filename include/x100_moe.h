@@ -35,6 +35,11 @@
 #include <stdint.h>
 
 #define X100_MOE_MAX_ROWS 512
+/* Size of moe_layer_hip_noalloc's static scratch array (8 MiB per GPU): enough for up to 64
+ * token rows at the Qwen3-30B-A3B shape (d 2048, ff 768, 128 experts, top 8) and 16 rows at
+ * d = ff = 4096. */
+#define X100_MOE_NOALLOC_MAX_BYTES ((size_t)8 << 20)
+#define X100_ESCRATCH   -8   /* the shape needs more scratch than X100_MOE_NOALLOC_MAX_BYTES    */
 
 #ifdef __cplusplus
 extern "C" {
@@ -54,6 +59,18 @@ size_t moe_layer_workspace_bytes(int M, int d, int ff, int n_exp, int n_act);
 int moe_layer_hip_ws(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                      const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
                      int *sel, float *sw, void *ws, size_t ws_bytes, void *stream);
+
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): moe_layer_hip with
+ * its scratch in a static device array of X100_MOE_NOALLOC_MAX_BYTES per GPU, set up on the first
+ * call on each GPU; the call allocates nothing, frees nothing and never synchronises.  A shape
+ * whose moe_layer_workspace_bytes exceeds the array returns X100_ESCRATCH with nothing enqueued.
+ * All calls on one GPU share the array: calls whose executions overlap on one GPU (other streams,
+ * or graphs replayed concurrently) race and must use moe_layer_hip_ws instead.  The array keeps
+ * the last call's contents; nothing in it needs clearing between calls. */
+int moe_layer_hip_noalloc(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                          const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
+                          int *sel, float *sw, void *stream);
 
 #ifdef __cplusplus
 }

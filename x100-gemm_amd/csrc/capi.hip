@@ -105,6 +105,33 @@ int stream_workspace(hipStream_t stream, size_t need, void **out)
 
 inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Scratch of moe_layer_hip_noalloc: a fixed array in the library's device image, one copy per GPU
+// (each GPU the library runs on holds it until the process ends).  In host code `scratch` only
+// names the symbol; its device address, which differs per GPU, comes from hipGetSymbolAddress
+// with that GPU current, once, and only that address is ever handed to kernels.  Calls on one
+// GPU share the array; nothing in it needs clearing (the kernels write every byte they read
+// within a call).
+static __device__ __align__(256) uint8_t scratch[X100_MOE_NOALLOC_MAX_BYTES];
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64];   // device address of `scratch` per device ordinal (null until set up)
+
+int static_scratch(void **out)
+{
+    int dev = 0;
+    X100_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return X100_ENODEV;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        X100_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return X100_EHIP;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return X100_OK;
+}
+
 // Shape checks of the MoE block (moe_layer_hip's contract in x100_moe.h).
 bool moe_shape_ok(int M, int d, int ff, int n_exp, int n_act)
 {
@@ -243,6 +270,8 @@ const char *x100_hip_strerror(int code)
     case X100_EIO: return "file could not be opened or mapped";
     case X100_EFORMAT: return "not a GGUF v2/v3 file, or a field lies outside the file";
     case X100_ENOTFOUND: return "no tensor or key of that name (or of that type)";
+    case X100_ESCRATCH: return "the shape needs more scratch than the static array of moe_layer_hip_noalloc "
+                               "holds (X100_MOE_NOALLOC_MAX_BYTES)";
     }
     return "unknown error";
 }
@@ -402,6 +431,19 @@ int moe_layer_hip(int M, int d, int ff, int n_exp, int n_act, const float *hn, c
     void *ws = nullptr;
     rc = stream_workspace((hipStream_t)stream, need, &ws);
     if (rc) return rc;
+    return moe_run(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, stream);
+}
+
+int moe_layer_hip_noalloc(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                          const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
+                          float *sw, void *stream)
+{
+    if (!moe_shape_ok(M, d, ff, n_exp, n_act) || !moe_ptrs_ok(hn, R, Wg, Wu, Wd, out)) return X100_EINVAL;
+    if (moe_layer_workspace_bytes(M, d, ff, n_exp, n_act) > X100_MOE_NOALLOC_MAX_BYTES) return X100_ESCRATCH;
+    int rc = check_device();
+    if (rc) return rc;
+    void *ws = nullptr;
+    if ((rc = static_scratch(&ws))) return rc;
     return moe_run(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, stream);
 }
 

@@ -24,7 +24,8 @@ LIB_PATH = os.path.join(HERE, "lib", "libx100hip.so")
 Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K = 2, 8, 11, 12, 13, 14
 
 X100_OK, X100_EINVAL, X100_ENODEV, X100_EHIP, X100_ENOMEM = 0, -1, -2, -3, -4
-X100_EIO, X100_EFORMAT, X100_ENOTFOUND = -5, -6, -7
+X100_EIO, X100_EFORMAT, X100_ENOTFOUND, X100_ESCRATCH = -5, -6, -7, -8
+MOE_NOALLOC_MAX_BYTES = 8 << 20
 
 # Every symbol declared in include/x100_gemm.h, x100_gemv_tile.h, x100_qgemv.h, x100_moe.h,
 # x100_gguf.h, x100_decode.h.
@@ -33,7 +34,7 @@ EXPORTS = (
     "x100_hip_detect", "x100_hip_caps_print", "x100_hip_strerror",
     "x100_tile_bytes", "x100_pack_w_int4", "x100_pack_w_int8", "gemv_int4_hip", "gemv_int8_hip",
     "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip",
-    "moe_layer_hip", "moe_layer_workspace_bytes", "moe_layer_hip_ws",
+    "moe_layer_hip", "moe_layer_workspace_bytes", "moe_layer_hip_ws", "moe_layer_hip_noalloc",
     "x100_gguf_open", "x100_gguf_close", "x100_gguf_version", "x100_gguf_n_tensors", "x100_gguf_n_kv",
     "x100_gguf_alignment", "x100_gguf_data_offset", "x100_gguf_tensor_at", "x100_gguf_find",
     "x100_gguf_kv_at", "x100_gguf_get_int", "x100_gguf_get_float", "x100_gguf_get_str",
@@ -106,6 +107,7 @@ def lib():
     L.moe_layer_workspace_bytes.argtypes = [i, i, i, i, i]
     L.moe_layer_workspace_bytes.restype = sz
     L.moe_layer_hip_ws.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p, sz, p]
+    L.moe_layer_hip_noalloc.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p]
     L.x100_tile_bytes.argtypes = [i, i, i]
     L.x100_tile_bytes.restype = sz
     L.x100_pack_w_int4.argtypes = [i, i, p, p]
@@ -154,7 +156,8 @@ def lib():
     L.x100_attn_decode_hip_ws.restype = i
     L.x100_decode_layer_hip_ws.restype = i
     for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant", "x100_hip_detect",
-                 "x100q_pack", "qgemv_hip", "moe_layer_hip", "moe_layer_hip_ws", "x100_pack_w_int4",
+                 "x100q_pack", "qgemv_hip", "moe_layer_hip", "moe_layer_hip_ws", "moe_layer_hip_noalloc",
+                 "x100_pack_w_int4",
                  "x100_pack_w_int8",
                  "gemv_int4_hip", "gemv_int8_hip"):
         getattr(L, name).restype = i
@@ -220,6 +223,14 @@ def moe_layer(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residu
     return _check("moe_layer_hip",
                   lib().moe_layer_hip(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out,
                                       1 if residual else 0, d_sel, d_sw, stream))
+
+
+def moe_layer_noalloc(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residual=False,
+                      d_sel=None, d_sw=None, stream=None):
+    """moe_layer with the library's static per-GPU scratch (allocates nothing)."""
+    return _check("moe_layer_hip_noalloc",
+                  lib().moe_layer_hip_noalloc(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out,
+                                              1 if residual else 0, d_sel, d_sw, stream))
 
 
 def moe_workspace_bytes(M, d, ff, n_exp, n_act):
