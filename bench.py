@@ -15,9 +15,10 @@ timed with HIP events on the launch stream.  The same JSON line carries:
                 speculative verify) and at 64 and 512 token rows (verify / prefill), the whole
                 decoder layer (attention + MoE, 1024 and 4096 cached positions), each beside its
                 scalar CPU time, and the per-token decode weight stream of bench/moe_decode.c
-                (x100-gemm_amd/moe_decode.py).  GEMV and MoE run back-to-back in a captured graph
-                over weight copies totalling more than 256 MB (so the 256 MB Infinity Cache cannot
-                hold them); single-launch latency is reported separately.
+                (the C program x100-gemm_amd/host/moe_decode.c, run as a child process).  GEMV and
+                MoE run back-to-back in a captured graph over weight copies totalling more than
+                256 MB (so the 256 MB Infinity Cache cannot hold them); single-launch latency is
+                reported separately.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
        python bench.py --probe     (for rocprofv3 --pmc: `--steps` GEMM 4096^3 launches, then one
@@ -28,6 +29,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-c
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -325,9 +327,15 @@ def bench_extra(torch, timer, dev, args):
         del dws
 
     # ---- Qwen3-30B-A3B decode weight stream (bench/moe_decode.c), q4 and q8 ----------------------
-    import moe_decode
-    md = moe_decode.run(torch, L=48, reps=3, us=(8, 24, 64), verbose=False)
-    for name, r in md.items():
+    # the C host program x100-gemm_amd/bin/moe_decode, run as a child process
+    exe = os.path.join(ROOT, "x100-gemm_amd", "bin", "moe_decode")
+    res = subprocess.run([exe, "--layers", "48", "--reps", "3", "--us", "8,24,64", "--json"], capture_output=True,
+                         text=True, timeout=600)
+    if res.returncode != 0:
+        raise RuntimeError("moe_decode failed: " + res.stderr[-1000:])
+    md = json.loads(res.stdout.strip().splitlines()[-1])
+    for name in ("q4", "q8"):
+        r = md[name]
         extra["moe_decode_stream_" + name] = r
         log("moe_decode %s: M=1 %.3f ms/tok (%.1f tok/s, %.0f GB/s); M=8 U=24 %.3f ms/pass (%.1f tok/s)" % (
             name, r["m1_ms_per_token"], r["m1_tok_s"], r["m1_GB_s"], r["m8_u24_ms_per_pass"], r["m8_u24_tok_s"]))

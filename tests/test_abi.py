@@ -52,3 +52,15 @@ def test_pure_host_entry_points():
     assert x100hip.packed_bytes(x100hip.Q3_K, 6144, 2048) == 6144 * 8 * 110
     assert x100hip.packed_bytes(x100hip.Q4_0, 4096, 4096) >= 4096 * 128 * 18
     assert x100hip.strerror(x100hip.X100_EINVAL).startswith("invalid")
+
+
+def test_integration_snippet_is_the_compiled_code():
+    """INTEGRATION.md's C integration of the engine's Lin (lin_hip_new / lin_hip_mm) is compiled,
+    verbatim, into x100-gemm_amd/host/x100_host.c (run by tests/test_host_gpu.py)."""
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    src = open(os.path.join(ROOT, "x100-gemm_amd", "host", "x100_host.c")).read()
+    blocks = re.findall(r"```c\n(.*?)```", doc, flags=re.S)
+    lin = [b for b in blocks if "lin_hip_new(LinHip" in b]
+    assert len(lin) == 1
+    body = "\n".join(l for l in lin[0].splitlines() if not l.startswith("#include")).strip()
+    assert body in src

@@ -126,18 +126,3 @@ def test_gemv_tile_rejects_bad_shapes(dev):
     for args in [(0, 8, 32), (9, 8, 32), (1, 12, 32), (1, 8, 48), (8, 8, 8192)]:
         with pytest.raises(x100hip.X100Error):
             x100hip.gemv_tile(True, *args, p, p, p)
-
-
-@pytest.mark.gpu
-def test_q4_gemv_cli(dev):
-    import os
-    import subprocess
-    import sys
-    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    cli = os.path.join(root, "x100-gemm_amd", "q4_gemv.py")
-    out = subprocess.run([sys.executable, cli, "4864", "896", "4", "1", "20"], capture_output=True, text=True,
-                         timeout=120)
-    assert out.returncode == 0, out.stdout + out.stderr
-    assert "int4 GEMV 4864x896 M=4: y==ref OK (0/19456 mismatch)" in out.stdout
-    bad = subprocess.run([sys.executable, cli, "4864", "900"], capture_output=True, text=True, timeout=120)
-    assert bad.returncode == 2
