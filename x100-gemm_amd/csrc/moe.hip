@@ -51,24 +51,6 @@ inline size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 // Bytes of one row's Q8_K record (nsb 256-element blocks).
 __host__ __device__ inline int q8k_rec_bytes(int nsb) { return (nsb * (256 + 64 + 4) + 15) & ~15; }
 
-// Quantize one 256-element block to Q8_K with one wave (same operations as pack_A_q3k): v is the
-// lane's float4 (elements 4*lane .. 4*lane+3).
-X100_DEV void q8k_wave(const float4 v, int8_t *qs, int *bs, float *dout)
-{
-    const int lane = threadIdx.x & 63;
-    const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    const float amax = wave_max_u(a);
-    const float d = amax / 127.0f;
-    const float rep = d != 0.0f ? 1.0f / d : 0.0f;
-    const int q0 = clamp_i8((int)roundf(v.x * rep)), q1 = clamp_i8((int)roundf(v.y * rep));
-    const int q2 = clamp_i8((int)roundf(v.z * rep)), q3 = clamp_i8((int)roundf(v.w * rep));
-    ((uint32_t *)qs)[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                             ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-    const int s = sum4_i(q0 + q1 + q2 + q3);
-    bs[lane >> 2] = s;   // the 4 lanes of a 16-group hold the same sum (no branch)
-    *dout = d;           // d is wave-uniform
-}
-
 // get_scale_min_k4 (repack.cpp:222-233) over the header dwords 1..3 of a Q4_K block.
 X100_DEV uint32_t hbyte(const v4i &h, int k)
 {
@@ -164,7 +146,7 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
     } else if (wave < n_exp + M * nsb) {
         const int q = wave - n_exp, m = q / nsb, sb = q - m * nsb;
         uint8_t *rec = ws.xrec + (size_t)m * q8k_rec_bytes(nsb);
-        q8k_wave(s_hn[q * 64 + lane], (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16,
+        q8_K_wave(s_hn[q * 64 + lane], (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16,
                  (float *)(rec + nsb * 320) + sb);
     }
 }
@@ -196,7 +178,7 @@ __global__ __launch_bounds__(256) void k_moe_route_rows(int M, int d, int n_exp,
         const int m = q / nsb, sb = q - m * nsb;
         const float4 v = *(const float4 *)(hn + (size_t)(row0 + m) * d + sb * 256 + 4 * lane);
         uint8_t *rec = ws.xrec + (size_t)(row0 + m) * q8k_rec_bytes(nsb);
-        q8k_wave(v, (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16, (float *)(rec + nsb * 320) + sb);
+        q8_K_wave(v, (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16, (float *)(rec + nsb * 320) + sb);
         return;
     }
 
@@ -629,7 +611,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
 }
 
 // Q8_K of every pair's activation row, once (5 or more token rows): wave q quantizes block
-// q % nsf of pair q / nsf with q8k_wave, into the pair's record of ws.xact.
+// q % nsf of pair q / nsf with q8_K_wave, into the pair's record of ws.xact.
 __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 {
     const int nsf = ff / 256, q = blockIdx.x * 4 + wave_id(), lane = threadIdx.x & 63;
@@ -637,7 +619,7 @@ __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
     const int p = q / nsf, sb = q - p * nsf;
     const float4 v = *(const float4 *)(ws.act + (size_t)p * ff + sb * 256 + 4 * lane);
     uint8_t *rec = ws.xact + (size_t)p * q8k_rec_bytes(nsf);
-    q8k_wave(v, (int8_t *)rec + sb * 256, (int *)(rec + nsf * 256) + sb * 16, (float *)(rec + nsf * 320) + sb);
+    q8_K_wave(v, (int8_t *)rec + sb * 256, (int *)(rec + nsf * 256) + sb * 16, (float *)(rec + nsf * 320) + sb);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -861,7 +843,7 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
 #define X100_ACT_QUANT(q0)                                                                        \
     _Pragma("unroll") for (int j = 0; j < 4; j++) {                                               \
         const int q = (q0) + 4 * j + w;                                                           \
-        if (q < nq) q8k_wave(v[j], aq + q * 256, abs_ + q * 16, ad + q);                          \
+        if (q < nq) q8_K_wave(v[j], aq + q * 256, abs_ + q * 16, ad + q);                          \
     }
     X100_ACT_LOADS(0)
     __builtin_amdgcn_sched_barrier(0);
@@ -947,7 +929,7 @@ __global__ __launch_bounds__(64 * FD_NWV) void k_moe_down_fused(int M, int d, in
         for (int j = 0; j < QJ; j++) {
             const int q = q0 + NWV * j + w;
             const int qd = q < nq ? q : nq;
-            q8k_wave(v[j], aq + qd * 256, abs_ + qd * 16, ad + qd);
+            q8_K_wave(v[j], aq + qd * 256, abs_ + qd * 16, ad + qd);
         }
     };
     // The first pass's activation loads, then every weight load, then the quantizer (which waits

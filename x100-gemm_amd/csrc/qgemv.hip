@@ -46,11 +46,6 @@ X100_DEV void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc
     m = j < 4 ? m_lo : m_hi;
 }
 
-// u / d and u % d for 0 <= u < 2^16 and 1 <= d <= 2^16 with the multiplier mg = ceil(2^32 / d)
-// (exact in that range).
-X100_DEV int fast_div(uint32_t u, uint32_t mg) { return (int)__umulhi(u, mg); }
-inline uint32_t div_magic(uint32_t d) { return (uint32_t)((0x100000000ull + d - 1) / d); }
-
 // ------------------------------------------------------------------------------------------------
 // Q4_0 x Q8_0
 // ------------------------------------------------------------------------------------------------
@@ -146,214 +141,240 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
 }
 
 // ------------------------------------------------------------------------------------------------
-// Q4_K x Q8_K
+// K-quants (Q4_K, Q3_K) x Q8_K
 // ------------------------------------------------------------------------------------------------
-// Work unit = (row, super-block), 8 lanes per unit: lane i of the unit loads the block header
-// (d, dmin, scales: 16 B) and qs bytes [16i, 16i+16): low nibbles = sub-block 2*(i/2), high
-// nibbles = sub-block 2*(i/2)+1, elements 16*(i%2) .. +15 of each.  A block of R rows has
-// R*nsb units; wave w takes units w*8 + lane/8 + (NT/8)*c.
-template <int MR, int UPL, int XPT, int NT>
-__global__ __launch_bounds__(NT) void k_q4_K(int M, int N, int K, int R, uint32_t nsb_mg,
-                                              const uint8_t *__restrict__ W,
-                                              const float *__restrict__ x, float *__restrict__ y)
+// Work unit = (row, super-block) on 4 lanes: lane s = lane % 4 takes elements 64s .. 64s+63 of the
+// super-block.  A block covers RB <= 16 * NP rows (16 units per wave per pass); RB is chosen so
+// that there is about one block per CU, since every block quantizes all of x.  The nsb super-blocks of
+// a row are dealt to the block's nw waves, wave w taking super-blocks w, w + nw, ... (SBW of
+// them), so a wave quantizes x (MR token rows) only on its own super-blocks and into its own LDS
+// records: no barrier separates the quantizer from the dot products.  Every weight load of a lane
+// is issued before its quantizer runs.  A unit's integer sums are reduced over its 4 lanes (two DPP
+// steps) and its fp32 term goes to LDS; after the block's one barrier, one thread per (token row,
+// row) adds the terms over super-blocks in order, the oracle's sequence (bit-identical to it).
+constexpr int KQ_REC = 256 + 64 + 16;   // one (token row, super-block) record: q[256] | bs[16] | d
+
+// LDS bytes of a K-quant block: the waves' x records and the terms [MR][RB][nsb] (+ a spare).
+__host__ __device__ constexpr size_t kq_lds(int MR, int RB, int nw, int sbw, int nsb)
 {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int nsb = K / 256;
-    const int ns1 = MR * nsb + 1;                  // + the quantizer's spare block
-    int8_t *xq = (int8_t *)smem;                   // [MR][nsb][256]
-    int *xbs = (int *)(xq + ns1 * 256);            // [MR][nsb][16]
-    float *xd = (float *)(xbs + ns1 * 16);         // [MR][nsb]
-    float *tv = xd + ns1;                          // [MR][R*nsb] + one spare
+    return (size_t)nw * sbw * MR * KQ_REC + ((size_t)MR * RB * nsb + 1) * 4;
+}
 
-    const int lane = threadIdx.x & 63, w = wave_id();
-    const int i = lane & 7, p = i >> 1, h = i & 1;
-    const int row0 = blockIdx.x * R;
-    const int nrows = min(R, N - row0);
-    const int U = nrows * nsb;
-
-    const int total4 = M * K / 4;
-    const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
-    float4 xv[XPT];
-    x_load<XPT, NT>(xr, 0, xv);
-
-    v4i hdr[UPL], qs[UPL];
+// x of super-block sb (< nsb, else a load past the end: zeros) for token rows 0..MR-1 into the
+// wave's records rec[MR].
+template <int MR>
+X100_DEV void kq_load_x(rsrc_t xr, int K, int sb, int nsb, float4 (&v)[MR])
+{
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        const int u = min(w * 8 + (lane >> 3) + (NT / 8) * c, U - 1);   // clamped: see k_q4_0
-        const uint8_t *blk = W + ((size_t)row0 * nsb + u) * 144;
-        hdr[c] = *(const v4i *)blk;
-        qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
-    }
+    for (int m = 0; m < MR; m++)
+        v[m] = buf_load_f4(xr, sb < nsb ? (uint32_t)(m * K + sb * 256 + 4 * lane) * 4u : 0xfffffff0u);
+}
+template <int MR>
+X100_DEV void kq_quant_x(const float4 (&v)[MR], uint8_t *rec)
+{
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+        q8_K_wave(v[m], (int8_t *)(rec + m * KQ_REC), (int *)(rec + m * KQ_REC + 256), (float *)(rec + m * KQ_REC + 320));
+}
 
-    __builtin_amdgcn_sched_barrier(0);   // keep every load above ahead of the quantizer's math
-    q8_K_from_regs<XPT, NT>(xv, 0, total4, xq, xbs, xd);
-    for (int c0 = NT * XPT; c0 < total4; c0 += NT * XPT) {
-        x_load<XPT, NT>(xr, c0, xv);
-        q8_K_from_regs<XPT, NT>(xv, c0, total4, xq, xbs, xd);
-    }
-    __syncthreads();
-
-#pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        const int u = w * 8 + (lane >> 3) + (NT / 8) * c;
-        const bool valid = u < U;  // uniform over the 8 lanes of a unit
-        const int sb = valid ? u - fast_div(u, nsb_mg) * nsb : 0;
-        const uint32_t h0 = (uint32_t)hdr[c][0];
-        const float d = h2f((uint16_t)(h0 & 0xffff)), dmin = h2f((uint16_t)(h0 >> 16));
-        int sc0, m0, sc1, m1;
-        scale_min_k4(2 * p, (uint32_t)hdr[c][1], (uint32_t)hdr[c][2], (uint32_t)hdr[c][3], sc0, m0);
-        scale_min_k4(2 * p + 1, (uint32_t)hdr[c][1], (uint32_t)hdr[c][2], (uint32_t)hdr[c][3], sc1, m1);
-        int lo[4], hi[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            lo[t] = qs[c][t] & 0x0F0F0F0F;
-            hi[t] = (qs[c][t] >> 4) & 0x0F0F0F0F;
-        }
-#pragma unroll
-        for (int m = 0; m < MR; m++) {
-            // Branch-free: rows m >= M compute on unused LDS and are never combined; the 8 lanes
-            // of a unit hold the same sums and store the same value; invalid units use the spare.
-            const int8_t *xb = xq + (m * nsb + sb) * 256;
-            const v4i xa = *(const v4i *)(xb + 64 * p + 16 * h);
-            const v4i xc = *(const v4i *)(xb + 64 * p + 32 + 16 * h);
-            int d0 = 0, d1 = 0;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                d0 = dot4(lo[t], xa[t], d0);
-                d1 = dot4(hi[t], xc[t], d1);
-            }
-            const int *bs = xbs + (m * nsb + sb) * 16;
-            const int isc = sum8_i(sc0 * d0 + sc1 * d1);
-            const int imn = sum8_i(m0 * bs[4 * p + h] + m1 * bs[4 * p + 2 + h]);
-            const float dx = xd[m * nsb + sb];
-            const float dd = dx * d, dm = dx * dmin;
-            tv[valid ? m * R * nsb + u : MR * R * nsb] = dd * (float)isc - dm * (float)imn;
-        }
-    }
-    __syncthreads();
-
-    // Sequential combine over super-blocks (same order and operations as the oracle).
-    for (int t = threadIdx.x; t < MR * nrows; t += blockDim.x) {
-        const int m = t / nrows, r = t - m * nrows;
-        if (m < M) {
+// Sequential combine over super-blocks (same order and operations as the oracle).
+template <int MR>
+X100_DEV void kq_combine(int M, int N, int nsb, int RB, int row0, const float *tv, float *y)
+{
+    for (int t = threadIdx.x; t < MR * RB; t += blockDim.x) {
+        const int m = t / RB, r = t - m * RB;
+        if (m < M && row0 + r < N) {
             float acc = 0.0f;
-            for (int sb = 0; sb < nsb; sb++) acc = acc + tv[m * R * nsb + r * nsb + sb];
+            for (int sb = 0; sb < nsb; sb++) acc = acc + tv[(m * RB + r) * nsb + sb];
             y[(size_t)m * N + row0 + r] = acc;
         }
     }
 }
 
-// ------------------------------------------------------------------------------------------------
-// Q3_K x Q8_K
-// ------------------------------------------------------------------------------------------------
-// Work unit = (row, super-block), 4 lanes per unit: lane i (hh = i/2, lh = i%2) loads qs bytes
-// [32hh + 16lh, +16) and hmask bytes [16lh, +16) and decodes the 64 elements
-// 128hh + 32j + 16lh + (0..15), j = 0..3 (shift 2j, hmask bit 4hh+j, scale index 8hh+2j+lh),
-// as in dequantize_q3_K_block (qwen_moe_q3k.c:565-575).  Wave w takes units w*16 + lane/4 + (NT/4)*c.
-template <int MR, int UPL, int XPT, int NT>
-__global__ __launch_bounds__(NT) void k_q3_K(int M, int N, int K, int R, uint32_t nsb_mg,
-                                              const uint8_t *__restrict__ hq,
+// Q4_K: lane s holds qs bytes [32s, 32s+32) (low nibbles: sub-block 2s, high nibbles: sub-block
+// 2s+1, get_scale_min_k4 of repack.cpp:222-233) and the 16-byte header (d, dmin, scales).
+template <int MR, int NP, int SBW>
+__global__ __launch_bounds__(512) void k_q4_K(int M, int N, int K, int RB, const uint8_t *__restrict__ W,
+                                              const float *__restrict__ x, float *__restrict__ y)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nsb = K / 256, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id(), s = lane & 3, ur = lane >> 2;
+    const int row0 = blockIdx.x * RB;
+    uint8_t *xw = smem + (size_t)w * SBW * MR * KQ_REC;
+    float *tv = (float *)(smem + (size_t)nw * SBW * MR * KQ_REC);
+
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
+    float4 xv[MR];
+    kq_load_x<MR>(xr, K, w, nsb, xv);
+
+    // Unconditional loads (row and super-block clamped into the matrix; results discarded).
+    v4i hdr[SBW][NP], q0[SBW][NP], q1[SBW][NP];
+#pragma unroll
+    for (int i = 0; i < SBW; i++)
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int sb = min(w + nw * i, nsb - 1), row = min(row0 + min(16 * p + ur, RB - 1), N - 1);
+            const uint8_t *blk = W + ((size_t)row * nsb + sb) * 144;
+            hdr[i][p] = *(const v4i *)blk;
+            q0[i][p] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 32 * s));
+            q1[i][p] = __builtin_nontemporal_load((const v4i *)(blk + 32 + 32 * s));
+        }
+    __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the quantizer
+    kq_quant_x<MR>(xv, xw);
+#pragma unroll
+    for (int i = 1; i < SBW; i++) {
+        kq_load_x<MR>(xr, K, w + nw * i, nsb, xv);
+        kq_quant_x<MR>(xv, xw + i * MR * KQ_REC);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the wave's own LDS records
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+#pragma unroll
+    for (int i = 0; i < SBW; i++) {
+        const int sb = w + nw * i;
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int rl = 16 * p + ur;
+            const bool valid = sb < nsb && rl < RB && row0 + rl < N;   // uniform over the unit's 4 lanes
+            const uint32_t h0 = (uint32_t)hdr[i][p][0];
+            const float d = h2f((uint16_t)(h0 & 0xffff)), dmin = h2f((uint16_t)(h0 >> 16));
+            int sc0, m0, sc1, m1;
+            scale_min_k4(2 * s, (uint32_t)hdr[i][p][1], (uint32_t)hdr[i][p][2], (uint32_t)hdr[i][p][3], sc0, m0);
+            scale_min_k4(2 * s + 1, (uint32_t)hdr[i][p][1], (uint32_t)hdr[i][p][2], (uint32_t)hdr[i][p][3], sc1, m1);
+            int lo[8], hi[8];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                lo[t] = q0[i][p][t] & 0x0F0F0F0F;
+                hi[t] = (q0[i][p][t] >> 4) & 0x0F0F0F0F;
+                lo[4 + t] = q1[i][p][t] & 0x0F0F0F0F;
+                hi[4 + t] = (q1[i][p][t] >> 4) & 0x0F0F0F0F;
+            }
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                // Branch-free: rows m >= M compute on zero records and are never combined; the 4
+                // lanes of a unit store the same value; invalid units write the spare slot.
+                const uint8_t *rec = xw + (i * MR + m) * KQ_REC;
+                const v4i xa0 = *(const v4i *)(rec + 64 * s), xa1 = *(const v4i *)(rec + 64 * s + 16);
+                const v4i xc0 = *(const v4i *)(rec + 64 * s + 32), xc1 = *(const v4i *)(rec + 64 * s + 48);
+                const v4i bs = *(const v4i *)(rec + 256 + 16 * s);
+                int d0 = 0, d1 = 0;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    d0 = dot4(lo[t], xa0[t], d0);
+                    d0 = dot4(lo[4 + t], xa1[t], d0);
+                    d1 = dot4(hi[t], xc0[t], d1);
+                    d1 = dot4(hi[4 + t], xc1[t], d1);
+                }
+                const int isc = sum4_i(sc0 * d0 + sc1 * d1);
+                const int imn = sum4_i(m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]));
+                const float dx = *(const float *)(rec + 320);
+                const float dd = dx * d, dm = dx * dmin;
+                tv[valid ? (m * RB + rl) * nsb + sb : MR * RB * nsb] = dd * (float)isc - dm * (float)imn;
+            }
+        }
+    }
+    __syncthreads();
+    kq_combine<MR>(M, N, nsb, RB, row0, tv, y);
+}
+
+// Q3_K: lane s (hh = s / 2, lh = s % 2) loads qs bytes [32hh + 16lh, +16) and hmask bytes
+// [16lh, +16) and decodes the 64 elements 128hh + 32j + 16lh + (0..15), j = 0..3 (shift 2j, hmask
+// bit 4hh + j, scale index 8hh + 2j + lh), as dequantize_q3_K_block does (qwen_moe_q3k.c:565-575).
+template <int MR, int NP, int SBW>
+__global__ __launch_bounds__(512) void k_q3_K(int M, int N, int K, int RB, const uint8_t *__restrict__ hq,
                                               const uint8_t *__restrict__ scl,
                                               const uint16_t *__restrict__ wdd,
                                               const float *__restrict__ x, float *__restrict__ y)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int nsb = K / 256;
-    const int ns1 = MR * nsb + 1;                  // + the quantizer's spare block
-    int8_t *xq = (int8_t *)smem;                   // [MR][nsb][256]
-    int *xbs = (int *)(xq + ns1 * 256);            // [MR][nsb][16]
-    float *xd = (float *)(xbs + ns1 * 16);         // [MR][nsb]
-    float *tv = xd + ns1;                          // [MR][R*nsb] + one spare
+    const int nsb = K / 256, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id(), s = lane & 3, ur = lane >> 2, hh = s >> 1, lh = s & 1;
+    const int row0 = blockIdx.x * RB;
+    uint8_t *xw = smem + (size_t)w * SBW * MR * KQ_REC;
+    float *tv = (float *)(smem + (size_t)nw * SBW * MR * KQ_REC);
 
-    const int lane = threadIdx.x & 63, w = wave_id();
-    const int i = lane & 3, hh = i >> 1, lh = i & 1;
-    const int row0 = blockIdx.x * R;
-    const int nrows = min(R, N - row0);
-    const int U = nrows * nsb;
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
+    float4 xv[MR];
+    kq_load_x<MR>(xr, K, w, nsb, xv);
 
-    const int total4 = M * K / 4;
-    const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
-    float4 xv[XPT];
-    x_load<XPT, NT>(xr, 0, xv);
-
-    v4i qv[UPL], hv[UPL];
-    uint32_t s0[UPL], s1[UPL], s2[UPL];
-    uint32_t dv[UPL];
+    v4i qv[SBW][NP], hv[SBW][NP];
+    uint32_t s0[SBW][NP], s1[SBW][NP], s2[SBW][NP], dv[SBW][NP];
 #pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        const int u = min(w * 16 + (lane >> 2) + (NT / 4) * c, U - 1);  // clamped: see k_q4_0
-        const size_t rec = (size_t)row0 * nsb + u;
-        qv[c] = __builtin_nontemporal_load((const v4i *)(hq + rec * 96 + 32 + 32 * hh + 16 * lh));
-        hv[c] = *(const v4i *)(hq + rec * 96 + 16 * lh);
-        const uint32_t *sp = (const uint32_t *)(scl + rec * 12);
-        s0[c] = sp[0];
-        s1[c] = sp[1];
-        s2[c] = sp[2];
-        dv[c] = wdd[rec];
-    }
-
-    __builtin_amdgcn_sched_barrier(0);   // keep every load above ahead of the quantizer's math
-    q8_K_from_regs<XPT, NT>(xv, 0, total4, xq, xbs, xd);
-    for (int c0 = NT * XPT; c0 < total4; c0 += NT * XPT) {
-        x_load<XPT, NT>(xr, c0, xv);
-        q8_K_from_regs<XPT, NT>(xv, c0, total4, xq, xbs, xd);
-    }
-    __syncthreads();
-
+    for (int i = 0; i < SBW; i++)
 #pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        const int u = w * 16 + (lane >> 2) + (NT / 4) * c;
-        const bool valid = u < U;
-        const int sb = valid ? u - fast_div(u, nsb_mg) * nsb : 0;
-        int scl_j[4];
-        int v[4][4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            // 6-bit scale of sub-block is = 8hh + 2j + lh: low nibble of byte (2j+lh) (hh = 0) or
-            // its high nibble (hh = 1); high 2 bits from byte 8 + is%4 at bit 2*(is/4).
-            const int k = 2 * j + lh;
-            const uint32_t low4 = (sbyte(s0[c], s1[c], s2[c], k) >> (4 * hh)) & 0xf;
-            const int is = 8 * hh + k;
-            const uint32_t high2 = (sbyte(s0[c], s1[c], s2[c], 8 + (is & 3)) >> (2 * (is >> 2))) & 3;
-            scl_j[j] = (int)(low4 | (high2 << 4)) - 32;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const uint32_t lo2 = ((uint32_t)qv[c][t] >> (2 * j)) & 0x03030303u;
-                const uint32_t hb = ((uint32_t)hv[c][t] >> (4 * hh + j)) & 0x01010101u;
-                v[j][t] = (int)(lo2 | (hb << 2));   // 3-bit value q + 4, q in [-4, 3]
-            }
+        for (int p = 0; p < NP; p++) {
+            const int sb = min(w + nw * i, nsb - 1), row = min(row0 + min(16 * p + ur, RB - 1), N - 1);
+            const size_t rec = (size_t)row * nsb + sb;
+            qv[i][p] = __builtin_nontemporal_load((const v4i *)(hq + rec * 96 + 32 + 32 * hh + 16 * lh));
+            hv[i][p] = *(const v4i *)(hq + rec * 96 + 16 * lh);
+            const uint32_t *sp = (const uint32_t *)(scl + rec * 12);
+            s0[i][p] = sp[0];
+            s1[i][p] = sp[1];
+            s2[i][p] = sp[2];
+            dv[i][p] = wdd[rec];
         }
-        const float dw = h2f((uint16_t)dv[c]);
+    __builtin_amdgcn_sched_barrier(0);
+    kq_quant_x<MR>(xv, xw);
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            // Branch-free, as in k_q4_K.
-            const int8_t *xb = xq + (m * nsb + sb) * 256 + 128 * hh + 16 * lh;
-            const int *bs = xbs + (m * nsb + sb) * 16 + 8 * hh + lh;
-            int isc = 0;
+    for (int i = 1; i < SBW; i++) {
+        kq_load_x<MR>(xr, K, w + nw * i, nsb, xv);
+        kq_quant_x<MR>(xv, xw + i * MR * KQ_REC);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+#pragma unroll
+    for (int i = 0; i < SBW; i++) {
+        const int sb = w + nw * i;
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int rl = 16 * p + ur;
+            const bool valid = sb < nsb && rl < RB && row0 + rl < N;
+            int scv[4];
+            int v[4][4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const v4i xv = *(const v4i *)(xb + 32 * j);
-                int dsum = 0;
+                // 6-bit scale of sub-block is = 8hh + 2j + lh: low nibble of byte 2j + lh (hh = 0)
+                // or its high nibble (hh = 1); high 2 bits from byte 8 + is % 4 at bit 2 (is / 4).
+                const int k = 2 * j + lh, is = 8 * hh + k;
+                const uint32_t low4 = (sbyte(s0[i][p], s1[i][p], s2[i][p], k) >> (4 * hh)) & 0xf;
+                const uint32_t high2 = (sbyte(s0[i][p], s1[i][p], s2[i][p], 8 + (is & 3)) >> (2 * (is >> 2))) & 3;
+                scv[j] = (int)(low4 | (high2 << 4)) - 32;
 #pragma unroll
-                for (int t = 0; t < 4; t++) dsum = dot4(v[j][t], xv[t], dsum);
-                dsum -= 4 * bs[2 * j];
-                isc += scl_j[j] * dsum;
+                for (int t = 0; t < 4; t++) {
+                    const uint32_t lo2 = ((uint32_t)qv[i][p][t] >> (2 * j)) & 0x03030303u;
+                    const uint32_t hb = ((uint32_t)hv[i][p][t] >> (4 * hh + j)) & 0x01010101u;
+                    v[j][t] = (int)(lo2 | (hb << 2));   // 3-bit value q + 4, q in [-4, 3]
+                }
             }
-            isc = sum4_i(isc);
-            const float dx = xd[m * nsb + sb];
-            tv[valid ? m * R * nsb + u : MR * R * nsb] = (dx * dw) * (float)isc;
+            const float dw = h2f((uint16_t)dv[i][p]);
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                // Branch-free, as in k_q4_K.
+                const uint8_t *rec = xw + (i * MR + m) * KQ_REC;
+                const int *bs = (const int *)(rec + 256) + 8 * hh + lh;
+                int isc = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const v4i xq = *(const v4i *)(rec + 128 * hh + 32 * j + 16 * lh);
+                    int dsum = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) dsum = dot4(v[j][t], xq[t], dsum);
+                    dsum -= 4 * bs[2 * j];
+                    isc += scv[j] * dsum;
+                }
+                isc = sum4_i(isc);
+                const float dx = *(const float *)(rec + 320);
+                tv[valid ? (m * RB + rl) * nsb + sb : MR * RB * nsb] = (dx * dw) * (float)isc;
+            }
         }
     }
     __syncthreads();
-
-    for (int t = threadIdx.x; t < MR * nrows; t += blockDim.x) {
-        const int m = t / nrows, r = t - m * nrows;
-        if (m < M) {
-            float acc = 0.0f;
-            for (int sb = 0; sb < nsb; sb++) acc = acc + tv[m * R * nsb + r * nsb + sb];
-            y[(size_t)m * N + row0 + r] = acc;
-        }
-    }
+    kq_combine<MR>(M, N, nsb, RB, row0, tv, y);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -779,87 +800,63 @@ hipError_t launch_q8_0(int M, int N, int K, const void *w, const float *x, float
     return launch_q8_0_x<MR, 64, 8>(M, N, K, w, x, y, s);
 }
 
-// Threads per block of the K-quant kernels (one block per CU).  With several token rows the dot
-// products and the activation quantizer are spread over more waves (Q4_K: 8, Q3_K: 16), so each
-// SIMD has other waves to issue while one waits on a DPP or LDS result; one row is fastest with
-// 4 waves.  LPU = lanes per work unit (Q4_K 8, Q3_K 4).
-template <int MR, int LPU> constexpr int kq_nt() { return MR == 1 ? 256 : (LPU == 8 ? 512 : 1024); }
-
-// Activation float4 per thread per load pass for NT threads: enough for M*K <= 4*NT*XPT.
-inline int xpt_kq(int M, int K, int nt)
+// K-quant launch plan: nw = min(nsb, 8) waves, SBW super-blocks per wave (a power of two, at most
+// 8, so K <= 16384), RB = ceil(N / 256) rows per block (about one block per CU) but at least 16
+// and at most 32 (two passes).  False when the block's LDS would exceed 160 KiB.
+struct KqPlan {
+    int nw, sbw, rb, np;
+    size_t lds;
+};
+inline bool kq_plan(int MR, int N, int K, KqPlan &pl)
 {
-    const int need = (M * K + 4 * nt - 1) / (4 * nt);
-    return need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+    const int nsb = K / 256;
+    if (nsb < 1) return false;
+    pl.nw = nsb < 8 ? nsb : 8;
+    const int need = (nsb + pl.nw - 1) / pl.nw;
+    pl.sbw = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+    if (need > 8) return false;
+    pl.rb = min(32, max(16, (N + 255) / 256));
+    pl.np = pl.sbw <= 4 ? (pl.rb + 15) / 16 : 1;   // eight super-blocks per wave: one pass
+    if (pl.np == 1) pl.rb = 16;
+    pl.lds = kq_lds(MR, pl.rb, pl.nw, pl.sbw, nsb);
+    return pl.lds <= 160 * 1024;
 }
 
-// One K-quant launch with a compile-time number of work units per lane.
-template <int MR, int LPU, int UPL, int XPT>
-hipError_t launch_kq_upl_x(dim3 grid, size_t lds, int M, int N, int K, int R, const void *w, const float *x,
-                           float *y, hipStream_t s)
+template <int MR, bool Q3, int SBW, int NP>
+hipError_t launch_kq_s(const KqPlan &pl, int M, int N, int K, const void *w, const float *x, float *y,
+                       hipStream_t s)
 {
-    constexpr int NT = kq_nt<MR, LPU>();
-    if constexpr (LPU == 8) {
-        hipLaunchKernelGGL((k_q4_K<MR, UPL, XPT, NT>), grid, dim3(NT), lds, s, M, N, K, R, div_magic(K / 256),
-                           (const uint8_t *)w, x, y);
-    } else {
+    const dim3 grid((N + pl.rb - 1) / pl.rb), blk(64 * pl.nw);
+    if constexpr (Q3) {
         const size_t nblk = (size_t)N * (K / 256);
         const uint8_t *hq = (const uint8_t *)w;
         const uint8_t *scl = hq + nblk * 96;
         const uint16_t *dd = (const uint16_t *)(scl + nblk * 12);
-        hipLaunchKernelGGL((k_q3_K<MR, UPL, XPT, NT>), grid, dim3(NT), lds, s, M, N, K, R, div_magic(K / 256), hq,
-                           scl, dd, x, y);
+        hipLaunchKernelGGL((k_q3_K<MR, NP, SBW>), grid, blk, pl.lds, s, M, N, K, pl.rb, hq, scl, dd, x, y);
+    } else {
+        hipLaunchKernelGGL((k_q4_K<MR, NP, SBW>), grid, blk, pl.lds, s, M, N, K, pl.rb, (const uint8_t *)w, x, y);
     }
     return hipGetLastError();
 }
 
-template <int MR, int LPU, int UPL>
-hipError_t launch_kq_upl(dim3 grid, size_t lds, int M, int N, int K, int R, const void *w, const float *x,
-                         float *y, hipStream_t s)
-{
-    switch (xpt_kq(M, K, kq_nt<MR, LPU>())) {
-    case 1: return launch_kq_upl_x<MR, LPU, UPL, 1>(grid, lds, M, N, K, R, w, x, y, s);
-    case 2: return launch_kq_upl_x<MR, LPU, UPL, 2>(grid, lds, M, N, K, R, w, x, y, s);
-    case 4: return launch_kq_upl_x<MR, LPU, UPL, 4>(grid, lds, M, N, K, R, w, x, y, s);
-    default: return launch_kq_upl_x<MR, LPU, UPL, 8>(grid, lds, M, N, K, R, w, x, y, s);
-    }
-}
-
-// Rows per block R for the K-quant kernels: about 256 blocks, each lane holding at most UPL_MAX
-// units (1024-thread blocks have 128 VGPRs per lane, which 8 units of Q3_K would exceed).  False
-// when K is too long for one row to fit in one pass or in LDS.
-template <int MR, int LPU>
-bool kq_plan(int N, int K, int &R, size_t &lds)
-{
-    const int nsb = K / 256;
-    constexpr int UNITS_PER_PASS = kq_nt<MR, LPU>() / LPU;
-    constexpr int UPL_MAX = kq_nt<MR, LPU>() >= 1024 ? 4 : 8;
-    R = (N + 255) / 256;
-    if (R < 1) R = 1;
-    if (R * nsb > UPL_MAX * UNITS_PER_PASS) R = (UPL_MAX * UNITS_PER_PASS) / nsb;
-    lds = ((size_t)MR * nsb + 1) * (256 + 64 + 4) + ((size_t)MR * R * nsb + 1) * 4;
-    return R >= 1 && lds <= 160 * 1024;
-}
-
-template <int MR, int LPU>
+template <int MR, bool Q3>
 hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *y, hipStream_t s)
 {
-    const int nsb = K / 256;
-    constexpr int UNITS_PER_PASS = kq_nt<MR, LPU>() / LPU;
-    constexpr int UPL_MAX = kq_nt<MR, LPU>() >= 1024 ? 4 : 8;
-    int R;
-    size_t lds;
-    if (!kq_plan<MR, LPU>(N, K, R, lds)) return hipErrorInvalidValue;
-    int upl = (R * nsb + UNITS_PER_PASS - 1) / UNITS_PER_PASS;
-    const dim3 grid((N + R - 1) / R);
-    if (upl <= 1) return launch_kq_upl<MR, LPU, 1>(grid, lds, M, N, K, R, w, x, y, s);
-    if (upl <= 2) return launch_kq_upl<MR, LPU, 2>(grid, lds, M, N, K, R, w, x, y, s);
-    if (upl <= 3) return launch_kq_upl<MR, LPU, 3>(grid, lds, M, N, K, R, w, x, y, s);
-    if (upl <= 4 || UPL_MAX == 4) return launch_kq_upl<MR, LPU, 4>(grid, lds, M, N, K, R, w, x, y, s);
-    if constexpr (UPL_MAX == 8) {
-        if (upl <= 6) return launch_kq_upl<MR, LPU, 6>(grid, lds, M, N, K, R, w, x, y, s);
-        return launch_kq_upl<MR, LPU, 8>(grid, lds, M, N, K, R, w, x, y, s);
+    KqPlan pl;
+    if (!kq_plan(MR, N, K, pl)) return hipErrorInvalidValue;
+    if (pl.np == 2) {
+        switch (pl.sbw) {
+        case 1: return launch_kq_s<MR, Q3, 1, 2>(pl, M, N, K, w, x, y, s);
+        case 2: return launch_kq_s<MR, Q3, 2, 2>(pl, M, N, K, w, x, y, s);
+        default: return launch_kq_s<MR, Q3, 4, 2>(pl, M, N, K, w, x, y, s);
+        }
     }
-    return hipErrorInvalidValue;
+    switch (pl.sbw) {
+    case 1: return launch_kq_s<MR, Q3, 1, 1>(pl, M, N, K, w, x, y, s);
+    case 2: return launch_kq_s<MR, Q3, 2, 1>(pl, M, N, K, w, x, y, s);
+    case 4: return launch_kq_s<MR, Q3, 4, 1>(pl, M, N, K, w, x, y, s);
+    default: return launch_kq_s<MR, Q3, 8, 1>(pl, M, N, K, w, x, y, s);
+    }
 }
 
 }  // namespace
@@ -874,12 +871,8 @@ bool x100_qgemv_supported(int qtype, int M, int N, int K)
         return K % (qtype == X100_Q8_0 ? 32 : 256) == 0 && K / 32 <= 512 && (mr * (K / 32) + 1) * 40 <= 160 * 1024 &&
                (size_t)N * (K / 32) < ((size_t)1 << 27);   // 32-bit buffer offsets
     if (qtype == X100_Q4_K || qtype == X100_Q3_K) {
-        if (K % 256) return false;
-        int R;
-        size_t lds;
-        if (qtype == X100_Q4_K)
-            return mr == 1 ? kq_plan<1, 8>(N, K, R, lds) : (mr == 4 ? kq_plan<4, 8>(N, K, R, lds) : kq_plan<8, 8>(N, K, R, lds));
-        return mr == 1 ? kq_plan<1, 4>(N, K, R, lds) : (mr == 4 ? kq_plan<4, 4>(N, K, R, lds) : kq_plan<8, 4>(N, K, R, lds));
+        KqPlan pl;
+        return K % 256 == 0 && kq_plan((int)mr, N, K, pl);
     }
     return false;
 }
@@ -898,15 +891,15 @@ hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, cons
         if (M <= 4) return launch_q8_0<4>(M, N, K, w, x, y, s);
         return launch_q8_0<8>(M, N, K, w, x, y, s);
     }
-    if (qtype == X100_Q4_K || qtype == X100_Q3_K) {
-        if (qtype == X100_Q4_K) {
-            if (M == 1) return launch_kq<1, 8>(M, N, K, w, x, y, s);
-            if (M <= 4) return launch_kq<4, 8>(M, N, K, w, x, y, s);
-            return launch_kq<8, 8>(M, N, K, w, x, y, s);
-        }
-        if (M == 1) return launch_kq<1, 4>(M, N, K, w, x, y, s);
-        if (M <= 4) return launch_kq<4, 4>(M, N, K, w, x, y, s);
-        return launch_kq<8, 4>(M, N, K, w, x, y, s);
+    if (qtype == X100_Q4_K) {
+        if (M == 1) return launch_kq<1, false>(M, N, K, w, x, y, s);
+        if (M <= 4) return launch_kq<4, false>(M, N, K, w, x, y, s);
+        return launch_kq<8, false>(M, N, K, w, x, y, s);
+    }
+    if (qtype == X100_Q3_K) {
+        if (M == 1) return launch_kq<1, true>(M, N, K, w, x, y, s);
+        if (M <= 4) return launch_kq<4, true>(M, N, K, w, x, y, s);
+        return launch_kq<8, true>(M, N, K, w, x, y, s);
     }
     return hipErrorInvalidValue;
 }

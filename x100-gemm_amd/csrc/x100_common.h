@@ -259,6 +259,25 @@ X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, 
     }
 }
 
+// Quantize one 256-element block to Q8_K with one wave (the operations of pack_A_q3k,
+// qwen_moe_q3k.c:612-624): v is the lane's float4 (elements 4*lane .. 4*lane+3); writes q[256],
+// the 16 sums bs[16] and the scale *dout.
+X100_DEV void q8_K_wave(const float4 v, int8_t *qs, int *bs, float *dout)
+{
+    const int lane = threadIdx.x & 63;
+    const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    const float amax = wave_max_u(a);
+    const float d = amax / 127.0f;
+    const float rep = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q0 = clamp_i8((int)roundf(v.x * rep)), q1 = clamp_i8((int)roundf(v.y * rep));
+    const int q2 = clamp_i8((int)roundf(v.z * rep)), q3 = clamp_i8((int)roundf(v.w * rep));
+    ((uint32_t *)qs)[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                             ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+    const int s = sum4_i(q0 + q1 + q2 + q3);
+    bs[lane >> 2] = s;   // the 4 lanes of a 16-group hold the same sum (no branch)
+    *dout = d;           // d is wave-uniform
+}
+
 template <int XPT, int NT = 256>
 X100_DEV void q8_K_from_regs(const float4 (&v)[XPT], int c0, int total4, int8_t *xq, int *xbs, float *xd)
 {
