@@ -365,13 +365,16 @@ def bench_extra(torch, timer, dev, args):
         dh = torch.from_numpy(hns).to(dev)
         out = torch.empty((M, d), dtype=torch.float32, device=dev)
         sel = torch.empty((n_h, M, n_act), dtype=torch.int32, device=dev)
+        # caller scratch: the graph is captured on a stream of its own (moe_layer_hip_ws)
+        wsb = x100hip.moe_workspace_bytes(M, d, ff, n_exp, n_act)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
 
         def call(i, with_sel=False):
             L = layers[i % 3]
-            x100hip.moe_layer(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
-                              L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False,
-                              sel[i].data_ptr() if with_sel else None, None,
-                              torch.cuda.current_stream().cuda_stream)
+            x100hip.moe_layer_ws(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
+                                 L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False,
+                                 sel[i].data_ptr() if with_sel else None, None, ws.data_ptr(), wsb,
+                                 torch.cuda.current_stream().cuda_stream)
 
         for i in range(n_h):
             call(i, True)
@@ -394,13 +397,15 @@ def bench_extra(torch, timer, dev, args):
         dh = torch.from_numpy(hns).to(dev)
         out = torch.empty((M, d), dtype=torch.float32, device=dev)
         sel = torch.empty((n_h, M, n_act), dtype=torch.int32, device=dev)
+        wsb = x100hip.moe_workspace_bytes(M, d, ff, n_exp, n_act)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
 
         def callm(i, with_sel=False):
             L = layers[i % 3]
-            x100hip.moe_layer(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
-                              L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False,
-                              sel[i].data_ptr() if with_sel else None, None,
-                              torch.cuda.current_stream().cuda_stream)
+            x100hip.moe_layer_ws(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
+                                 L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False,
+                                 sel[i].data_ptr() if with_sel else None, None, ws.data_ptr(), wsb,
+                                 torch.cuda.current_stream().cuda_stream)
 
         for i in range(n_h):
             callm(i, True)
@@ -461,9 +466,12 @@ def bench_extra(torch, timer, dev, args):
                      ((types[0], nh * hd, d), (types[1], nkv * hd, d), (types[2], nkv * hd, d), (types[3], d, nh * hd)))
     h0 = synth.normal_f32(532, (d,))
     dh = torch.from_numpy(h0).to(dev)
+    dwsb = x100hip.decode_workspace_bytes(cfg)
+    dws = torch.empty(dwsb, dtype=torch.uint8, device=dev)
     for pos in (1023, 4095):
-        fns = [lambda i=i: x100hip.decode_layer(cfg, lw[i % 4], pos, dh.data_ptr(), None, None,
-                                                torch.cuda.current_stream().cuda_stream) for i in range(16)]
+        fns = [lambda i=i: x100hip.decode_layer_ws(cfg, lw[i % 4], pos, dh.data_ptr(), None, None, dws.data_ptr(),
+                                                   dwsb, torch.cuda.current_stream().cuda_stream)
+               for i in range(16)]
         us = timer.graph(fns)
         lat = timer.single(fns[0])
         kv_bytes = 2 * nkv * (pos + 1) * hd * 4
