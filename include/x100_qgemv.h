@@ -44,7 +44,9 @@ extern "C" {
  * or K not a multiple of the block size. */
 size_t x100q_gguf_bytes(int qtype, int N, int K);
 
-/* Bytes of the device layout produced by x100q_pack. */
+/* Bytes of the device layout produced by x100q_pack: Q4_0 as GGUF (plus 256-byte alignment
+ * padding), Q4_K / Q3_K K/256 sections of 148 / 114 bytes per row (the 6-bit scales unpacked to
+ * bytes) each rounded up to 256 bytes, Q8_0 / Q5_K / Q6_K 34 bytes per 32 elements. */
 size_t x100q_packed_bytes(int qtype, int N, int K);
 
 /* Repack GGUF-native blocks (device pointer w_gguf, row n at n*row_bytes) into the device

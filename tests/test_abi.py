@@ -49,7 +49,11 @@ def test_pure_host_entry_points():
     assert x100hip.gguf_bytes(x100hip.Q4_K, 6144, 2048) == 6144 * 8 * 144
     assert x100hip.gguf_bytes(x100hip.Q3_K, 6144, 2048) == 6144 * 8 * 110
     assert x100hip.gguf_bytes(x100hip.Q4_K, 10, 100) == 0
-    assert x100hip.packed_bytes(x100hip.Q3_K, 6144, 2048) == 6144 * 8 * 110
+    # K-quants: one section per super-block column, 148 (Q4_K) / 114 (Q3_K) bytes per row, each
+    # section rounded up to 256 bytes
+    assert x100hip.packed_bytes(x100hip.Q4_K, 6144, 2048) == 8 * 6144 * 148
+    assert x100hip.packed_bytes(x100hip.Q3_K, 6144, 2048) == 8 * 6144 * 114
+    assert x100hip.packed_bytes(x100hip.Q3_K, 5, 512) == 2 * 768
     assert x100hip.packed_bytes(x100hip.Q4_0, 4096, 4096) >= 4096 * 128 * 18
     assert x100hip.strerror(x100hip.X100_EINVAL).startswith("invalid")
 

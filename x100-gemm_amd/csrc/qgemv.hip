@@ -11,13 +11,13 @@
 // it quantizes x, so a block's whole weight slice is in flight at once; no MFMA.
 //
 // Device weight layouts (made once at upload by x100q_pack):
-//   Q4_K  GGUF-native 144-byte blocks (16-byte aligned fields, consumed as is).
 //   Q4_0  split into d[N*K/32] (fp16) and qs[N*K/32][16], so nibble rows are 16-byte aligned.
-//   Q3_K  split into hq[N*K/256][96] (hmask 32 + qs 64), sc[N*K/256][12], d[N*K/256] (fp16).
+//   Q4_K, Q3_K  super-block-major planes (see the K-quant section): 148 / 114 bytes per 256
+//         elements (the GGUF blocks' 144 / 110 with the 6-bit scales unpacked to bytes).
 //   Q8_0, Q5_K, Q6_K  requantized to Q8_0 (the reference loader's lin_new_i8) and split into
 //         d[N*K/32] (fp16) and qs[N*K/32][32].
-// Q4_0 / Q4_K / Q3_K keep the GGUF blocks' byte count (plus alignment padding between the
-// arrays); the int8 path stores 34 bytes per 32 elements.
+// Q4_0 keeps the GGUF blocks' byte count (plus alignment padding between the arrays); the int8
+// path stores 34 bytes per 32 elements.
 //
 // The K-quant kernels reduce each row in the same order as the scalar oracle (sequential over
 // super-blocks, no fused multiply-add), so their fp32 outputs are bit-identical to it; Q4_0 sums
@@ -143,39 +143,122 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
 // ------------------------------------------------------------------------------------------------
 // K-quants (Q4_K, Q3_K) x Q8_K
 // ------------------------------------------------------------------------------------------------
-// Work unit = (row, super-block) on 4 lanes: lane s = lane % 4 takes elements 64s .. 64s+63 of the
-// super-block.  A block covers RB <= 16 * NP rows (16 units per wave per pass); RB is chosen so
-// that there is about one block per CU, since every block quantizes all of x.  The nsb super-blocks of
-// a row are dealt to the block's nw waves, wave w taking super-blocks w, w + nw, ... (SBW of
-// them), so a wave quantizes x (MR token rows) only on its own super-blocks and into its own LDS
-// records: no barrier separates the quantizer from the dot products.  Every weight load of a lane
-// is issued before its quantizer runs.  A unit's integer sums are reduced over its 4 lanes (two DPP
-// steps) and its fp32 term goes to LDS; after the block's one barrier, one thread per (token row,
-// row) adds the terms over super-blocks in order, the oracle's sequence (bit-identical to it).
-constexpr int KQ_REC = 256 + 64 + 16;   // one (token row, super-block) record: q[256] | bs[16] | d
+// Device layout (made once by x100q_pack): one section per super-block column sb (all N rows),
+// each section a set of planes in which the rows are contiguous, so that the lanes of a wave
+// holding consecutive rows of one super-block read one contiguous run per load:
+//   Q4_K section (148 bytes per row): 4 qs planes [N][2][16] (plane c, half h = qs bytes
+//        64h + 16c .. +16 of the GGUF block), the scales [N][2][8] (half h: the 6-bit sc of
+//        sub-blocks 4h .. 4h+3, then their 6-bit m, from get_scale_min_k4, repack.cpp:222-233),
+//        d | dmin [N] (the block's first 4 bytes).
+//   Q3_K section (114 bytes per row): 2 qs planes [N][2][16] (plane c, half h = qs bytes
+//        32h + 16c .. +16), the high bits [N][2][16] (half h: bits 4h .. 4h+3 of the 32 hmask
+//        bytes as nibbles, see k_pack_q3_K), the signed scales [N][2][8] (half h: scale - 32 of
+//        sub-blocks 8h .. 8h+7, dequantize_q3_K_block, qwen_moe_q3k.c:557-577), d [N] (fp16).
+// Every value is the GGUF block's own (no rounding): the layout only moves bits.
+//
+// Work unit = (row, super-block) on 2 lanes: half h takes elements 128h .. 128h+127.  A block
+// covers RB rows x all nsb super-blocks, units in super-block-major order (so a wave's 32 units
+// are consecutive rows of one or two super-blocks), RB about N / 256 so that there is about one
+// block per CU (every block quantizes all of x).  The block's waves quantize the M x nsb Q8_K
+// records of x into LDS between their weight loads and the first barrier; a unit's two lanes
+// reduce its integer sums with one DPP step and store its fp32 term; after the second barrier one
+// thread per (token row, row) adds the terms over super-blocks in order, the oracle's sequence
+// (bit-identical to it).
+constexpr int KR_S16 = 256, KR_S32 = 320, KR_D = 352, KREC = 368;   // Q8_K record: q[256] | s16[16] | s32[8] | d
 
-// LDS bytes of a K-quant block: the waves' x records and the terms [MR][RB][nsb] (+ a spare).
-__host__ __device__ constexpr size_t kq_lds(int MR, int RB, int nw, int sbw, int nsb)
+__host__ __device__ constexpr size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+__host__ __device__ constexpr size_t q4k_sec(int N) { return al256((size_t)148 * N); }
+__host__ __device__ constexpr size_t q3k_sec(int N) { return al256((size_t)114 * N); }
+
+// roundf(v) (half away from zero) for |v| < 2^23: trunc(v + copysign(0.5 - 2^-25, v)) with the add
+// rounded to nearest even.  Below a tie the sum stays under the next integer (its distance to it
+// exceeds half an ulp there), at or above a tie it reaches it; checked against roundf for every
+// float with |v| <= 128.
+X100_DEV int round_away(float v) { return (int)(v + __builtin_copysignf(0x1.fffffep-2f, v)); }
+
+// n / d for n, d < 2^16 with m = ceil(2^32 / d) precomputed on the host (exact in that range:
+// n * (m - 2^32 / d) / 2^32 < n / 2^32 < 1 / d); d = 1 is passed through.
+X100_DEV uint32_t udiv16(uint32_t n, uint32_t d, uint32_t m) { return d == 1 ? n : __umulhi(n, m); }
+inline uint32_t udiv16_magic(uint32_t d) { return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + d - 1) / d); }
+
+// Arguments of the K-quant kernels (RB rows per block, nsb = K / 256 super-blocks per row).
+struct KqArgs {
+    int M, N, K, RB, nsb;
+    uint32_t mrb, mnsb;   // udiv16 multipliers of RB and nsb
+    const uint8_t *W;
+    const float *x;
+    float *y;
+};
+
+// Q8_K records of x, four per wave pass: lane l works on record q = qb + l/16 (q = m*nsb + sb:
+// elements m*K + 256sb ..), elements 16(l%16) .. +15, with the operations of pack_A_q3k
+// (qwen_moe_q3k.c:612-624): amax over the record, d = amax/127, reciprocal 1/d (0 for d = 0),
+// q = roundf(x * (1/d)) clamped to [-128, 127], plus the sums of q per 16 and per 32 elements.
+// Records past nq read zeros and are not stored.
+X100_DEV void q8k_load(rsrc_t xr, const KqArgs &a, int nq, int qb, float4 (&v)[4])
 {
-    return (size_t)nw * sbw * MR * KQ_REC + ((size_t)MR * RB * nsb + 1) * 4;
+    const int lane = threadIdx.x & 63, q = qb + (lane >> 4);
+    const int m = (int)udiv16((uint32_t)q, (uint32_t)a.nsb, a.mnsb), sb = q - m * a.nsb, K = a.K;
+    const uint32_t base = q < nq ? (uint32_t)(m * K + sb * 256 + 16 * (lane & 15)) * 4u : 0xffffff00u;
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = buf_load_f4(xr, base + 16u * c);
+}
+X100_DEV void q8k_quant(const float4 (&v)[4], int nq, int qb, uint8_t *recs)
+{
+    const int lane = threadIdx.x & 63, i = lane & 15, q = qb + (lane >> 4);
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        a = fmaxf(a, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
+    // maximum over the record's 16 lanes, in every one of them (xor 1, xor 2, mirror in 8, mirror in 16)
+    a = fmaxf(a, dpp_f<0xB1>(a, a));
+    a = fmaxf(a, dpp_f<0x4E>(a, a));
+    a = fmaxf(a, dpp_f<0x141>(a, a));
+    a = fmaxf(a, dpp_f<0x140>(a, a));
+    const float d = a / 127.0f;
+    const float rep = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t pk[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int q0 = clamp_i8(round_away(v[c].x * rep)), q1 = clamp_i8(round_away(v[c].y * rep));
+        const int q2 = clamp_i8(round_away(v[c].z * rep)), q3 = clamp_i8(round_away(v[c].w * rep));
+        pk[c] = perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u) | (perm((uint32_t)q3, (uint32_t)q2, 0x0c0c0400u) << 16);
+    }
+    int s16 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) s16 = dot4((int)pk[c], 0x01010101, s16);
+    const int s32 = s16 + dpp_i<0xB1>(0, s16);   // + the neighbouring 16 elements
+    if (q < nq) {
+        uint8_t *rec = recs + (size_t)q * KREC;
+        *(v4u *)(rec + 16 * i) = v4u{pk[0], pk[1], pk[2], pk[3]};
+        ((int *)(rec + KR_S16))[i] = s16;
+        ((int *)(rec + KR_S32))[i >> 1] = s32;   // the two lanes of a pair store the same sum
+        if (i == 0) *(float *)(rec + KR_D) = d;
+    }
 }
 
-// x of super-block sb (< nsb, else a load past the end: zeros) for token rows 0..MR-1 into the
-// wave's records rec[MR].
-template <int MR>
-X100_DEV void kq_load_x(rsrc_t xr, int K, int sb, int nsb, float4 (&v)[MR])
+// The block's M x nsb records, passes of four: wave w takes passes w, w + nw, w + 2nw, ...  The
+// first two passes' loads are issued by q8k_first (before the weight loads), the rest are loaded
+// and quantized one pass at a time by q8k_rest.
+struct Q8kFirst {
+    float4 v0[4], v1[4];
+};
+X100_DEV void q8k_first(rsrc_t xr, const KqArgs &a, int nq, int nw, Q8kFirst &f)
 {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int m = 0; m < MR; m++)
-        v[m] = buf_load_f4(xr, sb < nsb ? (uint32_t)(m * K + sb * 256 + 4 * lane) * 4u : 0xfffffff0u);
+    const int w = wave_id();
+    q8k_load(xr, a, nq, 4 * w, f.v0);
+    if (4 * (w + nw) < nq) q8k_load(xr, a, nq, 4 * (w + nw), f.v1);
 }
-template <int MR>
-X100_DEV void kq_quant_x(const float4 (&v)[MR], uint8_t *rec)
+X100_DEV void q8k_rest(rsrc_t xr, const KqArgs &a, int nq, int nw, const Q8kFirst &f, uint8_t *recs)
 {
-#pragma unroll
-    for (int m = 0; m < MR; m++)
-        q8_K_wave(v[m], (int8_t *)(rec + m * KQ_REC), (int *)(rec + m * KQ_REC + 256), (float *)(rec + m * KQ_REC + 320));
+    const int w = wave_id();
+    q8k_quant(f.v0, nq, 4 * w, recs);
+    if (4 * (w + nw) < nq) q8k_quant(f.v1, nq, 4 * (w + nw), recs);
+    for (int qb = 4 * (w + 2 * nw); qb < nq; qb += 4 * nw) {
+        float4 v[4];
+        q8k_load(xr, a, nq, qb, v);
+        q8k_quant(v, nq, qb, recs);
+    }
 }
 
 // Sequential combine over super-blocks (same order and operations as the oracle).
@@ -192,189 +275,186 @@ X100_DEV void kq_combine(int M, int N, int nsb, int RB, int row0, const float *t
     }
 }
 
-// Q4_K: lane s holds qs bytes [32s, 32s+32) (low nibbles: sub-block 2s, high nibbles: sub-block
-// 2s+1, get_scale_min_k4 of repack.cpp:222-233) and the 16-byte header (d, dmin, scales).
-template <int MR, int NP, int SBW>
-__global__ __launch_bounds__(512) void k_q4_K(int M, int N, int K, int RB, const uint8_t *__restrict__ W,
-                                              const float *__restrict__ x, float *__restrict__ y)
+// LDS bytes of a K-quant block: the MR*nsb records + a spare, then the terms [MR][RB][nsb] + a spare.
+__host__ __device__ constexpr size_t kq_lds(int MR, int RB, int nsb)
 {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int nsb = K / 256, nw = blockDim.x >> 6;
-    const int lane = threadIdx.x & 63, w = wave_id(), s = lane & 3, ur = lane >> 2;
-    const int row0 = blockIdx.x * RB;
-    uint8_t *xw = smem + (size_t)w * SBW * MR * KQ_REC;
-    float *tv = (float *)(smem + (size_t)nw * SBW * MR * KQ_REC);
-
-    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
-    float4 xv[MR];
-    kq_load_x<MR>(xr, K, w, nsb, xv);
-
-    // Unconditional loads (row and super-block clamped into the matrix; results discarded).
-    v4i hdr[SBW][NP], q0[SBW][NP], q1[SBW][NP];
-#pragma unroll
-    for (int i = 0; i < SBW; i++)
-#pragma unroll
-        for (int p = 0; p < NP; p++) {
-            const int sb = min(w + nw * i, nsb - 1), row = min(row0 + min(16 * p + ur, RB - 1), N - 1);
-            const uint8_t *blk = W + ((size_t)row * nsb + sb) * 144;
-            hdr[i][p] = *(const v4i *)blk;
-            q0[i][p] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 32 * s));
-            q1[i][p] = __builtin_nontemporal_load((const v4i *)(blk + 32 + 32 * s));
-        }
-    __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the quantizer
-    kq_quant_x<MR>(xv, xw);
-#pragma unroll
-    for (int i = 1; i < SBW; i++) {
-        kq_load_x<MR>(xr, K, w + nw * i, nsb, xv);
-        kq_quant_x<MR>(xv, xw + i * MR * KQ_REC);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the wave's own LDS records
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-#pragma unroll
-    for (int i = 0; i < SBW; i++) {
-        const int sb = w + nw * i;
-#pragma unroll
-        for (int p = 0; p < NP; p++) {
-            const int rl = 16 * p + ur;
-            const bool valid = sb < nsb && rl < RB && row0 + rl < N;   // uniform over the unit's 4 lanes
-            const uint32_t h0 = (uint32_t)hdr[i][p][0];
-            const float d = h2f((uint16_t)(h0 & 0xffff)), dmin = h2f((uint16_t)(h0 >> 16));
-            int sc0, m0, sc1, m1;
-            scale_min_k4(2 * s, (uint32_t)hdr[i][p][1], (uint32_t)hdr[i][p][2], (uint32_t)hdr[i][p][3], sc0, m0);
-            scale_min_k4(2 * s + 1, (uint32_t)hdr[i][p][1], (uint32_t)hdr[i][p][2], (uint32_t)hdr[i][p][3], sc1, m1);
-            int lo[8], hi[8];
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                lo[t] = q0[i][p][t] & 0x0F0F0F0F;
-                hi[t] = (q0[i][p][t] >> 4) & 0x0F0F0F0F;
-                lo[4 + t] = q1[i][p][t] & 0x0F0F0F0F;
-                hi[4 + t] = (q1[i][p][t] >> 4) & 0x0F0F0F0F;
-            }
-#pragma unroll
-            for (int m = 0; m < MR; m++) {
-                // Branch-free: rows m >= M compute on zero records and are never combined; the 4
-                // lanes of a unit store the same value; invalid units write the spare slot.
-                const uint8_t *rec = xw + (i * MR + m) * KQ_REC;
-                const v4i xa0 = *(const v4i *)(rec + 64 * s), xa1 = *(const v4i *)(rec + 64 * s + 16);
-                const v4i xc0 = *(const v4i *)(rec + 64 * s + 32), xc1 = *(const v4i *)(rec + 64 * s + 48);
-                const v4i bs = *(const v4i *)(rec + 256 + 16 * s);
-                int d0 = 0, d1 = 0;
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    d0 = dot4(lo[t], xa0[t], d0);
-                    d0 = dot4(lo[4 + t], xa1[t], d0);
-                    d1 = dot4(hi[t], xc0[t], d1);
-                    d1 = dot4(hi[4 + t], xc1[t], d1);
-                }
-                const int isc = sum4_i(sc0 * d0 + sc1 * d1);
-                const int imn = sum4_i(m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]));
-                const float dx = *(const float *)(rec + 320);
-                const float dd = dx * d, dm = dx * dmin;
-                tv[valid ? (m * RB + rl) * nsb + sb : MR * RB * nsb] = dd * (float)isc - dm * (float)imn;
-            }
-        }
-    }
-    __syncthreads();
-    kq_combine<MR>(M, N, nsb, RB, row0, tv, y);
+    return (size_t)(MR * nsb + 1) * KREC + ((size_t)MR * RB * nsb + 1) * 4;
 }
 
-// Q3_K: lane s (hh = s / 2, lh = s % 2) loads qs bytes [32hh + 16lh, +16) and hmask bytes
-// [16lh, +16) and decodes the 64 elements 128hh + 32j + 16lh + (0..15), j = 0..3 (shift 2j, hmask
-// bit 4hh + j, scale index 8hh + 2j + lh), as dequantize_q3_K_block does (qwen_moe_q3k.c:565-575).
-template <int MR, int NP, int SBW>
-__global__ __launch_bounds__(512) void k_q3_K(int M, int N, int K, int RB, const uint8_t *__restrict__ hq,
-                                              const uint8_t *__restrict__ scl,
-                                              const uint16_t *__restrict__ wdd,
-                                              const float *__restrict__ x, float *__restrict__ y)
+// The lane's unit: u = sb * RB + r (clamped to the last unit; `valid` false for lanes past the
+// block's units or rows past N).
+struct KqUnit {
+    int sb, r, row;
+    bool valid;
+};
+X100_DEV KqUnit kq_unit(const KqArgs &a)
+{
+    const int lane = threadIdx.x & 63, N = a.N, RB = a.RB, nu = RB * a.nsb;
+    const int u0 = 32 * wave_id() + (lane >> 1), u = min(u0, nu - 1);
+    KqUnit k;
+    k.sb = (int)udiv16((uint32_t)u, (uint32_t)RB, a.mrb);
+    k.r = u - k.sb * RB;
+    const int row0 = blockIdx.x * RB;
+    k.row = min(row0 + k.r, N - 1);
+    k.valid = u0 < nu && row0 + k.r < N;
+    return k;
+}
+
+// Q4_K: half h holds qs bytes 64h .. 64h+63, i.e. sub-blocks j = 4h .. 4h+3 (plane c: low nibbles
+// of sub-block 4h + 2(c/2), high nibbles of 4h + 2(c/2) + 1, elements 16(c%2) .. +16), and x bytes
+// 128h .. 128h+127 of each record.
+template <int MR>
+__global__ __launch_bounds__(512) void k_q4_K(const KqArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int nsb = K / 256, nw = blockDim.x >> 6;
-    const int lane = threadIdx.x & 63, w = wave_id(), s = lane & 3, ur = lane >> 2, hh = s >> 1, lh = s & 1;
-    const int row0 = blockIdx.x * RB;
-    uint8_t *xw = smem + (size_t)w * SBW * MR * KQ_REC;
-    float *tv = (float *)(smem + (size_t)nw * SBW * MR * KQ_REC);
+    const int M = a.M, N = a.N, K = a.K, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
+    const uint8_t *__restrict__ W = a.W;
+    const float *__restrict__ x = a.x;
+    float *__restrict__ y = a.y;
+    const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1;
+    uint8_t *recs = smem;
+    float *tv = (float *)(smem + (size_t)(MR * nsb + 1) * KREC);
+    const KqUnit ku = kq_unit(a);
 
     const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
-    float4 xv[MR];
-    kq_load_x<MR>(xr, K, w, nsb, xv);
+    const bool wq = 4 * w < nq;   // the wave has records to quantize (wave-uniform)
+    Q8kFirst xf;
+    if (wq) q8k_first(xr, a, nq, nw, xf);
 
-    v4i qv[SBW][NP], hv[SBW][NP];
-    uint32_t s0[SBW][NP], s1[SBW][NP], s2[SBW][NP], dv[SBW][NP];
+    const uint8_t *sec = W + (size_t)ku.sb * q4k_sec(N);
+    v4i qv[4];
 #pragma unroll
-    for (int i = 0; i < SBW; i++)
+    for (int c = 0; c < 4; c++)
+        qv[c] = __builtin_nontemporal_load((const v4i *)(sec + (size_t)c * 32 * N + (size_t)ku.row * 32 + 16 * h));
+    const uint2 smv = *(const uint2 *)(sec + (size_t)128 * N + (size_t)ku.row * 16 + 8 * h);
+    const uint32_t ddv = *(const uint32_t *)(sec + (size_t)144 * N + (size_t)ku.row * 4);
+
+    __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the quantizer
+    if (wq) q8k_rest(xr, a, nq, nw, xf, recs);
+    __syncthreads();
+
+    int sc[4], mn[4];
 #pragma unroll
-        for (int p = 0; p < NP; p++) {
-            const int sb = min(w + nw * i, nsb - 1), row = min(row0 + min(16 * p + ur, RB - 1), N - 1);
-            const size_t rec = (size_t)row * nsb + sb;
-            qv[i][p] = __builtin_nontemporal_load((const v4i *)(hq + rec * 96 + 32 + 32 * hh + 16 * lh));
-            hv[i][p] = *(const v4i *)(hq + rec * 96 + 16 * lh);
-            const uint32_t *sp = (const uint32_t *)(scl + rec * 12);
-            s0[i][p] = sp[0];
-            s1[i][p] = sp[1];
-            s2[i][p] = sp[2];
-            dv[i][p] = wdd[rec];
-        }
-    __builtin_amdgcn_sched_barrier(0);
-    kq_quant_x<MR>(xv, xw);
-#pragma unroll
-    for (int i = 1; i < SBW; i++) {
-        kq_load_x<MR>(xr, K, w + nw * i, nsb, xv);
-        kq_quant_x<MR>(xv, xw + i * MR * KQ_REC);
+    for (int jj = 0; jj < 4; jj++) {
+        sc[jj] = (int)((smv.x >> (8 * jj)) & 0xff);
+        mn[jj] = (int)((smv.y >> (8 * jj)) & 0xff);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
+    const float d = h2f((uint16_t)(ddv & 0xffff)), dmin = h2f((uint16_t)(ddv >> 16));
+    int lo[4][4], hi[4][4];
 #pragma unroll
-    for (int i = 0; i < SBW; i++) {
-        const int sb = w + nw * i;
+    for (int c = 0; c < 4; c++)
 #pragma unroll
-        for (int p = 0; p < NP; p++) {
-            const int rl = 16 * p + ur;
-            const bool valid = sb < nsb && rl < RB && row0 + rl < N;
-            int scv[4];
-            int v[4][4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                // 6-bit scale of sub-block is = 8hh + 2j + lh: low nibble of byte 2j + lh (hh = 0)
-                // or its high nibble (hh = 1); high 2 bits from byte 8 + is % 4 at bit 2 (is / 4).
-                const int k = 2 * j + lh, is = 8 * hh + k;
-                const uint32_t low4 = (sbyte(s0[i][p], s1[i][p], s2[i][p], k) >> (4 * hh)) & 0xf;
-                const uint32_t high2 = (sbyte(s0[i][p], s1[i][p], s2[i][p], 8 + (is & 3)) >> (2 * (is >> 2))) & 3;
-                scv[j] = (int)(low4 | (high2 << 4)) - 32;
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const uint32_t lo2 = ((uint32_t)qv[i][p][t] >> (2 * j)) & 0x03030303u;
-                    const uint32_t hb = ((uint32_t)hv[i][p][t] >> (4 * hh + j)) & 0x01010101u;
-                    v[j][t] = (int)(lo2 | (hb << 2));   // 3-bit value q + 4, q in [-4, 3]
-                }
-            }
-            const float dw = h2f((uint16_t)dv[i][p]);
-#pragma unroll
-            for (int m = 0; m < MR; m++) {
-                // Branch-free, as in k_q4_K.
-                const uint8_t *rec = xw + (i * MR + m) * KQ_REC;
-                const int *bs = (const int *)(rec + 256) + 8 * hh + lh;
-                int isc = 0;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const v4i xq = *(const v4i *)(rec + 128 * hh + 32 * j + 16 * lh);
-                    int dsum = 0;
-#pragma unroll
-                    for (int t = 0; t < 4; t++) dsum = dot4(v[j][t], xq[t], dsum);
-                    dsum -= 4 * bs[2 * j];
-                    isc += scv[j] * dsum;
-                }
-                isc = sum4_i(isc);
-                const float dx = *(const float *)(rec + 320);
-                tv[valid ? (m * RB + rl) * nsb + sb : MR * RB * nsb] = (dx * dw) * (float)isc;
-            }
+        for (int t = 0; t < 4; t++) {
+            lo[c][t] = qv[c][t] & 0x0F0F0F0F;
+            hi[c][t] = (qv[c][t] >> 4) & 0x0F0F0F0F;
         }
+    const int spare = MR * RB * nsb;
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        // Branch-free: rows m >= M compute on unused LDS and are never combined.
+        const uint8_t *rec = recs + (size_t)(m * nsb + ku.sb) * KREC;
+        const v4i *xq = (const v4i *)(rec + 128 * h);
+        int dj[4];
+#pragma unroll
+        for (int p = 0; p < 2; p++) {   // plane pair p: sub-blocks 4h + 2p (low) and 4h + 2p + 1 (high)
+            const v4i x0 = xq[4 * p], x1 = xq[4 * p + 1], x2 = xq[4 * p + 2], x3 = xq[4 * p + 3];
+            int a = 0, b = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                a = dot4(lo[2 * p][t], x0[t], a);
+                a = dot4(lo[2 * p + 1][t], x1[t], a);
+                b = dot4(hi[2 * p][t], x2[t], b);
+                b = dot4(hi[2 * p + 1][t], x3[t], b);
+            }
+            dj[2 * p] = a;
+            dj[2 * p + 1] = b;
+        }
+        const v4i s32 = *(const v4i *)(rec + KR_S32 + 16 * h);
+        int isc = sc[0] * dj[0] + sc[1] * dj[1] + sc[2] * dj[2] + sc[3] * dj[3];
+        int imn = mn[0] * s32[0] + mn[1] * s32[1] + mn[2] * s32[2] + mn[3] * s32[3];
+        isc += dpp_i<0xB1>(0, isc);   // + the unit's other half
+        imn += dpp_i<0xB1>(0, imn);
+        const float dx = *(const float *)(rec + KR_D);
+        const float dd = dx * d, dm = dx * dmin;
+        tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = dd * (float)isc - dm * (float)imn;
     }
     __syncthreads();
-    kq_combine<MR>(M, N, nsb, RB, row0, tv, y);
+    kq_combine<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
+}
+
+// Q3_K: half h holds qs bytes 32h .. 32h+31 (dword t: elements 128h + 32j + 4t .. +3 at shift 2j,
+// j = 0..3) and their high bits, i.e. sub-blocks 8h + 2j + t/4; the 3-bit value q + 4 = the 2
+// low bits | high bit << 2 (dequantize_q3_K_block's q - (hbit ? 0 : 4), with the 4 taken out
+// through the sums s16).
+template <int MR>
+__global__ __launch_bounds__(512) void k_q3_K(const KqArgs a)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int M = a.M, N = a.N, K = a.K, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
+    const uint8_t *__restrict__ W = a.W;
+    const float *__restrict__ x = a.x;
+    float *__restrict__ y = a.y;
+    const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1;
+    uint8_t *recs = smem;
+    float *tv = (float *)(smem + (size_t)(MR * nsb + 1) * KREC);
+    const KqUnit ku = kq_unit(a);
+
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
+    const bool wq = 4 * w < nq;   // the wave has records to quantize (wave-uniform)
+    Q8kFirst xf;
+    if (wq) q8k_first(xr, a, nq, nw, xf);
+
+    const uint8_t *sec = W + (size_t)ku.sb * q3k_sec(N);
+    const size_t ro = (size_t)ku.row * 32 + 16 * h;
+    const v4i q0 = __builtin_nontemporal_load((const v4i *)(sec + ro));
+    const v4i q1 = __builtin_nontemporal_load((const v4i *)(sec + (size_t)32 * N + ro));
+    const v4i hm = __builtin_nontemporal_load((const v4i *)(sec + (size_t)64 * N + ro));
+    const uint2 scv = *(const uint2 *)(sec + (size_t)96 * N + (size_t)ku.row * 16 + 8 * h);
+    const uint16_t dw16 = *(const uint16_t *)(sec + (size_t)112 * N + (size_t)ku.row * 2);
+
+    __builtin_amdgcn_sched_barrier(0);
+    if (wq) q8k_rest(xr, a, nq, nw, xf, recs);
+    __syncthreads();
+
+    int sc[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) sc[k] = (int)(int8_t)(((k < 4 ? scv.x : scv.y) >> (8 * (k & 3))) & 0xff);
+    const uint32_t qd[8] = {(uint32_t)q0[0], (uint32_t)q0[1], (uint32_t)q0[2], (uint32_t)q0[3],
+                            (uint32_t)q1[0], (uint32_t)q1[1], (uint32_t)q1[2], (uint32_t)q1[3]};
+    int vq[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const uint32_t hb = ((uint32_t)hm[t >> 1] >> (4 * (t & 1) + j)) & 0x01010101u;
+            vq[j][t] = (int)(((qd[t] >> (2 * j)) & 0x03030303u) | (hb << 2));
+        }
+    const float dw = h2f(dw16);
+    const int spare = MR * RB * nsb;
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        const uint8_t *rec = recs + (size_t)(m * nsb + ku.sb) * KREC;
+        const v4i *xq = (const v4i *)(rec + 128 * h);
+        const v4i sa = *(const v4i *)(rec + KR_S16 + 32 * h), sbv = *(const v4i *)(rec + KR_S16 + 32 * h + 16);
+        const int s16[8] = {sa[0], sa[1], sa[2], sa[3], sbv[0], sbv[1], sbv[2], sbv[3]};
+        int isc = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const v4i xa = xq[2 * j], xb = xq[2 * j + 1];
+            int d0 = 0, d1 = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                d0 = dot4(vq[j][t], xa[t], d0);
+                d1 = dot4(vq[j][4 + t], xb[t], d1);
+            }
+            isc += sc[2 * j] * (d0 - 4 * s16[2 * j]) + sc[2 * j + 1] * (d1 - 4 * s16[2 * j + 1]);
+        }
+        isc += dpp_i<0xB1>(0, isc);
+        const float dx = *(const float *)(rec + KR_D);
+        tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = (dx * dw) * (float)isc;
+    }
+    __syncthreads();
+    kq_combine<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -534,15 +614,69 @@ __global__ void k_pack_q4_0(size_t nblk, const uint8_t *__restrict__ src, uint16
     for (int j = 0; j < 16; j++) o[j] = s[2 + j];
 }
 
-__global__ void k_pack_q3_K(size_t nblk, const uint8_t *__restrict__ src, uint8_t *__restrict__ hq,
-                            uint8_t *__restrict__ scl, uint16_t *__restrict__ d)
+// Q4_K GGUF blocks -> the planar layout of k_q4_K (one thread per (row, super-block) unit).
+__global__ void k_pack_q4_K(int N, int nsb, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst)
 {
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblk) return;
+    if (b >= (size_t)N * nsb) return;
+    const int n = (int)(b / nsb), sb = (int)(b % nsb);
+    const uint8_t *s = src + b * 144;
+    uint8_t *sec = dst + (size_t)sb * q4k_sec(N);
+    for (int c = 0; c < 4; c++)
+        for (int h = 0; h < 2; h++)
+            for (int k = 0; k < 16; k++) sec[(size_t)c * 32 * N + (size_t)n * 32 + 16 * h + k] = s[16 + 64 * h + 16 * c + k];
+    // get_scale_min_k4 (repack.cpp:222-233) of sub-blocks j = 0..7: half j/4, sc at j%4, m at 4 + j%4
+    const uint8_t *q = s + 4;
+    uint8_t *sm = sec + (size_t)128 * N + (size_t)n * 16;
+    for (int j = 0; j < 8; j++) {
+        int sc, m;
+        if (j < 4) {
+            sc = q[j] & 63;
+            m = q[j + 4] & 63;
+        } else {
+            sc = (q[j + 4] & 0xf) | ((q[j - 4] >> 6) << 4);
+            m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+        }
+        sm[8 * (j >> 2) + (j & 3)] = (uint8_t)sc;
+        sm[8 * (j >> 2) + 4 + (j & 3)] = (uint8_t)m;
+    }
+    uint8_t *dd = sec + (size_t)144 * N + (size_t)n * 4;
+    for (int k = 0; k < 4; k++) dd[k] = s[k];
+}
+
+// Q3_K GGUF blocks {hmask[32], qs[64], scales[12], d} -> the planar layout of k_q3_K.  The high
+// bits of half h: nib(l) = bits 4h .. 4h+3 of hmask[l]; byte 4t' + b holds nib(8t' + b) in its
+// low and nib(8t' + 4 + b) in its high nibble, so qs dword t of the half finds its four elements'
+// bit j at bit 4(t % 2) + j of each byte of high-bit dword t / 2.
+__global__ void k_pack_q3_K(int N, int nsb, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst)
+{
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= (size_t)N * nsb) return;
+    const int n = (int)(b / nsb), sb = (int)(b % nsb);
     const uint8_t *s = src + b * 110;
-    for (int j = 0; j < 96; j++) hq[b * 96 + j] = s[j];
-    for (int j = 0; j < 12; j++) scl[b * 12 + j] = s[96 + j];
-    d[b] = (uint16_t)(s[108] | (s[109] << 8));
+    const uint8_t *hmask = s, *qs = s + 32, *scales = s + 96;
+    uint8_t *sec = dst + (size_t)sb * q3k_sec(N);
+    for (int c = 0; c < 2; c++)
+        for (int h = 0; h < 2; h++)
+            for (int k = 0; k < 16; k++) sec[(size_t)c * 32 * N + (size_t)n * 32 + 16 * h + k] = qs[32 * h + 16 * c + k];
+    for (int h = 0; h < 2; h++) {
+        uint8_t *hb = sec + (size_t)64 * N + (size_t)n * 32 + 16 * h;
+        for (int t = 0; t < 4; t++)
+            for (int k = 0; k < 4; k++) {
+                const int lo = (hmask[8 * t + k] >> (4 * h)) & 15, hi = (hmask[8 * t + 4 + k] >> (4 * h)) & 15;
+                hb[4 * t + k] = (uint8_t)(lo | (hi << 4));
+            }
+    }
+    // the 6-bit scale of sub-block is (dequantize_q3_K_block, qwen_moe_q3k.c:557-577) minus 32
+    int8_t *sc = (int8_t *)(sec + (size_t)96 * N + (size_t)n * 16);
+    for (int is = 0; is < 16; is++) {
+        const int low4 = (scales[is & 7] >> (4 * (is >> 3))) & 15;
+        const int high2 = (scales[8 + (is & 3)] >> (2 * (is >> 2))) & 3;
+        sc[is] = (int8_t)((low4 | (high2 << 4)) - 32);
+    }
+    uint8_t *d = sec + (size_t)112 * N + (size_t)n * 2;
+    d[0] = s[108];
+    d[1] = s[109];
 }
 
 // Load-time requantization to Q8_0 (lin_new_i8, qwen_moe_q3k.c:872-886): thread g dequantizes
@@ -634,15 +768,12 @@ size_t x100_q_packed_bytes(int qtype, int N, int K)
         const size_t nblk = (size_t)N * (K / 32);
         return align256(nblk * 2) + nblk * 16;
     }
-    case X100_Q4_K: return (size_t)N * (K / 256) * 144;
+    case X100_Q4_K: return (size_t)(K / 256) * q4k_sec(N);
     case X100_Q8_0: case X100_Q5_K: case X100_Q6_K: {
         const size_t ngrp = (size_t)N * (K / 32);
         return align256(ngrp * 2) + ngrp * 32;
     }
-    case X100_Q3_K: {
-        const size_t nblk = (size_t)N * (K / 256);
-        return nblk * 96 + nblk * 12 + nblk * 2;
-    }
+    case X100_Q3_K: return (size_t)(K / 256) * q3k_sec(N);
     }
     return 0;
 }
@@ -658,8 +789,15 @@ hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *ds
                            (const uint8_t *)src, d, qs);
         return hipGetLastError();
     }
-    case X100_Q4_K:
-        return hipMemcpyAsync(dst, src, (size_t)N * (K / 256) * 144, hipMemcpyDeviceToDevice, s);
+    case X100_Q4_K: case X100_Q3_K: {
+        const size_t nblk = (size_t)N * (K / 256);
+        const dim3 grid((unsigned)((nblk + 255) / 256)), blk(256);
+        if (qtype == X100_Q4_K)
+            hipLaunchKernelGGL(k_pack_q4_K, grid, blk, 0, s, N, K / 256, (const uint8_t *)src, (uint8_t *)dst);
+        else
+            hipLaunchKernelGGL(k_pack_q3_K, grid, blk, 0, s, N, K / 256, (const uint8_t *)src, (uint8_t *)dst);
+        return hipGetLastError();
+    }
     case X100_Q8_0: case X100_Q5_K: case X100_Q6_K: {
         const size_t ngrp = (size_t)N * (K / 32);
         uint16_t *d = (uint16_t *)dst;
@@ -669,15 +807,6 @@ hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *ds
         if (qtype == X100_Q8_0) hipLaunchKernelGGL(k_requant_q8_0<X100_Q8_0>, grid, blk, 0, s, ngrp, sp, d, qs);
         else if (qtype == X100_Q5_K) hipLaunchKernelGGL(k_requant_q8_0<X100_Q5_K>, grid, blk, 0, s, ngrp, sp, d, qs);
         else hipLaunchKernelGGL(k_requant_q8_0<X100_Q6_K>, grid, blk, 0, s, ngrp, sp, d, qs);
-        return hipGetLastError();
-    }
-    case X100_Q3_K: {
-        const size_t nblk = (size_t)N * (K / 256);
-        uint8_t *hq = (uint8_t *)dst;
-        uint8_t *scl = hq + nblk * 96;
-        uint16_t *d = (uint16_t *)(scl + nblk * 12);
-        hipLaunchKernelGGL(k_pack_q3_K, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, nblk,
-                           (const uint8_t *)src, hq, scl, d);
         return hipGetLastError();
     }
     }
@@ -800,43 +929,20 @@ hipError_t launch_q8_0(int M, int N, int K, const void *w, const float *x, float
     return launch_q8_0_x<MR, 64, 8>(M, N, K, w, x, y, s);
 }
 
-// K-quant launch plan: nw = min(nsb, 8) waves, SBW super-blocks per wave (a power of two, at most
-// 8, so K <= 16384), RB = ceil(N / 256) rows per block (about one block per CU) but at least 16
-// and at most 32 (two passes).  False when the block's LDS would exceed 160 KiB.
+// K-quant launch plan: RB = ceil(N / 256) rows per block (about one block per CU), at most 256 / nsb
+// (at most 8 waves of 32 units); false when the block's LDS would exceed 160 KiB.
 struct KqPlan {
-    int nw, sbw, rb, np;
+    int rb, nw;
     size_t lds;
 };
 inline bool kq_plan(int MR, int N, int K, KqPlan &pl)
 {
     const int nsb = K / 256;
-    if (nsb < 1) return false;
-    pl.nw = nsb < 8 ? nsb : 8;
-    const int need = (nsb + pl.nw - 1) / pl.nw;
-    pl.sbw = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
-    if (need > 8) return false;
-    pl.rb = min(32, max(16, (N + 255) / 256));
-    pl.np = pl.sbw <= 4 ? (pl.rb + 15) / 16 : 1;   // eight super-blocks per wave: one pass
-    if (pl.np == 1) pl.rb = 16;
-    pl.lds = kq_lds(MR, pl.rb, pl.nw, pl.sbw, nsb);
+    if (nsb < 1 || nsb > 256) return false;
+    pl.rb = min(max(1, (N + 255) / 256), 256 / nsb);
+    pl.nw = (2 * pl.rb * nsb + 63) / 64;
+    pl.lds = kq_lds(MR, pl.rb, nsb);
     return pl.lds <= 160 * 1024;
-}
-
-template <int MR, bool Q3, int SBW, int NP>
-hipError_t launch_kq_s(const KqPlan &pl, int M, int N, int K, const void *w, const float *x, float *y,
-                       hipStream_t s)
-{
-    const dim3 grid((N + pl.rb - 1) / pl.rb), blk(64 * pl.nw);
-    if constexpr (Q3) {
-        const size_t nblk = (size_t)N * (K / 256);
-        const uint8_t *hq = (const uint8_t *)w;
-        const uint8_t *scl = hq + nblk * 96;
-        const uint16_t *dd = (const uint16_t *)(scl + nblk * 12);
-        hipLaunchKernelGGL((k_q3_K<MR, NP, SBW>), grid, blk, pl.lds, s, M, N, K, pl.rb, hq, scl, dd, x, y);
-    } else {
-        hipLaunchKernelGGL((k_q4_K<MR, NP, SBW>), grid, blk, pl.lds, s, M, N, K, pl.rb, (const uint8_t *)w, x, y);
-    }
-    return hipGetLastError();
 }
 
 template <int MR, bool Q3>
@@ -844,19 +950,14 @@ hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *
 {
     KqPlan pl;
     if (!kq_plan(MR, N, K, pl)) return hipErrorInvalidValue;
-    if (pl.np == 2) {
-        switch (pl.sbw) {
-        case 1: return launch_kq_s<MR, Q3, 1, 2>(pl, M, N, K, w, x, y, s);
-        case 2: return launch_kq_s<MR, Q3, 2, 2>(pl, M, N, K, w, x, y, s);
-        default: return launch_kq_s<MR, Q3, 4, 2>(pl, M, N, K, w, x, y, s);
-        }
-    }
-    switch (pl.sbw) {
-    case 1: return launch_kq_s<MR, Q3, 1, 1>(pl, M, N, K, w, x, y, s);
-    case 2: return launch_kq_s<MR, Q3, 2, 1>(pl, M, N, K, w, x, y, s);
-    case 4: return launch_kq_s<MR, Q3, 4, 1>(pl, M, N, K, w, x, y, s);
-    default: return launch_kq_s<MR, Q3, 8, 1>(pl, M, N, K, w, x, y, s);
-    }
+    const dim3 grid((N + pl.rb - 1) / pl.rb), blk(64 * pl.nw);
+    const KqArgs a{M, N, K, pl.rb, K / 256, udiv16_magic((uint32_t)pl.rb), udiv16_magic((uint32_t)(K / 256)),
+                   (const uint8_t *)w, x, y};
+    if constexpr (Q3)
+        hipLaunchKernelGGL(k_q3_K<MR>, grid, blk, pl.lds, s, a);
+    else
+        hipLaunchKernelGGL(k_q4_K<MR>, grid, blk, pl.lds, s, a);
+    return hipGetLastError();
 }
 
 }  // namespace
