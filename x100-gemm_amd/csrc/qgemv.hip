@@ -333,6 +333,7 @@ __global__ __launch_bounds__(512) void k_q4_K(const KqArgs a)
     if (wq) q8k_rest(xr, a, nq, nw, xf, recs);
     __syncthreads();
 
+    if (32 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
     int sc[4], mn[4];
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
@@ -378,6 +379,7 @@ __global__ __launch_bounds__(512) void k_q4_K(const KqArgs a)
         const float dd = dx * d, dm = dx * dmin;
         tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = dd * (float)isc - dm * (float)imn;
     }
+    }
     __syncthreads();
     kq_combine<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
 }
@@ -416,6 +418,7 @@ __global__ __launch_bounds__(512) void k_q3_K(const KqArgs a)
     if (wq) q8k_rest(xr, a, nq, nw, xf, recs);
     __syncthreads();
 
+    if (32 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
     int sc[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) sc[k] = (int)(int8_t)(((k < 4 ? scv.x : scv.y) >> (8 * (k & 3))) & 0xff);
@@ -452,6 +455,7 @@ __global__ __launch_bounds__(512) void k_q3_K(const KqArgs a)
         isc += dpp_i<0xB1>(0, isc);
         const float dx = *(const float *)(rec + KR_D);
         tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = (dx * dw) * (float)isc;
+    }
     }
     __syncthreads();
     kq_combine<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
@@ -940,7 +944,9 @@ inline bool kq_plan(int MR, int N, int K, KqPlan &pl)
     const int nsb = K / 256;
     if (nsb < 1 || nsb > 256) return false;
     pl.rb = min(max(1, (N + 255) / 256), 256 / nsb);
-    pl.nw = (2 * pl.rb * nsb + 63) / 64;
+    // waves for the units, or more (at most 8) so that every wave quantizes at most one pass of
+    // four x records; waves past the units only quantize
+    pl.nw = min(8, max((2 * pl.rb * nsb + 63) / 64, (MR * nsb + 3) / 4));
     pl.lds = kq_lds(MR, pl.rb, nsb);
     return pl.lds <= 160 * 1024;
 }
