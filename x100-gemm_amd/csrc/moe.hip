@@ -39,8 +39,9 @@ struct MoeWs {
     int *ucnt;            // [P]          pairs in union slot u
     int *upairs;          // [slot][8] pair ids (m*n_act + a) of union slot u, m ascending (M < 5);
                           // [chunk][32] from 5 rows (chunks of up to 32 pairs per expert)
-    uint8_t *xrec;        // [M][rec]: Q8_K of hn row m = q[nsb][256] | bsum[nsb][16] (int) |
-                          // d[nsb] (float), rec = that size rounded up to 16 bytes
+    uint8_t *xrec;        // Q8_K of the hn rows: below 5 rows the records [M][nsb] (KREC bytes
+                          // each, x100_common.h); from 5 rows [M][rec] = q[nsb][256] |
+                          // bsum[nsb][16] (int) | d[nsb] (float), rec rounded up to 16 bytes
     float *act;           // [P][ff]
     float *ydn;           // [P][d]
     uint8_t *xact;        // [P][recf]: Q8_K of act row p (5 or more token rows), layout of xrec
@@ -104,20 +105,29 @@ X100_DEV float swiglu(float g, float u)
 // ------------------------------------------------------------------------------------------------
 // Router.  Waves 0 .. n_exp-1 compute one expert's logits for all M rows (qwen_moe.c:296; lane l
 // sums elements 4l..4l+3, +256, ... in order, then a butterfly over the lanes); waves n_exp ..
-// n_exp + M*d/256 - 1 quantize one 256-element block of hn to Q8_K.
+// quantize four 256-element blocks of hn each into the Q8_K records ws.xrec[m * nsb + sb].
 // ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, const float *__restrict__ hn,
+__global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, uint32_t mnsb, const float *__restrict__ hn,
                                                    const float *__restrict__ R, MoeWs ws)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     float4 *s_hn = (float4 *)smem;   // [M][d/4]
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + wave_id();
-    const int nsb = d / 256;
+    const int nsb = d / 256, nq = M * nsb;
 
-    // The wave's router row (clamped expert; elements past d read as 0 and are not used).
-    const int e = min(wave, n_exp - 1);
-    const rsrc_t rr = buf_rsrc(R + (size_t)e * d, (uint32_t)d * 4u);
+    if (wave >= n_exp) {   // quantizer waves (wave-uniform)
+        const int qb = 4 * (wave - n_exp);
+        if (qb < nq) {
+            float4 v[4];
+            q8k_load(buf_rsrc(hn, (uint32_t)(M * d) * 4u), d, nsb, mnsb, nq, qb, v);
+            q8k_quant(v, nq, qb, ws.xrec);
+        }
+        if (4 * (int)blockIdx.x >= n_exp) return;   // a block of quantizer waves only
+    }
+
+    // The wave's router row (elements past d read as 0 and are not used; none for quantizer waves).
+    const rsrc_t rr = buf_rsrc(R + (size_t)min(wave, n_exp - 1) * d, wave < n_exp ? (uint32_t)d * 4u : 0u);
     float4 rv[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
@@ -143,11 +153,6 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, cons
             s = wave_sum_bfly_f(s);
             if (lane == 0) ws.logits[m * n_exp + wave] = s;
         }
-    } else if (wave < n_exp + M * nsb) {
-        const int q = wave - n_exp, m = q / nsb, sb = q - m * nsb;
-        uint8_t *rec = ws.xrec + (size_t)m * q8k_rec_bytes(nsb);
-        q8_K_wave(s_hn[q * 64 + lane], (int8_t *)rec + sb * 256, (int *)(rec + nsb * 256) + sb * 16,
-                 (float *)(rec + nsb * 320) + sb);
     }
 }
 
@@ -231,6 +236,9 @@ __global__ __launch_bounds__(256) void k_moe_route_rows(int M, int d, int n_exp,
 struct RouteLds {
     __attribute__((aligned(16))) int sel[8 * 8];
     float w[8 * 8];
+    uint32_t tk[8][8];     // row m's chosen keys in expert-id order, then in slot order (tw)
+    int ti[8][8];
+    uint32_t tw[8][8];
     int uniq[64];
     uint64_t mask[8][4];   // experts chosen by row m: bit l of mask[m][c] = expert 64c + l
     uint64_t umask[4];     // their union
@@ -247,9 +255,6 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
 #pragma unroll
     for (int c = 0; c < KC; c++) rowmask[c] = 0;
     for (int m = w; m < M; m += NWV) {
-        bool picked[KC];   // experts lane + 64c chosen for row m
-#pragma unroll
-        for (int c = 0; c < KC; c++) picked[c] = false;
         float p[KC];
         float mx = -1e30f;
 #pragma unroll
@@ -269,58 +274,82 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
         }
         s = wave_sum_bfly_f(s);
         const float inv = 1.0f / s;
-        // Selection keys: the bits of the probability (>= 0, so integer order = float order; NaN
-        // from bad input is treated as 0); absent or already chosen experts are INT_MIN, so every
-        // pass selects a distinct valid expert.
-        int key[KC];
+        // Selection keys: the bits of the probability (>= 0, so unsigned integer order = float
+        // order; NaN from bad input counts as 0).  Absent experts (ids >= n_exp, the highest) are
+        // 0 too: they lose every tie to a lower id, and n_exp >= n_act valid experts exist.
+        uint32_t key[KC];
 #pragma unroll
         for (int c = 0; c < KC; c++) {
             const float pv = p[c] * inv;
-            key[c] = (lane + 64 * c) < n_exp ? __float_as_int(pv == pv ? pv : 0.0f) : INT_MIN;
+            key[c] = ((lane + 64 * c) < n_exp && pv == pv) ? __float_as_uint(pv) : 0u;
         }
-        float wsel[8];
+        // The n_act largest keys with the lower expert id first on equal keys: the choice of
+        // n_act repeated strict argmax passes (qwen_moe.c:299-300).  T = the n_act-th largest key,
+        // found bit by bit from the counts of keys >= a candidate (ballots), then every key > T
+        // and the lowest-id keys == T up to n_act.
+        uint32_t T = 0;
+        for (int b = 30; b >= 0; b--) {
+            const uint32_t cand = T | (1u << b);
+            int cnt = 0;
 #pragma unroll
-        for (int a = 0; a < 8; a++) {
-            wsel[a] = 0.0f;
-            if (a < n_act) {
-                // Largest probability (wave maximum of the keys), then the lowest expert id holding
-                // it: per group c the lowest lane whose key matches (all ones when none does, so
-                // the unsigned minimum picks the lowest group that has one).
-                int kl = key[0];
+            for (int c = 0; c < KC; c++) cnt += __popcll(__ballot(key[c] >= cand));
+            T = cnt >= n_act ? cand : T;
+        }
+        int gt = 0;
 #pragma unroll
-                for (int c = 1; c < KC; c++) kl = max(kl, key[c]);
-                const int km = wave_max_iu(kl);
-                unsigned bi = 0xffffffffu;
+        for (int c = 0; c < KC; c++) gt += __popcll(__ballot(key[c] > T));
+        const uint64_t lt = (1ull << lane) - 1ull;
+        bool chosen[KC];
+        int below = 0;
 #pragma unroll
-                for (int c = 0; c < KC; c++) {
-                    const uint64_t h = __ballot(key[c] == km);
-                    bi = min(bi, (unsigned)(__ffsll((unsigned long long)h) - 1) | (unsigned)(64 * c));
-                }
-                wsel[a] = __int_as_float(km);
-                if (lane == 0) rl.sel[m * n_act + a] = (int)bi;
+        for (int c = 0; c < KC; c++) {
+            const uint64_t eq = __ballot(key[c] == T);
+            chosen[c] = key[c] > T || (key[c] == T && below + __popcll(eq & lt) < n_act - gt);
+            below += __popcll(eq);
+        }
+        // The chosen ones in expert-id order into lanes 0 .. n_act-1 (through LDS), then each one's
+        // slot = the number of chosen ones with a larger key, or an equal key and a lower id.
+        int base = 0;
 #pragma unroll
-                for (int c = 0; c < KC; c++) {
-                    const bool hit = (unsigned)(lane + 64 * c) == bi;
-                    picked[c] = picked[c] || hit;
-                    key[c] = hit ? INT_MIN : key[c];
-                }
+        for (int c = 0; c < KC; c++) {
+            rowmask[c] = __ballot(chosen[c]);
+            if (chosen[c]) {
+                const int pos = base + __popcll(rowmask[c] & lt);
+                rl.tk[m][pos] = key[c];
+                rl.ti[m][pos] = lane + 64 * c;
             }
+            base += __popcll(rowmask[c]);
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint32_t mk = rl.tk[m][lane & 7];
+        const int mi = rl.ti[m][lane & 7];
+        int slot = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (j < n_act) {
+                const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)mk, j);
+                const int ij = __builtin_amdgcn_readlane(mi, j);
+                slot += (kj > mk || (kj == mk && ij < mi)) ? 1 : 0;
+            }
+        if (lane < n_act) {
+            rl.sel[m * n_act + slot] = mi;
+            rl.tw[m][slot] = mk;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // Renormalise (qwen_moe.c:301): the sum in slot order, then one division per slot, lane a
         // doing slot a.
         float ssum = 0.0f;
 #pragma unroll
         for (int a = 0; a < 8; a++)
-            if (a < n_act) ssum += wsel[a];
-        float mine = wsel[0];
+            if (a < n_act) ssum += __uint_as_float(rl.tw[m][a]);
+        if (lane < n_act) rl.w[m * n_act + lane] = __uint_as_float(rl.tw[m][lane]) / ssum;
 #pragma unroll
-        for (int a = 1; a < 8; a++) mine = lane == a ? wsel[a] : mine;
-        if (lane < n_act) rl.w[m * n_act + lane] = mine / ssum;
-#pragma unroll
-        for (int c = 0; c < KC; c++) {
-            rowmask[c] = __ballot(picked[c]);
+        for (int c = 0; c < KC; c++)
             if (lane == 0) rl.mask[m][c] = rowmask[c];
-        }
     }
     // Union slots in ascending expert id: slot of expert e = number of chosen experts below e;
     // the union is the OR of the rows' masks, slots are prefix counts of its bits.
@@ -518,11 +547,10 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     __shared__ RouteLds rl;
     __shared__ int s_pairs[8], s_cnt;
     const int nsb = d / 256;
-    const int rec = q8k_rec_bytes(nsb);
 
-    // Q8_K records of all M hn rows -> LDS [M][rec], asynchronous (1 KiB chunks, one wave each;
-    // sources clamped to the records, the LDS area is padded to whole chunks).
-    const int totv = M * rec / 16;
+    // Q8_K records of all M hn rows (ws.xrec[m * nsb + sb]) -> LDS, asynchronous (1 KiB chunks, one
+    // wave each; sources clamped to the records, the LDS area is padded to whole chunks).
+    const int totv = M * nsb * KREC / 16;
     for (int ch = wave_id(); ch * 64 < totv; ch += NWV)
         dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
 
@@ -543,23 +571,26 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     }
     if (u >= U) return;
 
-    const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
+    // Units (matrix g/u, row, super-block) = 2 * GU_ROWS * nsb in that order, two lanes each (half
+    // h of the Q4_K block: qs bytes 64h .. 64h+63 and the header); lane pair i of wave w takes units
+    // i + 32 w, + 32 NWV, ... (UPL of them).
+    const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1;
     const int r0 = blockIdx.y * GU_ROWS;
     const int nunits = 2 * GU_ROWS * nsb;
     const size_t erow = (size_t)nsb * 144;               // bytes per row
     const size_t emat = erow * ff;                        // bytes per expert matrix
 
-    v4i hdr[UPL], qs[UPL];
-#pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        // Unconditional loads (unit clamped; results of units beyond nunits are discarded), so
-        // every load of the lane is in flight before the first one is waited for.
-        const int un = min(c * 8 * NWV + w * 8 + (lane >> 3), nunits - 1);
+    // The block's weight blocks -> LDS by global->LDS DMA, in unit order (144 bytes each): DMA op i
+    // of the block copies 16-byte chunks 64i .. 64i+63 (chunk c = 9 * unit + k is bytes 16k ..
+    // 16k+15 of the unit's block), so every op reads whole runs of consecutive blocks.  Chunks past
+    // the last unit are clamped onto it (the LDS area is padded to whole KiB).
+    uint8_t *wl = smem + ((size_t)M * nsb * KREC + 1023) / 1024 * 1024;
+    const int nch = nunits * 9;
+    for (int i = w; i * 64 < nch; i += NWV) {
+        const int c = min(i * 64 + lane, nch - 1), un = c / 9, k = c - un * 9;
         const int mat = un / (GU_ROWS * nsb), rem = un - mat * GU_ROWS * nsb;
         const int r = rem / nsb, sb = rem - r * nsb;
-        const uint8_t *blk = (mat ? Wu : Wg) + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
-        hdr[c] = *(const v4i *)blk;
-        qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
+        dma_1k((mat ? Wu : Wg) + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144 + 16 * k, wl + i * 1024);
     }
 
     // Pairs (token row m, slot a) of this expert, m ascending (distinct experts per row, so at
@@ -574,25 +605,32 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
                 if (rl.sel[m * n_act + a] == ex) s_pairs[c++] = m * n_act + a;
         s_cnt = c;
     }
-    __syncthreads();
+    __syncthreads();   // (waits for every wave's DMA)
     const int cnt = s_cnt;
-    float *tv = (float *)(smem + ((size_t)M * rec + 1023) / 1024 * 1024);   // [8][2][GU_ROWS][nsb]
+    float *tv = (float *)(wl + (nch + 63) / 64 * 1024);   // [8][2][GU_ROWS][nsb]
 
-    // Token rows outer, units inner (unrolled and branch-free so the scheduler interleaves them):
-    // the 8 lanes of a unit store the same value; invalid units write the spare slot.
+    // Both lanes of a unit store the same value; invalid units write the spare slot.
     const int tv_spare = 8 * 2 * GU_ROWS * nsb;
-    for (int k = 0; k < cnt; k++) {
-        const uint8_t *xr = smem + (size_t)(s_pairs[k] / n_act) * rec;
 #pragma unroll
-        for (int c = 0; c < UPL; c++) {
-            const int un = c * 8 * NWV + w * 8 + (lane >> 3);
-            const bool valid = un < nunits;
-            const int sb = valid ? un % nsb : 0;
+    for (int c = 0; c < UPL; c++) {
+        const int un = c * 32 * NWV + w * 32 + (lane >> 1);
+        const bool valid = un < nunits;
+        const int sb = valid ? un % nsb : 0;
+        const uint8_t *blk = wl + (size_t)(valid ? un : 0) * 144;
+        const v4i hdr = *(const v4i *)blk;
+        v4i qv[4];
+#pragma unroll
+        for (int pc = 0; pc < 4; pc++) qv[pc] = *(const v4i *)(blk + 16 + 64 * h + 16 * pc);
+        Q4kHalf uh;
+        q4k_scales_gguf(hdr, h, uh);
+        q4k_unpack(qv, uh);
+        const uint32_t h0 = (uint32_t)hdr[0];
+        const float dw = h2f((uint16_t)(h0 & 0xffff)), dmin = h2f((uint16_t)(h0 >> 16));
+        for (int k = 0; k < cnt; k++) {
+            const uint8_t *rec = smem + (size_t)((s_pairs[k] / n_act) * nsb + sb) * KREC;
             int isc, imn;
-            q4k_unit_dot(hdr[c], qs[c], (const int8_t *)xr + sb * 256, (const int *)(xr + nsb * 256) + sb * 16,
-                         i, isc, imn);
-            tv[valid ? k * 2 * GU_ROWS * nsb + un : tv_spare] =
-                q4k_combine(hdr[c], ((const float *)(xr + nsb * 320))[sb], isc, imn);
+            q4k_half_sums(uh, rec, h, isc, imn);
+            tv[valid ? k * 2 * GU_ROWS * nsb + un : tv_spare] = q4k_term(dw, dmin, *(const float *)(rec + KR_D), isc, imn);
         }
     }
     __syncthreads();
@@ -880,97 +918,95 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
 }
 
 // ------------------------------------------------------------------------------------------------
-// Down projection and weighted combine in one launch.  grid = d / DN blocks of NWV waves; a block
-// owns DN output rows for every (token row m, slot a) pair p = m*n_act + a.  Units (pair p, row r,
-// super-block sb) = P*DN*nsf, 8 lanes each: the unit's expert is sel[p] and its activation row is
-// act[p] (an expert chosen by several token rows is read once per pair, the repeats mostly from
-// cache), so the activation loads depend on nothing and the weight loads only on sel.  Every block
-// quantizes the P activation rows to Q8_K in LDS; y(p, r) sums the super-blocks in order and
+// Down projection and weighted combine in one launch.  grid = d / DN blocks; a block owns DN output
+// rows for every (token row m, slot a) pair p = m*n_act + a.  Units (pair p, row r, super-block
+// sb) = P*DN*nsf in that order, two lanes each (halves of the Q4_K block), UPL units per lane
+// pair: the unit's expert is sel[p] and its activation row is act[p] (an expert chosen by several
+// token rows is read once per pair, the repeats mostly from cache), so the activation loads depend
+// on nothing and the weight loads only on sel.  The block's waves quantize the P*nsf activation
+// records (Q8_K) into LDS, four per pass; y(p, r) sums the super-blocks in order and
 // out[m][r] (+)= sum over slots a = 0..n_act-1 of w_a * y (qwen_moe.c:310-311), as k_moe_down and
 // k_moe_combine do.
 // ------------------------------------------------------------------------------------------------
-constexpr int FD_NWV = 16;   // waves per block of k_moe_down_fused
 constexpr int FD_DN = 8;     // output rows per block
 
-template <int UPL, int QJ>   // QJ: activation blocks per wave per load pass
-__global__ __launch_bounds__(64 * FD_NWV) void k_moe_down_fused(int M, int d, int ff, int n_exp, int n_act,
-                                                                const uint8_t *__restrict__ Wd, MoeWs ws,
-                                                                float *__restrict__ out, int residual)
+template <int UPL>
+__global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, int n_exp, int n_act, uint32_t mnsf,
+                                                        uint32_t mdn, const uint8_t *__restrict__ Wd, MoeWs ws,
+                                                        float *__restrict__ out, int residual)
 {
-    constexpr int NWV = FD_NWV, DN = FD_DN;
+    constexpr int DN = FD_DN;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ float s_y[32][FD_DN];
     __shared__ float s_w[32];
-    const int lane = threadIdx.x & 63, w = wave_id(), i = lane & 7;
+    const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1, nw = blockDim.x >> 6;
     const int P = M * n_act;
     const int nsf = ff / 256;
     const int r0 = blockIdx.x * DN;
-    const int nunits = P * DN * nsf;
+    const int nunits = P * DN * nsf, nq = P * nsf;
     const size_t erow = (size_t)nsf * 144;
     const size_t emat = erow * d;
+    uint8_t *recs = smem;                              // [nq][KREC] activation records
+    uint8_t *wl = smem + (size_t)nq * KREC;            // [nunits][144] weight blocks (padded to KiB)
+    float *tv = (float *)(wl + ((size_t)nunits * 9 + 63) / 64 * 1024);   // [P][DN][nsf] + one spare
 
-    // LDS: Q8_K blocks of the P activation rows + one spare (blocks past nq write it, so the
-    // quantizations run unrolled and branch-free), then the unit results + one spare.
-    const int nq = P * nsf;
-    int8_t *aq = (int8_t *)smem;                       // [nq + 1][256]
-    int *abs_ = (int *)(aq + (nq + 1) * 256);          // [nq + 1][16]
-    float *ad = (float *)(abs_ + (nq + 1) * 16);       // [nq + 1]
-    float *tv = ad + nq + 1;                           // [P][DN][nsf] + one spare
-    auto act_loads = [&](int q0, float4 (&v)[QJ]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < QJ; j++) {
-            const int q = min(q0 + NWV * j + w, nq - 1);   // clamped; only q < nq is kept
-            const int p = q / nsf, sb = q - p * nsf;
-            v[j] = *(const float4 *)(ws.act + (size_t)p * ff + sb * 256 + 4 * lane);
-        }
-    };
-    auto act_quant = [&](int q0, const float4 (&v)[QJ]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < QJ; j++) {
-            const int q = q0 + NWV * j + w;
-            const int qd = q < nq ? q : nq;
-            q8_K_wave(v[j], aq + qd * 256, abs_ + qd * 16, ad + qd);
-        }
-    };
-    // The first pass's activation loads, then every weight load, then the quantizer (which waits
-    // only for the activations).
-    float4 av[QJ];
-    act_loads(0, av);
+    // The first two quantizer passes' activation loads, then every weight load, then the quantizer.
+    const rsrc_t ar = buf_rsrc(ws.act, (uint32_t)(P * ff) * 4u);
+    float4 v0[4], v1[4];
+    const bool q0 = 4 * w < nq, q1 = 4 * (w + nw) < nq;   // wave-uniform
+    if (q0) q8k_load(ar, ff, nsf, mnsf, nq, 4 * w, v0);
+    if (q1) q8k_load(ar, ff, nsf, mnsf, nq, 4 * (w + nw), v1);
+    __builtin_amdgcn_sched_barrier(0);   // the activation loads go out first (the quantizer waits only for them)
 
-    v4i hdr[UPL], qs[UPL];
-#pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        const int un = min(c * 8 * NWV + w * 8 + (lane >> 3), nunits - 1);   // clamped: see k_moe_gate_up
-        const int p = un / (DN * nsf), rem = un - p * DN * nsf;
-        const int r = rem / nsf, sb = rem - r * nsf;
-        const int ex = min((unsigned)ws.sel[p], (unsigned)(n_exp - 1));
-        const uint8_t *blk = Wd + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
-        hdr[c] = *(const v4i *)blk;
-        qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
+    // The weight blocks of the block's units -> LDS by global->LDS DMA, in unit order (144 bytes
+    // each, chunk c = 9 * unit + k), as in k_moe_gate_up; a unit's expert is sel[p].
+    // sel of every pair, one load per lane (P <= 32), then lane shuffles: the DMA addresses wait for
+    // one memory round trip, not one per DMA op.
+    const int selv = (int)min((unsigned)ws.sel[min(lane, P - 1)], (unsigned)(n_exp - 1));
+    const int nch = nunits * 9;
+    for (int i = w; i * 64 < nch; i += nw) {
+        const int c = min(i * 64 + lane, nch - 1), un = c / 9, k = c - un * 9;
+        const int p = (int)udiv16((uint32_t)un, (uint32_t)(DN * nsf), mdn), rem = un - p * DN * nsf;
+        const int r = (int)udiv16((uint32_t)rem, (uint32_t)nsf, mnsf), sb = rem - r * nsf;
+        const int ex = __shfl(selv, p, 64);
+        dma_1k(Wd + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144 + 16 * k, wl + i * 1024);
     }
     __builtin_amdgcn_sched_barrier(0);
-    act_quant(0, av);
-    for (int q0 = QJ * NWV; q0 < nq; q0 += QJ * NWV) {
-        act_loads(q0, av);
-        act_quant(q0, av);
+    if (q0) q8k_quant(v0, nq, 4 * w, recs);
+    if (q1) q8k_quant(v1, nq, 4 * (w + nw), recs);
+    for (int qb = 4 * (w + 2 * nw); qb < nq; qb += 4 * nw) {
+        float4 v[4];
+        q8k_load(ar, ff, nsf, mnsf, nq, qb, v);
+        q8k_quant(v, nq, qb, recs);
     }
     if ((int)threadIdx.x < P) s_w[threadIdx.x] = ws.sw[threadIdx.x];
     __syncthreads();
 
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int un = c * 8 * NWV + w * 8 + (lane >> 3);
+        const int un = c * 32 * nw + w * 32 + (lane >> 1);
         const bool valid = un < nunits;
         const int unc = valid ? un : 0;
-        const int p = unc / (DN * nsf), rem = unc - p * DN * nsf;
-        const int sb = rem - (rem / nsf) * nsf;
+        const int p = (int)udiv16((uint32_t)unc, (uint32_t)(DN * nsf), mdn), rem = unc - p * DN * nsf;
+        const int sb = rem - (int)udiv16((uint32_t)rem, (uint32_t)nsf, mnsf) * nsf;
+        const uint8_t *blk = wl + (size_t)unc * 144;
+        const v4i hdr = *(const v4i *)blk;
+        v4i qv[4];
+#pragma unroll
+        for (int pc = 0; pc < 4; pc++) qv[pc] = *(const v4i *)(blk + 16 + 64 * h + 16 * pc);
+        Q4kHalf uh;
+        q4k_scales_gguf(hdr, h, uh);
+        q4k_unpack(qv, uh);
+        const uint32_t h0 = (uint32_t)hdr[0];
+        const uint8_t *rec = recs + (size_t)(p * nsf + sb) * KREC;
         int isc, imn;
-        q4k_unit_dot(hdr[c], qs[c], aq + (p * nsf + sb) * 256, abs_ + (p * nsf + sb) * 16, i, isc, imn);
-        tv[valid ? un : nunits] = q4k_combine(hdr[c], ad[p * nsf + sb], isc, imn);
+        q4k_half_sums(uh, rec, h, isc, imn);
+        tv[valid ? un : nunits] = q4k_term(h2f((uint16_t)(h0 & 0xffff)), h2f((uint16_t)(h0 >> 16)),
+                                           *(const float *)(rec + KR_D), isc, imn);
     }
     __syncthreads();
     // y of each (pair, row): sequential over super-blocks (the oracle's order)
-    for (int t = threadIdx.x; t < P * DN; t += 64 * NWV) {
+    for (int t = threadIdx.x; t < P * DN; t += blockDim.x) {
         const int p = t / DN, r = t - p * DN;
         float y = 0.0f;
         for (int sb = 0; sb < nsf; sb++) y = y + tv[(p * DN + r) * nsf + sb];
@@ -978,7 +1014,7 @@ __global__ __launch_bounds__(64 * FD_NWV) void k_moe_down_fused(int M, int d, in
     }
     __syncthreads();
     // out[m][row] (+)= sum over slots a of w_a * y_a, a ascending (qwen_moe.c:310-311)
-    for (int t = threadIdx.x; t < M * DN; t += 64 * NWV) {
+    for (int t = threadIdx.x; t < M * DN; t += blockDim.x) {
         const int m = t / DN, r = t - m * DN;
         float eo = 0.0f;
         for (int a = 0; a < n_act; a++) eo = eo + s_w[m * n_act + a] * s_y[m * n_act + a][r];
@@ -1030,7 +1066,8 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     // union slots of 8 (M < 5: at most P of them) or chunks of 32 (at most P/32 + n_exp + 1, and
     // at most P)
     ws.upairs = (int *)take(sizeof(int) * ((size_t)P * 8 + 32 * (size_t)n_exp + 32));
-    ws.xrec = (uint8_t *)take((size_t)M * q8k_rec_bytes(nsb));
+    // hn records: Q8_K records [M][nsb] (below 5 rows) or per-row records (the matrix-core path)
+    ws.xrec = (uint8_t *)take(max((size_t)M * q8k_rec_bytes(nsb), (size_t)M * nsb * KREC));
     ws.act = (float *)take(sizeof(float) * (size_t)P * ff);
     ws.ydn = (float *)take(sizeof(float) * (size_t)P * d);
     ws.xact = (uint8_t *)take((size_t)P * q8k_rec_bytes(ff / 256));
@@ -1097,13 +1134,16 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     const int Umax = min(M * n_act, n_exp);
     if (M >= MF_MIN_ROWS) return moe_launch_mfma(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
 
-    const int nwaves = n_exp + M * nsb;
-    hipLaunchKernelGGL(k_moe_route, dim3((nwaves + 3) / 4), dim3(256), (size_t)M * d * 4, s, M, d, n_exp, hn, R, ws);
+    const int nwaves = n_exp + (M * nsb + 3) / 4;   // router waves, then quantizer waves of four records
+    hipLaunchKernelGGL(k_moe_route, dim3((nwaves + 3) / 4), dim3(256), (size_t)M * d * 4, s, M, d, n_exp,
+                       udiv16_magic((uint32_t)nsb), hn, R, ws);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
 
-    const size_t lds_gu = ((size_t)M * q8k_rec_bytes(nsb) + 1023) / 1024 * 1024 + ((size_t)8 * 2 * GU_ROWS * nsb + 1) * 4;
-    const int upl_gu = (2 * GU_ROWS * nsb + 8 * GU_NWV - 1) / (8 * GU_NWV);
+    const size_t lds_gu = ((size_t)M * nsb * KREC + 1023) / 1024 * 1024 +             // hn records
+                          ((size_t)2 * GU_ROWS * nsb * 9 + 63) / 64 * 1024 +           // weight blocks
+                          ((size_t)8 * 2 * GU_ROWS * nsb + 1) * 4;                      // terms
+    const int upl_gu = (2 * 2 * GU_ROWS * nsb + 64 * GU_NWV - 1) / (64 * GU_NWV);   // two lanes per unit
     const dim3 g_gu(Umax, ff / GU_ROWS);
     const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
     // One row routes inside the gate/up blocks (a separate launch costs more than it saves);
@@ -1122,47 +1162,32 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
             hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, false>), g_gu, dim3(64 * GU_NWV), lds_gu, s, M, d,  \
                                ff, n_exp, n_act, wg, wu, ws, sel, sw);                                   \
     } while (0)
-    switch (upl_gu) {
-    case 1: X100_GU(1); break;
-    case 2: X100_GU(2); break;
-    case 3: case 4: X100_GU(4); break;
-    default: X100_GU(8); break;
-    }
+    if (upl_gu == 1)
+        X100_GU(1);
+    else
+        X100_GU(2);   // at most 2 * GU_ROWS * 16 units (d <= 4096)
 #undef X100_GU
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
     {
-        // down + combine in one launch (k_moe_down_fused) when the units fit 8 per lane and the
-        // quantized activations fit LDS (every block quantizes all P rows); otherwise k_moe_down,
-        // then k_moe_combine
+        // down + combine in one launch (k_moe_down_fused) when the units fit two per lane pair in
+        // 16 waves and the activation records fit LDS (every block quantizes all P rows);
+        // otherwise k_moe_down, then k_moe_combine
         const int dn = FD_DN;
         const int P = M * n_act, nq = P * nsf, nun = P * dn * nsf;
-        const int upl = (nun + 8 * FD_NWV - 1) / (8 * FD_NWV);
-        const size_t ldsf = ((size_t)nq + 1) * (256 + 64 + 4) + ((size_t)nun + 1) * 4;
-        if (M <= 4 && d % dn == 0 && upl <= 8 && ldsf <= 96 * 1024) {
-            const dim3 gf(d / dn), bf(64 * FD_NWV);
-            const uint8_t *wdf = (const uint8_t *)Wd;
-#define X100_FD(U, QJ) hipLaunchKernelGGL((k_moe_down_fused<U, QJ>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, wdf, ws, out, residual)
-#define X100_FD_SW(QJ)                          \
-    switch (upl) {                              \
-    case 1: X100_FD(1, QJ); break;              \
-    case 2: X100_FD(2, QJ); break;              \
-    case 3: case 4: X100_FD(4, QJ); break;      \
-    case 5: case 6: X100_FD(6, QJ); break;      \
-    default: X100_FD(8, QJ); break;             \
-    }
-            // activation blocks per wave per pass: as many as nq needs, up to 8 (one pass up to
-            // 128 blocks, so no pass's loads wait behind another pass's quantization)
-            if (nq <= 2 * FD_NWV) {
-                X100_FD_SW(2)
-            } else if (nq <= 4 * FD_NWV) {
-                X100_FD_SW(4)
-            } else {
-                X100_FD_SW(8)
-            }
-#undef X100_FD_SW
-#undef X100_FD
+        const int upl = (2 * nun + 1023) / 1024;
+        const int nwf = (2 * nun + 64 * upl - 1) / (64 * upl);
+        const size_t ldsf = (size_t)nq * KREC + ((size_t)nun * 9 + 63) / 64 * 1024 + ((size_t)nun + 1) * 4;
+        if (M <= 4 && P <= 32 && d % dn == 0 && upl <= 2 && ldsf <= 160 * 1024) {
+            const dim3 gf(d / dn), bf(64 * nwf);
+            const uint32_t mnsf = udiv16_magic((uint32_t)nsf), mdn = udiv16_magic((uint32_t)(dn * nsf));
+            if (upl == 1)
+                hipLaunchKernelGGL((k_moe_down_fused<1>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn,
+                                   (const uint8_t *)Wd, ws, out, residual);
+            else
+                hipLaunchKernelGGL((k_moe_down_fused<2>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn,
+                                   (const uint8_t *)Wd, ws, out, residual);
             return hipGetLastError();
         }
     }

@@ -164,22 +164,12 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
 // reduce its integer sums with one DPP step and store its fp32 term; after the second barrier one
 // thread per (token row, row) adds the terms over super-blocks in order, the oracle's sequence
 // (bit-identical to it).
-constexpr int KR_S16 = 256, KR_S32 = 320, KR_D = 352, KREC = 368;   // Q8_K record: q[256] | s16[16] | s32[8] | d
 
 __host__ __device__ constexpr size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 __host__ __device__ constexpr size_t q4k_sec(int N) { return al256((size_t)148 * N); }
 __host__ __device__ constexpr size_t q3k_sec(int N) { return al256((size_t)114 * N); }
 
-// roundf(v) (half away from zero) for |v| < 2^23: trunc(v + copysign(0.5 - 2^-25, v)) with the add
-// rounded to nearest even.  Below a tie the sum stays under the next integer (its distance to it
-// exceeds half an ulp there), at or above a tie it reaches it; checked against roundf for every
-// float with |v| <= 128.
-X100_DEV int round_away(float v) { return (int)(v + __builtin_copysignf(0x1.fffffep-2f, v)); }
 
-// n / d for n, d < 2^16 with m = ceil(2^32 / d) precomputed on the host (exact in that range:
-// n * (m - 2^32 / d) / 2^32 < n / 2^32 < 1 / d); d = 1 is passed through.
-X100_DEV uint32_t udiv16(uint32_t n, uint32_t d, uint32_t m) { return d == 1 ? n : __umulhi(n, m); }
-inline uint32_t udiv16_magic(uint32_t d) { return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + d - 1) / d); }
 
 // Arguments of the K-quant kernels (RB rows per block, nsb = K / 256 super-blocks per row).
 struct KqArgs {
@@ -190,51 +180,9 @@ struct KqArgs {
     float *y;
 };
 
-// Q8_K records of x, four per wave pass: lane l works on record q = qb + l/16 (q = m*nsb + sb:
-// elements m*K + 256sb ..), elements 16(l%16) .. +15, with the operations of pack_A_q3k
-// (qwen_moe_q3k.c:612-624): amax over the record, d = amax/127, reciprocal 1/d (0 for d = 0),
-// q = roundf(x * (1/d)) clamped to [-128, 127], plus the sums of q per 16 and per 32 elements.
-// Records past nq read zeros and are not stored.
 X100_DEV void q8k_load(rsrc_t xr, const KqArgs &a, int nq, int qb, float4 (&v)[4])
 {
-    const int lane = threadIdx.x & 63, q = qb + (lane >> 4);
-    const int m = (int)udiv16((uint32_t)q, (uint32_t)a.nsb, a.mnsb), sb = q - m * a.nsb, K = a.K;
-    const uint32_t base = q < nq ? (uint32_t)(m * K + sb * 256 + 16 * (lane & 15)) * 4u : 0xffffff00u;
-#pragma unroll
-    for (int c = 0; c < 4; c++) v[c] = buf_load_f4(xr, base + 16u * c);
-}
-X100_DEV void q8k_quant(const float4 (&v)[4], int nq, int qb, uint8_t *recs)
-{
-    const int lane = threadIdx.x & 63, i = lane & 15, q = qb + (lane >> 4);
-    float a = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-        a = fmaxf(a, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
-    // maximum over the record's 16 lanes, in every one of them (xor 1, xor 2, mirror in 8, mirror in 16)
-    a = fmaxf(a, dpp_f<0xB1>(a, a));
-    a = fmaxf(a, dpp_f<0x4E>(a, a));
-    a = fmaxf(a, dpp_f<0x141>(a, a));
-    a = fmaxf(a, dpp_f<0x140>(a, a));
-    const float d = a / 127.0f;
-    const float rep = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t pk[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int q0 = clamp_i8(round_away(v[c].x * rep)), q1 = clamp_i8(round_away(v[c].y * rep));
-        const int q2 = clamp_i8(round_away(v[c].z * rep)), q3 = clamp_i8(round_away(v[c].w * rep));
-        pk[c] = perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u) | (perm((uint32_t)q3, (uint32_t)q2, 0x0c0c0400u) << 16);
-    }
-    int s16 = 0;
-#pragma unroll
-    for (int c = 0; c < 4; c++) s16 = dot4((int)pk[c], 0x01010101, s16);
-    const int s32 = s16 + dpp_i<0xB1>(0, s16);   // + the neighbouring 16 elements
-    if (q < nq) {
-        uint8_t *rec = recs + (size_t)q * KREC;
-        *(v4u *)(rec + 16 * i) = v4u{pk[0], pk[1], pk[2], pk[3]};
-        ((int *)(rec + KR_S16))[i] = s16;
-        ((int *)(rec + KR_S32))[i >> 1] = s32;   // the two lanes of a pair store the same sum
-        if (i == 0) *(float *)(rec + KR_D) = d;
-    }
+    q8k_load(xr, a.K, a.nsb, a.mnsb, nq, qb, v);
 }
 
 // The block's M x nsb records, passes of four: wave w takes passes w, w + nw, w + 2nw, ...  The
@@ -334,51 +282,23 @@ __global__ __launch_bounds__(512) void k_q4_K(const KqArgs a)
     __syncthreads();
 
     if (32 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
-    int sc[4], mn[4];
+        Q4kHalf u;
 #pragma unroll
-    for (int jj = 0; jj < 4; jj++) {
-        sc[jj] = (int)((smv.x >> (8 * jj)) & 0xff);
-        mn[jj] = (int)((smv.y >> (8 * jj)) & 0xff);
-    }
-    const float d = h2f((uint16_t)(ddv & 0xffff)), dmin = h2f((uint16_t)(ddv >> 16));
-    int lo[4][4], hi[4][4];
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            lo[c][t] = qv[c][t] & 0x0F0F0F0F;
-            hi[c][t] = (qv[c][t] >> 4) & 0x0F0F0F0F;
+        for (int jj = 0; jj < 4; jj++) {
+            u.sc[jj] = (int)((smv.x >> (8 * jj)) & 0xff);
+            u.mn[jj] = (int)((smv.y >> (8 * jj)) & 0xff);
         }
-    const int spare = MR * RB * nsb;
+        q4k_unpack(qv, u);
+        const float d = h2f((uint16_t)(ddv & 0xffff)), dmin = h2f((uint16_t)(ddv >> 16));
+        const int spare = MR * RB * nsb;
 #pragma unroll
-    for (int m = 0; m < MR; m++) {
-        // Branch-free: rows m >= M compute on unused LDS and are never combined.
-        const uint8_t *rec = recs + (size_t)(m * nsb + ku.sb) * KREC;
-        const v4i *xq = (const v4i *)(rec + 128 * h);
-        int dj[4];
-#pragma unroll
-        for (int p = 0; p < 2; p++) {   // plane pair p: sub-blocks 4h + 2p (low) and 4h + 2p + 1 (high)
-            const v4i x0 = xq[4 * p], x1 = xq[4 * p + 1], x2 = xq[4 * p + 2], x3 = xq[4 * p + 3];
-            int a = 0, b = 0;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                a = dot4(lo[2 * p][t], x0[t], a);
-                a = dot4(lo[2 * p + 1][t], x1[t], a);
-                b = dot4(hi[2 * p][t], x2[t], b);
-                b = dot4(hi[2 * p + 1][t], x3[t], b);
-            }
-            dj[2 * p] = a;
-            dj[2 * p + 1] = b;
+        for (int m = 0; m < MR; m++) {
+            // Branch-free: rows m >= M compute on unused LDS and are never combined.
+            const uint8_t *rec = recs + (size_t)(m * nsb + ku.sb) * KREC;
+            int isc, imn;
+            q4k_half_sums(u, rec, h, isc, imn);
+            tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = q4k_term(d, dmin, *(const float *)(rec + KR_D), isc, imn);
         }
-        const v4i s32 = *(const v4i *)(rec + KR_S32 + 16 * h);
-        int isc = sc[0] * dj[0] + sc[1] * dj[1] + sc[2] * dj[2] + sc[3] * dj[3];
-        int imn = mn[0] * s32[0] + mn[1] * s32[1] + mn[2] * s32[2] + mn[3] * s32[3];
-        isc += dpp_i<0xB1>(0, isc);   // + the unit's other half
-        imn += dpp_i<0xB1>(0, imn);
-        const float dx = *(const float *)(rec + KR_D);
-        const float dd = dx * d, dm = dx * dmin;
-        tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = dd * (float)isc - dm * (float)imn;
-    }
     }
     __syncthreads();
     kq_combine<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);

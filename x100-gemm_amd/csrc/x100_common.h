@@ -301,3 +301,136 @@ X100_DEV void q8_K_from_regs(const float4 (&v)[XPT], int c0, int total4, int8_t 
         xd[blk] = d;                       // d is wave-uniform
     }
 }
+
+// ------------------------------------------------------------------------------------------------
+// Q8_K records of 256 activations (the GEMV and the MoE block): q[256] int8 | s16[16] (int sums
+// of q per 16) | s32[8] (per 32) | d (fp32 scale), 368 bytes.  Record q = m * nsb + sb of an
+// M x K row-major activation holds elements m*K + 256sb .. +255.
+// ------------------------------------------------------------------------------------------------
+constexpr int KR_S16 = 256, KR_S32 = 320, KR_D = 352, KREC = 368;
+
+// n / d for n, d < 2^16 with m = ceil(2^32 / d) precomputed on the host (exact in that range:
+// n * (m - 2^32 / d) / 2^32 < n / 2^32 < 1 / d); d = 1 is passed through.
+X100_DEV uint32_t udiv16(uint32_t n, uint32_t d, uint32_t m) { return d == 1 ? n : __umulhi(n, m); }
+inline uint32_t udiv16_magic(uint32_t d) { return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + d - 1) / d); }
+// roundf(v) (half away from zero) for |v| < 2^23: trunc(v + copysign(0.5 - 2^-25, v)) with the add
+// rounded to nearest even.  Below a tie the sum stays under the next integer (its distance to it
+// exceeds half an ulp there), at or above a tie it reaches it; checked against roundf for every
+// float with |v| <= 128.
+X100_DEV int round_away(float v) { return (int)(v + __builtin_copysignf(0x1.fffffep-2f, v)); }
+
+// Q8_K records of x, four per wave pass: lane l works on record q = qb + l/16 (q = m*nsb + sb:
+// elements m*K + 256sb ..), elements 16(l%16) .. +15, with the operations of pack_A_q3k
+// (qwen_moe_q3k.c:612-624): amax over the record, d = amax/127, reciprocal 1/d (0 for d = 0),
+// q = roundf(x * (1/d)) clamped to [-128, 127], plus the sums of q per 16 and per 32 elements.
+// Records past nq read zeros and are not stored.
+X100_DEV void q8k_load(rsrc_t xr, int K, int nsb, uint32_t mnsb, int nq, int qb, float4 (&v)[4])
+{
+    const int lane = threadIdx.x & 63, q = qb + (lane >> 4);
+    const int m = (int)udiv16((uint32_t)q, (uint32_t)nsb, mnsb), sb = q - m * nsb;
+    const uint32_t base = q < nq ? (uint32_t)(m * K + sb * 256 + 16 * (lane & 15)) * 4u : 0xffffff00u;
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = buf_load_f4(xr, base + 16u * c);
+}
+X100_DEV void q8k_quant(const float4 (&v)[4], int nq, int qb, uint8_t *recs)
+{
+    const int lane = threadIdx.x & 63, i = lane & 15, q = qb + (lane >> 4);
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        a = fmaxf(a, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
+    // maximum over the record's 16 lanes, in every one of them (xor 1, xor 2, mirror in 8, mirror in 16)
+    a = fmaxf(a, dpp_f<0xB1>(a, a));
+    a = fmaxf(a, dpp_f<0x4E>(a, a));
+    a = fmaxf(a, dpp_f<0x141>(a, a));
+    a = fmaxf(a, dpp_f<0x140>(a, a));
+    const float d = a / 127.0f;
+    const float rep = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t pk[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int q0 = clamp_i8(round_away(v[c].x * rep)), q1 = clamp_i8(round_away(v[c].y * rep));
+        const int q2 = clamp_i8(round_away(v[c].z * rep)), q3 = clamp_i8(round_away(v[c].w * rep));
+        pk[c] = perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u) | (perm((uint32_t)q3, (uint32_t)q2, 0x0c0c0400u) << 16);
+    }
+    int s16 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) s16 = dot4((int)pk[c], 0x01010101, s16);
+    const int s32 = s16 + dpp_i<0xB1>(0, s16);   // + the neighbouring 16 elements
+    if (q < nq) {
+        uint8_t *rec = recs + (size_t)q * KREC;
+        *(v4u *)(rec + 16 * i) = v4u{pk[0], pk[1], pk[2], pk[3]};
+        ((int *)(rec + KR_S16))[i] = s16;
+        ((int *)(rec + KR_S32))[i >> 1] = s32;   // the two lanes of a pair store the same sum
+        if (i == 0) *(float *)(rec + KR_D) = d;
+    }
+}
+
+
+// ------------------------------------------------------------------------------------------------
+// Q4_K x Q8_K on half a super-block: the lane holds qs bytes 64h .. 64h+63 of a Q4_K block as four
+// 16-byte planes (plane c: low nibbles of sub-block 4h + 2(c/2), high nibbles of 4h + 2(c/2) + 1,
+// elements 16(c%2) .. +16), i.e. sub-blocks 4h .. 4h+3 = elements 128h .. 128h+127, and the 6-bit
+// (sc, m) of those four sub-blocks; the unit's other half is the neighbouring lane (lane ^ 1).
+// ------------------------------------------------------------------------------------------------
+struct Q4kHalf {
+    int lo[4][4], hi[4][4];   // [plane][dword] nibbles as bytes
+    int sc[4], mn[4];         // 6-bit scale and min of sub-blocks 4h + jj
+};
+X100_DEV void q4k_unpack(const v4i (&qv)[4], Q4kHalf &u)
+{
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            u.lo[c][t] = qv[c][t] & 0x0F0F0F0F;
+            u.hi[c][t] = (qv[c][t] >> 4) & 0x0F0F0F0F;
+        }
+}
+// get_scale_min_k4 (repack.cpp:222-233) of sub-blocks 4h .. 4h+3 from the GGUF header dwords
+// (hdr[1..3] = the 12 scale bytes s): j < 4 takes s[j] & 63 and s[j+4] & 63; j >= 4 takes
+// (s[j+4] & 15) | (s[j-4] >> 6) << 4 and (s[j+4] >> 4) | (s[j] >> 6) << 4, four bytes at a time.
+X100_DEV void q4k_scales_gguf(const v4i &hdr, int h, Q4kHalf &u)
+{
+    const uint32_t d1 = (uint32_t)hdr[1], d2 = (uint32_t)hdr[2], d3 = (uint32_t)hdr[3];
+    const uint32_t sc = h ? ((d3 & 0x0F0F0F0Fu) | ((d1 >> 2) & 0x30303030u)) : (d1 & 0x3F3F3F3Fu);
+    const uint32_t mn = h ? (((d3 >> 4) & 0x0F0F0F0Fu) | ((d2 >> 2) & 0x30303030u)) : (d2 & 0x3F3F3F3Fu);
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        u.sc[jj] = (int)((sc >> (8 * jj)) & 0xff);
+        u.mn[jj] = (int)((mn >> (8 * jj)) & 0xff);
+    }
+}
+// The unit's integers against record rec: isc = sum_j sc_j * (q_w . q_x over sub-block j), imn =
+// sum_j m_j * (sum of q_x over sub-block j), both over the whole super-block (the pair of lanes).
+X100_DEV void q4k_half_sums(const Q4kHalf &u, const uint8_t *rec, int h, int &isc, int &imn)
+{
+    const v4i *xq = (const v4i *)(rec + 128 * h);
+    int dj[4];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {   // planes 2p, 2p+1: sub-blocks 4h + 2p (low), 4h + 2p + 1 (high)
+        const v4i x0 = xq[4 * p], x1 = xq[4 * p + 1], x2 = xq[4 * p + 2], x3 = xq[4 * p + 3];
+        int a = 0, b = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            a = dot4(u.lo[2 * p][t], x0[t], a);
+            a = dot4(u.lo[2 * p + 1][t], x1[t], a);
+            b = dot4(u.hi[2 * p][t], x2[t], b);
+            b = dot4(u.hi[2 * p + 1][t], x3[t], b);
+        }
+        dj[2 * p] = a;
+        dj[2 * p + 1] = b;
+    }
+    const v4i s32 = *(const v4i *)(rec + KR_S32 + 16 * h);
+    isc = u.sc[0] * dj[0] + u.sc[1] * dj[1] + u.sc[2] * dj[2] + u.sc[3] * dj[3];
+    imn = u.mn[0] * s32[0] + u.mn[1] * s32[1] + u.mn[2] * s32[2] + u.mn[3] * s32[3];
+    isc += dpp_i<0xB1>(0, isc);   // + the other half
+    imn += dpp_i<0xB1>(0, imn);
+}
+// The super-block's fp32 term (d, dmin of the weight block; dx of the record), in the oracle's
+// operation order.
+X100_DEV float q4k_term(float d, float dmin, float dx, int isc, int imn)
+{
+    const float dd = dx * d, dm = dx * dmin;
+    return dd * (float)isc - dm * (float)imn;
+}
