@@ -236,9 +236,6 @@ __global__ __launch_bounds__(256) void k_moe_route_rows(int M, int d, int n_exp,
 struct RouteLds {
     __attribute__((aligned(16))) int sel[8 * 8];
     float w[8 * 8];
-    uint32_t tk[8][8];     // row m's chosen keys in expert-id order, then in slot order (tw)
-    int ti[8][8];
-    uint32_t tw[8][8];
     int uniq[64];
     uint64_t mask[8][4];   // experts chosen by row m: bit l of mask[m][c] = expert 64c + l
     uint64_t umask[4];     // their union
@@ -255,6 +252,9 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
 #pragma unroll
     for (int c = 0; c < KC; c++) rowmask[c] = 0;
     for (int m = w; m < M; m += NWV) {
+        bool picked[KC];   // experts lane + 64c chosen for row m
+#pragma unroll
+        for (int c = 0; c < KC; c++) picked[c] = false;
         float p[KC];
         float mx = -1e30f;
 #pragma unroll
@@ -274,82 +274,58 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
         }
         s = wave_sum_bfly_f(s);
         const float inv = 1.0f / s;
-        // Selection keys: the bits of the probability (>= 0, so unsigned integer order = float
-        // order; NaN from bad input counts as 0).  Absent experts (ids >= n_exp, the highest) are
-        // 0 too: they lose every tie to a lower id, and n_exp >= n_act valid experts exist.
-        uint32_t key[KC];
+        // Selection keys: the bits of the probability (>= 0, so integer order = float order; NaN
+        // from bad input is treated as 0); absent or already chosen experts are INT_MIN, so every
+        // pass selects a distinct valid expert.
+        int key[KC];
 #pragma unroll
         for (int c = 0; c < KC; c++) {
             const float pv = p[c] * inv;
-            key[c] = ((lane + 64 * c) < n_exp && pv == pv) ? __float_as_uint(pv) : 0u;
+            key[c] = (lane + 64 * c) < n_exp ? __float_as_int(pv == pv ? pv : 0.0f) : INT_MIN;
         }
-        // The n_act largest keys with the lower expert id first on equal keys: the choice of
-        // n_act repeated strict argmax passes (qwen_moe.c:299-300).  T = the n_act-th largest key,
-        // found bit by bit from the counts of keys >= a candidate (ballots), then every key > T
-        // and the lowest-id keys == T up to n_act.
-        uint32_t T = 0;
-        for (int b = 30; b >= 0; b--) {
-            const uint32_t cand = T | (1u << b);
-            int cnt = 0;
+        float wsel[8];
 #pragma unroll
-            for (int c = 0; c < KC; c++) cnt += __popcll(__ballot(key[c] >= cand));
-            T = cnt >= n_act ? cand : T;
-        }
-        int gt = 0;
+        for (int a = 0; a < 8; a++) {
+            wsel[a] = 0.0f;
+            if (a < n_act) {
+                // Largest probability (wave maximum of the keys), then the lowest expert id holding
+                // it: per group c the lowest lane whose key matches (all ones when none does, so
+                // the unsigned minimum picks the lowest group that has one).
+                int kl = key[0];
 #pragma unroll
-        for (int c = 0; c < KC; c++) gt += __popcll(__ballot(key[c] > T));
-        const uint64_t lt = (1ull << lane) - 1ull;
-        bool chosen[KC];
-        int below = 0;
+                for (int c = 1; c < KC; c++) kl = max(kl, key[c]);
+                const int km = wave_max_iu(kl);
+                unsigned bi = 0xffffffffu;
 #pragma unroll
-        for (int c = 0; c < KC; c++) {
-            const uint64_t eq = __ballot(key[c] == T);
-            chosen[c] = key[c] > T || (key[c] == T && below + __popcll(eq & lt) < n_act - gt);
-            below += __popcll(eq);
-        }
-        // The chosen ones in expert-id order into lanes 0 .. n_act-1 (through LDS), then each one's
-        // slot = the number of chosen ones with a larger key, or an equal key and a lower id.
-        int base = 0;
+                for (int c = 0; c < KC; c++) {
+                    const uint64_t h = __ballot(key[c] == km);
+                    bi = min(bi, (unsigned)(__ffsll((unsigned long long)h) - 1) | (unsigned)(64 * c));
+                }
+                wsel[a] = __int_as_float(km);
+                if (lane == 0) rl.sel[m * n_act + a] = (int)bi;
 #pragma unroll
-        for (int c = 0; c < KC; c++) {
-            rowmask[c] = __ballot(chosen[c]);
-            if (chosen[c]) {
-                const int pos = base + __popcll(rowmask[c] & lt);
-                rl.tk[m][pos] = key[c];
-                rl.ti[m][pos] = lane + 64 * c;
+                for (int c = 0; c < KC; c++) {
+                    const bool hit = (unsigned)(lane + 64 * c) == bi;
+                    picked[c] = picked[c] || hit;
+                    key[c] = hit ? INT_MIN : key[c];
+                }
             }
-            base += __popcll(rowmask[c]);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const uint32_t mk = rl.tk[m][lane & 7];
-        const int mi = rl.ti[m][lane & 7];
-        int slot = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (j < n_act) {
-                const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)mk, j);
-                const int ij = __builtin_amdgcn_readlane(mi, j);
-                slot += (kj > mk || (kj == mk && ij < mi)) ? 1 : 0;
-            }
-        if (lane < n_act) {
-            rl.sel[m * n_act + slot] = mi;
-            rl.tw[m][slot] = mk;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // Renormalise (qwen_moe.c:301): the sum in slot order, then one division per slot, lane a
         // doing slot a.
         float ssum = 0.0f;
 #pragma unroll
         for (int a = 0; a < 8; a++)
-            if (a < n_act) ssum += __uint_as_float(rl.tw[m][a]);
-        if (lane < n_act) rl.w[m * n_act + lane] = __uint_as_float(rl.tw[m][lane]) / ssum;
+            if (a < n_act) ssum += wsel[a];
+        float mine = wsel[0];
 #pragma unroll
-        for (int c = 0; c < KC; c++)
+        for (int a = 1; a < 8; a++) mine = lane == a ? wsel[a] : mine;
+        if (lane < n_act) rl.w[m * n_act + lane] = mine / ssum;
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            rowmask[c] = __ballot(picked[c]);
             if (lane == 0) rl.mask[m][c] = rowmask[c];
+        }
     }
     // Union slots in ascending expert id: slot of expert e = number of chosen experts below e;
     // the union is the OR of the rows' masks, slots are prefix counts of its bits.
@@ -580,17 +556,15 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
     const size_t erow = (size_t)nsb * 144;               // bytes per row
     const size_t emat = erow * ff;                        // bytes per expert matrix
 
-    // The block's weight blocks -> LDS by global->LDS DMA, in unit order (144 bytes each): DMA op i
-    // of the block copies 16-byte chunks 64i .. 64i+63 (chunk c = 9 * unit + k is bytes 16k ..
-    // 16k+15 of the unit's block), so every op reads whole runs of consecutive blocks.  Chunks past
-    // the last unit are clamped onto it (the LDS area is padded to whole KiB).
+    // The block's weight blocks -> LDS by global->LDS DMA, in unit order (144 bytes each).  The units
+    // of one matrix are rows r0 .. r0+GU_ROWS-1 of the expert, i.e. one contiguous span of GU_ROWS *
+    // erow bytes: DMA op i copies 16-byte chunks 64i .. 64i+63 of the two spans (gate, then up).
+    // Chunks past the end are clamped onto the last one (the LDS area is padded to whole KiB).
     uint8_t *wl = smem + ((size_t)M * nsb * KREC + 1023) / 1024 * 1024;
-    const int nch = nunits * 9;
+    const int nch = nunits * 9, span = GU_ROWS * nsb * 9;   // 16-byte chunks: total, per matrix
     for (int i = w; i * 64 < nch; i += NWV) {
-        const int c = min(i * 64 + lane, nch - 1), un = c / 9, k = c - un * 9;
-        const int mat = un / (GU_ROWS * nsb), rem = un - mat * GU_ROWS * nsb;
-        const int r = rem / nsb, sb = rem - r * nsb;
-        dma_1k((mat ? Wu : Wg) + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144 + 16 * k, wl + i * 1024);
+        const int c = min(i * 64 + lane, nch - 1), mat = c >= span;
+        dma_1k((mat ? Wu : Wg) + (size_t)ex * emat + (size_t)r0 * erow + 16 * (size_t)(c - mat * span), wl + i * 1024);
     }
 
     // Pairs (token row m, slot a) of this expert, m ascending (distinct experts per row, so at
@@ -932,7 +906,7 @@ constexpr int FD_DN = 8;     // output rows per block
 
 template <int UPL>
 __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, int n_exp, int n_act, uint32_t mnsf,
-                                                        uint32_t mdn, const uint8_t *__restrict__ Wd, MoeWs ws,
+                                                        uint32_t mdn, uint32_t mspan, const uint8_t *__restrict__ Wd, MoeWs ws,
                                                         float *__restrict__ out, int residual)
 {
     constexpr int DN = FD_DN;
@@ -950,34 +924,30 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, i
     uint8_t *wl = smem + (size_t)nq * KREC;            // [nunits][144] weight blocks (padded to KiB)
     float *tv = (float *)(wl + ((size_t)nunits * 9 + 63) / 64 * 1024);   // [P][DN][nsf] + one spare
 
-    // The first two quantizer passes' activation loads, then every weight load, then the quantizer.
-    const rsrc_t ar = buf_rsrc(ws.act, (uint32_t)(P * ff) * 4u);
-    float4 v0[4], v1[4];
-    const bool q0 = 4 * w < nq, q1 = 4 * (w + nw) < nq;   // wave-uniform
-    if (q0) q8k_load(ar, ff, nsf, mnsf, nq, 4 * w, v0);
-    if (q1) q8k_load(ar, ff, nsf, mnsf, nq, 4 * (w + nw), v1);
-    __builtin_amdgcn_sched_barrier(0);   // the activation loads go out first (the quantizer waits only for them)
-
-    // The weight blocks of the block's units -> LDS by global->LDS DMA, in unit order (144 bytes
-    // each, chunk c = 9 * unit + k), as in k_moe_gate_up; a unit's expert is sel[p].
-    // sel of every pair, one load per lane (P <= 32), then lane shuffles: the DMA addresses wait for
-    // one memory round trip, not one per DMA op.
-    const int selv = (int)min((unsigned)ws.sel[min(lane, P - 1)], (unsigned)(n_exp - 1));
-    const int nch = nunits * 9;
-    for (int i = w; i * 64 < nch; i += nw) {
-        const int c = min(i * 64 + lane, nch - 1), un = c / 9, k = c - un * 9;
-        const int p = (int)udiv16((uint32_t)un, (uint32_t)(DN * nsf), mdn), rem = un - p * DN * nsf;
-        const int r = (int)udiv16((uint32_t)rem, (uint32_t)nsf, mnsf), sb = rem - r * nsf;
-        const int ex = __shfl(selv, p, 64);
-        dma_1k(Wd + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144 + 16 * k, wl + i * 1024);
+    // Waves 0 .. nwq-1 quantize the activation records (four per pass); the others stage the weight
+    // blocks, so the two run side by side.  The units of pair p are rows r0 .. r0+DN-1 of expert
+    // sel[p], one contiguous span of DN * erow bytes: DMA op i copies 16-byte chunks 64i .. 64i+63
+    // of the P spans in pair order (chunks past the end clamped onto the last one, the LDS area
+    // padded to whole KiB), so LDS holds the units' blocks in unit order (144 bytes each).
+    // (One wave does both.)
+    const int nwq = nw / 2;
+    if (w < nwq || nw == 1) {
+        const rsrc_t ar = buf_rsrc(ws.act, (uint32_t)(P * ff) * 4u);
+        for (int qb = 4 * w; qb < nq; qb += 4 * max(nwq, 1)) {
+            float4 v[4];
+            q8k_load(ar, ff, nsf, mnsf, nq, qb, v);
+            q8k_quant(v, nq, qb, recs);
+        }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    if (q0) q8k_quant(v0, nq, 4 * w, recs);
-    if (q1) q8k_quant(v1, nq, 4 * (w + nw), recs);
-    for (int qb = 4 * (w + 2 * nw); qb < nq; qb += 4 * nw) {
-        float4 v[4];
-        q8k_load(ar, ff, nsf, mnsf, nq, qb, v);
-        q8k_quant(v, nq, qb, recs);
+    if (w >= nwq) {
+        const int selv = (int)min((unsigned)ws.sel[min(lane, P - 1)], (unsigned)(n_exp - 1));
+        const int nch = nunits * 9, span = DN * nsf * 9;   // 16-byte chunks: total, per pair
+        for (int i = w - nwq; i * 64 < nch; i += nw - nwq) {
+            const int c = min(i * 64 + lane, nch - 1);
+            const int p = (int)udiv16((uint32_t)c, (uint32_t)span, mspan);
+            const int ex = __shfl(selv, p, 64);
+            dma_1k(Wd + (size_t)ex * emat + (size_t)r0 * erow + 16 * (size_t)(c - p * span), wl + i * 1024);
+        }
     }
     if ((int)threadIdx.x < P) s_w[threadIdx.x] = ws.sw[threadIdx.x];
     __syncthreads();
@@ -1182,11 +1152,12 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
         if (M <= 4 && P <= 32 && d % dn == 0 && upl <= 2 && ldsf <= 160 * 1024) {
             const dim3 gf(d / dn), bf(64 * nwf);
             const uint32_t mnsf = udiv16_magic((uint32_t)nsf), mdn = udiv16_magic((uint32_t)(dn * nsf));
+            const uint32_t mspan = udiv16_magic((uint32_t)(dn * nsf * 9));
             if (upl == 1)
-                hipLaunchKernelGGL((k_moe_down_fused<1>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn,
+                hipLaunchKernelGGL((k_moe_down_fused<1>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn, mspan,
                                    (const uint8_t *)Wd, ws, out, residual);
             else
-                hipLaunchKernelGGL((k_moe_down_fused<2>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn,
+                hipLaunchKernelGGL((k_moe_down_fused<2>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn, mspan,
                                    (const uint8_t *)Wd, ws, out, residual);
             return hipGetLastError();
         }
