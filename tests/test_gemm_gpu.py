@@ -70,6 +70,24 @@ def test_gemm_skinny_8x4096x4096(dev):
     assert np.array_equal(gpu_gemm(A, B, C0, dev), oracle_gemm(A, B, C0))
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 128, 512), (16, 384, 1024), (7, 1152, 2560), (5, 768, 1536),
+                                   (16, 2048, 8192), (2, 4096, 512)])
+def test_gemm_skinny_matrix_cores(dev, M, N, K):
+    # M <= 16, N % 128 == 0, K % 512 == 0: the split-K matrix-core kernel (512 x 128 B slabs)
+    A, B = synth.gemm_inputs(M, N, K, seed=5 * M + N + K)
+    C0 = synth.rand_int8(8, (M, N)).astype(np.int32)
+    assert np.array_equal(gpu_gemm(A, B, C0, dev), oracle_gemm(A, B, C0))
+
+
+def test_gemm_skinny_matrix_cores_extremes(dev):
+    # every product -128 * -128: per element 16384 * K, the largest int8 sum
+    M, N, K = 16, 256, 2048
+    A = np.full((M, K), -128, np.int8)
+    B = np.full((K, N), -128, np.int8)
+    got = gpu_gemm(A, B, np.zeros((M, N), np.int32), dev)
+    assert np.array_equal(got, np.full((M, N), 16384 * K, np.int32))
+
+
 SHAPES = [(1, 16, 16), (2, 32, 48), (8, 4096, 256), (16, 272, 528), (17, 48, 80), (33, 48, 80),
           (128, 128, 64), (130, 144, 96), (255, 256, 256), (256, 256, 64), (300, 272, 1040),
           (512, 512, 512), (257, 528, 336), (1024, 768, 256)]

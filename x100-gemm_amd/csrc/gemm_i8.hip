@@ -750,6 +750,80 @@ __global__ __launch_bounds__(64 * W) void k_gemm_skinny(int M, int N, int K,
     }
 }
 
+// Skinny GEMM on the matrix cores: M <= 16 rows, N % 128 == 0, K % 512 == 0.  Block = 4 waves over
+// columns [n0, n0+128) and k rows [k0, k0+512) (split-K over blockIdx.y).  The block's B slab
+// (512 k-rows x 128 bytes, 64 KiB) reaches LDS by global->LDS DMA in eight 64-row chunks, the
+// 16-byte chunk c of k-row k stored at position c ^ 2((k >> 1) & 3) ^ ((k >> 4) & 1), so that each
+// transposing read below serves 32 lanes from 32 distinct banks; each chunk is multiplied as soon as
+// every wave's part of it has landed.  Wave w owns columns n0 + 32w .. +31 (two 16-column tiles)
+// and runs v_mfma_i32_16x16x64_i8 with A = the token rows (lane l: row l % 16 (zero from M), bytes
+// 16(l / 16) .. +15 of the 64-k chunk; the rows' 512-byte slice is staged in LDS too) and B = 64 k x
+// 16 columns (lane l: column l % 16, the same 16 k), two ds_read_b64_tr_b8 each (lane q of a 16-lane
+// group receives column q of an 8 x 16 byte block).  The accumulator holds C[4(l / 16) + r][column
+// l % 16]; the block's partial sums are added into C with int32 atomics (exact, order independent).
+X100_DEV int skm_swz(int k, int c) { return c ^ (2 * ((k >> 1) & 3)) ^ ((k >> 4) & 1); }
+
+// Global -> LDS DMA of 16 bytes per lane from a per-lane address, issued from inline asm: the
+// compiler does not count it, so it inserts no wait for it; the kernel waits for it itself.
+X100_DEV void dma16v(const void *src, uint32_t lds_base)
+{
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+
+__global__ __launch_bounds__(256) void k_gemm_skinny_mfma(int M, int N, int K, const int8_t *__restrict__ A,
+                                                         const int8_t *__restrict__ B, int32_t *__restrict__ C)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[512 * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t As[16 * 512];   // token rows, chunk c of row q at c ^ (q & 15)
+    const int lane = threadIdx.x & 63, w = wave_id(), g = lane >> 4, q = lane & 15;
+    const int n0 = blockIdx.x * 128, k0 = blockIdx.y * 512;
+    const uint32_t sb = lds_addr(Bs), sa = lds_addr(As);
+
+    // Every wave's DMA ops, oldest first: its two A ops (rows 4w .. 4w+3, clamped to M - 1; rows from
+    // M are zeroed in registers), then its 16 B ops: op i = 4t + w (t = 0..15) copies k-rows
+    // 8i .. 8i+7 (chunk t / 2 of 64 rows); lane L lands at row 8i + L/8, position L%8 and fetches the
+    // chunk stored there.
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int i = 2 * w + t, row = 2 * i + (lane >> 5);
+        dma16v(A + (size_t)min(row, M - 1) * K + k0 + 16 * ((lane & 31) ^ (row & 15)),
+               __builtin_amdgcn_readfirstlane(sa + (uint32_t)(1024 * i)));
+    }
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+        const int i = 4 * t + w, kr = 8 * i + (lane >> 3);
+        dma16v(B + (size_t)(k0 + kr) * N + n0 + 16 * skm_swz(kr, lane & 7),
+               __builtin_amdgcn_readfirstlane(sb + (uint32_t)(1024 * i)));
+    }
+
+    v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+    const int r8 = q >> 1, h8 = q & 1;
+    static_for<8>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        wait_vmcnt<2 * (7 - j)>();   // this wave's A ops and its two B ops of chunk j have landed
+        lds_barrier();                // and every other wave's
+        v4i a = *(const v4i *)(As + q * 512 + 16 * ((4 * j + g) ^ q));
+        a = q < M ? a : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int c = 2 * w + t;   // the tile's 16-byte column chunk
+            const int kr0 = 64 * j + 16 * g + r8, kr1 = kr0 + 8;
+            const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (lds_v2i *)(const lds_u8 *)(Bs + kr0 * 128 + 16 * skm_swz(kr0, c) + 8 * h8));
+            const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (lds_v2i *)(const lds_u8 *)(Bs + kr1 * 128 + 16 * skm_swz(kr1, c) + 8 * h8));
+            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, v4i{lo.x, lo.y, hi.x, hi.y}, acc[t], 0, 0, 0);
+        }
+    });
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 4 * g + r;
+            if (m < M) atomicAdd(&C[(size_t)m * N + n0 + 32 * w + 16 * t + q], acc[t][r]);
+        }
+}
+
 // Generic fallback: 64x64 tile, 256 threads (4x4 outputs each), 32-deep byte tiles in LDS.
 __global__ __launch_bounds__(256) void k_gemm_generic(int M, int N, int K, const int8_t *__restrict__ A,
                                                       const int8_t *__restrict__ B,
@@ -849,6 +923,10 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
     case X100_GEMM_SKINNY: {
         if (M > 16 || (size_t)K * N >= ((size_t)1 << 32)) return hipErrorInvalidValue;
         dim3 grid((N + 255) / 256, (K + 255) / 256);
+        if (N % 128 == 0 && K % 512 == 0) {   // whole 512 x 128 slabs: the matrix-core kernel
+            hipLaunchKernelGGL(k_gemm_skinny_mfma, dim3(N / 128, K / 512), dim3(256), 0, s, M, N, K, A, B, C);
+            return hipGetLastError();
+        }
         if (M <= 8)
             hipLaunchKernelGGL((k_gemm_skinny<8, 4>), grid, dim3(256), 0, s, M, N, K, A, B, C);
         else
