@@ -5,7 +5,9 @@ One step = one int8 GEMM C += A.B at M = N = K = 4096 (i.i.d. uniform int8 input
 inputs resident in HBM.  `value` is TOPS = 2*M*N*K / time over `--steps` back-to-back launches
 timed with HIP events on the launch stream.  The same JSON line carries:
   roofline      the GEMM kernel against the dense int8 MFMA peak (5.0 POPS), plus the HBM bytes
-                per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/ (if any);
+                per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/ (if any),
+                and the same GEMM timed over three rotating A/B/C sets of 96 MiB each (288 MiB,
+                more than the 256 MB Infinity Cache holds);
   cpu_baseline  the reference's scalar gemm_ref_i8 (built from its sources into oracle/_ref, or the
                 oracle's restatement when that is absent) on a bounded row sample, 1 core;
   extra         the other measured shapes: skinny 8x4096x4096 GEMM, Q4_0 / Q4_K / Q3_K GEMV at
@@ -160,35 +162,48 @@ def cpu_time(fn, min_s=0.5):
 
 # ------------------------------------------------------------------------------------------------
 def bench_gemm(torch, timer, dev, args):
+    """The headline: C += A.B at 4096^3, back-to-back launches on one A/B/C set (96 MiB, which the
+    256 MB Infinity Cache may hold between launches).  The same launches cycling over three
+    distinct sets (288 MiB, so every launch reads A, B and C from HBM and writes C back) are
+    reported beside it."""
     M = N = K = 4096
     A, B = synth.gemm_inputs(M, N, K, seed=2026)
-    dA = torch.from_numpy(A).to(dev)
-    dB = torch.from_numpy(B).to(dev)
-    dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    sets = []
+    for i in range(3):
+        dA = torch.from_numpy(A).to(dev)
+        dB = torch.from_numpy(B).to(dev)
+        dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+        sets.append((dA, dB, dC))
     s = torch.cuda.current_stream().cuda_stream
 
-    def step():
-        x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
+    def run(nsets):
+        for i in range(args.warmup):
+            dA, dB, dC = sets[i % nsets]
+            x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for i in range(args.steps):
+            dA, dB, dC = sets[i % nsets]
+            x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps, time.perf_counter() - t0
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
+    ms, wall = run(1)
+    msr, _ = run(3)
     ops = 2.0 * M * N * K
     tops = ops / (ms * 1e-3) / 1e12
-    log("gemm 4096^3: %.2f us/launch  %.1f TOPS  (wall %.3f s for %d steps)" % (ms * 1e3, tops, wall, args.steps))
+    topsr = ops / (msr * 1e-3) / 1e12
+    log("gemm 4096^3: %.2f us/launch  %.1f TOPS (wall %.3f s for %d steps); over 3 rotating A/B/C sets "
+        "(288 MiB): %.2f us  %.1f TOPS" % (ms * 1e3, tops, wall, args.steps, msr * 1e3, topsr))
     traffic = read_traffic("gemm_i8_4096")
     roof = {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
             "frac": tops / PEAK_INT8_TOPS, "traffic": traffic,
-            "kernel": "k_gemm_big<8, 2> (256x256 tile, 8 waves, 2 K stages per barrier)", "algorithmic_ops_per_launch": ops}
+            "kernel": "k_gemm_big<8, 2> (256x256 tile, 8 waves, 2 K stages per barrier)", "algorithmic_ops_per_launch": ops,
+            "rotating_sets": {"sets": 3, "bytes": 3 * (M * K + K * N + 4 * M * N), "us": msr * 1e3,
+                              "TOPS": topsr, "frac": topsr / PEAK_INT8_TOPS}}
     return ms, tops, roof
 
 
@@ -493,8 +508,8 @@ def bench_extra(torch, timer, dev, args):
 def probe_paths(torch, dev, s, reps=3):
     """Launches of every other kernel family at its benchmark shape, for hardware counters:
     skinny GEMM, the Q4_0 / Q4_K / Q3_K GEMVs and the int8-path GEMV of the Q6_K lm_head at M = 1
-    and 4, the int4 / int8 tile GEMV at M = 1, and the MoE layer at M = 1 and 4, each `reps` times
-    on distinct weight copies."""
+    and 4, the int4 / int8 tile GEMV at M = 1, and the MoE layer at M = 1, 4, 8 and 64 (the last
+    two on the matrix-core expert GEMMs), each `reps` times on distinct weight copies."""
     M, N, K = 8, 4096, 4096
     A, B = synth.gemm_inputs(M, N, K, seed=2027)
     dA = torch.from_numpy(A).to(dev)
@@ -535,7 +550,7 @@ def probe_paths(torch, dev, s, reps=3):
     dR = torch.from_numpy(synth.moe_router(n_exp, d, seed=501)).to(dev)
     base = [torch.from_numpy(np.ascontiguousarray(w).view(np.uint8).reshape(-1)).to(dev) for w in (Wg, Wu, Wd)]
     layers = [base] + [[b.clone() for b in base] for _ in range(reps - 1)]
-    for M in (1, 4):
+    for M in (1, 4, 8, 64):
         dh = torch.from_numpy(synth.normal_f32(900 + M, (reps, M, d))).to(dev)
         out = torch.empty((M, d), dtype=torch.float32, device=dev)
         for i in range(reps):
