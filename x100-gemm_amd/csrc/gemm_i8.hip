@@ -214,7 +214,6 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i lds_v2i;
 
-X100_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(const lds_u8 *)p; }
 
 // LDS swizzles for a 64-bank (256 bytes per cycle) LDS: ds_read_b128 serves 16 lanes and
 // ds_read_b64_tr_b8 32 lanes per cycle, so those lanes must hit distinct 16-byte granules of a
@@ -763,12 +762,6 @@ __global__ __launch_bounds__(64 * W) void k_gemm_skinny(int M, int N, int K,
 // l % 16]; the block's partial sums are added into C with int32 atomics (exact, order independent).
 X100_DEV int skm_swz(int k, int c) { return c ^ (2 * ((k >> 1) & 3)) ^ ((k >> 4) & 1); }
 
-// Global -> LDS DMA of 16 bytes per lane from a per-lane address, issued from inline asm: the
-// compiler does not count it, so it inserts no wait for it; the kernel waits for it itself.
-X100_DEV void dma16v(const void *src, uint32_t lds_base)
-{
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
-}
 
 __global__ __launch_bounds__(256) void k_gemm_skinny_mfma(int M, int N, int K, const int8_t *__restrict__ A,
                                                          const int8_t *__restrict__ B, int32_t *__restrict__ C)

@@ -374,9 +374,6 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
         route_rows<NWV, 4>(M, n_exp, n_act, logits, rl);
 }
 
-// ------------------------------------------------------------------------------------------------
-// grid (U_max, ff / GU_ROWS).  Units (matrix g/u, row, super-block) = 2*GU_ROWS*nsb, 8 lanes each.
-// ------------------------------------------------------------------------------------------------
 // Routing of the rows (computed by route_block into rl) -> workspace: sel, sw (and the caller's
 // copies), the union (ascending expert id), its pair lists (token row ascending) and size.
 X100_DEV void publish_routing(int M, int n_act, const RouteLds &rl, MoeWs ws, int *__restrict__ sel_out,
@@ -513,6 +510,10 @@ __global__ __launch_bounds__(512) void k_moe_topk_group(int M, int n_exp, int n_
     group_pairs<PCH>(P, n_exp, [&](int p) { return rl.sel[p]; }, ws);
 }
 
+// ------------------------------------------------------------------------------------------------
+// grid (U_max, ff / GU_ROWS).  Units (matrix g/u, row, super-block) = 2*GU_ROWS*nsb, two lanes each,
+// the weight blocks and the Q8_K records read from LDS.
+// ------------------------------------------------------------------------------------------------
 template <int UPL, int NWV, bool ROUTED>
 __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
                                                      const uint8_t *__restrict__ Wg,
@@ -620,6 +621,111 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, 
         ws.act[(size_t)s_pairs[k] * ff + r0 + r] = swiglu(g, up);
     }
     __syncthreads();
+}
+
+// ------------------------------------------------------------------------------------------------
+// Gate/up for 2 .. 4 token rows (routing from k_moe_topk), persistent: each block stages the Q8_K
+// records of all M rows and the whole routing in LDS once, then walks the work items it =
+// blockIdx.x, + gridDim.x, ... (item = union slot u, GU_ROWS rows of ff).  The next item's weights
+// are staged into the second of two LDS buffers while the current item is computed, so a block
+// always has one item's weights in flight.  Per item the work is k_moe_gate_up's: units (matrix,
+// row, super-block), two lanes each, from LDS; SwiGLU after the sums over super-blocks in order.
+// The weight DMA is issued from inline asm (dma16v) and waited for with an exact s_waitcnt: on
+// this GPU global stores count in vmcnt too, and only wave 0 stores act (one instruction per item,
+// cnt * GU_ROWS <= 32 values), so at the top of an item wave 0 lets its last store stay
+// outstanding.
+// ------------------------------------------------------------------------------------------------
+template <int UPL, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff, int n_act,
+                                                            const uint8_t *__restrict__ Wg,
+                                                            const uint8_t *__restrict__ Wu, MoeWs ws)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int s_uniq[32], s_cnt[32], s_pairs[32 * 8], s_U;
+    const int nsb = d / 256, P = M * n_act;
+    const int t = threadIdx.x, lane = t & 63, w = wave_id(), h = lane & 1;
+
+    // Records of all M rows and the routing -> LDS, once.
+    const int totv = M * nsb * KREC / 16;
+    for (int ch = w; ch * 64 < totv; ch += NWV)
+        dma_1k((const v4i *)ws.xrec + min(ch * 64 + lane, totv - 1), smem + ch * 1024);
+    if (t < P) {
+        s_uniq[t] = ws.uniq[t];
+        s_cnt[t] = ws.ucnt[t];
+    }
+    for (int i = t; i < P * 8; i += 64 * NWV) s_pairs[i] = ws.upairs[i];
+    if (t == 0) s_U = *ws.nuniq;
+    __syncthreads();   // (waits for the DMA and the loads)
+
+    const int nrg = ff / GU_ROWS, items = s_U * nrg;
+    const int nunits = 2 * GU_ROWS * nsb;
+    const size_t erow = (size_t)nsb * 144, emat = erow * ff;
+    const int nch = nunits * 9, span = GU_ROWS * nsb * 9;   // 16-byte chunks: item, one matrix
+    const uint32_t wbytes = (uint32_t)((nch + 63) / 64 * 1024);
+    uint8_t *wl0 = smem + ((size_t)M * nsb * KREC + 1023) / 1024 * 1024;
+    float *tv = (float *)(wl0 + 2 * (size_t)wbytes);   // [4][2][GU_ROWS][nsb] + one spare
+    const uint32_t wlds = lds_addr(wl0);
+
+    // Weight blocks of item `it` into buffer b: DMA op i copies chunks 64i .. 64i+63 of the gate
+    // span then the up span (chunks past the end clamped onto the last one; the buffer is whole KiB).
+    auto issue = [&](int it, int b) __attribute__((always_inline)) {
+        const int u = it / nrg, r0 = (it - u * nrg) * GU_ROWS;
+        const size_t off = (size_t)s_uniq[u] * emat + (size_t)r0 * erow;
+        for (int i = w; i * 64 < nch; i += NWV) {
+            const int c = min(i * 64 + lane, nch - 1), mat = c >= span;
+            dma16v((mat ? Wu : Wg) + off + 16 * (size_t)(c - mat * span),
+                   __builtin_amdgcn_readfirstlane(wlds + b * wbytes + (uint32_t)i * 1024u));
+        }
+    };
+    int it = blockIdx.x, b = 0;
+    if (it < items) issue(it, 0);
+    for (bool first = true; it < items; it += gridDim.x, b ^= 1, first = false) {
+        // This item's weights are in (this wave's operations; then every wave's, by the barrier),
+        // and every wave is done with the other buffer and tv.
+        if (w == 0 && !first)
+            asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (it + (int)gridDim.x < items) issue(it + gridDim.x, b ^ 1);
+
+        const int u = it / nrg, r0 = (it - u * nrg) * GU_ROWS, cnt = s_cnt[u];
+        const uint8_t *wl = wl0 + (size_t)b * wbytes;
+        const int tv_spare = 4 * 2 * GU_ROWS * nsb;
+#pragma unroll
+        for (int c = 0; c < UPL; c++) {
+            const int un = c * 32 * NWV + w * 32 + (lane >> 1);
+            const bool valid = un < nunits;
+            const int sb = valid ? un % nsb : 0;
+            const uint8_t *blk = wl + (size_t)(valid ? un : 0) * 144;
+            const v4i hdr = *(const v4i *)blk;
+            v4i qv[4];
+#pragma unroll
+            for (int pc = 0; pc < 4; pc++) qv[pc] = *(const v4i *)(blk + 16 + 64 * h + 16 * pc);
+            Q4kHalf uh;
+            q4k_scales_gguf(hdr, h, uh);
+            q4k_unpack(qv, uh);
+            const uint32_t h0 = (uint32_t)hdr[0];
+            const float dw = h2f((uint16_t)(h0 & 0xffff)), dmin = h2f((uint16_t)(h0 >> 16));
+            for (int k = 0; k < cnt; k++) {
+                const uint8_t *rec = smem + (size_t)((s_pairs[u * 8 + k] / n_act) * nsb + sb) * KREC;
+                int isc, imn;
+                q4k_half_sums(uh, rec, h, isc, imn);
+                tv[valid ? k * 2 * GU_ROWS * nsb + un : tv_spare] = q4k_term(dw, dmin, *(const float *)(rec + KR_D), isc, imn);
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // g, u sequential over super-blocks; SwiGLU (qwen_moe.c:309): wave 0 only (cnt * GU_ROWS <= 32)
+        if (t < cnt * GU_ROWS) {
+            const int k = t / GU_ROWS, r = t - k * GU_ROWS;
+            const float *tg = tv + k * 2 * GU_ROWS * nsb + r * nsb;
+            const float *tu = tg + GU_ROWS * nsb;
+            float g = 0.0f, up = 0.0f;
+            for (int sb = 0; sb < nsb; sb++) g = g + tg[sb];
+            for (int sb = 0; sb < nsb; sb++) up = up + tu[sb];
+            ws.act[(size_t)s_pairs[u * 8 + k] * ff + r0 + r] = swiglu(g, up);
+        }
+    }
 }
 
 // Q8_K of every pair's activation row, once (5 or more token rows): wave q quantizes block
@@ -932,11 +1038,18 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, i
     // (One wave does both.)
     const int nwq = nw / 2;
     if (w < nwq || nw == 1) {
+        // The activation rows were written by the previous launch, so every load is a round trip
+        // to memory: the loads of four passes are issued before the first is quantized (passes past
+        // the last record read out of range, which returns zeros and touches no memory).
         const rsrc_t ar = buf_rsrc(ws.act, (uint32_t)(P * ff) * 4u);
-        for (int qb = 4 * w; qb < nq; qb += 4 * max(nwq, 1)) {
-            float4 v[4];
-            q8k_load(ar, ff, nsf, mnsf, nq, qb, v);
-            q8k_quant(v, nq, qb, recs);
+        const int step = 4 * max(nwq, 1);
+        for (int qb0 = 4 * w; qb0 < nq; qb0 += 4 * step) {
+            float4 v[4][4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) q8k_load(ar, ff, nsf, mnsf, nq, qb0 + p * step, v[p]);
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+                if (qb0 + p * step < nq) q8k_quant(v[p], nq, qb0 + p * step, recs);
         }
     }
     if (w >= nwq) {
@@ -1123,12 +1236,19 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
         err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
+    // Several rows: the persistent gate/up, as many blocks as are resident at once (at most one per
+    // work item), each with two weight buffers.
+    const size_t lds_gp = ((size_t)M * nsb * KREC + 1023) / 1024 * 1024 +
+                          2 * (((size_t)2 * GU_ROWS * nsb * 9 + 63) / 64 * 1024) +
+                          ((size_t)4 * 2 * GU_ROWS * nsb + 1) * 4;
 #define X100_GU(U)                                                                                       \
     do {                                                                                                 \
-        if (M > 1)                                                                                       \
-            hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, true>), g_gu, dim3(64 * GU_NWV), lds_gu, s, M, d, ff, \
-                               n_exp, n_act, wg, wu, ws, sel, sw);                                       \
-        else                                                                                             \
+        if (M > 1) {                                                                                     \
+            const int nb = min(Umax * (ff / GU_ROWS),                                                    \
+                               resident_blocks(k_moe_gate_up_p<U, GU_NWV>, 64 * GU_NWV, lds_gp));         \
+            hipLaunchKernelGGL((k_moe_gate_up_p<U, GU_NWV>), dim3(nb), dim3(64 * GU_NWV), lds_gp, s, M, d, ff, \
+                               n_act, wg, wu, ws);                                                       \
+        } else                                                                                           \
             hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, false>), g_gu, dim3(64 * GU_NWV), lds_gu, s, M, d,  \
                                ff, n_exp, n_act, wg, wu, ws, sel, sw);                                   \
     } while (0)

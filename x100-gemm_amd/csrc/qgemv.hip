@@ -786,28 +786,6 @@ hipError_t launch_q4_0(int M, int N, int K, const void *w, const float *x, float
     return launch_q4_0_x<MR, 16>(M, N, K, w, x, y, s);
 }
 
-// Blocks of kernel k that are resident on the whole device at once with lds bytes of dynamic LDS
-// (the runtime's occupancy for the kernel times the CU count): the grid of a persistent launch.
-// Cached per kernel for the last (device, lds) pair of the calling thread.
-template <typename Kern>
-int resident_blocks(Kern k, int nt, size_t lds)
-{
-    static thread_local int c_dev = -1, c_blocks = 0;
-    static thread_local size_t c_lds = 0;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    if (dev != c_dev || lds != c_lds) {
-        int occ = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, nt, lds) != hipSuccess || occ < 1) occ = 1;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-            cus = 256;
-        c_dev = dev;
-        c_lds = lds;
-        c_blocks = occ * cus;
-    }
-    return c_blocks;
-}
-
 // int8 path: 256 threads.  Lanes per row LPR and blocks per lane BPL from nb = K/32 (a slot covers
 // the row with at most 4 blocks per lane up to K = 8192); RPW row slots per wave so that a
 // group's loads (RPW * BPL blocks of 34 B per lane, twice for the prefetch) stay within about 64

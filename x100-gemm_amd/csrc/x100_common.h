@@ -209,6 +209,20 @@ X100_DEV void dma_1k(const void *src, void *lds_base)
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_base, 16, 0, 0);
 }
 
+// LDS byte address of a pointer into LDS (the M0 operand of the DMA below).
+X100_DEV uint32_t lds_addr(const void *p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+
+// The same 16-byte-per-lane global -> LDS DMA from a per-lane address, issued from inline asm: the
+// compiler does not count it, so it inserts no wait for it and the kernel waits for it itself
+// (s_waitcnt vmcnt; each wave's operations complete in issue order).  lds_base is wave-uniform.
+X100_DEV void dma16v(const void *src, uint32_t lds_base)
+{
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+
 // ------------------------------------------------------------------------------------------------
 // Activation quantizers for a 256-thread block.  The M x K fp32 rows are read as float4 (float4
 // f = c0 + tid + 256*i holds elements 4f .. 4f+3 of the flattened rows) in chunks of XPT float4
@@ -433,4 +447,26 @@ X100_DEV float q4k_term(float d, float dmin, float dx, int isc, int imn)
 {
     const float dd = dx * d, dm = dx * dmin;
     return dd * (float)isc - dm * (float)imn;
+}
+
+// Blocks of kernel k that are resident on the whole device at once with lds bytes of dynamic LDS
+// (the runtime's occupancy for the kernel times the CU count): the grid of a persistent launch.
+// Cached per kernel for the last (device, lds) pair of the calling thread.
+template <typename Kern>
+inline int resident_blocks(Kern k, int nt, size_t lds)
+{
+    static thread_local int c_dev = -1, c_blocks = 0;
+    static thread_local size_t c_lds = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    if (dev != c_dev || lds != c_lds) {
+        int occ = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, nt, lds) != hipSuccess || occ < 1) occ = 1;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        c_dev = dev;
+        c_lds = lds;
+        c_blocks = occ * cus;
+    }
+    return c_blocks;
 }
