@@ -3,16 +3,16 @@
 // chunks of 32 on the matrix cores (k_moe_mfma).  Both give each row the same bits as a one-row
 // call.
 //
-// Below 5 rows, three to five launches on one stream; each kernel only reads what an earlier launch
+// Below 5 rows, three or four launches on one stream; each kernel only reads what an earlier launch
 // wrote, so no block ever waits for, or signals, another block (no fences, no atomics):
 //   k_moe_route       router logits R.hn (one wave per expert) and the Q8_K form of every hn row.
-//   k_moe_topk        (M > 1) softmax, top-k and the expert union of all rows, once, in one block.
-//   k_moe_gate_up     grid (union slot, GU_ROWS rows of ff).  With one token row every block
-//                     derives the routing itself (cheaper than another launch; block (0, 0)
-//                     publishes it), with several it reads k_moe_topk's.  It streams its GU_ROWS
-//                     rows of the expert's gate and up matrices once for all token rows that chose
-//                     the expert (Q4_K x Q8_K, the MUL_MAT_ID grouping of ime.cpp:667-697) and
-//                     writes SwiGLU(g, u) per (token row, slot) pair.
+//   k_moe_gate_up_p   persistent blocks over the work items (union slot, GU_ROWS rows of ff).  Every
+//                     block derives the routing of all rows itself (cheaper than another launch;
+//                     block 0 publishes it), then streams the items' rows of the expert's gate and
+//                     up matrices once for all token rows that chose the expert (Q4_K x Q8_K, the
+//                     MUL_MAT_ID grouping of ime.cpp:667-697), the next item's weights in flight
+//                     while the current one is computed, and writes SwiGLU(g, u) per (token row,
+//                     slot) pair.
 //   k_moe_down_fused  grid (FD_DN rows of d): every pair's activation row quantized to Q8_K in
 //                     LDS, the down projection of those rows for all pairs, and the weighted
 //                     combine in slot order, written to out.
@@ -24,8 +24,8 @@
 
 namespace {
 
-constexpr int GU_ROWS = 8;    // gate/up rows of ff per block
-constexpr int GU_NWV = 4;     // waves per block of k_moe_gate_up (more waves: fewer blocks resident per CU, each re-deriving the routing)
+constexpr int GU_ROWS = 8;    // gate/up rows of ff per work item
+constexpr int GU_NWV = 4;     // waves per block of k_moe_gate_up_p (one per token row for the routing)
 constexpr int DN_ROWS = 16;   // down rows of d per block
 constexpr int MF_MIN_ROWS = 5;   // token rows from which the expert products run on the matrix cores
 
@@ -374,6 +374,24 @@ X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__
         route_rows<NWV, 4>(M, n_exp, n_act, logits, rl);
 }
 
+// Pair t = (token row m, slot a) of the routing in rl: the union slot of its expert, its place in
+// the slot's list (earlier rows that chose the expert come first: token rows ascending) and the
+// list length.
+X100_DEV void pair_slot(int M, int n_act, const RouteLds &rl, int t, int &slot, int &pos, int &cnt)
+{
+    const int e = rl.sel[t], m = t / n_act, c = e >> 6;
+    const uint64_t bit = 1ull << (e & 63);
+    slot = __popcll(rl.umask[c] & (bit - 1ull));
+    for (int k = 0; k < c; k++) slot += __popcll(rl.umask[k]);
+    pos = 0;
+    cnt = 0;
+    for (int r = 0; r < M; r++) {
+        const int has = (rl.mask[r][c] & bit) != 0;
+        pos += r < m ? has : 0;
+        cnt += has;
+    }
+}
+
 // Routing of the rows (computed by route_block into rl) -> workspace: sel, sw (and the caller's
 // copies), the union (ascending expert id), its pair lists (token row ascending) and size.
 X100_DEV void publish_routing(int M, int n_act, const RouteLds &rl, MoeWs ws, int *__restrict__ sel_out,
@@ -382,22 +400,13 @@ X100_DEV void publish_routing(int M, int n_act, const RouteLds &rl, MoeWs ws, in
     const int t = threadIdx.x;
     const int U = rl.U;
     if (t < M * n_act) {
-        const int e = rl.sel[t], m = t / n_act, c = e >> 6;
-        const uint64_t bit = 1ull << (e & 63);
+        const int e = rl.sel[t];
         ws.sel[t] = e;
         ws.sw[t] = rl.w[t];
         if (sel_out) sel_out[t] = e;
         if (sw_out) sw_out[t] = rl.w[t];
-        // union slot of e, the pair's place in the slot's list (earlier rows that chose e come
-        // first: token rows ascending) and the list length
-        int slot = __popcll(rl.umask[c] & (bit - 1ull));
-        for (int k = 0; k < c; k++) slot += __popcll(rl.umask[k]);
-        int pos = 0, cnt = 0;
-        for (int r = 0; r < M; r++) {
-            const int has = (rl.mask[r][c] & bit) != 0;
-            pos += r < m ? has : 0;
-            cnt += has;
-        }
+        int slot, pos, cnt;
+        pair_slot(M, n_act, rl, t, slot, pos, cnt);
         ws.upairs[slot * 8 + pos] = t;
         if (pos == 0) {
             ws.uniq[slot] = e;
@@ -405,18 +414,6 @@ X100_DEV void publish_routing(int M, int n_act, const RouteLds &rl, MoeWs ws, in
         }
     }
     if (t == 0) *ws.nuniq = U;
-}
-
-// ------------------------------------------------------------------------------------------------
-// Routing of M > 1 token rows, once, in one block (one wave per row): the gate/up blocks then read
-// it from the workspace instead of each re-deriving it.
-// ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(512) void k_moe_topk(int M, int n_exp, int n_act, MoeWs ws,
-                                                  int *__restrict__ sel_out, float *__restrict__ sw_out)
-{
-    __shared__ RouteLds rl;
-    route_block<8>(M, n_exp, n_act, ws.logits, rl);
-    publish_routing(M, n_act, rl, ws, sel_out, sw_out);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -511,153 +508,53 @@ __global__ __launch_bounds__(512) void k_moe_topk_group(int M, int n_exp, int n_
 }
 
 // ------------------------------------------------------------------------------------------------
-// grid (U_max, ff / GU_ROWS).  Units (matrix g/u, row, super-block) = 2*GU_ROWS*nsb, two lanes each,
-// the weight blocks and the Q8_K records read from LDS.
-// ------------------------------------------------------------------------------------------------
-template <int UPL, int NWV, bool ROUTED>
-__global__ __launch_bounds__(64 * NWV) void k_moe_gate_up(int M, int d, int ff, int n_exp, int n_act,
-                                                     const uint8_t *__restrict__ Wg,
-                                                     const uint8_t *__restrict__ Wu, MoeWs ws,
-                                                     int *__restrict__ sel_out, float *__restrict__ sw_out)
-{
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ RouteLds rl;
-    __shared__ int s_pairs[8], s_cnt;
-    const int nsb = d / 256;
-
-    // Q8_K records of all M hn rows (ws.xrec[m * nsb + sb]) -> LDS, asynchronous (1 KiB chunks, one
-    // wave each; sources clamped to the records, the LDS area is padded to whole chunks).
-    const int totv = M * nsb * KREC / 16;
-    for (int ch = wave_id(); ch * 64 < totv; ch += NWV)
-        dma_1k((const v4i *)ws.xrec + min(ch * 64 + (int)(threadIdx.x & 63), totv - 1), smem + ch * 1024);
-
-    const int u = blockIdx.x;
-    int U, ex, pr = 0, cnt_r = 0;
-    if constexpr (ROUTED) {
-        // routing from k_moe_topk: union entry, its pairs and the union size in one round trip
-        // (u < gridDim.x = M * n_act, so every index is inside the workspace arrays)
-        ex = ws.uniq[u];
-        pr = ws.upairs[u * 8 + min((int)(threadIdx.x & 63), 7)];
-        cnt_r = ws.ucnt[u];
-        U = *ws.nuniq;
-    } else {
-        route_block<NWV>(M, n_exp, n_act, ws.logits, rl);
-        if (blockIdx.x == 0 && blockIdx.y == 0) publish_routing(M, n_act, rl, ws, sel_out, sw_out);
-        U = rl.U;
-        ex = rl.uniq[min(u, U - 1)];
-    }
-    if (u >= U) return;
-
-    // Units (matrix g/u, row, super-block) = 2 * GU_ROWS * nsb in that order, two lanes each (half
-    // h of the Q4_K block: qs bytes 64h .. 64h+63 and the header); lane pair i of wave w takes units
-    // i + 32 w, + 32 NWV, ... (UPL of them).
-    const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1;
-    const int r0 = blockIdx.y * GU_ROWS;
-    const int nunits = 2 * GU_ROWS * nsb;
-    const size_t erow = (size_t)nsb * 144;               // bytes per row
-    const size_t emat = erow * ff;                        // bytes per expert matrix
-
-    // The block's weight blocks -> LDS by global->LDS DMA, in unit order (144 bytes each).  The units
-    // of one matrix are rows r0 .. r0+GU_ROWS-1 of the expert, i.e. one contiguous span of GU_ROWS *
-    // erow bytes: DMA op i copies 16-byte chunks 64i .. 64i+63 of the two spans (gate, then up).
-    // Chunks past the end are clamped onto the last one (the LDS area is padded to whole KiB).
-    uint8_t *wl = smem + ((size_t)M * nsb * KREC + 1023) / 1024 * 1024;
-    const int nch = nunits * 9, span = GU_ROWS * nsb * 9;   // 16-byte chunks: total, per matrix
-    for (int i = w; i * 64 < nch; i += NWV) {
-        const int c = min(i * 64 + lane, nch - 1), mat = c >= span;
-        dma_1k((mat ? Wu : Wg) + (size_t)ex * emat + (size_t)r0 * erow + 16 * (size_t)(c - mat * span), wl + i * 1024);
-    }
-
-    // Pairs (token row m, slot a) of this expert, m ascending (distinct experts per row, so at
-    // most one slot per row).
-    if constexpr (ROUTED) {
-        if (threadIdx.x < 8) s_pairs[threadIdx.x] = pr;
-        if (threadIdx.x == 0) s_cnt = cnt_r;
-    } else if (threadIdx.x == 0) {
-        int c = 0;
-        for (int m = 0; m < M; m++)
-            for (int a = 0; a < n_act; a++)
-                if (rl.sel[m * n_act + a] == ex) s_pairs[c++] = m * n_act + a;
-        s_cnt = c;
-    }
-    __syncthreads();   // (waits for every wave's DMA)
-    const int cnt = s_cnt;
-    float *tv = (float *)(wl + (nch + 63) / 64 * 1024);   // [8][2][GU_ROWS][nsb]
-
-    // Both lanes of a unit store the same value; invalid units write the spare slot.
-    const int tv_spare = 8 * 2 * GU_ROWS * nsb;
-#pragma unroll
-    for (int c = 0; c < UPL; c++) {
-        const int un = c * 32 * NWV + w * 32 + (lane >> 1);
-        const bool valid = un < nunits;
-        const int sb = valid ? un % nsb : 0;
-        const uint8_t *blk = wl + (size_t)(valid ? un : 0) * 144;
-        const v4i hdr = *(const v4i *)blk;
-        v4i qv[4];
-#pragma unroll
-        for (int pc = 0; pc < 4; pc++) qv[pc] = *(const v4i *)(blk + 16 + 64 * h + 16 * pc);
-        Q4kHalf uh;
-        q4k_scales_gguf(hdr, h, uh);
-        q4k_unpack(qv, uh);
-        const uint32_t h0 = (uint32_t)hdr[0];
-        const float dw = h2f((uint16_t)(h0 & 0xffff)), dmin = h2f((uint16_t)(h0 >> 16));
-        for (int k = 0; k < cnt; k++) {
-            const uint8_t *rec = smem + (size_t)((s_pairs[k] / n_act) * nsb + sb) * KREC;
-            int isc, imn;
-            q4k_half_sums(uh, rec, h, isc, imn);
-            tv[valid ? k * 2 * GU_ROWS * nsb + un : tv_spare] = q4k_term(dw, dmin, *(const float *)(rec + KR_D), isc, imn);
-        }
-    }
-    __syncthreads();
-
-    // g, u sequential over super-blocks; SwiGLU (qwen_moe.c:309).
-    for (int t = threadIdx.x; t < cnt * GU_ROWS; t += 64 * NWV) {
-        const int k = t / GU_ROWS, r = t - k * GU_ROWS;
-        const float *tg = tv + k * 2 * GU_ROWS * nsb + r * nsb;
-        const float *tu = tg + GU_ROWS * nsb;
-        float g = 0.0f, up = 0.0f;
-        for (int sb = 0; sb < nsb; sb++) g = g + tg[sb];
-        for (int sb = 0; sb < nsb; sb++) up = up + tu[sb];
-        ws.act[(size_t)s_pairs[k] * ff + r0 + r] = swiglu(g, up);
-    }
-    __syncthreads();
-}
-
-// ------------------------------------------------------------------------------------------------
-// Gate/up for 2 .. 4 token rows (routing from k_moe_topk), persistent: each block stages the Q8_K
-// records of all M rows and the whole routing in LDS once, then walks the work items it =
+// Gate/up for 1 .. 4 token rows, persistent: each block derives the routing of all M rows from the
+// logits once (route_block, one wave per row; block 0 publishes it for the down projection and the
+// caller) and stages the Q8_K records of all M rows in LDS, then walks the work items it =
 // blockIdx.x, + gridDim.x, ... (item = union slot u, GU_ROWS rows of ff).  The next item's weights
 // are staged into the second of two LDS buffers while the current item is computed, so a block
-// always has one item's weights in flight.  Per item the work is k_moe_gate_up's: units (matrix,
-// row, super-block), two lanes each, from LDS; SwiGLU after the sums over super-blocks in order.
+// always has one item's weights in flight.  An item's expert rows of one matrix are one contiguous
+// span, so its DMA walks two spans (gate, then up).  Work units (matrix, row, super-block), two
+// lanes each (half h of the Q4_K block), read the weight block and the record from LDS and store
+// one fp32 term per token row that chose the expert; g and u are then summed over super-blocks in
+// order and SwiGLU(g, u) written per (token row, slot) pair.
 // The weight DMA is issued from inline asm (dma16v) and waited for with an exact s_waitcnt: on
 // this GPU global stores count in vmcnt too, and only wave 0 stores act (one instruction per item,
 // cnt * GU_ROWS <= 32 values), so at the top of an item wave 0 lets its last store stay
 // outstanding.
 // ------------------------------------------------------------------------------------------------
 template <int UPL, int NWV>
-__global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff, int n_act,
+__global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff, int n_exp, int n_act,
                                                             const uint8_t *__restrict__ Wg,
-                                                            const uint8_t *__restrict__ Wu, MoeWs ws)
+                                                            const uint8_t *__restrict__ Wu, MoeWs ws,
+                                                            int *__restrict__ sel_out, float *__restrict__ sw_out)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int s_uniq[32], s_cnt[32], s_pairs[32 * 8], s_U;
+    __shared__ RouteLds rl;
+    __shared__ int s_uniq[32], s_cnt[32], s_pairs[32 * 8];
     const int nsb = d / 256, P = M * n_act;
     const int t = threadIdx.x, lane = t & 63, w = wave_id(), h = lane & 1;
 
-    // Records of all M rows and the routing -> LDS, once.
+    // Routing of all rows, then each union slot's expert, pair list and size -> LDS.
+    route_block<NWV>(M, n_exp, n_act, ws.logits, rl);
+    if (blockIdx.x == 0) publish_routing(M, n_act, rl, ws, sel_out, sw_out);
+    if (t < P) {
+        int slot, pos, cnt;
+        pair_slot(M, n_act, rl, t, slot, pos, cnt);
+        s_pairs[slot * 8 + pos] = t;
+        if (pos == 0) {
+            s_uniq[slot] = rl.sel[t];
+            s_cnt[slot] = cnt;
+        }
+    }
+    // Records of all M rows -> LDS (waited for with the first item's weights).
     const int totv = M * nsb * KREC / 16;
     for (int ch = w; ch * 64 < totv; ch += NWV)
-        dma_1k((const v4i *)ws.xrec + min(ch * 64 + lane, totv - 1), smem + ch * 1024);
-    if (t < P) {
-        s_uniq[t] = ws.uniq[t];
-        s_cnt[t] = ws.ucnt[t];
-    }
-    for (int i = t; i < P * 8; i += 64 * NWV) s_pairs[i] = ws.upairs[i];
-    if (t == 0) s_U = *ws.nuniq;
-    __syncthreads();   // (waits for the DMA and the loads)
+        dma16v((const v4i *)ws.xrec + min(ch * 64 + lane, totv - 1),
+               __builtin_amdgcn_readfirstlane(lds_addr(smem) + (uint32_t)ch * 1024u));
+    __syncthreads();
 
-    const int nrg = ff / GU_ROWS, items = s_U * nrg;
+    const int nrg = ff / GU_ROWS, items = rl.U * nrg;
     const int nunits = 2 * GU_ROWS * nsb;
     const size_t erow = (size_t)nsb * 144, emat = erow * ff;
     const int nch = nunits * 9, span = GU_ROWS * nsb * 9;   // 16-byte chunks: item, one matrix
@@ -1223,34 +1120,19 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
 
-    const size_t lds_gu = ((size_t)M * nsb * KREC + 1023) / 1024 * 1024 +             // hn records
-                          ((size_t)2 * GU_ROWS * nsb * 9 + 63) / 64 * 1024 +           // weight blocks
-                          ((size_t)8 * 2 * GU_ROWS * nsb + 1) * 4;                      // terms
-    const int upl_gu = (2 * 2 * GU_ROWS * nsb + 64 * GU_NWV - 1) / (64 * GU_NWV);   // two lanes per unit
-    const dim3 g_gu(Umax, ff / GU_ROWS);
+    // Gate/up (k_moe_gate_up_p): as many persistent blocks as are resident at once, at most one per
+    // work item, each deriving the routing itself (cheaper than a separate routing launch) and
+    // holding two weight buffers.
     const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
-    // One row routes inside the gate/up blocks (a separate launch costs more than it saves);
-    // several rows route once in k_moe_topk.
-    if (M > 1) {
-        hipLaunchKernelGGL(k_moe_topk, dim3(1), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
-        err = hipGetLastError();
-        if (err != hipSuccess) return err;
-    }
-    // Several rows: the persistent gate/up, as many blocks as are resident at once (at most one per
-    // work item), each with two weight buffers.
-    const size_t lds_gp = ((size_t)M * nsb * KREC + 1023) / 1024 * 1024 +
-                          2 * (((size_t)2 * GU_ROWS * nsb * 9 + 63) / 64 * 1024) +
-                          ((size_t)4 * 2 * GU_ROWS * nsb + 1) * 4;
+    const size_t lds_gp = ((size_t)M * nsb * KREC + 1023) / 1024 * 1024 +                // hn records
+                          2 * (((size_t)2 * GU_ROWS * nsb * 9 + 63) / 64 * 1024) +       // weight blocks x 2
+                          ((size_t)4 * 2 * GU_ROWS * nsb + 1) * 4;                        // terms
+    const int upl_gu = (2 * 2 * GU_ROWS * nsb + 64 * GU_NWV - 1) / (64 * GU_NWV);   // two lanes per unit
 #define X100_GU(U)                                                                                       \
     do {                                                                                                 \
-        if (M > 1) {                                                                                     \
-            const int nb = min(Umax * (ff / GU_ROWS),                                                    \
-                               resident_blocks(k_moe_gate_up_p<U, GU_NWV>, 64 * GU_NWV, lds_gp));         \
-            hipLaunchKernelGGL((k_moe_gate_up_p<U, GU_NWV>), dim3(nb), dim3(64 * GU_NWV), lds_gp, s, M, d, ff, \
-                               n_act, wg, wu, ws);                                                       \
-        } else                                                                                           \
-            hipLaunchKernelGGL((k_moe_gate_up<U, GU_NWV, false>), g_gu, dim3(64 * GU_NWV), lds_gu, s, M, d,  \
-                               ff, n_exp, n_act, wg, wu, ws, sel, sw);                                   \
+        const int nb = min(Umax * (ff / GU_ROWS), resident_blocks(k_moe_gate_up_p<U, GU_NWV>, 64 * GU_NWV, lds_gp)); \
+        hipLaunchKernelGGL((k_moe_gate_up_p<U, GU_NWV>), dim3(nb), dim3(64 * GU_NWV), lds_gp, s, M, d, ff, n_exp, \
+                           n_act, wg, wu, ws, sel, sw);                                                   \
     } while (0)
     if (upl_gu == 1)
         X100_GU(1);
