@@ -5,7 +5,8 @@
 //
 // Below 5 rows, three or four launches on one stream; each kernel only reads what an earlier launch
 // wrote, so no block ever waits for, or signals, another block (no fences, no atomics):
-//   k_moe_route       router logits R.hn (one wave per expert) and the Q8_K form of every hn row.
+//   k_moe_route       router logits R.hn (one wave per expert and token row) and the Q8_K form of
+//                     every hn row.
 //   k_moe_gate_up_p   persistent blocks over the work items (union slot, GU_ROWS rows of ff).  Every
 //                     block derives the routing of all rows itself (cheaper than another launch;
 //                     block 0 publishes it), then streams the items' rows of the expert's gate and
@@ -103,9 +104,10 @@ X100_DEV float swiglu(float g, float u)
 }
 
 // ------------------------------------------------------------------------------------------------
-// Router.  Waves 0 .. n_exp-1 compute one expert's logits for all M rows (qwen_moe.c:296; lane l
-// sums elements 4l..4l+3, +256, ... in order, then a butterfly over the lanes); waves n_exp ..
-// quantize four 256-element blocks of hn each into the Q8_K records ws.xrec[m * nsb + sb].
+// Router.  Wave g < n_exp * M computes the logit of expert g / M for token row g % M (qwen_moe.c:296;
+// lane l sums elements 4l..4l+3, +256, ... in order, then a butterfly over the lanes), one row per
+// wave so that no wave runs the dependent add chains of several rows; the following waves quantize
+// four 256-element blocks of hn each into the Q8_K records ws.xrec[m * nsb + sb].
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, uint32_t mnsb, const float *__restrict__ hn,
                                                    const float *__restrict__ R, MoeWs ws)
@@ -114,20 +116,22 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, uint
     float4 *s_hn = (float4 *)smem;   // [M][d/4]
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + wave_id();
-    const int nsb = d / 256, nq = M * nsb;
+    const int nsb = d / 256, nq = M * nsb, nrw = n_exp * M;
 
-    if (wave >= n_exp) {   // quantizer waves (wave-uniform)
-        const int qb = 4 * (wave - n_exp);
+    if (wave >= nrw) {   // quantizer waves (wave-uniform)
+        const int qb = 4 * (wave - nrw);
         if (qb < nq) {
             float4 v[4];
             q8k_load(buf_rsrc(hn, (uint32_t)(M * d) * 4u), d, nsb, mnsb, nq, qb, v);
             q8k_quant(v, nq, qb, ws.xrec);
         }
-        if (4 * (int)blockIdx.x >= n_exp) return;   // a block of quantizer waves only
+        if (4 * (int)blockIdx.x >= nrw) return;   // a block of quantizer waves only
     }
 
-    // The wave's router row (elements past d read as 0 and are not used; none for quantizer waves).
-    const rsrc_t rr = buf_rsrc(R + (size_t)min(wave, n_exp - 1) * d, wave < n_exp ? (uint32_t)d * 4u : 0u);
+    // The wave's expert and token row, and its router row (elements past d read as 0 and are not
+    // used; none for quantizer waves).
+    const int gw = min(wave, nrw - 1), e = gw / M, m = gw - e * M;
+    const rsrc_t rr = buf_rsrc(R + (size_t)e * d, wave < nrw ? (uint32_t)d * 4u : 0u);
     float4 rv[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
@@ -137,22 +141,20 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, uint
         dma_1k(hn + (size_t)ch * 256 + 4 * lane, smem + ch * 1024);
     __syncthreads();
 
-    if (wave < n_exp) {
-        for (int m = 0; m < M; m++) {
-            const float4 *h = s_hn + m * (d / 4);
-            float s = 0.0f;
+    if (wave < nrw) {
+        const float4 *h = s_hn + m * (d / 4);
+        float sum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 16; j++)
-                if (j < nsb) {
-                    const float4 hv = h[lane + 64 * j];
-                    s += rv[j].x * hv.x;
-                    s += rv[j].y * hv.y;
-                    s += rv[j].z * hv.z;
-                    s += rv[j].w * hv.w;
-                }
-            s = wave_sum_bfly_f(s);
-            if (lane == 0) ws.logits[m * n_exp + wave] = s;
-        }
+        for (int j = 0; j < 16; j++)
+            if (j < nsb) {
+                const float4 hv = h[lane + 64 * j];
+                sum += rv[j].x * hv.x;
+                sum += rv[j].y * hv.y;
+                sum += rv[j].z * hv.z;
+                sum += rv[j].w * hv.w;
+            }
+        sum = wave_sum_bfly_f(sum);
+        if (lane == 0) ws.logits[m * n_exp + e] = sum;
     }
 }
 
@@ -1114,7 +1116,7 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     const int Umax = min(M * n_act, n_exp);
     if (M >= MF_MIN_ROWS) return moe_launch_mfma(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
 
-    const int nwaves = n_exp + (M * nsb + 3) / 4;   // router waves, then quantizer waves of four records
+    const int nwaves = n_exp * M + (M * nsb + 3) / 4;   // router waves, then quantizer waves of four records
     hipLaunchKernelGGL(k_moe_route, dim3((nwaves + 3) / 4), dim3(256), (size_t)M * d * 4, s, M, d, n_exp,
                        udiv16_magic((uint32_t)nsb), hn, R, ws);
     hipError_t err = hipGetLastError();
