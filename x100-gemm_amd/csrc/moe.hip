@@ -533,28 +533,12 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ RouteLds rl;
-    __shared__ int s_uniq[32], s_cnt[32], s_pairs[32 * 8];
+    __shared__ int s_cnt[32], s_pairs[32 * 8];
     const int nsb = d / 256, P = M * n_act;
     const int t = threadIdx.x, lane = t & 63, w = wave_id(), h = lane & 1;
 
-    // Routing of all rows, then each union slot's expert, pair list and size -> LDS.
+    // Routing of all rows: rl.uniq holds the union slots' experts (ascending).
     route_block<NWV>(M, n_exp, n_act, ws.logits, rl);
-    if (blockIdx.x == 0) publish_routing(M, n_act, rl, ws, sel_out, sw_out);
-    if (t < P) {
-        int slot, pos, cnt;
-        pair_slot(M, n_act, rl, t, slot, pos, cnt);
-        s_pairs[slot * 8 + pos] = t;
-        if (pos == 0) {
-            s_uniq[slot] = rl.sel[t];
-            s_cnt[slot] = cnt;
-        }
-    }
-    // Records of all M rows -> LDS (waited for with the first item's weights).
-    const int totv = M * nsb * KREC / 16;
-    for (int ch = w; ch * 64 < totv; ch += NWV)
-        dma16v((const v4i *)ws.xrec + min(ch * 64 + lane, totv - 1),
-               __builtin_amdgcn_readfirstlane(lds_addr(smem) + (uint32_t)ch * 1024u));
-    __syncthreads();
 
     const int nrg = ff / GU_ROWS, items = rl.U * nrg;
     const int nunits = 2 * GU_ROWS * nsb;
@@ -569,15 +553,28 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
     // span then the up span (chunks past the end clamped onto the last one; the buffer is whole KiB).
     auto issue = [&](int it, int b) __attribute__((always_inline)) {
         const int u = it / nrg, r0 = (it - u * nrg) * GU_ROWS;
-        const size_t off = (size_t)s_uniq[u] * emat + (size_t)r0 * erow;
+        const size_t off = (size_t)rl.uniq[u] * emat + (size_t)r0 * erow;
         for (int i = w; i * 64 < nch; i += NWV) {
             const int c = min(i * 64 + lane, nch - 1), mat = c >= span;
             dma16v((mat ? Wu : Wg) + off + 16 * (size_t)(c - mat * span),
                    __builtin_amdgcn_readfirstlane(wlds + b * wbytes + (uint32_t)i * 1024u));
         }
     };
+    // The first item's weights first, then the records of all M rows (both waited for at the top
+    // of the first item), then each union slot's pair list and size -> LDS.
     int it = blockIdx.x, b = 0;
     if (it < items) issue(it, 0);
+    const int totv = M * nsb * KREC / 16;
+    for (int ch = w; ch * 64 < totv; ch += NWV)
+        dma16v((const v4i *)ws.xrec + min(ch * 64 + lane, totv - 1),
+               __builtin_amdgcn_readfirstlane(lds_addr(smem) + (uint32_t)ch * 1024u));
+    if (blockIdx.x == 0) publish_routing(M, n_act, rl, ws, sel_out, sw_out);
+    if (t < P) {
+        int slot, pos, cnt;
+        pair_slot(M, n_act, rl, t, slot, pos, cnt);
+        s_pairs[slot * 8 + pos] = t;
+        if (pos == 0) s_cnt[slot] = cnt;
+    }
     for (bool first = true; it < items; it += gridDim.x, b ^= 1, first = false) {
         // This item's weights are in (this wave's operations; then every wave's, by the barrier),
         // and every wave is done with the other buffer and tv.
