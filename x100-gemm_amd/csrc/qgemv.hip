@@ -381,6 +381,128 @@ __global__ __launch_bounds__(512) void k_q3_K(const KqArgs a)
     kq_combine<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
 }
 
+// Row-major form of k_q4_K / k_q3_K (used for one token row) for nsb = 1, 2, 4 or 8 super-blocks
+// per row: units u = row * nsb + sb, so that the 2 * nsb lanes of a row lie in one 16-lane DPP
+// row.  Each unit's fp32 term
+// (the same integers and operations as above) is summed over the super-blocks in order by a chain
+// of row_shr:2 steps inside the wave, starting from 0.0f + t0 as the oracle does, and the row's
+// last unit writes y: no terms in LDS and no second barrier.  The weight loads of a wave cover
+// 32 / nsb consecutive rows of every super-block section (whole 128-byte lines).
+template <int MR, bool Q3>
+__global__ __launch_bounds__(512) void k_kq_rm(const KqArgs a)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int M = a.M, N = a.N, K = a.K, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
+    const uint8_t *__restrict__ W = a.W;
+    const float *__restrict__ x = a.x;
+    float *__restrict__ y = a.y;
+    const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1;
+    uint8_t *recs = smem;
+    const int u0 = 32 * w + (lane >> 1), lgn = __builtin_ctz((unsigned)nsb);
+    const int rib = u0 >> lgn, sb = u0 & (nsb - 1), row0 = blockIdx.x * RB;
+    const bool valid = rib < RB && row0 + rib < N;
+    const int row = min(row0 + min(rib, RB - 1), N - 1);
+
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
+    const bool wq = 4 * w < nq;   // the wave has records to quantize (wave-uniform)
+    Q8kFirst xf;
+    if (wq) q8k_first(xr, a, nq, nw, xf);
+
+    v4i qv[4], hm = {};
+    uint2 sv;
+    uint32_t dv;
+    if constexpr (!Q3) {
+        const uint8_t *sec = W + (size_t)sb * q4k_sec(N);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            qv[c] = __builtin_nontemporal_load((const v4i *)(sec + (size_t)c * 32 * N + (size_t)row * 32 + 16 * h));
+        sv = *(const uint2 *)(sec + (size_t)128 * N + (size_t)row * 16 + 8 * h);
+        dv = *(const uint32_t *)(sec + (size_t)144 * N + (size_t)row * 4);
+    } else {
+        const uint8_t *sec = W + (size_t)sb * q3k_sec(N);
+        const size_t ro = (size_t)row * 32 + 16 * h;
+        qv[0] = __builtin_nontemporal_load((const v4i *)(sec + ro));
+        qv[1] = __builtin_nontemporal_load((const v4i *)(sec + (size_t)32 * N + ro));
+        hm = __builtin_nontemporal_load((const v4i *)(sec + (size_t)64 * N + ro));
+        sv = *(const uint2 *)(sec + (size_t)96 * N + (size_t)row * 16 + 8 * h);
+        dv = *(const uint16_t *)(sec + (size_t)112 * N + (size_t)row * 2);
+    }
+
+    __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the quantizer
+    if (wq) q8k_rest(xr, a, nq, nw, xf, recs);
+    __syncthreads();
+    if (32 * w >= RB * nsb) return;   // waves past the block's units only quantized (wave-uniform)
+
+    float term[MR];
+    if constexpr (!Q3) {
+        Q4kHalf u;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            u.sc[jj] = (int)((sv.x >> (8 * jj)) & 0xff);
+            u.mn[jj] = (int)((sv.y >> (8 * jj)) & 0xff);
+        }
+        q4k_unpack(qv, u);
+        const float d = h2f((uint16_t)(dv & 0xffff)), dmin = h2f((uint16_t)(dv >> 16));
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            // Rows m >= M compute on unused LDS and are never stored.
+            const uint8_t *rec = recs + (size_t)(m * nsb + sb) * KREC;
+            int isc, imn;
+            q4k_half_sums(u, rec, h, isc, imn);
+            term[m] = q4k_term(d, dmin, *(const float *)(rec + KR_D), isc, imn);
+        }
+    } else {
+        int sc[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) sc[k] = (int)(int8_t)(((k < 4 ? sv.x : sv.y) >> (8 * (k & 3))) & 0xff);
+        const uint32_t qd[8] = {(uint32_t)qv[0][0], (uint32_t)qv[0][1], (uint32_t)qv[0][2], (uint32_t)qv[0][3],
+                                (uint32_t)qv[1][0], (uint32_t)qv[1][1], (uint32_t)qv[1][2], (uint32_t)qv[1][3]};
+        int vq[4][8];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const uint32_t hb = ((uint32_t)hm[t >> 1] >> (4 * (t & 1) + j)) & 0x01010101u;
+                vq[j][t] = (int)(((qd[t] >> (2 * j)) & 0x03030303u) | (hb << 2));
+            }
+        const float dw = h2f((uint16_t)dv);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            const uint8_t *rec = recs + (size_t)(m * nsb + sb) * KREC;
+            const v4i *xq = (const v4i *)(rec + 128 * h);
+            const v4i sa = *(const v4i *)(rec + KR_S16 + 32 * h), sbv = *(const v4i *)(rec + KR_S16 + 32 * h + 16);
+            const int s16[8] = {sa[0], sa[1], sa[2], sa[3], sbv[0], sbv[1], sbv[2], sbv[3]};
+            int isc = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const v4i xa = xq[2 * j], xb = xq[2 * j + 1];
+                int d0 = 0, d1 = 0;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    d0 = dot4(vq[j][t], xa[t], d0);
+                    d1 = dot4(vq[j][4 + t], xb[t], d1);
+                }
+                isc += sc[2 * j] * (d0 - 4 * s16[2 * j]) + sc[2 * j + 1] * (d1 - 4 * s16[2 * j + 1]);
+            }
+            isc += dpp_i<0xB1>(0, isc);
+            term[m] = (*(const float *)(rec + KR_D) * dw) * (float)isc;
+        }
+    }
+    // y[m][row] = ((0 + t_0) + t_1) + ... + t_{nsb-1}: step k takes the running sum of unit k-1 (two
+    // lanes down, row_shr:2) and adds t_k in the lanes of unit k.
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        float acc = sb == 0 ? 0.0f + term[m] : 0.0f;
+#pragma unroll
+        for (int k = 1; k < 8; k++)
+            if (k < nsb) {
+                const float prev = dpp_f<0x112>(acc, acc);
+                acc = sb == k ? prev + term[m] : acc;
+            }
+        if (m < M && valid && h == 0 && sb == nsb - 1) y[(size_t)m * N + row] = acc;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Q8_0 x int8 activation: the int8 path of Q8_0 / Q5_K / Q6_K weights
 // ------------------------------------------------------------------------------------------------
@@ -857,7 +979,13 @@ hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *
     const dim3 grid((N + pl.rb - 1) / pl.rb), blk(64 * pl.nw);
     const KqArgs a{M, N, K, pl.rb, K / 256, udiv16_magic((uint32_t)pl.rb), udiv16_magic((uint32_t)(K / 256)),
                    (const uint8_t *)w, x, y};
-    if constexpr (Q3)
+    // One token row with nsb = 1, 2, 4 or 8 (a row's units within one DPP row): the row-major form
+    // (Q4_K 6144 x 2048: 3.86 vs 3.93 us; with several rows its per-row add chains cost more than
+    // the barrier and combine they replace: 6.09 vs 5.47 us at M = 4).
+    const int nsb = K / 256;
+    if (MR == 1 && (nsb == 1 || nsb == 2 || nsb == 4 || nsb == 8))
+        hipLaunchKernelGGL((k_kq_rm<MR, Q3>), grid, blk, (size_t)(MR * nsb + 1) * KREC, s, a);
+    else if constexpr (Q3)
         hipLaunchKernelGGL(k_q3_K<MR>, grid, blk, pl.lds, s, a);
     else
         hipLaunchKernelGGL(k_q4_K<MR>, grid, blk, pl.lds, s, a);
