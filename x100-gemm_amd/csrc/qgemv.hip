@@ -94,12 +94,13 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
     }
     __syncthreads();
 
+    // Every row's lane partials first, then the row reductions, so that the rows' independent DPP
+    // chains interleave (each row's order is unchanged).
+    float acc[RPW][MR];
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
-        const int row = rowb + r;
-        float acc[MR];
 #pragma unroll
-        for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+        for (int m = 0; m < MR; m++) acc[r][m] = 0.0f;
 #pragma unroll
         for (int c = 0; c < BPL; c++) {
             // Branch-free (the scheduler interleaves the unrolled blocks): a lane past the last
@@ -127,17 +128,21 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
                 }
                 s -= 8 * xs[m * nb + b];  // nibble offset: (q-8).x = q.x - 8*sum(x)
                 const float term = (float)s * (dwf * xd[m * nb + b]);
-                acc[m] += inb ? term : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < MR; m++) {
-            if (m < M) {
-                const float v = wave_sum_uf(acc[m]);
-                if (lane == 0 && row < N) y[(size_t)m * N + row] = v;
+                acc[r][m] += inb ? term : 0.0f;
             }
         }
     }
+    float v[RPW * MR];
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) v[r * MR + m] = acc[r][m];
+    wave_sum_uf_n(v);   // rows m >= M reduce unused values and are not stored
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+            if (m < M && lane == 0 && rowb + r < N) y[(size_t)m * N + rowb + r] = v[r * MR + m];
 }
 
 // ------------------------------------------------------------------------------------------------

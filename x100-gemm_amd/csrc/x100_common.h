@@ -179,6 +179,26 @@ X100_DEV float wave_sum_uf(float v)
     v += dpp_f<0x143, 0xc>(0.0f, v);
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// wave_sum_uf of N values at once, each step applied to all of them so that their DPP chains
+// interleave (each value's additions in the same order as wave_sum_uf).
+template <int N>
+X100_DEV void wave_sum_uf_n(float (&v)[N])
+{
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f<0x111>(0.0f, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f<0x112>(0.0f, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f<0x114>(0.0f, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f<0x118>(0.0f, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f<0x142, 0xa>(0.0f, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_f<0x143, 0xc>(0.0f, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), 63));
+}
 
 // Device-side Q8 activation formats (kept in LDS or a workspace; internal to the library).
 //   Q8_0 (per 32): fp16 d, int8 q[32], int sum(q)     -- quantize_q8_0_native rounding
