@@ -39,7 +39,8 @@ int gemm_hip_i8_dev(int M, int N, int K, const int8_t *dA, const int8_t *dB, int
                     void *stream);
 
 /* Same as gemm_hip_i8_dev with an explicit kernel choice (0 auto, 1 256x256 MFMA tile,
- * 2 128x128 MFMA tile, 3 skinny M<=16 split-K, 4 generic).  For tests and measurement. */
+ * 2 128x128 MFMA tile, 3 skinny M<=16 split-K, 4 generic, 5 256x256 tile with 4 waves,
+ * 6 64x64 MFMA tile, 7 32x32 MFMA tile).  For tests and measurement. */
 int gemm_hip_i8_dev_variant(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
                             void *stream, int variant);
 

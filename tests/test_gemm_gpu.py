@@ -101,7 +101,8 @@ def test_gemm_shapes_auto(dev, M, N, K):
 
 
 @pytest.mark.parametrize("variant", [x100hip.GEMM_TILE256, x100hip.GEMM_TILE128, x100hip.GEMM_SKINNY,
-                                     x100hip.GEMM_GENERIC, x100hip.GEMM_TILE256_W4])
+                                     x100hip.GEMM_GENERIC, x100hip.GEMM_TILE256_W4, x100hip.GEMM_TILE64,
+                                     x100hip.GEMM_TILE32])
 @pytest.mark.parametrize("M,N,K", [(8, 256, 256), (16, 512, 320), (3, 48, 64), (256, 256, 512),
                                    (40, 96, 144), (512, 768, 1024), (768, 512, 576)])
 def test_gemm_forced_variants(dev, variant, M, N, K):

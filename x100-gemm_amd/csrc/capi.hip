@@ -165,7 +165,7 @@ extern "C" {
 int gemm_hip_i8_dev_variant(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
                             void *stream, int variant)
 {
-    if (M < 0 || N < 0 || K < 0 || variant < 0 || variant > 5) return X100_EINVAL;
+    if (M < 0 || N < 0 || K < 0 || variant < 0 || variant > 7) return X100_EINVAL;
     if (M == 0 || N == 0 || K == 0) return X100_OK;  // C += (empty product) leaves C unchanged
     if (!dA || !dB || !dC) return X100_EINVAL;
     if (K >= (1 << 17)) return X100_EINVAL;          // keeps |sum| < 2^31 (no int32 wrap)

@@ -882,10 +882,16 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
             variant = X100_GEMM_GENERIC;
         else if (M <= 16 && (size_t)K * N < ((size_t)1 << 32))   // B must fit one buffer resource
             variant = X100_GEMM_SKINNY;
-        else if ((long)M * N >= 1024L * 1024L)
+        // Tile by output size, measured at K = 1024-4096 (graph replay, us): 256x256 tiles from
+        // 4M outputs (2048^2 x 4096: 50.3 vs 52.6 with 128x128), 64x64 from 1M (1024^2 x 4096:
+        // 27.3 vs 39.9 / 45.2), 32x32 below (256^3: 3.5 vs 5.7; 512^3: 4.9 vs 7.9).  Smaller tiles
+        // put enough blocks on the 256 CUs when the product has few 256x256 tiles.
+        else if ((long)M * N >= 4L * 1024L * 1024L)
             variant = X100_GEMM_TILE256;
+        else if ((long)M * N >= 1024L * 1024L)
+            variant = X100_GEMM_TILE64;
         else
-            variant = X100_GEMM_TILE128;
+            variant = X100_GEMM_TILE32;
     }
     if (!aligned && variant != X100_GEMM_GENERIC) return hipErrorInvalidValue;
     switch (variant) {
@@ -913,6 +919,8 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
         return hipGetLastError();
     }
     case X100_GEMM_TILE128: return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
+    case X100_GEMM_TILE64: return launch_mfma<1, 1, 2, 2>(M, N, K, A, B, C, s);
+    case X100_GEMM_TILE32: return launch_mfma<1, 1, 1, 1>(M, N, K, A, B, C, s);
     case X100_GEMM_SKINNY: {
         if (M > 16 || (size_t)K * N >= ((size_t)1 << 32)) return hipErrorInvalidValue;
         dim3 grid((N + 255) / 256, (K + 255) / 256);

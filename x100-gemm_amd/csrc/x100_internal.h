@@ -13,6 +13,8 @@ enum {
     X100_GEMM_SKINNY = 3,
     X100_GEMM_GENERIC = 4,
     X100_GEMM_TILE256_W4 = 5,   // 256x256 tile, 4 waves of 128x128
+    X100_GEMM_TILE64 = 6,       // 64x64 tile, 4 waves of 32x32
+    X100_GEMM_TILE32 = 7,       // 32x32 tile, 1 wave
 };
 
 hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,

@@ -44,7 +44,8 @@ EXPORTS = (
     "x100_attn_decode_hip_ws", "x100_decode_layer_hip_ws",
 )
 
-GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC, GEMM_TILE256_W4 = 0, 1, 2, 3, 4, 5
+GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC, GEMM_TILE256_W4, GEMM_TILE64, GEMM_TILE32 = \
+    0, 1, 2, 3, 4, 5, 6, 7
 
 
 class X100Error(RuntimeError):
