@@ -34,7 +34,9 @@ void gemm_ime_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t 
 /* Same contract as gemm_ime_i8 but returns an error code instead of aborting. */
 int gemm_hip_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C);
 
-/* Device pointers, asynchronous on `stream` (C += A*B).  No host synchronisation. */
+/* Device pointers, asynchronous on `stream` (C += A*B).  No host synchronisation.  For every
+ * entry point C is int32 arithmetic modulo 2^32: from K = 2^17 a sum can leave the int32 range,
+ * and it then wraps as the reference's int32 accumulation does. */
 int gemm_hip_i8_dev(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
                     void *stream);
 

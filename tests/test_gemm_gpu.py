@@ -153,6 +153,27 @@ def test_gemm_host_dropin(dev):
     assert np.array_equal(C2, oracle_gemm(A, B, np.zeros((96, 80), np.int32)))
 
 
+@pytest.mark.parametrize("variant,M,N", [(x100hip.GEMM_AUTO, 4, 256), (x100hip.GEMM_AUTO, 32, 256),
+                                         (x100hip.GEMM_TILE256, 256, 256), (x100hip.GEMM_TILE64, 64, 128)])
+def test_gemm_long_k_wraps_like_int32(dev, variant, M, N):
+    # K = 2^17 + 512: all -128 inputs give K * 16384 = 2,155,872,256 per element, past 2^31; the
+    # result (and C += on top of it) is the int32 wrap of the exact sum, as the reference's int32
+    # accumulation gives.  A random slice is checked against an exact int64 product.
+    K = (1 << 17) + 512
+    A = np.full((M, K), -128, np.int8)
+    B = np.full((K, N), -128, np.int8)
+    C0 = np.full((M, N), 7, np.int32)
+    want = np.int64(7) + np.int64(K) * 16384
+    got = gpu_gemm(A, B, C0, dev, variant)
+    assert np.all(got == np.int32(((want + 2**31) % 2**32) - 2**31))
+    rng = np.random.default_rng(41)
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    exact = A[:, :].astype(np.int64) @ B[:, :8].astype(np.int64)
+    got = gpu_gemm(A, B, np.zeros((M, N), np.int32), dev, variant)
+    assert np.array_equal(got[:, :8], (((exact + 2**31) % 2**32) - 2**31).astype(np.int32))
+
+
 def test_gemm_rejects_bad_args(dev):
     with pytest.raises(x100hip.X100Error):
         x100hip.gemm_dev(-1, 4, 4, 1, 1, 1, _stream())

@@ -168,7 +168,9 @@ int gemm_hip_i8_dev_variant(int M, int N, int K, const int8_t *dA, const int8_t 
     if (M < 0 || N < 0 || K < 0 || variant < 0 || variant > 7) return X100_EINVAL;
     if (M == 0 || N == 0 || K == 0) return X100_OK;  // C += (empty product) leaves C unchanged
     if (!dA || !dB || !dC) return X100_EINVAL;
-    if (K >= (1 << 17)) return X100_EINVAL;          // keeps |sum| < 2^31 (no int32 wrap)
+    // Any K: from K = 2^17 a dot product can leave the int32 range, and then C wraps modulo 2^32
+    // exactly as the reference's int32 accumulation does (integer addition modulo 2^32 is
+    // associative, so the kernels' summation order does not matter).
     int rc = check_device();
     if (rc) return rc;
     hipError_t e = x100_gemm_i8_launch(M, N, K, dA, dB, dC, (hipStream_t)stream, variant);
