@@ -266,29 +266,63 @@ X100_DEV void x_load(rsrc_t xr, int c0, float4 (&v)[XPT])
 // F16D: the block scale is stored as fp16 by the reference's truncating conversion
 // (quantize_q8_0_native, qwen_moe_hp.c:408-414) or kept in fp32 (pack_A_i8,
 // qwen_moe_q3k.c:420-427); the q values are the same either way (they use the fp32 scale).
+//
+// The arithmetic is the reference's (d = amax / 127.0f, inv = 1.0f / d, q = lrintf(x * inv), fp16 d
+// by truncation), computed without IEEE division and without a clamp:
+// * d by one product with RN(1/127) and an FMA correction, inv by v_rcp_f32 and one Newton step.
+//   For every amax in [1e-6, FLT_MAX] (all 1,241,106,499 floats) both equal the correctly
+//   rounded quotients, checked exhaustively on gfx950.
+// * q: x * inv is rounded to float, then 1.5 * 2^23 is added, which rounds it to an integer with
+//   ties to even (rintf); the sum's low byte is q modulo 256.  |x * inv| <= 127 * (1 + 2^-23), so
+//   q is in [-127, 127] and the reference's clamp never applies.
+// * fp16 truncation of d (> 0, finite): the top 10 mantissa bits from 2^-14 up, multiples of
+//   2^-24 below, infinity from 65536 (equal to f32_to_f16 then f16_to_f32 for every positive
+//   float).
+// Non-finite activations give unspecified bytes (the reference's lrintf of NaN is
+// implementation-defined too).
+X100_DEV float div127_rn(float a)
+{
+    const float c = 0x1.020408p-7f;   // RN(1/127)
+    const float q0 = a * c;
+    const float r = __builtin_fmaf(-q0, 127.0f, a);
+    return __builtin_fmaf(r, c, q0);
+}
+X100_DEV float rcp_rn(float d)
+{
+    const float y0 = __builtin_amdgcn_rcpf(d);
+    const float e = __builtin_fmaf(-d, y0, 1.0f);
+    return __builtin_fmaf(e, y0, y0);
+}
+X100_DEV float f16_trunc_pos(float d)
+{
+    const float nrm = __uint_as_float(__float_as_uint(d) & 0xffffe000u);
+    const float sub = __builtin_truncf(d * 0x1p24f) * 0x1p-24f;
+    const float r = d >= 0x1p-14f ? nrm : sub;
+    return d >= 65536.0f ? __builtin_inff() : r;
+}
 template <int XPT, int NT = 256, bool F16D = true>
 X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, int8_t *xlo,
                              int8_t *xhi, float *xd, int *xs)
 {
-    const int nb = K / 32;
+    (void)K;   // rows are contiguous and K % 32 == 0: element e is in 32-block e / 32
+    constexpr float RND = 0x1.8p23f;
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
         const int f = c0 + threadIdx.x + NT * i;
         const float a = max8_f(fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
         const float amax = fmaxf(a, 1e-6f);
-        const float d = amax / 127.0f;
-        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-        const int q0 = clamp_i8((int)rintf(v[i].x * inv)), q1 = clamp_i8((int)rintf(v[i].y * inv));
-        const int q2 = clamp_i8((int)rintf(v[i].z * inv)), q3 = clamp_i8((int)rintf(v[i].w * inv));
-        const int s = sum8_i(q0 + q1 + q2 + q3);
-        const int e = 4 * f, m = e / K, k = e - m * K;
-        const int pos = k & 31;
-        const int b = f < total4 ? m * nb + k / 32 : total4 / 8;   // spare block past the end
-        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+        const float d = div127_rn(amax);
+        const float inv = rcp_rn(d);
+        const float p0 = v[i].x * inv, p1 = v[i].y * inv, p2 = v[i].z * inv, p3 = v[i].w * inv;
+        const uint32_t t0 = __float_as_uint(p0 + RND), t1 = __float_as_uint(p1 + RND);
+        const uint32_t t2 = __float_as_uint(p2 + RND), t3 = __float_as_uint(p3 + RND);
+        const uint32_t packed = perm(t1, t0, 0x0c0c0400u) | perm(t3, t2, 0x04000c0cu);
+        const int s = sum8_i(dot4((int)packed, 0x01010101, 0));
+        const int pos = 4 * (f & 7);
+        const int b = f < total4 ? f >> 3 : total4 >> 3;   // spare block past the end
         int8_t *dst = pos < 16 ? xlo + b * 16 + pos : xhi + b * 16 + (pos - 16);
         *(uint32_t *)dst = packed;
-        xd[b] = F16D ? h2f(f2h_trunc(d)) : d;   // the 8 lanes of a block hold the same d and sum
+        xd[b] = F16D ? f16_trunc_pos(d) : d;   // the 8 lanes of a block hold the same d and sum
         xs[b] = s;
     }
 }
