@@ -60,6 +60,16 @@ int x100q_pack(int qtype, int N, int K, const void *w_gguf, void *w_packed, void
 int qgemv_hip(int qtype, int M, int N, int K, const void *w_packed, const float *x, float *y,
               void *stream);
 
+/* Self-check of the activation quantizer's arithmetic on the installed GPU; no counterpart in the
+ * reference.  The quantizers compute amax / 127.0f, 1.0f / d and the fp16 truncation of d without
+ * IEEE division; this runs those device functions over every float bit pattern in
+ * [lo_bits, hi_bits] (<= 0x7f7fffff) and adds, into the device counters d_counts[0..2]
+ * (zeroed by the caller), the inputs where they differ from the correctly rounded 1.0f / u, from
+ * u / 127.0f and from the reference's truncating fp16 conversion.  The quantizers rely on zero
+ * for 1/d over d in [RN(1e-6 / 127), FLT_MAX / 127] and for amax / 127 over amax in
+ * [1e-6, FLT_MAX].  Asynchronous on stream. */
+int x100q_check_quant_div(uint32_t lo_bits, uint32_t hi_bits, unsigned long long *d_counts, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

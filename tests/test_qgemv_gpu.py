@@ -104,3 +104,36 @@ def test_qgemv_batched_rows_equal_single_rows(dev, qtype, M):
     for m in range(M):
         y1 = gpu_qgemv(qtype, W, x[m:m + 1], dev)
         assert np.array_equal(y[m].view(np.uint32), y1[0].view(np.uint32)), "row %d differs" % m
+
+
+def _fbits(f):
+    import struct
+    return struct.unpack("<I", struct.pack("<f", f))[0]
+
+
+def _stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def test_quantizer_division_free_arithmetic_is_exact(dev):
+    # The activation quantizers compute amax / 127.0f, 1.0f / d and d's fp16 truncation without
+    # IEEE division.  Exhaustively on this GPU: 1/d over every d the Q8_0 quantizer can form
+    # (amax >= 1e-6), amax / 127 over every amax >= 1e-6, and the fp16 truncation over every
+    # positive float; zero mismatches against the correctly rounded quotients and the reference's
+    # conversion (the checker runs the quantizer's own device functions).
+    import torch
+    fmax = 0x7f7fffff
+    d_lo, d_hi = _fbits(np.float32(np.float32(1e-6) / np.float32(127.0))), _fbits(np.float32(3.4028234663852886e38 / 127.0))
+    cnt = torch.zeros(3, dtype=torch.int64, device=dev)
+    x100hip.check_quant_div(d_lo, d_hi, cnt.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    assert int(cnt[0]) == 0, "rcp_rn mismatches over the d range: %d" % int(cnt[0])
+    cnt.zero_()
+    x100hip.check_quant_div(_fbits(np.float32(1e-6)), fmax, cnt.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    assert int(cnt[1]) == 0, "div127_rn mismatches for amax >= 1e-6: %d" % int(cnt[1])
+    cnt.zero_()
+    x100hip.check_quant_div(1, fmax, cnt.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    assert int(cnt[2]) == 0, "f16_trunc_pos mismatches: %d" % int(cnt[2])

@@ -341,6 +341,16 @@ int qgemv_hip(int qtype, int M, int N, int K, const void *w_packed, const float 
     return X100_OK;
 }
 
+int x100q_check_quant_div(uint32_t lo_bits, uint32_t hi_bits, unsigned long long *d_counts, void *stream)
+{
+    if (!d_counts || lo_bits > hi_bits || hi_bits > 0x7f7fffffu) return X100_EINVAL;
+    int rc = check_device();
+    if (rc) return rc;
+    hipError_t e = x100_check_quant_div_launch(lo_bits, hi_bits, d_counts, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
 // ---------------------------------------------------------------------------------------------
 // integer tile GEMV (int4 / int8 weights)
 // ---------------------------------------------------------------------------------------------

@@ -26,6 +26,7 @@ hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, cons
                              hipStream_t s);
 // True when x100_qgemv_launch accepts the shape (it then launches without further checks).
 bool x100_qgemv_supported(int qtype, int M, int N, int K);
+hipError_t x100_check_quant_div_launch(uint32_t lo, uint32_t hi, unsigned long long *cnt, hipStream_t s);
 
 size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act);
 hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,

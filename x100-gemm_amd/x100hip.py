@@ -33,7 +33,7 @@ EXPORTS = (
     "gemm_ime_i8", "gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant",
     "x100_hip_detect", "x100_hip_caps_print", "x100_hip_strerror",
     "x100_tile_bytes", "x100_pack_w_int4", "x100_pack_w_int8", "gemv_int4_hip", "gemv_int8_hip",
-    "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip",
+    "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip", "x100q_check_quant_div",
     "moe_layer_hip", "moe_layer_workspace_bytes", "moe_layer_hip_ws", "moe_layer_hip_noalloc",
     "x100_gguf_open", "x100_gguf_close", "x100_gguf_version", "x100_gguf_n_tensors", "x100_gguf_n_kv",
     "x100_gguf_alignment", "x100_gguf_data_offset", "x100_gguf_tensor_at", "x100_gguf_find",
@@ -104,6 +104,7 @@ def lib():
     L.x100q_packed_bytes.restype = sz
     L.x100q_pack.argtypes = [i, i, i, p, p, p]
     L.qgemv_hip.argtypes = [i, i, i, i, p, p, p, p]
+    L.x100q_check_quant_div.argtypes = [ctypes.c_uint32, ctypes.c_uint32, p, p]
     L.moe_layer_hip.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p]
     L.moe_layer_workspace_bytes.argtypes = [i, i, i, i, i]
     L.moe_layer_workspace_bytes.restype = sz
@@ -157,7 +158,7 @@ def lib():
     L.x100_attn_decode_hip_ws.restype = i
     L.x100_decode_layer_hip_ws.restype = i
     for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant", "x100_hip_detect",
-                 "x100q_pack", "qgemv_hip", "moe_layer_hip", "moe_layer_hip_ws", "moe_layer_hip_noalloc",
+                 "x100q_pack", "qgemv_hip", "x100q_check_quant_div", "moe_layer_hip", "moe_layer_hip_ws", "moe_layer_hip_noalloc",
                  "x100_pack_w_int4",
                  "x100_pack_w_int8",
                  "gemv_int4_hip", "gemv_int8_hip"):
@@ -216,6 +217,10 @@ def pack(qtype, N, K, d_src, d_dst, stream=None):
 
 def qgemv(qtype, M, N, K, d_w, d_x, d_y, stream=None):
     return _check("qgemv_hip", lib().qgemv_hip(qtype, M, N, K, d_w, d_x, d_y, stream))
+
+
+def check_quant_div(lo_bits, hi_bits, d_counts, stream=None):
+    return _check("x100q_check_quant_div", lib().x100q_check_quant_div(lo_bits, hi_bits, d_counts, stream))
 
 
 # ---- MoE layer ---------------------------------------------------------------------------------
