@@ -50,14 +50,16 @@ X100_DEV void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc
 // Q4_0 x Q8_0
 // ------------------------------------------------------------------------------------------------
 // Block = NT/64 waves; wave w owns rows row0 + w*RPW .. +RPW-1; lane l owns blocks l, l+64, ...
-// (BPL per row).  All RPW*BPL nibble loads (16 B) and scale loads are issued first.
-template <int MR, int RPW, int BPL, int XPT, int NT>
+// (BPL per row).  All RPW*BPL nibble loads (16 B) and scale loads are issued first.  FULL: K is
+// exactly 2048 * BPL, so every lane has all BPL blocks of a row and the LDS layout is known at
+// compile time (no clamped block indices, no range selects, immediate LDS offsets).
+template <int MR, int RPW, int BPL, int XPT, int NT, bool FULL>
 __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t *__restrict__ wd,
                                               const uint8_t *__restrict__ wq,
                                               const float *__restrict__ x, float *__restrict__ y)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int nb = K / 32;
+    const int nb = FULL ? 64 * BPL : K / 32;
     const int nb1 = MR * nb + 1;                 // + the quantizer's spare block
     int8_t *xlo = (int8_t *)smem;
     int8_t *xhi = xlo + nb1 * 16;
@@ -80,7 +82,7 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
     for (int r = 0; r < RPW; r++)
 #pragma unroll
         for (int c = 0; c < BPL; c++) {
-            const int row = min(rowb + r, N - 1), b = min(lane + 64 * c, nb - 1);
+            const int row = min(rowb + r, N - 1), b = FULL ? lane + 64 * c : min(lane + 64 * c, nb - 1);
             const size_t blk = (size_t)row * nb + b;
             q[r][c] = __builtin_nontemporal_load((const v4i *)(wq + blk * 16));
             dwb[r][c] = wd[blk];
@@ -106,8 +108,8 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
             // Branch-free (the scheduler interleaves the unrolled blocks): a lane past the last
             // block reads block nb-1 and adds 0.  Rows m >= M compute on unused LDS and are not
             // stored.
-            const bool inb = lane + 64 * c < nb;
-            const int b = min(lane + 64 * c, nb - 1);
+            const bool inb = FULL || lane + 64 * c < nb;
+            const int b = FULL ? lane + 64 * c : min(lane + 64 * c, nb - 1);
             const v4i qq = q[r][c];
             const float dwf = h2f((uint16_t)dwb[r][c]);
             int lo[4], hi[4];
@@ -120,13 +122,12 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
             for (int m = 0; m < MR; m++) {
                 const v4i xl = *(const v4i *)(xlo + (m * nb + b) * 16);
                 const v4i xh = *(const v4i *)(xhi + (m * nb + b) * 16);
-                int s = 0;
+                int s = xs[m * nb + b];   // -8 * sum(x): the nibble offset, (q-8).x = q.x - 8*sum(x)
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     s = dot4(lo[t], xl[t], s);
                     s = dot4(hi[t], xh[t], s);
                 }
-                s -= 8 * xs[m * nb + b];  // nibble offset: (q-8).x = q.x - 8*sum(x)
                 const float term = (float)s * (dwf * xd[m * nb + b]);
                 acc[r][m] += inb ? term : 0.0f;
             }
@@ -595,10 +596,10 @@ __global__ __launch_bounds__(NT) void k_q8_0(int M, int N, int K, int ngroups, c
     i8_load_group<LPR, RPW, BPL, NT>(cur, g, N, nb, qr, dr, nblk);
 
     __builtin_amdgcn_sched_barrier(0);   // keep the first group's loads ahead of the quantizer
-    q8_0_from_regs<XPT, NT, false>(xv, 0, total4, K, xlo, xhi, xd, xs);
+    q8_0_from_regs<XPT, NT, false, false>(xv, 0, total4, K, xlo, xhi, xd, xs);
     for (int c0 = NT * XPT; c0 < total4; c0 += NT * XPT) {
         x_load<XPT, NT>(xr, c0, xv);
-        q8_0_from_regs<XPT, NT, false>(xv, c0, total4, K, xlo, xhi, xd, xs);
+        q8_0_from_regs<XPT, NT, false, false>(xv, c0, total4, K, xlo, xhi, xd, xs);
     }
     __syncthreads();
 
@@ -881,7 +882,10 @@ void launch_q4_0_b(int M, int N, int K, const uint16_t *wd, const uint8_t *wq, s
     constexpr int NT = q40_wide(MR, BPL) ? 1024 : 256, RPW = q40_wide(MR, BPL) ? 1 : 4;
     const int rows = (NT / 64) * RPW;
     const dim3 grid((N + rows - 1) / rows);
-    hipLaunchKernelGGL((k_q4_0<MR, RPW, BPL, XPT, NT>), grid, dim3(NT), lds, s, M, N, K, wd, wq, x, y);
+    if (K == 2048 * BPL)
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, BPL, XPT, NT, true>), grid, dim3(NT), lds, s, M, N, K, wd, wq, x, y);
+    else
+        hipLaunchKernelGGL((k_q4_0<MR, RPW, BPL, XPT, NT, false>), grid, dim3(NT), lds, s, M, N, K, wd, wq, x, y);
 }
 
 template <int MR, int XPT>

@@ -266,6 +266,8 @@ X100_DEV void x_load(rsrc_t xr, int c0, float4 (&v)[XPT])
 // F16D: the block scale is stored as fp16 by the reference's truncating conversion
 // (quantize_q8_0_native, qwen_moe_hp.c:408-414) or kept in fp32 (pack_A_i8,
 // qwen_moe_q3k.c:420-427); the q values are the same either way (they use the fp32 scale).
+// OFS: also store -8 * (sum of the block's q), the offset term of a Q4_0 dot ((u - 8).q =
+// u.q - 8 * sum q for nibbles u), so that the dot starts from it; the int8 path needs no sums.
 //
 // The arithmetic is the reference's (d = amax / 127.0f, inv = 1.0f / d, q = lrintf(x * inv), fp16 d
 // by truncation), computed without IEEE division and without a clamp:
@@ -300,7 +302,7 @@ X100_DEV float f16_trunc_pos(float d)
     const float r = d >= 0x1p-14f ? nrm : sub;
     return d >= 65536.0f ? __builtin_inff() : r;
 }
-template <int XPT, int NT = 256, bool F16D = true>
+template <int XPT, int NT = 256, bool F16D = true, bool OFS = true>
 X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, int8_t *xlo,
                              int8_t *xhi, float *xd, int *xs)
 {
@@ -317,13 +319,12 @@ X100_DEV void q8_0_from_regs(const float4 (&v)[XPT], int c0, int total4, int K, 
         const uint32_t t0 = __float_as_uint(p0 + RND), t1 = __float_as_uint(p1 + RND);
         const uint32_t t2 = __float_as_uint(p2 + RND), t3 = __float_as_uint(p3 + RND);
         const uint32_t packed = perm(t1, t0, 0x0c0c0400u) | perm(t3, t2, 0x04000c0cu);
-        const int s = sum8_i(dot4((int)packed, 0x01010101, 0));
         const int pos = 4 * (f & 7);
         const int b = f < total4 ? f >> 3 : total4 >> 3;   // spare block past the end
         int8_t *dst = pos < 16 ? xlo + b * 16 + pos : xhi + b * 16 + (pos - 16);
         *(uint32_t *)dst = packed;
         xd[b] = F16D ? f16_trunc_pos(d) : d;   // the 8 lanes of a block hold the same d and sum
-        xs[b] = s;
+        if constexpr (OFS) xs[b] = -8 * sum8_i(dot4((int)packed, 0x01010101, 0));
     }
 }
 
