@@ -59,7 +59,7 @@ def test_pure_host_entry_points():
 
 
 def test_integration_snippet_is_the_compiled_code():
-    """INTEGRATION.md's C integration of the engine's Lin (lin_hip_new / lin_hip_mm) is compiled,
+    """The integration guide's C code for the engine's Lin (lin_hip_new / lin_hip_mm) is compiled,
     verbatim, into x100-gemm_amd/host/x100_host.c (run by tests/test_host_gpu.py)."""
     doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     src = open(os.path.join(ROOT, "x100-gemm_amd", "host", "x100_host.c")).read()

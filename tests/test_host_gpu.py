@@ -1,6 +1,6 @@
 """The C host programs over libx100hip (x100-gemm_amd/host/, built into x100-gemm_amd/bin/):
   q4_gemv     the reference's bench/q4_gemv.c command line, output lines and exit status;
-  x100_host   INTEGRATION.md's C integration (lin_hip_new / lin_hip_mm, moe_layer_hip and its
+  x100_host   the integration guide's C code (lin_hip_new / lin_hip_mm, moe_layer_hip and its
               _ws / _noalloc forms) fed the oracle's inputs through files, outputs compared with
               the oracle bit for bit;
   moe_decode  the decode weight stream of bench/moe_decode.c with --check: every launch of the
@@ -60,7 +60,7 @@ def test_q4_gemv_cli_draws_the_reference_inputs(dev):
     assert ref == y[0, :4].tolist()
 
 
-# ---- x100_host: INTEGRATION.md's C code ----------------------------------------------------------
+# ---- x100_host: the integration guide's C code ------------------------------------------------
 @pytest.mark.parametrize("qtype,N,K,M", [(synth.Q4_0, 4096, 4096, 1), (synth.Q4_K, 6144, 2048, 4),
                                          (synth.Q3_K, 6144, 2048, 1), (synth.Q5_K, 2048, 4096, 1),
                                          (synth.Q6_K, 1000, 2048, 3), (synth.Q8_0, 512, 2048, 8)])

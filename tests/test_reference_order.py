@@ -17,7 +17,7 @@ avoid:
     their last bit lands on the other side of a Q8_K rounding boundary, changing one int8 by 1;
     the error must lie within the flip's contribution w_a * d_act * |W[j, k]| (plus the
     conditioning allowance).
-The number of such elements is capped at what was measured (listed in DESIGN.md)."""
+The number of such elements is capped at the count measured when these tests were written."""
 import numpy as np
 import pytest
 

@@ -1,4 +1,4 @@
-/* x100_host -- the C integration of INTEGRATION.md, compiled: a reference-side caller of the
+/* x100_host -- the integration guide's C code, compiled: a reference-side caller of the
  * block-quantized GEMV (the engine's lin_mm, qwen_moe.c:101-107) and of the MoE block
  * (qwen_moe.c:294-311) on top of libx100hip, driven through files so that the tests can feed it
  * the oracle's inputs and compare its outputs.
@@ -68,7 +68,7 @@ static void *to_device(const void *host, size_t bytes)
     return d;
 }
 
-/* ---- the engine's Lin on the GPU --------------------------------- */
+/* ---- integration guide, section 2: the engine's Lin on the GPU ---------------------------- */
 typedef struct { int N, K, qtype; void *w; } LinHip;     /* w: device, x100q_packed_bytes */
 
 static int lin_hip_new(LinHip *l, int qtype, int N, int K, const void *gguf_host, void *stream) {
@@ -114,7 +114,7 @@ static int cmd_lin(int argc, char **argv)
     return 0;
 }
 
-/* ---- the MoE block ----------------------------------------------- */
+/* ---- integration guide, section 4: the MoE block ------------------------------------------ */
 static int cmd_moe(int argc, char **argv)
 {
     if (argc != 13 && argc != 14)
