@@ -246,9 +246,12 @@ struct RouteLds {
 
 // Softmax, top-k and expert union of the M token rows (qwen_moe.c:296-301), one wave per row;
 // KC = 64-expert groups per lane (2 for n_exp <= 128, else 4).
-template <int NWV, int KC>
-X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
+template <int NWV, int KC, int NE = 0, int NA = 0>
+X100_DEV void route_rows(int M, int n_exp_rt, int n_act_rt, const float *__restrict__ logits, RouteLds &rl)
 {
+    // NE, NA: the expert count and top-k known at compile time (0: taken from the arguments), so
+    // that the selection rounds unroll without range tests
+    const int n_exp = NE ? NE : n_exp_rt, n_act = NA ? NA : n_act_rt;
     const int lane = threadIdx.x & 63, w = wave_id();
     uint64_t rowmask[KC];   // ballots of the chosen experts of this wave's last row
 #pragma unroll
@@ -286,9 +289,11 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
             key[c] = (lane + 64 * c) < n_exp ? __float_as_int(pv == pv ? pv : 0.0f) : INT_MIN;
         }
         float wsel[8];
+        int isel[8];
 #pragma unroll
         for (int a = 0; a < 8; a++) {
             wsel[a] = 0.0f;
+            isel[a] = 0;
             if (a < n_act) {
                 // Largest probability (wave maximum of the keys), then the lowest expert id holding
                 // it: per group c the lowest lane whose key matches (all ones when none does, so
@@ -304,7 +309,7 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
                     bi = min(bi, (unsigned)(__ffsll((unsigned long long)h) - 1) | (unsigned)(64 * c));
                 }
                 wsel[a] = __int_as_float(km);
-                if (lane == 0) rl.sel[m * n_act + a] = (int)bi;
+                isel[a] = (int)bi;
 #pragma unroll
                 for (int c = 0; c < KC; c++) {
                     const bool hit = (unsigned)(lane + 64 * c) == bi;
@@ -320,9 +325,16 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
         for (int a = 0; a < 8; a++)
             if (a < n_act) ssum += wsel[a];
         float mine = wsel[0];
+        int mine_e = isel[0];
 #pragma unroll
-        for (int a = 1; a < 8; a++) mine = lane == a ? wsel[a] : mine;
-        if (lane < n_act) rl.w[m * n_act + lane] = mine / ssum;
+        for (int a = 1; a < 8; a++) {
+            mine = lane == a ? wsel[a] : mine;
+            mine_e = lane == a ? isel[a] : mine_e;
+        }
+        if (lane < n_act) {
+            rl.w[m * n_act + lane] = mine / ssum;
+            rl.sel[m * n_act + lane] = mine_e;
+        }
 #pragma unroll
         for (int c = 0; c < KC; c++) {
             rowmask[c] = __ballot(picked[c]);
@@ -370,7 +382,9 @@ X100_DEV void route_rows(int M, int n_exp, int n_act, const float *__restrict__ 
 template <int NWV>
 X100_DEV void route_block(int M, int n_exp, int n_act, const float *__restrict__ logits, RouteLds &rl)
 {
-    if (n_exp <= 128)
+    if (n_exp == 128 && n_act == 8)   // Qwen3-30B-A3B
+        route_rows<NWV, 2, 128, 8>(M, n_exp, n_act, logits, rl);
+    else if (n_exp <= 128)
         route_rows<NWV, 2>(M, n_exp, n_act, logits, rl);
     else
         route_rows<NWV, 4>(M, n_exp, n_act, logits, rl);
