@@ -170,13 +170,12 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, 
     }
 
     // merge the 8 position groups (lanes l, l^8, l^16, l^32 hold the same dimensions): xor 8 is a
-    // rotation by 8 within a row of 16 (DPP), xor 16 and xor 32 go through ds_bpermute
+    // rotation by 8 within a row of 16 (DPP), xor 16 and xor 32 are permlane swaps
 #pragma unroll
     for (int g = 0; g < QPW; g++) {
 #pragma unroll
         for (int lvl = 0; lvl < 3; lvl++) {
-            const int off = 8 << lvl;
-            auto xch = [&](float v) { return lvl == 0 ? dpp_f<0x128>(v, v) : __shfl_xor(v, off, 64); };
+            auto xch = [&](float v) { return lvl == 0 ? dpp_f<0x128>(v, v) : (lvl == 1 ? xor16_f(v) : xor32_f(v)); };
             const float m2 = xch(m[g]), l2 = xch(l[g]);
             // a = e^(m - max), b = e^(m2 - max): one of them is 1
             const bool mine = m[g] >= m2;
@@ -218,8 +217,8 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
         se[c] = P[c];
         mx = fmaxf(mx, se[c]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, xor32_f(mx));
+    mx = fmaxf(mx, xor16_f(mx));
     mx = fmaxf(mx, dpp_f<0x128>(mx, mx));
     mx = fmaxf(mx, dpp_f<0x124>(mx, mx));
     mx = fmaxf(mx, dpp_f<0x4E>(mx, mx));

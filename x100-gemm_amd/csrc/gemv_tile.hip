@@ -45,8 +45,8 @@ X100_DEV void xstore(const v4u (&t)[4], int v0, int nv, int8_t *xs, int *xsum)
 X100_DEV int sum_stride8(int v)
 {
     v += dpp_i<0x128>(0, v);         // row_ror:8 = lane (i + 8) mod 16 within a row: xor 8
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+    v += xor16_i(v);
+    v += xor32_i(v);
     return v;
 }
 

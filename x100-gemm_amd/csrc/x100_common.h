@@ -66,17 +66,40 @@ X100_DEV void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, u
 // it (buffer resources, M0) stay in scalar registers.
 X100_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
+// The value of lane l^32 / l^16 (what __shfl_xor(v, 32 / 16, 64) returns), in VALU instructions
+// instead of an LDS permute: v_permlane32_swap / v_permlane16_swap with both operands v leave the
+// lower row (half) of each pair in the first result and the upper one in the second, and the lane
+// takes the one that is not its own.
+X100_DEV uint32_t xor32_u(uint32_t v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? r[0] : r[1];
+}
+X100_DEV uint32_t xor16_u(uint32_t v)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? r[0] : r[1];
+}
+X100_DEV float xor32_f(float v) { return __uint_as_float(xor32_u(__float_as_uint(v))); }
+X100_DEV float xor16_f(float v) { return __uint_as_float(xor16_u(__float_as_uint(v))); }
+X100_DEV int xor32_i(int v) { return (int)xor32_u((uint32_t)v); }
+X100_DEV int xor16_i(int v) { return (int)xor16_u((uint32_t)v); }
+
 // Wave-wide (64 lanes) reductions.
 X100_DEV int wave_sum_i(int v)
 {
+    v += xor32_i(v);
+    v += xor16_i(v);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
 X100_DEV float wave_max_f(float v)
 {
+    v = fmaxf(v, xor32_f(v));
+    v = fmaxf(v, xor16_f(v));
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
 
@@ -144,13 +167,14 @@ X100_DEV int wave_max_iu(int v)
     return __builtin_amdgcn_readlane(v, 63);
 }
 // Sum over the 64 lanes in xor-butterfly order (lane l adds lane l^32, then l^16, l^8, l^4, l^2,
-// l^1): the value six __shfl_xor steps give, bit for bit.  After the first two levels a lane's
-// value depends only on l mod 16, after the third only on l mod 8, so row_ror:8 and row_ror:4
-// (rotations within a row of 16) deliver the l^8 and l^4 partners' values; quad_perm does l^2, l^1.
+// l^1): the value six __shfl_xor steps give, bit for bit.  The l^32 and l^16 partners come from
+// permlane swaps.  After the first two levels a lane's value depends only on l mod 16, after the
+// third only on l mod 8, so row_ror:8 and row_ror:4 (rotations within a row of 16) deliver the l^8
+// and l^4 partners' values; quad_perm does l^2, l^1.
 X100_DEV float wave_sum_bfly_f(float s)
 {
-    s += __shfl_xor(s, 32, 64);
-    s += __shfl_xor(s, 16, 64);
+    s += xor32_f(s);
+    s += xor16_f(s);
     s += dpp_f<0x128>(0.0f, s);
     s += dpp_f<0x124>(0.0f, s);
     s += dpp_f<0x4E>(0.0f, s);
