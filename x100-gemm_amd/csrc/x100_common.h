@@ -85,23 +85,6 @@ X100_DEV float xor16_f(float v) { return __uint_as_float(xor16_u(__float_as_uint
 X100_DEV int xor32_i(int v) { return (int)xor32_u((uint32_t)v); }
 X100_DEV int xor16_i(int v) { return (int)xor16_u((uint32_t)v); }
 
-// Wave-wide (64 lanes) reductions.
-X100_DEV int wave_sum_i(int v)
-{
-    v += xor32_i(v);
-    v += xor16_i(v);
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-X100_DEV float wave_max_f(float v)
-{
-    v = fmaxf(v, xor32_f(v));
-    v = fmaxf(v, xor16_f(v));
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
 
 // ------------------------------------------------------------------------------------------------
 // Lane reductions with DPP (data-parallel primitives: a VALU operand read from another lane of
