@@ -66,8 +66,9 @@ int qgemv_hip(int qtype, int M, int N, int K, const void *w_packed, const float 
  * [lo_bits, hi_bits] (<= 0x7f7fffff) and adds, into the device counters d_counts[0..2]
  * (zeroed by the caller), the inputs where they differ from the correctly rounded 1.0f / u, from
  * u / 127.0f and from the reference's truncating fp16 conversion.  The quantizers rely on zero
- * for 1/d over d in [RN(1e-6 / 127), FLT_MAX / 127] and for amax / 127 over amax in
- * [1e-6, FLT_MAX].  Asynchronous on stream. */
+ * for 1/d over every positive d up to FLT_MAX / 127 and for amax / 127 over every positive
+ * amax (the Q8_0 forms need only d >= RN(1e-6 / 127) and amax >= 1e-6).  Asynchronous on
+ * stream. */
 int x100q_check_quant_div(uint32_t lo_bits, uint32_t hi_bits, unsigned long long *d_counts, void *stream);
 
 #ifdef __cplusplus

@@ -118,22 +118,20 @@ def _stream():
 
 def test_quantizer_division_free_arithmetic_is_exact(dev):
     # The activation quantizers compute amax / 127.0f, 1.0f / d and d's fp16 truncation without
-    # IEEE division.  Exhaustively on this GPU: 1/d over every d the Q8_0 quantizer can form
-    # (amax >= 1e-6), amax / 127 over every amax >= 1e-6, and the fp16 truncation over every
-    # positive float; zero mismatches against the correctly rounded quotients and the reference's
-    # conversion (the checker runs the quantizer's own device functions).
+    # IEEE division.  Exhaustively on this GPU: 1/d over every positive d up to FLT_MAX / 127
+    # (subnormal d included: the Q8_K quantizers have no amax floor), amax / 127 over every
+    # positive amax, and the fp16 truncation over every positive float; zero mismatches against
+    # the correctly rounded quotients and the reference's conversion (the checker runs the
+    # quantizers' own device functions).
     import torch
     fmax = 0x7f7fffff
-    d_lo, d_hi = _fbits(np.float32(np.float32(1e-6) / np.float32(127.0))), _fbits(np.float32(3.4028234663852886e38 / 127.0))
+    d_hi = _fbits(np.float32(3.4028234663852886e38 / 127.0))
     cnt = torch.zeros(3, dtype=torch.int64, device=dev)
-    x100hip.check_quant_div(d_lo, d_hi, cnt.data_ptr(), _stream())
+    x100hip.check_quant_div(1, d_hi, cnt.data_ptr(), _stream())
     torch.cuda.synchronize()
-    assert int(cnt[0]) == 0, "rcp_rn mismatches over the d range: %d" % int(cnt[0])
-    cnt.zero_()
-    x100hip.check_quant_div(_fbits(np.float32(1e-6)), fmax, cnt.data_ptr(), _stream())
-    torch.cuda.synchronize()
-    assert int(cnt[1]) == 0, "div127_rn mismatches for amax >= 1e-6: %d" % int(cnt[1])
+    assert int(cnt[0]) == 0, "1/d mismatches over the d range: %d" % int(cnt[0])
     cnt.zero_()
     x100hip.check_quant_div(1, fmax, cnt.data_ptr(), _stream())
     torch.cuda.synchronize()
+    assert int(cnt[1]) == 0, "div127_rn mismatches: %d" % int(cnt[1])
     assert int(cnt[2]) == 0, "f16_trunc_pos mismatches: %d" % int(cnt[2])

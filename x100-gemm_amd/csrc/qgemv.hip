@@ -1002,8 +1002,9 @@ hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *
 }
 
 // Exhaustive check of the activation quantizer's division-free arithmetic (x100_common.h) on the
-// device: for every float u in [lo, hi] (bit patterns), cnt[0] counts rcp_rn(u) != 1.0f / u,
-// cnt[1] div127_rn(u) != u / 127.0f and cnt[2] f16_trunc_pos(u) != the reference's fp16
+// device: for every float u in [lo, hi] (bit patterns), cnt[0] counts rcp_rn_any(u) != 1.0f / u
+// (rcp_rn_any is rcp_rn from 2^-126 up, so this covers both), cnt[1] div127_rn(u) != u / 127.0f
+// and cnt[2] f16_trunc_pos(u) != the reference's fp16
 // truncation (f2h_trunc then h2f).  The divisions here are IEEE (built with correctly rounded
 // division).
 __global__ __launch_bounds__(256) void k_check_quant_div(uint32_t lo, uint32_t hi, unsigned long long *cnt)
@@ -1012,7 +1013,7 @@ __global__ __launch_bounds__(256) void k_check_quant_div(uint32_t lo, uint32_t h
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t u = (uint64_t)lo + blockIdx.x * blockDim.x + threadIdx.x; u <= hi; u += stride) {
         const float v = __uint_as_float((uint32_t)u);
-        c0 += __float_as_uint(rcp_rn(v)) != __float_as_uint(1.0f / v);
+        c0 += __float_as_uint(rcp_rn_any(v)) != __float_as_uint(1.0f / v);
         c1 += __float_as_uint(div127_rn(v)) != __float_as_uint(v / 127.0f);
         c2 += __float_as_uint(f16_trunc_pos(v)) != __float_as_uint(h2f(f2h_trunc(v)));
     }

@@ -302,6 +302,17 @@ X100_DEV float rcp_rn(float d)
     const float e = __builtin_fmaf(-d, y0, 1.0f);
     return __builtin_fmaf(e, y0, y0);
 }
+// 1.0f / d correctly rounded for every d in [0, 2^126], and 0 for d = 0 (the Q8_K quantizers'
+// reciprocal, whose amax has no floor).  rcp_rn is exact on [2^-126, 2^126] (checked on gfx950
+// for every float there; it fails on subnormals).  A subnormal d is scaled by 2^64 into that range
+// and the reciprocal scaled back: both scalings are exact, and the product overflows to infinity
+// exactly when 1/d rounds to infinity, so the result is RN(1/d) there too.
+X100_DEV float rcp_rn_any(float d)
+{
+    const bool sub = d < 0x1p-126f;
+    const float r = rcp_rn(sub ? d * 0x1p64f : d);
+    return d == 0.0f ? 0.0f : (sub ? r * 0x1p64f : r);
+}
 X100_DEV float f16_trunc_pos(float d)
 {
     const float nrm = __uint_as_float(__float_as_uint(d) & 0xffffe000u);
@@ -343,8 +354,8 @@ X100_DEV void q8_K_wave(const float4 v, int8_t *qs, int *bs, float *dout)
     const int lane = threadIdx.x & 63;
     const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     const float amax = wave_max_u(a);
-    const float d = amax / 127.0f;
-    const float rep = d != 0.0f ? 1.0f / d : 0.0f;
+    const float d = div127_rn(amax);
+    const float rep = rcp_rn_any(d);
     const int q0 = clamp_i8((int)roundf(v.x * rep)), q1 = clamp_i8((int)roundf(v.y * rep));
     const int q2 = clamp_i8((int)roundf(v.z * rep)), q3 = clamp_i8((int)roundf(v.w * rep));
     ((uint32_t *)qs)[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
@@ -363,8 +374,8 @@ X100_DEV void q8_K_from_regs(const float4 (&v)[XPT], int c0, int total4, int8_t 
         const int f = c0 + threadIdx.x + NT * i;
         const float a = fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
         const float amax = wave_max_u(a);
-        const float d = amax / 127.0f;
-        const float rep = d != 0.0f ? 1.0f / d : 0.0f;
+        const float d = div127_rn(amax);
+        const float rep = rcp_rn_any(d);
         const int q0 = clamp_i8((int)roundf(v[i].x * rep)), q1 = clamp_i8((int)roundf(v[i].y * rep));
         const int q2 = clamp_i8((int)roundf(v[i].z * rep)), q3 = clamp_i8((int)roundf(v[i].w * rep));
         const int s = sum4_i(q0 + q1 + q2 + q3);
@@ -420,8 +431,8 @@ X100_DEV void q8k_quant(const float4 (&v)[4], int nq, int qb, uint8_t *recs)
     a = fmaxf(a, dpp_f<0x4E>(a, a));
     a = fmaxf(a, dpp_f<0x141>(a, a));
     a = fmaxf(a, dpp_f<0x140>(a, a));
-    const float d = a / 127.0f;
-    const float rep = d != 0.0f ? 1.0f / d : 0.0f;
+    const float d = div127_rn(a);
+    const float rep = rcp_rn_any(d);
     uint32_t pk[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
