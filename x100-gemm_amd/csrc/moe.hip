@@ -574,14 +574,15 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
                    __builtin_amdgcn_readfirstlane(wlds + b * wbytes + (uint32_t)i * 1024u));
         }
     };
-    // The first item's weights first, then the records of all M rows (both waited for at the top
-    // of the first item), then each union slot's pair list and size -> LDS.
+    // The records of all M rows first, then the first item's weights (both waited for at the top
+    // of the first item), then each union slot's pair list and size -> LDS.  Records first: every
+    // item needs them, and behind the weight requests they arrived later (M = 1 16.0 -> 15.85 us).
     int it = blockIdx.x, b = 0;
-    if (it < items) issue(it, 0);
     const int totv = M * nsb * KREC / 16;
     for (int ch = w; ch * 64 < totv; ch += NWV)
         dma16v((const v4i *)ws.xrec + min(ch * 64 + lane, totv - 1),
                __builtin_amdgcn_readfirstlane(lds_addr(smem) + (uint32_t)ch * 1024u));
+    if (it < items) issue(it, 0);
     if (blockIdx.x == 0) publish_routing(M, n_act, rl, ws, sel_out, sw_out);
     if (t < P) {
         int slot, pos, cnt;
