@@ -84,7 +84,10 @@ def test_moe_m8_and_residual(dev):
 
 @pytest.mark.parametrize("M,n_exp,d,ff,n_act", [(1, 16, 512, 256, 4), (3, 16, 512, 256, 4),
                                                 (2, 8, 256, 512, 8), (5, 64, 1024, 512, 2),
-                                                (4, 200, 256, 256, 6)])
+                                                (4, 200, 256, 256, 6),
+                                                # odd router-wave counts: a router block that also
+                                                # holds a quantizer wave
+                                                (1, 9, 256, 256, 4), (3, 15, 512, 256, 4)])
 def test_moe_small_shapes(dev, M, n_exp, d, ff, n_act):
     check(M, n_exp, d, ff, n_act, seed=600 + M + n_exp, dev=dev)
 

@@ -107,15 +107,21 @@ X100_DEV float swiglu(float g, float u)
 // Router.  Wave g < n_exp * M computes the logit of expert g / M for token row g % M (qwen_moe.c:296;
 // lane l sums elements 4l..4l+3, +256, ... in order, then a butterfly over the lanes), one row per
 // wave so that no wave runs the dependent add chains of several rows; the following waves quantize
-// four 256-element blocks of hn each into the Q8_K records ws.xrec[m * nsb + sb].
+// four 256-element blocks of hn each into the Q8_K records ws.xrec[m * nsb + sb].  Blocks of
+// RT_WPB = 2 waves, so that the 128 router waves of one token row spread over 64 CUs (each CU
+// pulls its router rows and hn through its own load path): M = 1 15.85 -> 15.67 us against 4
+// waves per block; 1 wave per block was as fast at M = 1 but slower at M = 4.  A block that holds
+// both kinds of wave (n_exp * M odd) works as before: its quantizer wave loads no router row, takes
+// part in the hn DMA and the barrier, and skips the dot.
 // ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, uint32_t mnsb, const float *__restrict__ hn,
+constexpr int RT_WPB = 2;
+__global__ __launch_bounds__(64 * RT_WPB) void k_moe_route(int M, int d, int n_exp, uint32_t mnsb, const float *__restrict__ hn,
                                                    const float *__restrict__ R, MoeWs ws)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     float4 *s_hn = (float4 *)smem;   // [M][d/4]
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + wave_id();
+    const int wave = blockIdx.x * RT_WPB + wave_id();
     const int nsb = d / 256, nq = M * nsb, nrw = n_exp * M;
 
     if (wave >= nrw) {   // quantizer waves (wave-uniform)
@@ -125,7 +131,7 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, uint
             q8k_load(buf_rsrc(hn, (uint32_t)(M * d) * 4u), d, nsb, mnsb, nq, qb, v);
             q8k_quant(v, nq, qb, ws.xrec);
         }
-        if (4 * (int)blockIdx.x >= nrw) return;   // a block of quantizer waves only
+        if (RT_WPB * (int)blockIdx.x >= nrw) return;   // a block of quantizer waves only
     }
 
     // The wave's expert and token row, and its router row (elements past d read as 0 and are not
@@ -137,7 +143,7 @@ __global__ __launch_bounds__(256) void k_moe_route(int M, int d, int n_exp, uint
     for (int j = 0; j < 16; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
 
     // hn -> LDS (all M rows; M*d/256 chunks of 1 KiB, one wave each), asynchronous.
-    for (int ch = wave_id(); ch < M * nsb; ch += 4)
+    for (int ch = wave_id(); ch < M * nsb; ch += RT_WPB)
         dma_1k(hn + (size_t)ch * 256 + 4 * lane, smem + ch * 1024);
     __syncthreads();
 
@@ -1129,7 +1135,7 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     if (M >= MF_MIN_ROWS) return moe_launch_mfma(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
 
     const int nwaves = n_exp * M + (M * nsb + 3) / 4;   // router waves, then quantizer waves of four records
-    hipLaunchKernelGGL(k_moe_route, dim3((nwaves + 3) / 4), dim3(256), (size_t)M * d * 4, s, M, d, n_exp,
+    hipLaunchKernelGGL(k_moe_route, dim3((nwaves + RT_WPB - 1) / RT_WPB), dim3(64 * RT_WPB), (size_t)M * d * 4, s, M, d, n_exp,
                        udiv16_magic((uint32_t)nsb), hn, R, ws);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
