@@ -195,21 +195,20 @@ X100_DEV void q8k_load(rsrc_t xr, const KqArgs &a, int nq, int qb, float4 (&v)[4
     q8k_load(xr, a.K, a.nsb, a.mnsb, nq, qb, v);
 }
 
-// The block's M x nsb records, passes of four: wave w takes passes w, w + nw, w + 2nw, ...  The
+// The block's M x nsb records, passes of four: the wave with quantizer index w (a permutation of
+// the wave ids) takes passes w, w + nw, w + 2nw, ...  The
 // first two passes' loads are issued by q8k_first (before the weight loads), the rest are loaded
 // and quantized one pass at a time by q8k_rest.
 struct Q8kFirst {
     float4 v0[4], v1[4];
 };
-X100_DEV void q8k_first(rsrc_t xr, const KqArgs &a, int nq, int nw, Q8kFirst &f)
+X100_DEV void q8k_first(rsrc_t xr, const KqArgs &a, int nq, int nw, Q8kFirst &f, int w)
 {
-    const int w = wave_id();
     q8k_load(xr, a, nq, 4 * w, f.v0);
     if (4 * (w + nw) < nq) q8k_load(xr, a, nq, 4 * (w + nw), f.v1);
 }
-X100_DEV void q8k_rest(rsrc_t xr, const KqArgs &a, int nq, int nw, const Q8kFirst &f, uint8_t *recs)
+X100_DEV void q8k_rest(rsrc_t xr, const KqArgs &a, int nq, int nw, const Q8kFirst &f, uint8_t *recs, int w)
 {
-    const int w = wave_id();
     q8k_quant(f.v0, nq, 4 * w, recs);
     if (4 * (w + nw) < nq) q8k_quant(f.v1, nq, 4 * (w + nw), recs);
     for (int qb = 4 * (w + 2 * nw); qb < nq; qb += 4 * nw) {
@@ -275,9 +274,10 @@ __global__ __launch_bounds__(512) void k_q4_K(const KqArgs a)
     const KqUnit ku = kq_unit(a);
 
     const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
-    const bool wq = 4 * w < nq;   // the wave has records to quantize (wave-uniform)
+    const int qw = w;              // quantizer index of the wave
+    const bool wq = 4 * qw < nq;   // the wave has records to quantize (wave-uniform)
     Q8kFirst xf;
-    if (wq) q8k_first(xr, a, nq, nw, xf);
+    if (wq) q8k_first(xr, a, nq, nw, xf, qw);
     // every wave's x loads before any wave's weight loads (s_barrier, no wait), as in k_q4_0
     __builtin_amdgcn_s_barrier();
 
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(512) void k_q4_K(const KqArgs a)
     const uint32_t ddv = *(const uint32_t *)(sec + (size_t)144 * N + (size_t)ku.row * 4);
 
     __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the quantizer
-    if (wq) q8k_rest(xr, a, nq, nw, xf, recs);
+    if (wq) q8k_rest(xr, a, nq, nw, xf, recs, qw);
     __syncthreads();
 
     if (32 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
@@ -334,9 +334,10 @@ __global__ __launch_bounds__(512) void k_q3_K(const KqArgs a)
     const KqUnit ku = kq_unit(a);
 
     const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
-    const bool wq = 4 * w < nq;   // the wave has records to quantize (wave-uniform)
+    const int qw = w;              // quantizer index of the wave
+    const bool wq = 4 * qw < nq;   // the wave has records to quantize (wave-uniform)
     Q8kFirst xf;
-    if (wq) q8k_first(xr, a, nq, nw, xf);
+    if (wq) q8k_first(xr, a, nq, nw, xf, qw);
     // every wave's x loads before any wave's weight loads (s_barrier, no wait), as in k_q4_0
     __builtin_amdgcn_s_barrier();
 
@@ -349,7 +350,7 @@ __global__ __launch_bounds__(512) void k_q3_K(const KqArgs a)
     const uint16_t dw16 = *(const uint16_t *)(sec + (size_t)112 * N + (size_t)ku.row * 2);
 
     __builtin_amdgcn_sched_barrier(0);
-    if (wq) q8k_rest(xr, a, nq, nw, xf, recs);
+    if (wq) q8k_rest(xr, a, nq, nw, xf, recs, qw);
     __syncthreads();
 
     if (32 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
@@ -418,9 +419,14 @@ __global__ __launch_bounds__(512) void k_kq_rm(const KqArgs a)
     const int row = min(row0 + min(rib, RB - 1), N - 1);
 
     const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
-    const bool wq = 4 * w < nq;   // the wave has records to quantize (wave-uniform)
+    // Quantizer index rotated by two: with 6 waves (one token row, 24 rows of 8 super-blocks) the
+    // two quantizing waves are 2 and 3, alone on their SIMDs (waves map to SIMDs round-robin, so
+    // 0-1 share theirs with dot waves 4-5): Q4_K 3.90 -> 3.84 us, Q3_K 3.89 -> 3.76 us.  Any
+    // rotation is a permutation of the waves, so every record is still quantized once.
+    const int qw = (w + nw - 2) % nw;
+    const bool wq = 4 * qw < nq;   // the wave has records to quantize (wave-uniform)
     Q8kFirst xf;
-    if (wq) q8k_first(xr, a, nq, nw, xf);
+    if (wq) q8k_first(xr, a, nq, nw, xf, qw);
 
     v4i qv[4], hm = {};
     uint2 sv;
@@ -443,7 +449,7 @@ __global__ __launch_bounds__(512) void k_kq_rm(const KqArgs a)
     }
 
     __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the quantizer
-    if (wq) q8k_rest(xr, a, nq, nw, xf, recs);
+    if (wq) q8k_rest(xr, a, nq, nw, xf, recs, qw);
     __syncthreads();
     if (32 * w >= RB * nsb) return;   // waves past the block's units only quantized (wave-uniform)
 
