@@ -40,6 +40,14 @@ int gemm_hip_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *
 int gemm_hip_i8_dev(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
                     void *stream);
 
+/* The overwrite form C = A*B of gemm_ime2_i8_st / gemm_ime2_i8_mt (reference
+ * src/gemm_ime2_i8.c:102-147, which store each tile without reading C).  Device pointers,
+ * asynchronous on `stream`: C is cleared by a kernel (no hipMemsetAsync, so the call can be
+ * captured in a graph), then accumulated as gemm_hip_i8_dev does; K = 0 leaves C = 0.  The
+ * reference's pre-packed A/B layouts are not needed: A and B are row-major as above. */
+int gemm_hip_i8_dev_set(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
+                        void *stream);
+
 /* Same as gemm_hip_i8_dev with an explicit kernel choice (0 auto, 1 256x256 MFMA tile,
  * 2 128x128 MFMA tile, 3 skinny M<=16 split-K, 4 generic, 5 256x256 tile with 4 waves,
  * 6 64x64 MFMA tile, 7 32x32 MFMA tile).  For tests and measurement. */

@@ -41,6 +41,44 @@ def test_gemm_256_cube(dev):
     assert np.array_equal(gpu_gemm(A, B, C0, dev), oracle_gemm(A, B, C0))
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (8, 4096, 4096), (300, 200, 96), (2048, 2048, 1024)])
+def test_gemm_overwrite_form(dev, M, N, K):
+    # C = A*B whatever C held before (the overwrite form of gemm_ime2_i8_st / _mt): the MFMA tiles,
+    # the skinny split-K kernel (atomics into the cleared C) and the generic kernel.
+    import torch
+    A, B = synth.gemm_inputs(M, N, K, seed=3030 + M)
+    garbage = synth.rand_int8(5, (M, N)).astype(np.int32) * 12345
+    dA = torch.from_numpy(A).to(dev)
+    dB = torch.from_numpy(B).to(dev)
+    dC = torch.from_numpy(garbage.copy()).to(dev)
+    x100hip.gemm_dev_set(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(dC.cpu().numpy(), oracle_gemm(A, B, np.zeros((M, N), np.int32)))
+
+
+def test_gemm_overwrite_form_k0_and_unaligned_c(dev):
+    # K = 0 gives C = 0 (A and B may be null); a C 4 bytes past a 16-byte boundary takes the
+    # clear's scalar head; the words around C keep their values.
+    import torch
+    M, N = 33, 47
+    buf = torch.full((M * N + 8,), 99, dtype=torch.int32, device=dev)
+    assert buf.data_ptr() % 16 == 0
+    ptr = buf.data_ptr() + 4
+    x100hip.gemm_dev_set(M, N, 0, 0, 0, ptr, _stream())
+    torch.cuda.synchronize()
+    h = buf.cpu().numpy()
+    assert h[0] == 99 and np.all(h[1:1 + M * N] == 0) and np.all(h[1 + M * N:] == 99)
+    A, B = synth.gemm_inputs(M, N, 64, seed=31)
+    dA = torch.from_numpy(A).to(dev)
+    dB = torch.from_numpy(B).to(dev)
+    buf.fill_(7)
+    x100hip.gemm_dev_set(M, N, 64, dA.data_ptr(), dB.data_ptr(), ptr, _stream())
+    torch.cuda.synchronize()
+    h = buf.cpu().numpy()
+    assert h[0] == 7 and np.all(h[1 + M * N:] == 7)
+    assert np.array_equal(h[1:1 + M * N].reshape(M, N), oracle_gemm(A, B, np.zeros((M, N), np.int32)))
+
+
 def test_gemm_4096_cube(dev):
     A, B = synth.gemm_inputs(4096, 4096, 4096, seed=2026)
     C0 = np.zeros((4096, 4096), np.int32)

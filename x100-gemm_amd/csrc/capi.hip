@@ -185,6 +185,19 @@ int gemm_hip_i8_dev(int M, int N, int K, const int8_t *dA, const int8_t *dB, int
     return gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, 0);
 }
 
+int gemm_hip_i8_dev_set(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC, void *stream)
+{
+    if (M < 0 || N < 0 || K < 0) return X100_EINVAL;
+    if (M == 0 || N == 0) return X100_OK;   // no output elements
+    if (!dC || (K > 0 && (!dA || !dB))) return X100_EINVAL;
+    int rc = check_device();
+    if (rc) return rc;
+    hipError_t e = x100_zero_i32_launch(dC, (size_t)M * N, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e);
+    if (K == 0) return X100_OK;   // C = (empty product) = 0
+    return gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, 0);
+}
+
 int gemm_hip_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C)
 {
     if (M < 0 || N < 0 || K < 0) return X100_EINVAL;

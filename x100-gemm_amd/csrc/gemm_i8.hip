@@ -880,7 +880,29 @@ hipError_t launch_mfma(int M, int N, int K, const int8_t *A, const int8_t *B, in
     return hipGetLastError();
 }
 
+// C = 0 for the overwrite form (C = A*B): 16-byte stores from the first 16-byte boundary, single
+// int32 stores before it and for the tail (a kernel rather than hipMemsetAsync, so that a caller
+// can capture it in a graph).
+__global__ __launch_bounds__(256) void k_zero_i32(int32_t *__restrict__ C, size_t n)
+{
+    const size_t head = min(n, (size_t)((16 - ((uintptr_t)C & 15)) & 15) / 4);
+    const size_t nv = (n - head) / 4;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+    v4i *cv = (v4i *)(C + head);
+    for (size_t i = t; i < nv; i += stride) cv[i] = v4i{0, 0, 0, 0};
+    if (t < head) C[t] = 0;
+    for (size_t i = head + 4 * nv + t; i < n; i += stride) C[i] = 0;
+}
+
 }  // namespace
+
+hipError_t x100_zero_i32_launch(int32_t *C, size_t n, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    const size_t blocks = min((n / 4 + 255) / 256 + 1, (size_t)4096);
+    hipLaunchKernelGGL(k_zero_i32, dim3((unsigned)blocks), dim3(256), 0, s, C, n);
+    return hipGetLastError();
+}
 
 // Kernel selection.  Returns the HIP launch status.
 hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,

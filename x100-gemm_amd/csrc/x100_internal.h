@@ -19,6 +19,7 @@ enum {
 
 hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
                                hipStream_t s, int variant);
+hipError_t x100_zero_i32_launch(int32_t *C, size_t n, hipStream_t s);
 
 size_t x100_q_packed_bytes(int qtype, int N, int K);
 hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *dst, hipStream_t s);

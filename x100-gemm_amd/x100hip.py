@@ -30,7 +30,7 @@ MOE_NOALLOC_MAX_BYTES = 8 << 20
 # Every symbol declared in include/x100_gemm.h, x100_gemv_tile.h, x100_qgemv.h, x100_moe.h,
 # x100_gguf.h, x100_decode.h.
 EXPORTS = (
-    "gemm_ime_i8", "gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant",
+    "gemm_ime_i8", "gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_set", "gemm_hip_i8_dev_variant",
     "x100_hip_detect", "x100_hip_caps_print", "x100_hip_strerror",
     "x100_tile_bytes", "x100_pack_w_int4", "x100_pack_w_int8", "gemv_int4_hip", "gemv_int8_hip",
     "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip", "x100q_check_quant_div",
@@ -93,6 +93,7 @@ def lib():
     L.gemm_hip_i8.argtypes = [i, i, i, p, p, p]
     L.gemm_hip_i8_dev.argtypes = [i, i, i, p, p, p, p]
     L.gemm_hip_i8_dev_variant.argtypes = [i, i, i, p, p, p, p, i]
+    L.gemm_hip_i8_dev_set.argtypes = [i, i, i, p, p, p, p]
     L.x100_hip_detect.argtypes = [ctypes.POINTER(Caps)]
     L.x100_hip_caps_print.argtypes = [ctypes.POINTER(Caps)]
     L.x100_hip_caps_print.restype = None
@@ -157,7 +158,7 @@ def lib():
                                            p]
     L.x100_attn_decode_hip_ws.restype = i
     L.x100_decode_layer_hip_ws.restype = i
-    for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_variant", "x100_hip_detect",
+    for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_set", "gemm_hip_i8_dev_variant", "x100_hip_detect",
                  "x100q_pack", "qgemv_hip", "x100q_check_quant_div", "moe_layer_hip", "moe_layer_hip_ws", "moe_layer_hip_noalloc",
                  "x100_pack_w_int4",
                  "x100_pack_w_int8",
@@ -188,6 +189,11 @@ def gemm_dev(M, N, K, dA, dB, dC, stream=None, variant=GEMM_AUTO):
     """C += A*B on device pointers (ints); asynchronous on stream."""
     return _check("gemm_hip_i8_dev_variant",
                   lib().gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, variant))
+
+
+def gemm_dev_set(M, N, K, dA, dB, dC, stream=None):
+    """C = A*B (overwrite form) on device pointers; asynchronous on stream."""
+    return _check("gemm_hip_i8_dev_set", lib().gemm_hip_i8_dev_set(M, N, K, dA, dB, dC, stream))
 
 
 def gemm_host(A, B, C):
