@@ -27,6 +27,13 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-c
                                     256 MiB device-to-device copy as the byte-count calibration)
        python bench.py --probe-all (the same with every other kernel family in between, 3 launches
                                     each at its benchmark shape)
+       python bench.py --ceilings  (only the measured ceilings: int8 MFMA rate and shader clock with
+                                    random and constant operands, the empty-kernel launch floor in a
+                                    graph, and the streaming-read floor at the rows' byte counts)
+
+The default run also measures those ceilings: the GEMM's roofline carries its fraction of the
+measured MFMA ceiling, and every GEMV / MoE / decode row carries floor_us (the streaming kernel
+reading the row's bytes, same graph setting) and floor_frac = floor_us / us.
 """
 import argparse
 import json
@@ -125,6 +132,100 @@ class Timer:
 
 
 # ------------------------------------------------------------------------------------------------
+# Measured ceilings (x100-gemm_amd/lib/libx100ceil.so): the int8 MFMA rate and shader clock with no
+# memory traffic, the per-launch floor in a graph, and the time a plain streaming kernel needs to
+# read N bytes (the floor of any kernel that must read them in one launch).
+# ------------------------------------------------------------------------------------------------
+class Ceilings:
+    def __init__(self, torch, dev, timer):
+        import ctypes
+        self.torch, self.dev, self.timer = torch, dev, timer
+        path = os.path.join(ROOT, "x100-gemm_amd", "lib", "libx100ceil.so")
+        if not os.path.exists(path):
+            raise SystemExit("libx100ceil.so is not built (run __graft_entry__.build())")
+        L = ctypes.CDLL(path)
+        p, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        L.x100ceil_mfma_i8.argtypes = [i, i, i, p, p, p, p]
+        L.x100ceil_stream.argtypes = [p, sz, p, i, p]
+        L.x100ceil_empty.argtypes = [i, i, p]
+        self.L = L
+        self._floor = {}
+        self._buf = None
+        self.cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def _s(self):
+        return self.torch.cuda.current_stream().cuda_stream
+
+    def mfma(self, random, iters=20000, reps=5):
+        """Back-to-back v_mfma_i32_32x32x32_i8 on every SIMD (one 8-wave block per CU): TOPS and
+        the shader clock (s_memtime cycles per 100 MHz s_memrealtime tick)."""
+        t = self.torch
+        blocks = self.cus
+        ops = t.randint(-2 ** 31, 2 ** 31 - 1, (512 * 8 * 4,), dtype=t.int32, device=self.dev)
+        out = t.empty(blocks * 512, dtype=t.int32, device=self.dev)
+        clk = t.zeros(blocks * 2, dtype=t.int64, device=self.dev)
+
+        def f():
+            rc = self.L.x100ceil_mfma_i8(blocks, iters, 1 if random else 0, ops.data_ptr(), out.data_ptr(),
+                                         clk.data_ptr(), self._s())
+            if rc:
+                raise RuntimeError("x100ceil_mfma_i8 rc=%d" % rc)
+
+        us = self.timer.run(f, reps, 1)
+        c = clk.cpu().numpy().reshape(-1, 2).astype(np.float64)
+        ghz = float(np.mean(c[:, 0] / c[:, 1])) * 0.1
+        tops = blocks * 8 * iters * 8 * 65536.0 / us / 1e6
+        return {"TOPS": tops, "clock_GHz": ghz, "us": us, "frac_of_5000": tops / PEAK_INT8_TOPS,
+                "TOPS_at_2.4GHz_equivalent": tops * 2.4 / ghz}
+
+    def launch_floor(self, blocks, n=64):
+        f = lambda: self.L.x100ceil_empty(blocks, 256, self._s())
+        return self.timer.graph([f] * n)
+
+    def stream_floor(self, nbytes):
+        """Best time (graph, back to back, over rotating slices totalling more than the 256 MB
+        Infinity Cache) of the streaming kernel reading nbytes, over 1, 2, 4 loads per lane."""
+        nbytes = max(16, int(nbytes) // 16 * 16)
+        if nbytes in self._floor:
+            return self._floor[nbytes]
+        t = self.torch
+        pitch = (nbytes + 255) // 256 * 256
+        copies = int(300e6 // nbytes) + 1
+        need = copies * pitch
+        if self._buf is None or self._buf.numel() < need:
+            self._buf = None
+            self._buf = t.randint(0, 255, (need,), dtype=t.uint8, device=self.dev)
+        out = t.empty((nbytes // 16 + 255) // 256 + 1, dtype=t.int32, device=self.dev)
+        base = self._buf.data_ptr()
+        best = None
+        for lpl in (1, 2, 4):
+            fns = [lambda c=c: self.L.x100ceil_stream(base + c * pitch, nbytes, out.data_ptr(), lpl, self._s())
+                   for c in range(copies)]
+            us = self.timer.graph(fns)
+            best = us if best is None else min(best, us)
+        self._floor[nbytes] = best
+        return best
+
+    def annotate(self, row, nbytes, us):
+        """Adds the streaming floor for the row's bytes and floor_frac = floor / measured time."""
+        fl = self.stream_floor(nbytes)
+        row["floor_us"] = fl
+        row["floor_frac"] = fl / us
+        return row
+
+    def summary(self):
+        res = {"mfma_i8_random": self.mfma(True), "mfma_i8_constant": self.mfma(False)}
+        res["launch_floor_us"] = {str(b): self.launch_floor(b) for b in (1, 256, 1024)}
+        fl = {}
+        for mb in (1.12, 2.18, 5.44, 7.11, 9.47, 16.0, 22.3, 28.0, 78.7, 136.9, 331.2):
+            nb = int(mb * 1e6)
+            us = self.stream_floor(nb)
+            fl["%.2f MB" % mb] = {"us": us, "GB/s": nb / us / 1e3, "hbm_frac": nb / us / 1e3 / PEAK_HBM_GBS}
+        res["stream_floor"] = fl
+        return res
+
+
+# ------------------------------------------------------------------------------------------------
 # CPU baseline (oracle / reference build; the checker, never the product)
 # ------------------------------------------------------------------------------------------------
 def cpu_gemm_baseline(K=4096, N=4096, target_s=10.0):
@@ -161,7 +262,7 @@ def cpu_time(fn, min_s=0.5):
 
 
 # ------------------------------------------------------------------------------------------------
-def bench_gemm(torch, timer, dev, args):
+def bench_gemm(torch, timer, dev, args, ceil=None):
     """The headline: C += A.B at 4096^3, back-to-back launches on one A/B/C set (96 MiB, which the
     256 MB Infinity Cache may hold between launches).  The same launches cycling over three
     distinct sets (288 MiB, so every launch reads A, B and C from HBM and writes C back) are
@@ -176,38 +277,61 @@ def bench_gemm(torch, timer, dev, args):
         sets.append((dA, dB, dC))
     s = torch.cuda.current_stream().cuda_stream
 
-    def run(nsets):
+    def run(nsets, fn=x100hip.gemm_dev):
         for i in range(args.warmup):
             dA, dB, dC = sets[i % nsets]
-            x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
+            fn(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record()
         for i in range(args.steps):
             dA, dB, dC = sets[i % nsets]
-            x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
+            fn(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / args.steps, time.perf_counter() - t0
 
+    # Clock pre-roll (untimed): the shader clock takes about 40 ms of sustained load to settle
+    # (series of 30 launches from a cold start measured 178, 85, 79, 77, 74, 74, then 71 us), so
+    # without it the timed steps would measure the ramp rather than the kernel.
+    t_end = time.perf_counter() + args.preroll_ms / 1e3
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            x100hip.gemm_dev(M, N, K, sets[0][0].data_ptr(), sets[0][1].data_ptr(), sets[0][2].data_ptr(), s)
+        torch.cuda.synchronize()
     ms, wall = run(1)
     msr, _ = run(3)
+    # the overwrite form C = A.B (gemm_hip_i8_dev_set: the tile kernel stores C without reading it)
+    mss, _ = run(1, x100hip.gemm_dev_set)
+    mssr, _ = run(3, x100hip.gemm_dev_set)
     ops = 2.0 * M * N * K
     tops = ops / (ms * 1e-3) / 1e12
     topsr = ops / (msr * 1e-3) / 1e12
     log("gemm 4096^3: %.2f us/launch  %.1f TOPS (wall %.3f s for %d steps); over 3 rotating A/B/C sets "
         "(288 MiB): %.2f us  %.1f TOPS" % (ms * 1e3, tops, wall, args.steps, msr * 1e3, topsr))
+    log("gemm 4096^3 overwrite form C = A.B: %.2f us  %.1f TOPS; 3 rotating sets %.2f us  %.1f TOPS" % (
+        mss * 1e3, ops / mss / 1e9, mssr * 1e3, ops / mssr / 1e9))
     traffic = read_traffic("gemm_i8_4096")
     roof = {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
             "frac": tops / PEAK_INT8_TOPS, "traffic": traffic,
             "kernel": "k_gemm_big<8, 2> (256x256 tile, 8 waves, 2 K stages per barrier)", "algorithmic_ops_per_launch": ops,
             "rotating_sets": {"sets": 3, "bytes": 3 * (M * K + K * N + 4 * M * N), "us": msr * 1e3,
-                              "TOPS": topsr, "frac": topsr / PEAK_INT8_TOPS}}
+                              "TOPS": topsr, "frac": topsr / PEAK_INT8_TOPS},
+            "overwrite_form": {"entry": "gemm_hip_i8_dev_set (C = A.B, C not read)", "us": mss * 1e3,
+                               "TOPS": ops / mss / 1e9, "frac": ops / mss / 1e9 / PEAK_INT8_TOPS,
+                               "rotating_sets_us": mssr * 1e3, "rotating_sets_TOPS": ops / mssr / 1e9}}
+    if ceil is not None:
+        mf = ceil.mfma(True)
+        roof["measured_mfma_ceiling"] = {"TOPS": mf["TOPS"], "clock_GHz": mf["clock_GHz"],
+                                         "operands": "random int8, registers only (x100ceil_mfma_i8)",
+                                         "frac": tops / mf["TOPS"]}
+        log("gemm 4096^3 against the measured int8 MFMA ceiling (%.0f TOPS at %.2f GHz, random operands): %.3f" % (
+            mf["TOPS"], mf["clock_GHz"], tops / mf["TOPS"]))
     return ms, tops, roof
 
 
-def bench_extra(torch, timer, dev, args):
+def bench_extra(torch, timer, dev, args, ceil):
     import oracle_lib as ol
     extra = {}
     s = torch.cuda.current_stream().cuda_stream
@@ -242,9 +366,9 @@ def bench_extra(torch, timer, dev, args):
     byts = M * K + K * N + 2 * M * N * 4
     Cc = np.zeros((M, N), np.int32)
     cpu_us = cpu_time(lambda: ol.oracle().gemm_ref_i8(M, N, K, A.ctypes.data, B.ctypes.data, Cc.ctypes.data))
-    extra["gemm_i8_8x4096x4096"] = {"us": us, "TOPS": 2.0 * M * N * K / us / 1e6, "GB/s": byts / us / 1e3,
-                                    "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS, "single_launch_us": lat,
-                                    "cpu_us_1core": cpu_us}
+    extra["gemm_i8_8x4096x4096"] = ceil.annotate({"us": us, "TOPS": 2.0 * M * N * K / us / 1e6, "GB/s": byts / us / 1e3,
+                                                  "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS, "single_launch_us": lat,
+                                                  "cpu_us_1core": cpu_us}, byts, us)
     log("gemm 8x4096x4096: %.2f us  %.0f GB/s (single %.2f us)" % (us, byts / us / 1e3, lat))
     del dBs
 
@@ -269,11 +393,12 @@ def bench_extra(torch, timer, dev, args):
             byts = raw.numel() + M * K * 4 + M * N * 4
             cpu_us = cpu_time(lambda: ol.qgemv(qt, W, x))
             key = "%s_gemv_%dx%d_m%d" % (name, N, K, M)
-            extra[key] = {"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
-                          "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
-                          "cpu_us_1core": cpu_us}
-            log("%s: %.2f us  %.0f GB/s  (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
-                key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
+            extra[key] = ceil.annotate({"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                                        "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
+                                        "cpu_us_1core": cpu_us}, byts, us)
+            log("%s: %.2f us  %.0f GB/s  (%.1f%% HBM, %.2f of the %.2f us streaming floor)  single %.2f us  cpu %.0f us" % (
+                key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, extra[key]["floor_frac"],
+                extra[key]["floor_us"], lat, cpu_us))
         del packs, raw
 
     # ---- int8 path: Q6_K / Q5_K / Q8_0 weights requantized to Q8_0 at load (lin_new_i8) ----------
@@ -308,11 +433,12 @@ def bench_extra(torch, timer, dev, args):
             byts = wbytes + M * K * 4 + M * N * 4
             cpu_us = cpu_time(lambda: ol.qgemv_q8w(Wq8, x), min_s=0.3)
             key = "%s_gemv_%dx%d_m%d" % (name, N, K, M)
-            extra[key] = {"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
-                          "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
-                          "cpu_us_1core": cpu_us}
-            log("%s: %.2f us  %.0f GB/s  (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
-                key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
+            extra[key] = ceil.annotate({"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                                        "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
+                                        "cpu_us_1core": cpu_us}, byts, us)
+            log("%s: %.2f us  %.0f GB/s  (%.1f%% HBM, %.2f of the %.2f us streaming floor)  single %.2f us  cpu %.0f us" % (
+                key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, extra[key]["floor_frac"],
+                extra[key]["floor_us"], lat, cpu_us))
         del packs, W, Wq8
 
     # ---- integer tile GEMV (bench/q4_gemv.c defaults: N = 4864, K = 896) ----------------------
@@ -335,10 +461,11 @@ def bench_extra(torch, timer, dev, args):
             byts = pb + M * K + 4 * M * N
             cpu_us = cpu_time(lambda: ol.gemv_int(Wt, xt), min_s=0.3)
             key = "%s_gemv_%dx%d_m%d" % ("int4" if int4 else "int8", N, K, M)
-            extra[key] = {"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
-                          "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
-                          "cpu_us_1core": cpu_us}
-            log("%s: %.2f us  %.0f GB/s  single %.2f us  cpu %.0f us" % (key, us, byts / us / 1e3, lat, cpu_us))
+            extra[key] = ceil.annotate({"us": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                                        "single_launch_us": lat, "bytes": byts, "weight_copies": copies,
+                                        "cpu_us_1core": cpu_us}, byts, us)
+            log("%s: %.2f us  %.0f GB/s  floor_frac %.2f  single %.2f us  cpu %.0f us" % (
+                key, us, byts / us / 1e3, extra[key]["floor_frac"], lat, cpu_us))
         del dws
 
     # ---- Qwen3-30B-A3B decode weight stream (bench/moe_decode.c), q4 and q8 ----------------------
@@ -400,9 +527,9 @@ def bench_extra(torch, timer, dev, args):
         byts = float(n_exp * d * 4 + U.mean() * 3 * (ff * d // 256 * 144) + M * d * 4 * 2)
         cpu_us = cpu_time(lambda: ol.moe_layer(hns[0], R, Wg, Wu, Wd, n_act), min_s=0.3)
         key = "moe_layer_qwen3_30b_a3b_m%d" % M
-        extra[key] = {"us_per_layer": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
-                      "single_launch_us": lat, "experts_union_mean": float(U.mean()),
-                      "bytes_per_layer": byts, "cpu_us_1core": cpu_us}
+        extra[key] = ceil.annotate({"us_per_layer": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                                    "single_launch_us": lat, "experts_union_mean": float(U.mean()),
+                                    "bytes_per_layer": byts, "cpu_us_1core": cpu_us}, byts, us)
         log("%s: %.2f us/layer  U=%.1f  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
             key, us, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
     # many token rows (verify / prefill): pairs grouped by expert in chunks of 32, matrix cores
@@ -430,10 +557,10 @@ def bench_extra(torch, timer, dev, args):
         byts = float(n_exp * d * 4 + U.mean() * 3 * (ff * d // 256 * 144) + M * d * 4 * 2)
         cpu_us = cpu_time(lambda: ol.moe_layer(hns[0][:8], R, Wg, Wu, Wd, n_act), min_s=0.3) * M / 8
         key = "moe_layer_qwen3_30b_a3b_m%d" % M
-        extra[key] = {"us_per_layer": us, "us_per_token": us / M, "tokens_per_s": M / us * 1e6,
-                      "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
-                      "experts_union_mean": float(U.mean()), "bytes_per_layer": byts,
-                      "cpu_us_1core": cpu_us, "cpu_note": "8-row sample scaled to M rows"}
+        extra[key] = ceil.annotate({"us_per_layer": us, "us_per_token": us / M, "tokens_per_s": M / us * 1e6,
+                                    "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                                    "experts_union_mean": float(U.mean()), "bytes_per_layer": byts,
+                                    "cpu_us_1core": cpu_us, "cpu_note": "8-row sample scaled to M rows"}, byts, us)
         log("%s: %.2f us/layer (%.3f us/token)  U=%.1f  %.0f GB/s (%.1f%% HBM)  cpu %.0f us" % (
             key, us, us / M, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, cpu_us))
     del layers, base
@@ -496,9 +623,9 @@ def bench_extra(torch, timer, dev, args):
         hh = h0.copy()
         cpu_us = cpu_time(lambda: ol.decode_layer(host_cfg, Ld, hk, hv, pos, hh), min_s=0.3)
         key = "decode_layer_qwen3_30b_a3b_pos%d" % (pos + 1)
-        extra[key] = {"us_per_layer": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
-                      "single_launch_us": lat, "bytes_per_layer": byts, "kv_positions": pos + 1,
-                      "cpu_us_1core": cpu_us}
+        extra[key] = ceil.annotate({"us_per_layer": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
+                                    "single_launch_us": lat, "bytes_per_layer": byts, "kv_positions": pos + 1,
+                                    "cpu_us_1core": cpu_us}, byts, us)
         log("%s: %.2f us/layer  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us  (x48 layers: %.2f ms/token)" % (
             key, us, byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us, 48 * us / 1e3))
     del lw, keep
@@ -588,9 +715,13 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--preroll-ms", type=float, default=150.0,
+                    help="untimed GEMM launches before the warmup, so the shader clock has settled")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--probe", action="store_true")
     ap.add_argument("--probe-all", action="store_true")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="measure only the ceilings (MFMA rate and clock, launch and streaming floors)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this backend has no multi-GPU path "
@@ -608,8 +739,16 @@ def main():
     if args.probe or args.probe_all:
         probe(torch, dev, args)
         return
-    ms, tops, roof = bench_gemm(torch, timer, dev, args)
-    extra = {} if args.no_extra else bench_extra(torch, timer, dev, args)
+    ceil = Ceilings(torch, dev, timer)
+    if args.ceilings:
+        print(json.dumps({"ceilings": ceil.summary(), "device": {"name": caps.name.decode(),
+                                                                 "arch": caps.arch.decode(), "cus": caps.cu_count}}),
+              flush=True)
+        return
+    ms, tops, roof = bench_gemm(torch, timer, dev, args, ceil)
+    extra = {} if args.no_extra else bench_extra(torch, timer, dev, args, ceil)
+    if not args.no_extra:
+        extra["ceilings"] = ceil.summary()
     cpu = None if args.no_cpu else cpu_gemm_baseline()
     line = {
         "metric": METRIC, "value": tops, "unit": "TOPS", "n_gpus": 1, "steps": args.steps,

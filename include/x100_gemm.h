@@ -28,7 +28,9 @@ extern "C" {
 /* Replaces gemm_ime_i8 (reference include/x100_gemm.h:60-61, src/gemm_ime_i8.c:60-89).  Host
  * pointers; copies A, B, C to the GPU, computes C += A*B there, copies C back and returns when C
  * is valid.  Same signature and void return as the reference; on failure it prints the reason
- * to stderr and aborts (there is no CPU fallback). */
+ * to stderr and aborts (there is no CPU fallback).  The device buffers are allocated on the
+ * first call, grow with the largest shape seen and are kept until the process ends; calls on one
+ * device run one at a time (on a stream of the library's own, synchronised before returning). */
 void gemm_ime_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C);
 
 /* Same contract as gemm_ime_i8 but returns an error code instead of aborting. */
@@ -42,15 +44,18 @@ int gemm_hip_i8_dev(int M, int N, int K, const int8_t *dA, const int8_t *dB, int
 
 /* The overwrite form C = A*B of gemm_ime2_i8_st / gemm_ime2_i8_mt (reference
  * src/gemm_ime2_i8.c:102-147, which store each tile without reading C).  Device pointers,
- * asynchronous on `stream`: C is cleared by a kernel (no hipMemsetAsync, so the call can be
- * captured in a graph), then accumulated as gemm_hip_i8_dev does; K = 0 leaves C = 0.  The
- * reference's pre-packed A/B layouts are not needed: A and B are row-major as above. */
+ * asynchronous on `stream`.  The MFMA tile kernels and the generic kernel write C without reading
+ * it; the split-K skinny kernels (M <= 16) add partial sums atomically, so for them C is first
+ * cleared by a kernel (no hipMemsetAsync, so the call can be captured in a graph).  K = 0 leaves
+ * C = 0.  The reference's pre-packed A/B layouts are not needed: A and B are row-major as above. */
 int gemm_hip_i8_dev_set(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
                         void *stream);
 
 /* Same as gemm_hip_i8_dev with an explicit kernel choice (0 auto, 1 256x256 MFMA tile,
  * 2 128x128 MFMA tile, 3 skinny M<=16 split-K, 4 generic, 5 256x256 tile with 4 waves,
- * 6 64x64 MFMA tile, 7 32x32 MFMA tile).  For tests and measurement. */
+ * 6 64x64 MFMA tile, 7 32x32 MFMA tile); variant | X100_GEMM_SET selects the overwrite form
+ * C = A*B of gemm_hip_i8_dev_set.  For tests and measurement. */
+#define X100_GEMM_SET   16
 int gemm_hip_i8_dev_variant(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
                             void *stream, int variant);
 

@@ -56,6 +56,36 @@ def test_gemm_overwrite_form(dev, M, N, K):
     assert np.array_equal(dC.cpu().numpy(), oracle_gemm(A, B, np.zeros((M, N), np.int32)))
 
 
+# (variant, M, N, K): every kernel's overwrite form.  The 256x256 kernel with superstages (K / 64 a
+# multiple of 8) and without (K = 576), 8 and 4 waves; the register-staged tiles with and without
+# edges; the generic kernel; the skinny split-K kernels (cleared C + atomics).
+SET_CASES = [(x100hip.GEMM_TILE256, 4096, 4096, 4096), (x100hip.GEMM_TILE256, 512, 768, 576),
+             (x100hip.GEMM_TILE256_W4, 1024, 512, 1024), (x100hip.GEMM_TILE256_W4, 256, 512, 576),
+             (x100hip.GEMM_TILE128, 384, 256, 320), (x100hip.GEMM_TILE128, 130, 144, 96),
+             (x100hip.GEMM_TILE64, 256, 192, 128), (x100hip.GEMM_TILE64, 65, 80, 48),
+             (x100hip.GEMM_TILE32, 96, 64, 64), (x100hip.GEMM_TILE32, 33, 48, 80),
+             (x100hip.GEMM_GENERIC, 70, 50, 33), (x100hip.GEMM_SKINNY, 8, 4096, 4096),
+             (x100hip.GEMM_SKINNY, 5, 272, 96)]
+
+
+@pytest.mark.parametrize("variant,M,N,K", SET_CASES)
+def test_gemm_overwrite_form_variants(dev, variant, M, N, K):
+    # C = A*B with C holding garbage before; a second call on the result must not accumulate.
+    import torch
+    A, B = synth.gemm_inputs(M, N, K, seed=4040 + M + N + K)
+    garbage = synth.rand_int8(6, (M, N)).astype(np.int32) * 54321
+    dA = torch.from_numpy(A).to(dev)
+    dB = torch.from_numpy(B).to(dev)
+    dC = torch.from_numpy(garbage.copy()).to(dev)
+    ref = oracle_gemm(A, B, np.zeros((M, N), np.int32))
+    x100hip.gemm_dev_set(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), _stream(), variant)
+    torch.cuda.synchronize()
+    assert np.array_equal(dC.cpu().numpy(), ref)
+    x100hip.gemm_dev_set(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), _stream(), variant)
+    torch.cuda.synchronize()
+    assert np.array_equal(dC.cpu().numpy(), ref)
+
+
 def test_gemm_overwrite_form_k0_and_unaligned_c(dev):
     # K = 0 gives C = 0 (A and B may be null); a C 4 bytes past a 16-byte boundary takes the
     # clear's scalar head; the words around C keep their values.
@@ -189,6 +219,40 @@ def test_gemm_host_dropin(dev):
     C2 = np.zeros((96, 80), np.int32)
     x100hip.lib().gemm_ime_i8(96, 80, 64, A.ctypes.data, B.ctypes.data, C2.ctypes.data)
     assert np.array_equal(C2, oracle_gemm(A, B, np.zeros((96, 80), np.int32)))
+
+
+def test_gemm_host_dropin_reuses_buffers(dev):
+    # The host path keeps its device buffers between calls and grows them: a small call, a larger
+    # one (the buffers grow), a smaller one again (the larger buffers hold stale data beyond it),
+    # and two host threads at once (calls on one device run one at a time).
+    import threading
+    for i, (M, N, K) in enumerate([(40, 48, 32), (512, 384, 256), (24, 16, 48), (256, 272, 1040)]):
+        A, B = synth.gemm_inputs(M, N, K, seed=60 + i)
+        C = synth.rand_int8(61 + i, (M, N)).astype(np.int32)
+        ref = oracle_gemm(A, B, C)
+        x100hip.gemm_host(A, B, C)
+        assert np.array_equal(C, ref), (M, N, K)
+    jobs = []
+    for i in range(4):
+        A, B = synth.gemm_inputs(128 + 64 * i, 96, 64 * (i + 1), seed=70 + i)
+        C = np.zeros((A.shape[0], 96), np.int32)
+        jobs.append((A, B, C, oracle_gemm(A, B, C)))
+    errs = []
+
+    def run(job):
+        try:
+            x100hip.gemm_host(job[0], job[1], job[2])
+        except Exception as e:   # collected and re-raised in the main thread
+            errs.append(e)
+
+    ts = [threading.Thread(target=run, args=(j,)) for j in jobs]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errs
+    for A, B, C, ref in jobs:
+        assert np.array_equal(C, ref)
 
 
 @pytest.mark.parametrize("variant,M,N", [(x100hip.GEMM_AUTO, 4, 256), (x100hip.GEMM_AUTO, 32, 256),

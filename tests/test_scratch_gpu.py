@@ -118,6 +118,46 @@ def test_moe_two_streams_concurrent(dev):
             assert same_bits(bufs[k][3][it].cpu().numpy(), refs[k]), "convenience stream %d call %d" % (k, it)
 
 
+def test_moe_per_thread_stream_two_threads(dev):
+    """hipStreamPerThread is one handle for a different stream in each host thread: two threads
+    calling the convenience entry point with it at once (4 rows and 1 row) each get a workspace of
+    their own, and every output equals the oracle's."""
+    import threading
+    import torch
+    HIP_STREAM_PER_THREAD = 2   # (hipStream_t)2
+    L = layer(NE, D, FF, 500, dev)
+    dR, dg, du, dd = dev_ptrs(L)
+    cases = [(4, synth.normal_f32(970, (4, D))), (1, synth.normal_f32(971, (1, D)))]
+    refs = [oracle_out(L, hn)[0] for _, hn in cases]
+    reps = 6
+    bufs = [(torch.from_numpy(hn).to(dev), [torch.full((M, D), float("nan"), device=dev) for _ in range(reps)])
+            for M, hn in cases]
+    torch.cuda.synchronize()
+    errs = []
+
+    def run(k):
+        try:
+            M = cases[k][0]
+            dh, outs = bufs[k]
+            for it in range(reps):
+                x100hip.moe_layer(M, D, FF, NE, NA, dh.data_ptr(), dR, dg, du, dd, outs[it].data_ptr(), False, None,
+                                  None, HIP_STREAM_PER_THREAD)
+            torch.cuda.synchronize()
+        except Exception as e:   # collected and re-raised in the main thread
+            errs.append(e)
+
+    ts = [threading.Thread(target=run, args=(k,)) for k in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errs, errs
+    for k in range(2):
+        for it in range(reps):
+            assert same_bits(bufs[k][1][it].cpu().numpy(), refs[k]), "thread %d call %d" % (k, it)
+
+
 def test_moe_graph_captured_at_a_larger_shape(dev):
     """A graph holding moe_layer_hip_ws at 16 rows, after eager calls at 2 rows only: three
     replays, with eager layers and synchronisations between them, each bit-identical to the

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <thread>
 #include <vector>
 #include <stdio.h>
 #include <stdlib.h>
@@ -57,15 +58,19 @@ int check_device()
 
 // Workspaces of the convenience entry points (moe_layer_hip, x100_attn_decode_hip,
 // x100_decode_layer_hip), one per (device, stream), so that calls on different streams never
-// share scratch.  A workspace only grows: the larger one is allocated with hipMalloc and the old
-// one is kept until the process ends (never freed, no synchronisation), because work already
-// queued on the stream, or a graph captured earlier at a smaller shape, may still use it.  The
-// kernels write every workspace byte they read within the same call, so the contents never
-// need clearing.  Growth is impossible while the stream is being captured: such a call returns
-// X100_EINVAL (callers that capture graphs use the _ws entry points with their own scratch).
+// share scratch.  hipStreamPerThread is one handle for a distinct stream in every host thread, so
+// for it the calling thread is part of the key as well.  A workspace only grows: the larger one
+// is allocated with hipMalloc and the old one is kept until the process ends (never freed, no
+// synchronisation), because work already queued on the stream, or a graph captured earlier at a
+// smaller shape, may still use it.  Workspaces are not released when their stream is destroyed
+// either (the library cannot see that); each is at most a few MB at decode shapes.  The kernels
+// write every workspace byte they read within the same call, so the contents never need clearing.
+// Growth is impossible while the stream is being captured: such a call returns X100_EINVAL
+// (callers that capture graphs use the _ws entry points with their own scratch).
 struct StreamWs {
     int dev;
     hipStream_t stream;
+    std::thread::id thread;   // the calling thread for hipStreamPerThread, else a default id
     void *ptr;
     size_t bytes;
 };
@@ -77,10 +82,11 @@ int stream_workspace(hipStream_t stream, size_t need, void **out)
 {
     int dev = 0;
     X100_TRY(hipGetDevice(&dev));
+    const std::thread::id tid = stream == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
     std::lock_guard<std::mutex> lk(g_ws_mu);
     StreamWs *w = nullptr;
     for (StreamWs &e : g_ws)
-        if (e.dev == dev && e.stream == stream) w = &e;
+        if (e.dev == dev && e.stream == stream && e.thread == tid) w = &e;
     if (w && w->bytes >= need) {
         *out = w->ptr;
         return X100_OK;
@@ -97,7 +103,7 @@ int stream_workspace(hipStream_t stream, size_t need, void **out)
         w->ptr = p;
         w->bytes = bytes;
     } else {
-        g_ws.push_back(StreamWs{dev, stream, p, bytes});
+        g_ws.push_back(StreamWs{dev, stream, tid, p, bytes});
     }
     *out = p;
     return X100_OK;
@@ -145,6 +151,37 @@ bool moe_ptrs_ok(const float *hn, const float *R, const void *Wg, const void *Wu
     return !(((uintptr_t)hn | (uintptr_t)R | (uintptr_t)Wg | (uintptr_t)Wu | (uintptr_t)Wd) & 15);
 }
 
+// Device buffers and stream of the host-pointer GEMM (gemm_hip_i8 / gemm_ime_i8), per device.  The
+// buffers only grow (hipMalloc of the larger size; the old one is freed, which is safe because every
+// call has synchronised its stream before returning) and are kept for the life of the process, so
+// a caller timing gemm_ime_i8 in a loop pays for the PCIe copies and the kernel only.
+struct HostGemmState {
+    std::mutex mu;
+    hipStream_t stream = nullptr;
+    void *ab = nullptr, *c = nullptr;
+    size_t ab_bytes = 0, c_bytes = 0;
+};
+HostGemmState g_host_gemm[64];
+
+int host_gemm_grow(HostGemmState &h, size_t ab, size_t c)
+{
+    if (h.ab_bytes < ab) {
+        if (h.ab) X100_TRY(hipFree(h.ab));
+        h.ab = nullptr;
+        h.ab_bytes = 0;
+        X100_TRY(hipMalloc(&h.ab, ab));
+        h.ab_bytes = ab;
+    }
+    if (h.c_bytes < c) {
+        if (h.c) X100_TRY(hipFree(h.c));
+        h.c = nullptr;
+        h.c_bytes = 0;
+        X100_TRY(hipMalloc(&h.c, c));
+        h.c_bytes = c;
+    }
+    return X100_OK;
+}
+
 int moe_run(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R, const void *Wg,
             const void *Wu, const void *Wd, float *out, int residual, int *sel, float *sw, void *ws, void *stream)
 {
@@ -165,15 +202,19 @@ extern "C" {
 int gemm_hip_i8_dev_variant(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
                             void *stream, int variant)
 {
+    const bool set = (variant & X100_GEMM_SET) != 0;
+    variant &= ~X100_GEMM_SET;
     if (M < 0 || N < 0 || K < 0 || variant < 0 || variant > 7) return X100_EINVAL;
-    if (M == 0 || N == 0 || K == 0) return X100_OK;  // C += (empty product) leaves C unchanged
-    if (!dA || !dB || !dC) return X100_EINVAL;
+    if (M == 0 || N == 0) return X100_OK;   // no output elements
+    if (!dC || (K > 0 && (!dA || !dB))) return X100_EINVAL;
+    if (K == 0 && !set) return X100_OK;     // C += (empty product) leaves C unchanged
     // Any K: from K = 2^17 a dot product can leave the int32 range, and then C wraps modulo 2^32
     // exactly as the reference's int32 accumulation does (integer addition modulo 2^32 is
     // associative, so the kernels' summation order does not matter).
     int rc = check_device();
     if (rc) return rc;
-    hipError_t e = x100_gemm_i8_launch(M, N, K, dA, dB, dC, (hipStream_t)stream, variant);
+    hipError_t e = K == 0 ? x100_zero_i32_launch(dC, (size_t)M * N, (hipStream_t)stream)   // C = 0
+                          : x100_gemm_i8_launch(M, N, K, dA, dB, dC, (hipStream_t)stream, variant, !set);
     if (e == hipErrorInvalidValue) return X100_EINVAL;
     if (e != hipSuccess) return hip_fail(e);
     return X100_OK;
@@ -182,20 +223,12 @@ int gemm_hip_i8_dev_variant(int M, int N, int K, const int8_t *dA, const int8_t 
 int gemm_hip_i8_dev(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC,
                     void *stream)
 {
-    return gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, 0);
+    return gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, X100_GEMM_AUTO);
 }
 
 int gemm_hip_i8_dev_set(int M, int N, int K, const int8_t *dA, const int8_t *dB, int32_t *dC, void *stream)
 {
-    if (M < 0 || N < 0 || K < 0) return X100_EINVAL;
-    if (M == 0 || N == 0) return X100_OK;   // no output elements
-    if (!dC || (K > 0 && (!dA || !dB))) return X100_EINVAL;
-    int rc = check_device();
-    if (rc) return rc;
-    hipError_t e = x100_zero_i32_launch(dC, (size_t)M * N, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(e);
-    if (K == 0) return X100_OK;   // C = (empty product) = 0
-    return gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, 0);
+    return gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, X100_GEMM_AUTO | X100_GEMM_SET);
 }
 
 int gemm_hip_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C)
@@ -205,27 +238,28 @@ int gemm_hip_i8(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *
     if (!A || !B || !C) return X100_EINVAL;
     int rc = check_device();
     if (rc) return rc;
+    int dev = 0;
+    X100_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return X100_ENODEV;
     const size_t sa = (size_t)M * K, sb = (size_t)K * N, sc = (size_t)M * N * sizeof(int32_t);
-    int8_t *dA = nullptr, *dB = nullptr;
-    int32_t *dC = nullptr;
-    hipError_t e = hipMalloc((void **)&dA, sa);
-    if (e == hipSuccess) e = hipMalloc((void **)&dB, sb);
-    if (e == hipSuccess) e = hipMalloc((void **)&dC, sc);
-    if (e == hipSuccess) e = hipMemcpy(dA, A, sa, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemcpy(dB, B, sb, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemcpy(dC, C, sc, hipMemcpyHostToDevice);
-    if (e == hipSuccess) {
-        rc = gemm_hip_i8_dev(M, N, K, dA, dB, dC, nullptr);
-        if (rc == X100_OK) {
-            e = hipMemcpy(C, dC, sc, hipMemcpyDeviceToHost);
-            if (e == hipSuccess) e = hipDeviceSynchronize();
-        }
+    // One call at a time per device: the staging buffers and the stream are shared.
+    HostGemmState &h = g_host_gemm[dev];
+    std::lock_guard<std::mutex> lk(h.mu);
+    if (!h.stream) X100_TRY(hipStreamCreateWithFlags(&h.stream, hipStreamNonBlocking));
+    rc = host_gemm_grow(h, sa + sb, sc);
+    if (rc) return rc;
+    int8_t *dA = (int8_t *)h.ab, *dB = dA + sa;
+    int32_t *dC = (int32_t *)h.c;
+    X100_TRY(hipMemcpyAsync(dA, A, sa, hipMemcpyHostToDevice, h.stream));
+    X100_TRY(hipMemcpyAsync(dB, B, sb, hipMemcpyHostToDevice, h.stream));
+    X100_TRY(hipMemcpyAsync(dC, C, sc, hipMemcpyHostToDevice, h.stream));
+    rc = gemm_hip_i8_dev(M, N, K, dA, dB, dC, h.stream);
+    if (rc != X100_OK) {
+        (void)hipStreamSynchronize(h.stream);
+        return rc;
     }
-    if (dA) (void)hipFree(dA);
-    if (dB) (void)hipFree(dB);
-    if (dC) (void)hipFree(dC);
-    if (rc != X100_OK) return rc;
-    if (e != hipSuccess) return hip_fail(e);
+    X100_TRY(hipMemcpyAsync(C, dC, sc, hipMemcpyDeviceToHost, h.stream));
+    X100_TRY(hipStreamSynchronize(h.stream));
     return X100_OK;
 }
 

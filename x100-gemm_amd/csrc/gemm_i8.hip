@@ -44,7 +44,7 @@ X100_DEV void tile_coords(int bid, int nblk, int tiles_m, int tiles_n, int &tm, 
 // so that 8 consecutive lanes reading one chunk column hit 8 distinct 16-byte bank groups.
 X100_DEV int a_lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 3)) << 4); }
 
-template <int FM, int FN, int WM, int WN, bool EDGE>
+template <int FM, int FN, int WM, int WN, bool EDGE, bool ACC>
 __global__ __launch_bounds__(WM *WN * 64) void k_gemm_mfma(int M, int N, int K,
                                                            const int8_t *__restrict__ A,
                                                            const int8_t *__restrict__ B,
@@ -71,8 +71,8 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm_mfma(int M, int N, int K,
     // EDGE = false is only launched when M % BM == 0, N % BN == 0 and K % BK == 0.
     const bool full_mn = !EDGE || ((m0 + BM <= M) && (n0 + BN <= N));
 
-    // Accumulators start from C (C += A.B).  32x32 MFMA output layout: lane l, register r holds
-    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    // Accumulators start from C (ACC: C += A.B) or from zero (C = A.B, C never read).  32x32 MFMA
+    // output layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
     v16i acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm_mfma(int M, int N, int K,
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int gm = m0 + wm * FM * 32 + 32 * i + 8 * (r >> 2) + 4 * lgrp + (r & 3);
-                acc[i][j][r] = (full_mn || (gm < M && gn < N)) ? C[(size_t)gm * N + gn] : 0;
+                acc[i][j][r] = (ACC && (full_mn || (gm < M && gn < N))) ? C[(size_t)gm * N + gn] : 0;
             }
         }
 
@@ -257,12 +257,14 @@ X100_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" :
 // 16-byte global store of a finished C chunk with the system-scope policy bits (sc0 sc1): C is
 // written once and not read back by the kernel, and this form measured 69.5 -> 68.5 us at
 // 4096^3 (a plain store, the same bits on a buffer store and nt all measured slower).  The
-// trailing s_nop is the one wait state a VALU write to the store's data registers needs after a
-// store of more than 8 bytes; the compiler does not add it after inline asm.  The compiler does
-// not count this store in vmcnt either, so no vector-memory load may follow it in the kernel.
+// trailing s_nop 1 gives the two wait states that gfx950 requires between a store of more than
+// 8 bytes and a VALU write to its data registers (the compiler's own hazard recognizer emits
+// s_nop 1 for this pattern on gfx950); the compiler does not add them after inline asm.  The
+// compiler does not count this store in vmcnt either, so no vector-memory load may follow it in
+// the kernel.
 X100_DEV void store_c16(int32_t *dst, v4i v)
 {
-    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 0" ::"v"(dst), "v"(v) : "memory");
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" ::"v"(dst), "v"(v) : "memory");
 }
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (indices usable as constants).
@@ -275,7 +277,7 @@ template <int I, int N, class F> X100_DEV void static_for_impl(F &&f)
 }
 template <int N, class F> X100_DEV void static_for(F &&f) { static_for_impl<0, N>(f); }
 
-template <int NW, int SUPER>
+template <int NW, int SUPER, bool ACC>
 __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const int8_t *__restrict__ A,
                                                      const int8_t *__restrict__ B,
                                                      int32_t *__restrict__ C, int tiles_m, int tiles_n)
@@ -462,8 +464,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     // one MFMA group ahead of their use.
     // The K loop runs in NPART segments; C part p is added at the end of segment p, when part
     // p+1 is prefetched (part 0 right after the prologue's DMAs).
-    constexpr int DPS = 2 * OPS;   // DMA ops per wave per stage
-    constexpr int CQ = 4;          // C DMA ops per wave per part
+    constexpr int DPS = 2 * OPS;      // DMA ops per wave per stage
+    constexpr int CQ = ACC ? 4 : 0;   // C DMA ops per wave per part (none in the overwrite form)
     // Vector-memory operations of this wave issued after stage s+1's DMAs when iteration s waits
     // for them: stages s+2 and s+3 (always issued: the prologue issues 0..3, step t issues t+4),
     // C part 0 (issued after the prologue's 4 stages, so after stage s+1 when s+1 <= 3) and every
@@ -581,7 +583,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         issue(2);
         issue(3);
     }
-    load_c(0);
+    if constexpr (ACC) load_c(0);
     if constexpr (SUPER == 2) {
         wait_vmcnt_le(2 * DPS + CQ);   // stages 0 and 1 complete
         lds_barrier();
@@ -591,12 +593,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
             const int ub = p * nsup / NPART, ue = (p + 1) * nsup / NPART;
             if constexpr (p + 1 < NPART) {
                 for (int u = ub; u < ue; u++) superstep(u);
-                add_c(pc, 2 * DPS * (ue - ub));
-                load_c(p + 1);
+                if constexpr (ACC) {
+                    add_c(pc, 2 * DPS * (ue - ub));
+                    load_c(p + 1);
+                }
             } else {
                 for (int u = ub; u < ue - 1; u++) superstep(u);
                 last_super();
-                add_c(pc, 2 * DPS * (ue - 1 - ub));
+                if constexpr (ACC) add_c(pc, 2 * DPS * (ue - 1 - ub));
             }
         });
     } else {
@@ -608,12 +612,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
         const int kb = p * nk / NPART, ke = (p + 1) * nk / NPART;
         if constexpr (p + 1 < NPART) {
             for (int kt = kb; kt < ke; kt++) step(kt);
-            add_c(pc, DPS * (ke - kb));
-            load_c(p + 1);
+            if constexpr (ACC) {
+                add_c(pc, DPS * (ke - kb));
+                load_c(p + 1);
+            }
         } else {
             for (int kt = kb; kt < ke - 1; kt++) step(kt);
             last_step();
-            add_c(pc, DPS * (ke - 1 - kb));
+            if constexpr (ACC) add_c(pc, DPS * (ke - 1 - kb));
         }
     });
     }
@@ -829,6 +835,8 @@ __global__ __launch_bounds__(256) void k_gemm_skinny_mfma(int M, int N, int K, c
 }
 
 // Generic fallback: 64x64 tile, 256 threads (4x4 outputs each), 32-deep byte tiles in LDS.
+// ACC: C += A.B; otherwise C = A.B (C not read).
+template <bool ACC>
 __global__ __launch_bounds__(256) void k_gemm_generic(int M, int N, int K, const int8_t *__restrict__ A,
                                                       const int8_t *__restrict__ B,
                                                       int32_t *__restrict__ C)
@@ -860,23 +868,50 @@ __global__ __launch_bounds__(256) void k_gemm_generic(int M, int N, int K, const
     for (int i = 0; i < 4; i++)
         for (int j = 0; j < 4; j++) {
             int gm = m0 + ty * 4 + i, gn = n0 + tx * 4 + j;
-            if (gm < M && gn < N) C[(size_t)gm * N + gn] += acc[i][j];
+            if (gm < M && gn < N) C[(size_t)gm * N + gn] = ACC ? C[(size_t)gm * N + gn] + acc[i][j] : acc[i][j];
         }
 }
 
-template <int FM, int FN, int WM, int WN>
-hipError_t launch_mfma(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
-                       hipStream_t s)
+template <int FM, int FN, int WM, int WN, bool ACC>
+hipError_t launch_mfma_acc(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
+                           hipStream_t s)
 {
     constexpr int BM = WM * FM * 32, BN = WN * FN * 32;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const bool edge = (M % BM) || (N % BN) || (K % BK);
     if (edge)
-        hipLaunchKernelGGL((k_gemm_mfma<FM, FN, WM, WN, true>), dim3(tiles_m * tiles_n),
+        hipLaunchKernelGGL((k_gemm_mfma<FM, FN, WM, WN, true, ACC>), dim3(tiles_m * tiles_n),
                            dim3(WM * WN * 64), 0, s, M, N, K, A, B, C, tiles_m, tiles_n);
     else
-        hipLaunchKernelGGL((k_gemm_mfma<FM, FN, WM, WN, false>), dim3(tiles_m * tiles_n),
+        hipLaunchKernelGGL((k_gemm_mfma<FM, FN, WM, WN, false, ACC>), dim3(tiles_m * tiles_n),
                            dim3(WM * WN * 64), 0, s, M, N, K, A, B, C, tiles_m, tiles_n);
+    return hipGetLastError();
+}
+
+template <int FM, int FN, int WM, int WN>
+hipError_t launch_mfma(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C, hipStream_t s,
+                       bool acc)
+{
+    return acc ? launch_mfma_acc<FM, FN, WM, WN, true>(M, N, K, A, B, C, s)
+               : launch_mfma_acc<FM, FN, WM, WN, false>(M, N, K, A, B, C, s);
+}
+
+// The 256x256 tile kernel k_gemm_big<NW, SUPER, ACC> (M, N multiples of 256, K % 64 == 0,
+// K >= 512); superstages when K / 64 is a multiple of 8 (the K shapes that path is tested on).
+template <int NW>
+hipError_t launch_big(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C, hipStream_t s, bool acc)
+{
+    const int tiles_m = M / 256, tiles_n = N / 256;
+    const dim3 grid(tiles_m * tiles_n), block(NW * 64);
+    const bool super = (K / BK) % 8 == 0;
+    if (super && acc)
+        hipLaunchKernelGGL((k_gemm_big<NW, 2, true>), grid, block, 0, s, M, N, K, A, B, C, tiles_m, tiles_n);
+    else if (super)
+        hipLaunchKernelGGL((k_gemm_big<NW, 2, false>), grid, block, 0, s, M, N, K, A, B, C, tiles_m, tiles_n);
+    else if (acc)
+        hipLaunchKernelGGL((k_gemm_big<NW, 1, true>), grid, block, 0, s, M, N, K, A, B, C, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((k_gemm_big<NW, 1, false>), grid, block, 0, s, M, N, K, A, B, C, tiles_m, tiles_n);
     return hipGetLastError();
 }
 
@@ -904,9 +939,11 @@ hipError_t x100_zero_i32_launch(int32_t *C, size_t n, hipStream_t s)
     return hipGetLastError();
 }
 
-// Kernel selection.  Returns the HIP launch status.
+// Kernel selection.  acc: C += A.B; otherwise C = A.B (the tile kernels never read C; the
+// split-K skinny kernels add partial sums with atomics, so their C is cleared first).  Returns the
+// HIP launch status.
 hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
-                               hipStream_t s, int variant)
+                               hipStream_t s, int variant, bool acc)
 {
     const bool aligned = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) &&
                          (((uintptr_t)B & 15) == 0) && (((uintptr_t)C & 15) == 0);
@@ -928,34 +965,22 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
     }
     if (!aligned && variant != X100_GEMM_GENERIC) return hipErrorInvalidValue;
     switch (variant) {
-    case X100_GEMM_TILE256: {
+    case X100_GEMM_TILE256:
         // Full 256x256 tiles only; other shapes use the 128x128 tile with edge guards.
-        if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
-        const int tiles_m = M / 256, tiles_n = N / 256;
-        if ((K / BK) % 8 == 0)   // superstages (the K shapes the superstage path is tested on)
-            hipLaunchKernelGGL((k_gemm_big<8, 2>), dim3(tiles_m * tiles_n), dim3(512), 0, s, M, N, K, A, B, C,
-                               tiles_m, tiles_n);
-        else
-            hipLaunchKernelGGL((k_gemm_big<8, 1>), dim3(tiles_m * tiles_n), dim3(512), 0, s, M, N, K, A, B, C,
-                               tiles_m, tiles_n);
-        return hipGetLastError();
-    }
-    case X100_GEMM_TILE256_W4: {
-        if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
-        const int tiles_m = M / 256, tiles_n = N / 256;
-        if ((K / BK) % 8 == 0)
-            hipLaunchKernelGGL((k_gemm_big<4, 2>), dim3(tiles_m * tiles_n), dim3(256), 0, s, M, N, K, A, B, C,
-                               tiles_m, tiles_n);
-        else
-            hipLaunchKernelGGL((k_gemm_big<4, 1>), dim3(tiles_m * tiles_n), dim3(256), 0, s, M, N, K, A, B, C,
-                               tiles_m, tiles_n);
-        return hipGetLastError();
-    }
-    case X100_GEMM_TILE128: return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s);
-    case X100_GEMM_TILE64: return launch_mfma<1, 1, 2, 2>(M, N, K, A, B, C, s);
-    case X100_GEMM_TILE32: return launch_mfma<1, 1, 1, 1>(M, N, K, A, B, C, s);
+        if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s, acc);
+        return launch_big<8>(M, N, K, A, B, C, s, acc);
+    case X100_GEMM_TILE256_W4:
+        if (M % 256 || N % 256 || K % BK || K < 512) return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s, acc);
+        return launch_big<4>(M, N, K, A, B, C, s, acc);
+    case X100_GEMM_TILE128: return launch_mfma<2, 2, 2, 2>(M, N, K, A, B, C, s, acc);
+    case X100_GEMM_TILE64: return launch_mfma<1, 1, 2, 2>(M, N, K, A, B, C, s, acc);
+    case X100_GEMM_TILE32: return launch_mfma<1, 1, 1, 1>(M, N, K, A, B, C, s, acc);
     case X100_GEMM_SKINNY: {
         if (M > 16 || (size_t)K * N >= ((size_t)1 << 32)) return hipErrorInvalidValue;
+        if (!acc) {
+            const hipError_t e = x100_zero_i32_launch(C, (size_t)M * N, s);
+            if (e != hipSuccess) return e;
+        }
         dim3 grid((N + 255) / 256, (K + 255) / 256);
         if (N % 128 == 0 && K % 512 == 0) {   // whole 512 x 128 slabs: the matrix-core kernel
             hipLaunchKernelGGL(k_gemm_skinny_mfma, dim3(N / 128, K / 512), dim3(256), 0, s, M, N, K, A, B, C);
@@ -969,7 +994,10 @@ hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_
     }
     case X100_GEMM_GENERIC: {
         dim3 grid((N + 63) / 64, (M + 63) / 64);
-        hipLaunchKernelGGL(k_gemm_generic, grid, dim3(256), 0, s, M, N, K, A, B, C);
+        if (acc)
+            hipLaunchKernelGGL(k_gemm_generic<true>, grid, dim3(256), 0, s, M, N, K, A, B, C);
+        else
+            hipLaunchKernelGGL(k_gemm_generic<false>, grid, dim3(256), 0, s, M, N, K, A, B, C);
         return hipGetLastError();
     }
     }

@@ -749,7 +749,7 @@ __global__ void k_pack_q3_K(int N, int nsb, const uint8_t *__restrict__ src, uin
 // the 32-element group g from its GGUF block in fp32 with the operation order of
 // gguf_dequant_into (qwen_moe_q3k.c:1129-1158; Q6_K qwen_moe.c:168-177) and re-encodes it with
 // quantize_q8_0_native's rounding (amax floor 1e-6, d = amax/127, q = rint(w * (1/d)), d stored
-// as fp16 rounded to nearest even).
+// as fp16 by the reference's truncating f32_to_f16, qwen_moe_hp.c:71-79).
 template <int QT>
 __global__ void k_requant_q8_0(size_t ngrp, const uint8_t *__restrict__ src, uint16_t *__restrict__ dq,
                                int8_t *__restrict__ qs)

@@ -524,22 +524,30 @@ X100_DEV float q4k_term(float d, float dmin, float dx, int isc, int imn)
 
 // Blocks of kernel k that are resident on the whole device at once with lds bytes of dynamic LDS
 // (the runtime's occupancy for the kernel times the CU count): the grid of a persistent launch.
-// Cached per kernel for the last (device, lds) pair of the calling thread.
+// Cached per calling thread, keyed by (kernel address, block size, device, lds): template
+// instances with the same signature are distinct kernels with distinct occupancy.
+struct ResidentKey {
+    const void *k;
+    int nt, dev;
+    size_t lds;
+    int blocks;
+};
 template <typename Kern>
 inline int resident_blocks(Kern k, int nt, size_t lds)
 {
-    static thread_local int c_dev = -1, c_blocks = 0;
-    static thread_local size_t c_lds = 0;
+    static thread_local ResidentKey cache[16];
+    static thread_local int used = 0, next = 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    if (dev != c_dev || lds != c_lds) {
-        int occ = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, nt, lds) != hipSuccess || occ < 1) occ = 1;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-            cus = 256;
-        c_dev = dev;
-        c_lds = lds;
-        c_blocks = occ * cus;
-    }
-    return c_blocks;
+    const void *kp = (const void *)k;
+    for (int i = 0; i < used; i++)
+        if (cache[i].k == kp && cache[i].nt == nt && cache[i].dev == dev && cache[i].lds == lds)
+            return cache[i].blocks;
+    int occ = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, nt, lds) != hipSuccess || occ < 1) occ = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    ResidentKey &e = cache[used < 16 ? used++ : (next++ & 15)];
+    e = ResidentKey{kp, nt, dev, lds, occ * cus};
+    return e.blocks;
 }

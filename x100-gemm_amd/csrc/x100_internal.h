@@ -17,8 +17,9 @@ enum {
     X100_GEMM_TILE32 = 7,       // 32x32 tile, 1 wave
 };
 
+// acc: C += A.B; otherwise the overwrite form C = A.B.
 hipError_t x100_gemm_i8_launch(int M, int N, int K, const int8_t *A, const int8_t *B, int32_t *C,
-                               hipStream_t s, int variant);
+                               hipStream_t s, int variant, bool acc);
 hipError_t x100_zero_i32_launch(int32_t *C, size_t n, hipStream_t s);
 
 size_t x100_q_packed_bytes(int qtype, int N, int K);

@@ -46,6 +46,7 @@ EXPORTS = (
 
 GEMM_AUTO, GEMM_TILE256, GEMM_TILE128, GEMM_SKINNY, GEMM_GENERIC, GEMM_TILE256_W4, GEMM_TILE64, GEMM_TILE32 = \
     0, 1, 2, 3, 4, 5, 6, 7
+GEMM_SET = 16   # variant flag: the overwrite form C = A*B (X100_GEMM_SET)
 
 
 class X100Error(RuntimeError):
@@ -191,9 +192,13 @@ def gemm_dev(M, N, K, dA, dB, dC, stream=None, variant=GEMM_AUTO):
                   lib().gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, variant))
 
 
-def gemm_dev_set(M, N, K, dA, dB, dC, stream=None):
-    """C = A*B (overwrite form) on device pointers; asynchronous on stream."""
-    return _check("gemm_hip_i8_dev_set", lib().gemm_hip_i8_dev_set(M, N, K, dA, dB, dC, stream))
+def gemm_dev_set(M, N, K, dA, dB, dC, stream=None, variant=None):
+    """C = A*B (overwrite form) on device pointers; asynchronous on stream.  With a variant, that
+    kernel choice through gemm_hip_i8_dev_variant(variant | GEMM_SET)."""
+    if variant is None:
+        return _check("gemm_hip_i8_dev_set", lib().gemm_hip_i8_dev_set(M, N, K, dA, dB, dC, stream))
+    return _check("gemm_hip_i8_dev_variant",
+                  lib().gemm_hip_i8_dev_variant(M, N, K, dA, dB, dC, stream, variant | GEMM_SET))
 
 
 def gemm_host(A, B, C):
