@@ -148,6 +148,7 @@ class Ceilings:
         L.x100ceil_mfma_i8.argtypes = [i, i, i, p, p, p, p]
         L.x100ceil_stream.argtypes = [p, sz, p, i, p]
         L.x100ceil_empty.argtypes = [i, i, p]
+        L.x100ceil_handoff.argtypes = [i, i, i, i, p, p, p, p, p, p]
         self.L = L
         self._floor = {}
         self._buf = None
@@ -177,6 +178,42 @@ class Ceilings:
         tops = blocks * 8 * iters * 8 * 65536.0 / us / 1e6
         return {"TOPS": tops, "clock_GHz": ghz, "us": us, "frac_of_5000": tops / PEAK_INT8_TOPS,
                 "TOPS_at_2.4GHz_equivalent": tops * 2.4 / ghz}
+
+    def handoff(self, dirty_ints, mode=0, reps=20, spin_limit=200000):
+        """Grid-wide in-kernel handoff (x100ceil_handoff, one 256-thread block per CU): each block
+        leaves dirty_ints ints of its own in its L2, publishes a value, releases at agent scope,
+        bumps a device counter and waits (bounded) for every block.  Returns the time from the last
+        block's arrival to each block's release (mean and max over blocks, median over reps)."""
+        t = self.torch
+        G = self.cus
+        counter = t.zeros(1, dtype=t.int32, device=self.dev)
+        payload = t.zeros(G, dtype=t.int32, device=self.dev)
+        scratch = t.zeros(max(1, G * dirty_ints), dtype=t.int32, device=self.dev)
+        times = t.zeros(2 * G, dtype=t.int64, device=self.dev)
+        status = t.zeros(G, dtype=t.int32, device=self.dev)
+        mean_us, max_us = [], []
+        for _ in range(reps):
+            counter.zero_()
+            payload.zero_()
+            status.zero_()
+            rc = self.L.x100ceil_handoff(G, dirty_ints, spin_limit, mode, counter.data_ptr(),
+                                         payload.data_ptr(),
+                                         scratch.data_ptr(), times.data_ptr(), status.data_ptr(), self._s())
+            if rc:
+                raise RuntimeError("x100ceil_handoff rc=%d" % rc)
+            t.cuda.synchronize()
+            st = status.cpu().numpy()
+            if not (st == 1).all():
+                return {"error": "status counts %s" % np.bincount(st, minlength=4).tolist()}
+            tm = times.cpu().numpy().reshape(-1, 2).astype(np.float64) * 0.01   # 100 MHz ticks -> us
+            last = tm[:, 0].max()
+            mean_us.append(float(np.mean(tm[:, 1] - last)))
+            max_us.append(float(np.max(tm[:, 1] - last)))
+        return {"dirty_bytes_per_block": 4 * dirty_ints, "blocks": G,
+                "protocol": ["release fence + acquire load per poll", "release fence, relaxed polls, one acquire",
+                             "no fences: atomic data stores/loads, s_waitcnt, relaxed counter"][mode],
+                "release_after_last_arrival_us_mean": float(np.median(mean_us)),
+                "release_after_last_arrival_us_max": float(np.median(max_us))}
 
     def launch_floor(self, blocks, n=64):
         f = lambda: self.L.x100ceil_empty(blocks, 256, self._s())
@@ -216,6 +253,8 @@ class Ceilings:
     def summary(self):
         res = {"mfma_i8_random": self.mfma(True), "mfma_i8_constant": self.mfma(False)}
         res["launch_floor_us"] = {str(b): self.launch_floor(b) for b in (1, 256, 1024)}
+        res["grid_handoff"] = [self.handoff(n, mode) for mode in (0, 1) for n in (0, 4096, 65536)] + \
+            [self.handoff(0, 2)]
         fl = {}
         for mb in (1.12, 2.18, 5.44, 7.11, 9.47, 16.0, 22.3, 28.0, 78.7, 136.9, 331.2):
             nb = int(mb * 1e6)

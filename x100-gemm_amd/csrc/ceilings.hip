@@ -9,6 +9,9 @@
 //   x100ceil_stream   read-only streaming kernel, 16-byte loads, every load issued before the first
 //                     is consumed: the floor of a kernel that must read `bytes` from memory.
 //   x100ceil_empty    an empty kernel: the per-launch floor (in a graph, back to back).
+//   x100ceil_handoff  a grid-wide release / counter / acquire handoff across one block per CU,
+//                     with a bounded wait: the cost of passing results between blocks inside one
+//                     kernel, against the kernel boundary it would replace.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -87,6 +90,74 @@ __global__ __launch_bounds__(256) void k_ceil_stream(const v4i *__restrict__ w, 
 
 __global__ void k_ceil_empty() {}
 
+// Grid-wide handoff, the in-kernel alternative to a kernel boundary: every block (one per CU,
+// all resident) first writes `dirty` ints of its own (results a producer would leave in its L2),
+// then publishes one value, releases it at agent scope (the fence writes the XCD's dirty L2 lines
+// back so that other XCDs can see them), and increments a device counter; then it waits for the
+// counter to reach the grid size, acquires, and reads every block's value.  The wait is bounded:
+// after spin_limit polls a block gives up and records status 2, so every wave always exits.
+// times[b] = {s_memrealtime at arrival, at release of the wait} (100 MHz ticks); status[b]:
+// 1 = every value seen, 2 = gave up, 3 = a value was missing.
+// MODE 0: acquire load per poll.  MODE 1: relaxed polls and one acquire after the wait (one L2
+// invalidate instead of one per poll).  MODE 2: no fences: the published value is stored and read
+// with agent-scope atomic accesses (coherent across XCDs without an L2 writeback or invalidate),
+// and the block waits for its stores (s_waitcnt) before the relaxed counter increment; the
+// cheapest handoff possible for data written that way.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_ceil_handoff(int dirty, int spin_limit, unsigned *__restrict__ counter,
+                                                      int *__restrict__ payload, int *__restrict__ scratch,
+                                                      unsigned long long *__restrict__ times, int *__restrict__ status)
+{
+    const int b = blockIdx.x, G = gridDim.x, t = threadIdx.x;
+    for (int i = t; i < dirty; i += 256) scratch[(size_t)b * dirty + i] = b + i;
+    __syncthreads();
+    __shared__ int s_ok;
+    unsigned long long t0 = 0, t1 = 0;
+    if (t == 0) {
+        t0 = __builtin_amdgcn_s_memrealtime();
+        if constexpr (MODE == 2) {
+            __hip_atomic_store(&payload[b], b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            payload[b] = b + 1;
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        int it = 0;
+        if constexpr (MODE == 2) {
+            while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)G && it < spin_limit) {
+                __builtin_amdgcn_s_sleep(1);
+                it++;
+            }
+        } else if constexpr (MODE == 1) {
+            while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)G && it < spin_limit) {
+                __builtin_amdgcn_s_sleep(1);
+                it++;
+            }
+            __atomic_thread_fence(__ATOMIC_ACQUIRE);
+        } else {
+            while (__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)G && it < spin_limit) {
+                __builtin_amdgcn_s_sleep(1);
+                it++;
+            }
+        }
+        t1 = __builtin_amdgcn_s_memrealtime();
+        s_ok = it < spin_limit ? 1 : 2;
+    }
+    __syncthreads();
+    if (s_ok == 1) {
+        int miss = 0;
+        for (int i = t; i < G; i += 256) miss |= __hip_atomic_load(&payload[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != i + 1;
+        if (__syncthreads_or(miss) && t == 0) s_ok = 3;
+        __syncthreads();
+    }
+    if (t == 0) {
+        times[2 * b] = t0;
+        times[2 * b + 1] = t1;
+        status[b] = s_ok;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -121,6 +192,33 @@ __attribute__((visibility("default"))) int x100ceil_stream(const void *w, size_t
     case 4: hipLaunchKernelGGL(k_ceil_stream<4>, grid, dim3(256), 0, s, (const v4i *)w, n16, out); break;
     default: return -1;
     }
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// One block per CU (blocks <= the CU count, so all are resident); counter must be zero, payload
+// holds blocks ints, scratch blocks * dirty ints, times 2 * blocks, status blocks.
+__attribute__((visibility("default"))) int x100ceil_handoff(int blocks, int dirty, int spin_limit, int mode,
+                                                           unsigned *counter, int *payload, int *scratch,
+                                                           unsigned long long *times, int *status, void *stream)
+{
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return -3;
+    if (blocks < 1 || blocks > cus || dirty < 0 || spin_limit < 1 || !counter || !payload || !times || !status ||
+        (dirty && !scratch))
+        return -1;
+    if (mode == 2)
+        hipLaunchKernelGGL(k_ceil_handoff<2>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, dirty, spin_limit,
+                           counter, payload, scratch, times, status);
+    else if (mode == 1)
+        hipLaunchKernelGGL(k_ceil_handoff<1>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, dirty, spin_limit,
+                           counter, payload, scratch, times, status);
+    else if (mode == 0)
+        hipLaunchKernelGGL(k_ceil_handoff<0>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, dirty, spin_limit,
+                           counter, payload, scratch, times, status);
+    else
+        return -1;
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
