@@ -27,6 +27,9 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-c
                                     256 MiB device-to-device copy as the byte-count calibration)
        python bench.py --probe-all (the same with every other kernel family in between, 3 launches
                                     each at its benchmark shape)
+       python bench.py --probe --gemm-variant V [--gemm-set]
+                                   (the GEMM probe with kernel choice V of gemm_hip_i8_dev_variant,
+                                    or the overwrite form C = A.B)
        python bench.py --ceilings  (only the measured ceilings: int8 MFMA rate and shader clock with
                                     random and constant operands, the empty-kernel launch floor in a
                                     graph, and the streaming-read floor at the rows' byte counts)
@@ -735,8 +738,9 @@ def probe(torch, dev, args):
     dA, dB = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
     dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
     s = torch.cuda.current_stream().cuda_stream
+    fn = x100hip.gemm_dev_set if args.gemm_set else x100hip.gemm_dev
     for _ in range(args.steps):
-        x100hip.gemm_dev(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s)
+        fn(M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), s, args.gemm_variant)
     torch.cuda.synchronize()
     if args.probe_all:
         del dA, dB, dC
@@ -759,6 +763,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--probe", action="store_true")
     ap.add_argument("--probe-all", action="store_true")
+    ap.add_argument("--gemm-variant", type=int, default=0,
+                    help="--probe: kernel choice of gemm_hip_i8_dev_variant (0 auto, 1 256x256 8 waves, 5 4 waves)")
+    ap.add_argument("--gemm-set", action="store_true", help="--probe: the overwrite form C = A.B")
     ap.add_argument("--ceilings", action="store_true",
                     help="measure only the ceilings (MFMA rate and clock, launch and streaming floors)")
     args = ap.parse_args()

@@ -71,9 +71,11 @@ def test_kquant_6144x2048(dev, qtype, M):
     (synth.Q4_0, 33, 16384, 1), (synth.Q4_K, 1, 256, 1), (synth.Q4_K, 5, 768, 2), (synth.Q4_K, 2048, 768, 8),
     (synth.Q4_K, 100, 4096, 3), (synth.Q4_K, 9, 8192, 1), (synth.Q3_K, 1, 256, 1), (synth.Q3_K, 13, 768, 5),
     (synth.Q3_K, 700, 4096, 8), (synth.Q3_K, 3, 16384, 2),
-    # the matrix-core K-quant kernel (2 to 8 token rows): ragged row tiles, odd super-block counts
+    # the several-row kernels (2 to 8 token rows): ragged row tiles, odd super-block counts
     (synth.Q4_K, 17, 2560, 7), (synth.Q3_K, 31, 1280, 6), (synth.Q4_K, 6144, 2048, 2),
-    (synth.Q3_K, 6144, 2048, 8), (synth.Q4_K, 4100, 4096, 5), (synth.Q3_K, 16, 256, 4)])
+    (synth.Q3_K, 6144, 2048, 8), (synth.Q4_K, 4100, 4096, 5), (synth.Q3_K, 16, 256, 4),
+    # one token row with 3 or 16 super-blocks per row (the four-lane kernels, not the row-major one)
+    (synth.Q3_K, 40, 768, 1), (synth.Q4_K, 300, 4096, 1), (synth.Q3_K, 257, 4096, 1)])
 def test_qgemv_shapes(dev, qtype, N, K, M):
     check(qtype, N, K, M, seed=N + K + M, dev=dev)
 

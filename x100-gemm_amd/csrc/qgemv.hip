@@ -166,14 +166,16 @@ __global__ __launch_bounds__(NT) void k_q4_0(int M, int N, int K, const uint16_t
 //        sub-blocks 8h .. 8h+7, dequantize_q3_K_block, qwen_moe_q3k.c:557-577), d [N] (fp16).
 // Every value is the GGUF block's own (no rounding): the layout only moves bits.
 //
-// Work unit = (row, super-block) on 2 lanes: half h takes elements 128h .. 128h+127.  A block
-// covers RB rows x all nsb super-blocks, units in super-block-major order (so a wave's 32 units
-// are consecutive rows of one or two super-blocks), RB about N / 256 so that there is about one
-// block per CU (every block quantizes all of x).  The block's waves quantize the M x nsb Q8_K
-// records of x into LDS between their weight loads and the first barrier; a unit's two lanes
-// reduce its integer sums with one DPP step and store its fp32 term; after the second barrier one
-// thread per (token row, row) adds the terms over super-blocks in order, the oracle's sequence
-// (bit-identical to it).
+// Work unit = (row, super-block).  A block covers RB rows x all nsb super-blocks, RB about N / 256
+// so that there is about one block per CU (every block quantizes all of x); its waves quantize the
+// M x nsb Q8_K records of x into LDS between their weight loads and the first barrier.
+//   k_q4_K4 / k_q3_K4 (several token rows, and one row when nsb is not 1, 2, 4 or 8): four lanes per
+//     unit, units in super-block-major order (a wave's 16 units are consecutive rows of one or two
+//     super-blocks); the quad reduces its integer sums with two DPP steps and stores the fp32
+//     term; after the second barrier one thread per (token row, row) adds the terms over
+//     super-blocks in order, the oracle's sequence (bit-identical to it).
+//   k_kq_rm (one token row, nsb = 1, 2, 4 or 8): two lanes per unit (half h takes elements 128h ..
+//     128h+127), units row-major, the sum over super-blocks inside the wave.
 
 __host__ __device__ constexpr size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 __host__ __device__ constexpr size_t q4k_sec(int N) { return al256((size_t)148 * N); }
@@ -238,16 +240,24 @@ __host__ __device__ constexpr size_t kq_lds(int MR, int RB, int nsb)
     return (size_t)(MR * nsb + 1) * KREC + ((size_t)MR * RB * nsb + 1) * 4;
 }
 
-// The lane's unit: u = sb * RB + r (clamped to the last unit; `valid` false for lanes past the
-// block's units or rows past N).
+// The unit struct of the four-lanes-per-unit kernels (kq_unit4): u = sb * RB + r, clamped to the
+// last unit; `valid` false for lanes past the block's units or rows past N.
 struct KqUnit {
     int sb, r, row;
     bool valid;
 };
-X100_DEV KqUnit kq_unit(const KqArgs &a)
+
+// Several token rows, four lanes per unit: lane q = lane % 4 of unit u takes half h = q / 2 and,
+// within it, the pair p = q % 2 of sub-blocks (Q4_K: planes 2p, 2p + 1 = sub-blocks 4h + 2p and
+// 4h + 2p + 1; Q3_K: the even (p = 0) or odd (p = 1) sub-blocks 8h + 2j + p of the half).  Against
+// two lanes per unit this halves every lane's chain of record reads and dot products per token
+// row (the phase after the weights land), with 16 units per wave and up to 16 waves; the unit's
+// integer sums are completed by two DPP steps across the quad (integer addition, so the same
+// bits).  Q4_K 6144 x 2048, M = 4: 12 waves for 192 units.
+X100_DEV KqUnit kq_unit4(const KqArgs &a)
 {
     const int lane = threadIdx.x & 63, N = a.N, RB = a.RB, nu = RB * a.nsb;
-    const int u0 = 32 * wave_id() + (lane >> 1), u = min(u0, nu - 1);
+    const int u0 = 16 * wave_id() + (lane >> 2), u = min(u0, nu - 1);
     KqUnit k;
     k.sb = (int)udiv16((uint32_t)u, (uint32_t)RB, a.mrb);
     k.r = u - k.sb * RB;
@@ -257,149 +267,189 @@ X100_DEV KqUnit kq_unit(const KqArgs &a)
     return k;
 }
 
-// Q4_K: half h holds qs bytes 64h .. 64h+63, i.e. sub-blocks j = 4h .. 4h+3 (plane c: low nibbles
-// of sub-block 4h + 2(c/2), high nibbles of 4h + 2(c/2) + 1, elements 16(c%2) .. +16), and x bytes
-// 128h .. 128h+127 of each record.
+// Sequential combine over NSB super-blocks (compile-time), each thread's terms read with 16-byte
+// LDS loads; same order and operations as kq_combine.
+template <int MR, int NSB>
+X100_DEV void kq_combine_n(int M, int N, int RB, int row0, const float *tv, float *y)
+{
+    for (int t = threadIdx.x; t < MR * RB; t += blockDim.x) {
+        const int m = t / RB, r = t - m * RB;
+        if (m < M && row0 + r < N) {
+            const float4 *tp = (const float4 *)(tv + (size_t)(m * RB + r) * NSB);
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NSB / 4; c++) {
+                const float4 v = tp[c];
+                acc = acc + v.x;
+                acc = acc + v.y;
+                acc = acc + v.z;
+                acc = acc + v.w;
+            }
+            y[(size_t)m * N + row0 + r] = acc;
+        }
+    }
+}
 template <int MR>
-__global__ __launch_bounds__(512) void k_q4_K(const KqArgs a)
+X100_DEV void kq_combine_any(int M, int N, int nsb, int RB, int row0, const float *tv, float *y)
+{
+    if (nsb == 8)
+        kq_combine_n<MR, 8>(M, N, RB, row0, tv, y);
+    else if (nsb == 4)
+        kq_combine_n<MR, 4>(M, N, RB, row0, tv, y);
+    else
+        kq_combine<MR>(M, N, nsb, RB, row0, tv, y);
+}
+
+template <int MR>
+__global__ __launch_bounds__(1024) void k_q4_K4(const KqArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int M = a.M, N = a.N, K = a.K, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
+    const int M = a.M, N = a.N, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
     const uint8_t *__restrict__ W = a.W;
     const float *__restrict__ x = a.x;
     float *__restrict__ y = a.y;
-    const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1;
+    const int lane = threadIdx.x & 63, w = wave_id(), q = lane & 3, h = q >> 1, p = q & 1;
     uint8_t *recs = smem;
     float *tv = (float *)(smem + (size_t)(MR * nsb + 1) * KREC);
-    const KqUnit ku = kq_unit(a);
+    const KqUnit ku = kq_unit4(a);
 
-    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
-    const int qw = w;              // quantizer index of the wave
-    const bool wq = 4 * qw < nq;   // the wave has records to quantize (wave-uniform)
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * a.K) * 4u);
+    const bool wq = 4 * w < nq;   // the wave has records to quantize (wave-uniform)
     Q8kFirst xf;
-    if (wq) q8k_first(xr, a, nq, nw, xf, qw);
-    // every wave's x loads before any wave's weight loads (s_barrier, no wait), as in k_q4_0
+    if (wq) q8k_first(xr, a, nq, nw, xf, w);
+    // every wave's x loads before any wave's weight loads (s_barrier, no wait)
     __builtin_amdgcn_s_barrier();
 
     const uint8_t *sec = W + (size_t)ku.sb * q4k_sec(N);
-    v4i qv[4];
+    v4i qv[2];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-        qv[c] = __builtin_nontemporal_load((const v4i *)(sec + (size_t)c * 32 * N + (size_t)ku.row * 32 + 16 * h));
+    for (int c = 0; c < 2; c++)
+        qv[c] = __builtin_nontemporal_load(
+            (const v4i *)(sec + (size_t)(2 * p + c) * 32 * N + (size_t)ku.row * 32 + 16 * h));
     const uint2 smv = *(const uint2 *)(sec + (size_t)128 * N + (size_t)ku.row * 16 + 8 * h);
     const uint32_t ddv = *(const uint32_t *)(sec + (size_t)144 * N + (size_t)ku.row * 4);
 
     __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the quantizer
-    if (wq) q8k_rest(xr, a, nq, nw, xf, recs, qw);
+    if (wq) q8k_rest(xr, a, nq, nw, xf, recs, w);
     __syncthreads();
 
-    if (32 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
-        Q4kHalf u;
+    if (16 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
+        // sub-blocks j0 = 4h + 2p (low nibbles) and j0 + 1 (high nibbles)
+        const int sc0 = (int)((smv.x >> (16 * p)) & 0xff), sc1 = (int)((smv.x >> (16 * p + 8)) & 0xff);
+        const int mn0 = (int)((smv.y >> (16 * p)) & 0xff), mn1 = (int)((smv.y >> (16 * p + 8)) & 0xff);
+        int lo[2][4], hi[2][4];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            u.sc[jj] = (int)((smv.x >> (8 * jj)) & 0xff);
-            u.mn[jj] = (int)((smv.y >> (8 * jj)) & 0xff);
-        }
-        q4k_unpack(qv, u);
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                lo[c][t] = qv[c][t] & 0x0F0F0F0F;
+                hi[c][t] = (qv[c][t] >> 4) & 0x0F0F0F0F;
+            }
         const float d = h2f((uint16_t)(ddv & 0xffff)), dmin = h2f((uint16_t)(ddv >> 16));
         const int spare = MR * RB * nsb;
 #pragma unroll
         for (int m = 0; m < MR; m++) {
             // Branch-free: rows m >= M compute on unused LDS and are never combined.
             const uint8_t *rec = recs + (size_t)(m * nsb + ku.sb) * KREC;
-            int isc, imn;
-            q4k_half_sums(u, rec, h, isc, imn);
+            const v4i *xq = (const v4i *)(rec + 128 * h + 64 * p);
+            const v4i x0 = xq[0], x1 = xq[1], x2 = xq[2], x3 = xq[3];
+            const int2 s32 = *(const int2 *)(rec + KR_S32 + 16 * h + 8 * p);
+            int da = 0, db = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                da = dot4(lo[0][t], x0[t], da);
+                da = dot4(lo[1][t], x1[t], da);
+                db = dot4(hi[0][t], x2[t], db);
+                db = dot4(hi[1][t], x3[t], db);
+            }
+            int isc = sc0 * da + sc1 * db;
+            int imn = mn0 * s32.x + mn1 * s32.y;
+            isc += dpp_i<0xB1>(0, isc);   // + the pair's other lane (q ^ 1)
+            imn += dpp_i<0xB1>(0, imn);
+            isc += dpp_i<0x4E>(0, isc);   // + the other half (q ^ 2)
+            imn += dpp_i<0x4E>(0, imn);
             tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = q4k_term(d, dmin, *(const float *)(rec + KR_D), isc, imn);
         }
     }
     __syncthreads();
-    kq_combine<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
+    kq_combine_any<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
 }
 
-// Q3_K: half h holds qs bytes 32h .. 32h+31 (dword t: elements 128h + 32j + 4t .. +3 at shift 2j,
-// j = 0..3) and their high bits, i.e. sub-blocks 8h + 2j + t/4; the 3-bit value q + 4 = the 2
-// low bits | high bit << 2 (dequantize_q3_K_block's q - (hbit ? 0 : 4), with the 4 taken out
-// through the sums s16).
 template <int MR>
-__global__ __launch_bounds__(512) void k_q3_K(const KqArgs a)
+__global__ __launch_bounds__(1024) void k_q3_K4(const KqArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int M = a.M, N = a.N, K = a.K, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
+    const int M = a.M, N = a.N, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
     const uint8_t *__restrict__ W = a.W;
     const float *__restrict__ x = a.x;
     float *__restrict__ y = a.y;
-    const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1;
+    const int lane = threadIdx.x & 63, w = wave_id(), q = lane & 3, h = q >> 1, p = q & 1;
     uint8_t *recs = smem;
     float *tv = (float *)(smem + (size_t)(MR * nsb + 1) * KREC);
-    const KqUnit ku = kq_unit(a);
+    const KqUnit ku = kq_unit4(a);
 
-    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * K) * 4u);
-    const int qw = w;              // quantizer index of the wave
-    const bool wq = 4 * qw < nq;   // the wave has records to quantize (wave-uniform)
+    const rsrc_t xr = buf_rsrc(x, (uint32_t)(M * a.K) * 4u);
+    const bool wq = 4 * w < nq;   // the wave has records to quantize (wave-uniform)
     Q8kFirst xf;
-    if (wq) q8k_first(xr, a, nq, nw, xf, qw);
-    // every wave's x loads before any wave's weight loads (s_barrier, no wait), as in k_q4_0
+    if (wq) q8k_first(xr, a, nq, nw, xf, w);
     __builtin_amdgcn_s_barrier();
 
+    // plane p of the half: qs bytes 32h + 16p .. +16 (dword t: elements 128h + 32j + 16p + 4t ..
+    // +3 at shift 2j, sub-block 8h + 2j + p); its high bits are the high-bit plane's dwords 2p, 2p+1
     const uint8_t *sec = W + (size_t)ku.sb * q3k_sec(N);
     const size_t ro = (size_t)ku.row * 32 + 16 * h;
-    const v4i q0 = __builtin_nontemporal_load((const v4i *)(sec + ro));
-    const v4i q1 = __builtin_nontemporal_load((const v4i *)(sec + (size_t)32 * N + ro));
-    const v4i hm = __builtin_nontemporal_load((const v4i *)(sec + (size_t)64 * N + ro));
+    const v4i qp = __builtin_nontemporal_load((const v4i *)(sec + (size_t)32 * p * N + ro));
+    const uint2 hm = *(const uint2 *)(sec + (size_t)64 * N + ro + 8 * p);
     const uint2 scv = *(const uint2 *)(sec + (size_t)96 * N + (size_t)ku.row * 16 + 8 * h);
     const uint16_t dw16 = *(const uint16_t *)(sec + (size_t)112 * N + (size_t)ku.row * 2);
 
     __builtin_amdgcn_sched_barrier(0);
-    if (wq) q8k_rest(xr, a, nq, nw, xf, recs, qw);
+    if (wq) q8k_rest(xr, a, nq, nw, xf, recs, w);
     __syncthreads();
 
-    if (32 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
-    int sc[8];
+    if (16 * w < RB * nsb) {   // waves past the block's units only quantized (wave-uniform)
+        int sc[4];   // signed scales of sub-blocks 8h + 2j + p
 #pragma unroll
-    for (int k = 0; k < 8; k++) sc[k] = (int)(int8_t)(((k < 4 ? scv.x : scv.y) >> (8 * (k & 3))) & 0xff);
-    const uint32_t qd[8] = {(uint32_t)q0[0], (uint32_t)q0[1], (uint32_t)q0[2], (uint32_t)q0[3],
-                            (uint32_t)q1[0], (uint32_t)q1[1], (uint32_t)q1[2], (uint32_t)q1[3]};
-    int vq[4][8];
+        for (int j = 0; j < 4; j++) sc[j] = (int)(int8_t)((((j < 2) ? scv.x : scv.y) >> (8 * (2 * (j & 1) + p))) & 0xff);
+        int vq[4][4];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const uint32_t hb = ((uint32_t)hm[t >> 1] >> (4 * (t & 1) + j)) & 0x01010101u;
-            vq[j][t] = (int)(((qd[t] >> (2 * j)) & 0x03030303u) | (hb << 2));
-        }
-    const float dw = h2f(dw16);
-    const int spare = MR * RB * nsb;
-#pragma unroll
-    for (int m = 0; m < MR; m++) {
-        const uint8_t *rec = recs + (size_t)(m * nsb + ku.sb) * KREC;
-        const v4i *xq = (const v4i *)(rec + 128 * h);
-        const v4i sa = *(const v4i *)(rec + KR_S16 + 32 * h), sbv = *(const v4i *)(rec + KR_S16 + 32 * h + 16);
-        const int s16[8] = {sa[0], sa[1], sa[2], sa[3], sbv[0], sbv[1], sbv[2], sbv[3]};
-        int isc = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const v4i xa = xq[2 * j], xb = xq[2 * j + 1];
-            int d0 = 0, d1 = 0;
+        for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                d0 = dot4(vq[j][t], xa[t], d0);
-                d1 = dot4(vq[j][4 + t], xb[t], d1);
+                const uint32_t hb = (((t >> 1) ? hm.y : hm.x) >> (4 * (t & 1) + j)) & 0x01010101u;
+                vq[j][t] = (int)((((uint32_t)qp[t] >> (2 * j)) & 0x03030303u) | (hb << 2));
             }
-            isc += sc[2 * j] * (d0 - 4 * s16[2 * j]) + sc[2 * j + 1] * (d1 - 4 * s16[2 * j + 1]);
+        const float dw = h2f(dw16);
+        const int spare = MR * RB * nsb;
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            const uint8_t *rec = recs + (size_t)(m * nsb + ku.sb) * KREC;
+            const v4i *xq = (const v4i *)(rec + 128 * h);
+            const v4i sa = *(const v4i *)(rec + KR_S16 + 32 * h), sbv = *(const v4i *)(rec + KR_S16 + 32 * h + 16);
+            const int s16[4] = {p ? sa[1] : sa[0], p ? sa[3] : sa[2], p ? sbv[1] : sbv[0], p ? sbv[3] : sbv[2]};
+            int isc = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const v4i xa = xq[2 * j + p];
+                int dj = 0;
+#pragma unroll
+                for (int t = 0; t < 4; t++) dj = dot4(vq[j][t], xa[t], dj);
+                isc += sc[j] * (dj - 4 * s16[j]);
+            }
+            isc += dpp_i<0xB1>(0, isc);   // + the other parity (q ^ 1)
+            isc += dpp_i<0x4E>(0, isc);   // + the other half (q ^ 2)
+            const float dx = *(const float *)(rec + KR_D);
+            tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = (dx * dw) * (float)isc;
         }
-        isc += dpp_i<0xB1>(0, isc);
-        const float dx = *(const float *)(rec + KR_D);
-        tv[ku.valid ? (m * RB + ku.r) * nsb + ku.sb : spare] = (dx * dw) * (float)isc;
-    }
     }
     __syncthreads();
-    kq_combine<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
+    kq_combine_any<MR>(M, N, nsb, RB, blockIdx.x * RB, tv, y);
 }
 
-// Row-major form of k_q4_K / k_q3_K (used for one token row) for nsb = 1, 2, 4 or 8 super-blocks
-// per row: units u = row * nsb + sb, so that the 2 * nsb lanes of a row lie in one 16-lane DPP
-// row.  Each unit's fp32 term
-// (the same integers and operations as above) is summed over the super-blocks in order by a chain
+// Row-major kernel for one token row with nsb = 1, 2, 4 or 8 super-blocks per row, two lanes per
+// unit (half h of the super-block, q4k_half_sums / the Q3_K half below): units u = row * nsb + sb,
+// so that the 2 * nsb lanes of a row lie in one 16-lane DPP row.  Each unit's fp32 term
+// (the same integers and operations as k_q4_K4 / k_q3_K4) is summed over the super-blocks in order by a chain
 // of row_shr:2 steps inside the wave, starting from 0.0f + t0 as the oracle does, and the row's
 // last unit writes y: no terms in LDS and no second barrier.  The weight loads of a wave cover
 // 32 / nsb consecutive rows of every super-block section (whole 128-byte lines).
@@ -680,7 +730,7 @@ __global__ void k_pack_q4_0(size_t nblk, const uint8_t *__restrict__ src, uint16
     for (int j = 0; j < 16; j++) o[j] = s[2 + j];
 }
 
-// Q4_K GGUF blocks -> the planar layout of k_q4_K (one thread per (row, super-block) unit).
+// Q4_K GGUF blocks -> the planar layout of the K-quant GEMV kernels (one thread per (row, super-block) unit).
 __global__ void k_pack_q4_K(int N, int nsb, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst)
 {
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -710,7 +760,7 @@ __global__ void k_pack_q4_K(int N, int nsb, const uint8_t *__restrict__ src, uin
     for (int k = 0; k < 4; k++) dd[k] = s[k];
 }
 
-// Q3_K GGUF blocks {hmask[32], qs[64], scales[12], d} -> the planar layout of k_q3_K.  The high
+// Q3_K GGUF blocks {hmask[32], qs[64], scales[12], d} -> the planar layout of the K-quant GEMVs.  The high
 // bits of half h: nib(l) = bits 4h .. 4h+3 of hmask[l]; byte 4t' + b holds nib(8t' + b) in its
 // low and nib(8t' + 4 + b) in its high nibble, so qs dword t of the half finds its four elements'
 // bit j at bit 4(t % 2) + j of each byte of high-bit dword t / 2.
@@ -977,7 +1027,8 @@ hipError_t launch_q8_0(int M, int N, int K, const void *w, const float *x, float
 }
 
 // K-quant launch plan: RB = ceil(N / 256) rows per block (about one block per CU), at most 256 / nsb
-// (at most 8 waves of 32 units); false when the block's LDS would exceed 160 KiB.
+// (so at most 16 waves of 16 four-lane units); nw = the waves of the two-lane row-major kernel;
+// false when the block's LDS would exceed 160 KiB.
 struct KqPlan {
     int rb, nw;
     size_t lds;
@@ -1006,12 +1057,17 @@ hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *
     // (Q4_K 6144 x 2048: 3.86 vs 3.93 us; with several rows its per-row add chains cost more than
     // the barrier and combine they replace: 6.09 vs 5.47 us at M = 4).
     const int nsb = K / 256;
-    if (MR == 1 && (nsb == 1 || nsb == 2 || nsb == 4 || nsb == 8))
+    if (MR == 1 && (nsb == 1 || nsb == 2 || nsb == 4 || nsb == 8)) {
         hipLaunchKernelGGL((k_kq_rm<MR, Q3>), grid, blk, (size_t)(MR * nsb + 1) * KREC, s, a);
-    else if constexpr (Q3)
-        hipLaunchKernelGGL(k_q3_K<MR>, grid, blk, pl.lds, s, a);
-    else
-        hipLaunchKernelGGL(k_q4_K<MR>, grid, blk, pl.lds, s, a);
+    } else {
+        // four lanes per unit: waves for the units (16 per wave; rb * nsb <= 256), or more so that
+        // every wave quantizes at most one pass of four records, at most 16
+        const dim3 blk4(64 * min(16, max((4 * pl.rb * nsb + 63) / 64, (MR * nsb + 3) / 4)));
+        if constexpr (Q3)
+            hipLaunchKernelGGL(k_q3_K4<MR>, grid, blk4, pl.lds, s, a);
+        else
+            hipLaunchKernelGGL(k_q4_K4<MR>, grid, blk4, pl.lds, s, a);
+    }
     return hipGetLastError();
 }
 
