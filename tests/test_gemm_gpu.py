@@ -226,7 +226,10 @@ def test_gemm_host_dropin_reuses_buffers(dev):
     # one (the buffers grow), a smaller one again (the larger buffers hold stale data beyond it),
     # and two host threads at once (calls on one device run one at a time).
     import threading
-    for i, (M, N, K) in enumerate([(40, 48, 32), (512, 384, 256), (24, 16, 48), (256, 272, 1040)]):
+    # (2048, 1280, 1024): C is 10 MiB, two 8 MiB staging chunks, the second partial; A and B share
+    # the chunk stream with C
+    for i, (M, N, K) in enumerate([(40, 48, 32), (512, 384, 256), (24, 16, 48), (256, 272, 1040),
+                                   (2048, 1280, 1024), (64, 48, 16)]):
         A, B = synth.gemm_inputs(M, N, K, seed=60 + i)
         C = synth.rand_int8(61 + i, (M, N)).astype(np.int32)
         ref = oracle_gemm(A, B, C)

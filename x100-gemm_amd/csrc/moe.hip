@@ -479,14 +479,33 @@ X100_DEV void group_pairs(int P, int n_exp, Sel sel, MoeWs ws)
     if (on)
         for (int p = t; p < P; p += 256) atomicAdd(&s_cnt[sel(p)], 1);
     __syncthreads();
-    if (t == 0) {
-        int v = 0;
-        for (int e = 0; e < n_exp; e++) {
-            s_vbase[e] = v;
-            v += (s_cnt[e] + PCH - 1) / PCH;
+    if (t < 64) {
+        // chunk bases: exclusive prefix sum of ceil(count / PCH) over the experts, wave 0 with four
+        // experts per lane (n_exp <= 256) and a 6-step wave scan, instead of one thread walking them
+        int c[4], sum = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = 4 * t + k;
+            c[k] = e < n_exp ? (s_cnt[e] + PCH - 1) / PCH : 0;
+            sum += c[k];
         }
-        s_vbase[n_exp] = v;
-        *ws.nuniq = v;
+        int incl = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(incl, off, 64);
+            if (t >= off) incl += y;
+        }
+        int v = incl - sum;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = 4 * t + k;
+            if (e < n_exp) s_vbase[e] = v;
+            v += c[k];
+        }
+        if (t == 63) {
+            s_vbase[n_exp] = incl;
+            *ws.nuniq = incl;
+        }
     }
     __syncthreads();
     if (t < n_exp) {
