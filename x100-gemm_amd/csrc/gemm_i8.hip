@@ -628,6 +628,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_big(int M, int N, int K, const
     // once every wave has passed the barrier) so that every global store writes whole row segments
     // of the wave's FN*128-byte column range: 1 KiB contiguous per instruction instead of 32 rows
     // x 32 bytes.  Row pitch FN*128 + 16 bytes keeps both LDS access patterns conflict-free.
+    // The last steps issued clamped copies of the final stage into the ring (never read); every
+    // wave waits for its DMA to land (vmcnt(0)) before the barrier, or a late copy could overwrite
+    // the C values staged in the same LDS below.
+    wait_vmcnt<0>();
     lds_barrier();
     constexpr int PB = FN * 128 + 16;   // LDS row pitch (bytes)
     constexpr int CPR = FN * 8;         // 16-byte chunks per row
