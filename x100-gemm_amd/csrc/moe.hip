@@ -662,6 +662,9 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
             ws.act[(size_t)s_pairs[u * 8 + k] * ff + r0 + r] = swiglu(g, up);
         }
     }
+    // A block with no item issued the records' DMA and never waited for it: let it land in this
+    // block's LDS before the block ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Q8_K of every pair's activation row, once (5 or more token rows): wave q quantizes block
