@@ -25,6 +25,8 @@
 
 namespace {
 
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
 constexpr int GU_ROWS = 8;    // gate/up rows of ff per work item
 constexpr int GU_NWV = 4;     // waves per block of k_moe_gate_up_p (one per token row for the routing)
 constexpr int DN_ROWS = 16;   // down rows of d per block
@@ -767,18 +769,17 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     // Accumulator registers 4q .. 4q+3 hold chunk pairs 8q .. 8q+7: only the first nq quads hold
     // pairs of the chunk, so the scaling and the combine skip the others (a block-uniform branch).
     const int nq = (cnt + 7) / 8;
-    // Sub-block j's dot is issued before sub-block j-1's is scaled (two dot accumulators in
-    // flight) and its A operand is read from LDS one step earlier.  The empty asm statements fix
-    // each partial isc where it is computed and the scheduling barriers keep the steps in place:
-    // otherwise the compiler reassociates the sum and holds all eight dot accumulators at once,
-    // which halves the occupancy.
+    // The 6-bit scale is folded into the weight operand: sc = sc_lo + 8 sc_hi with 3-bit halves, and
+    // q * sc_lo, q * sc_hi <= 15 * 7 = 105 fit a signed byte, so two MFMAs per sub-block with
+    // B = q * sc_lo and B = q * sc_hi accumulate sum_j sc_lo_j dot_j and sum_j sc_hi_j dot_j in
+    // the matrix core, and isc = lo + 8 hi is the same integer as sum_j sc_j dot_j (no per-register
+    // scale multiply-adds).  A lane's 16 weight bytes are one row and one sub-block, so one packed
+    // 16-bit multiply per dword scales four bytes at once (each byte product stays below 256).
     auto compute = [&](int sb, const Wt &o) {
         const uint8_t *as = smem + (sb < nh1 ? sb : sb - nh1) * 8 * 1024 + lane * 16;
-        int isc[16], sc[8], mm[8];
-        v16i imn = {}, dot[2];
+        int sc[8], mm[8];
+        v16i lo = {}, hi = {}, imn = {};
         v4i a[9];
-#pragma unroll
-        for (int r = 0; r < 16; r++) isc[r] = 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             int m;
@@ -787,23 +788,23 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
         }
         a[0] = *(const v4i *)as;
 #pragma unroll
-        for (int j = 0; j <= 8; j++) {
+        for (int j = 0; j < 8; j++) {
             if (j < 7) a[j + 1] = *(const v4i *)(as + (j + 1) * 1024);
-            if (j < 8) {
-                const v4i b = (o.q[j >> 1] >> (4 * (j & 1))) & 0x0F0F0F0F;
-                dot[j & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], b, v16i{}, 0, 0, 0);
-                imn = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], v4i{mm[j], mm[j], mm[j], mm[j]}, imn, 0, 0, 0);
+            const v4i b = (o.q[j >> 1] >> (4 * (j & 1))) & 0x0F0F0F0F;
+            const u16x2 slo = u16x2{(uint16_t)(sc[j] & 7), (uint16_t)(sc[j] & 7)};
+            const u16x2 shi = u16x2{(uint16_t)(sc[j] >> 3), (uint16_t)(sc[j] >> 3)};
+            v4i blo, bhi;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int bv = b[t];   // bit-cast a scalar copy: clang's bit cast of a vector
+                                       // element subscript reads element 0 whatever the index
+                const u16x2 bt = __builtin_bit_cast(u16x2, bv);
+                blo[t] = __builtin_bit_cast(int, bt * slo);
+                bhi[t] = __builtin_bit_cast(int, bt * shi);
             }
-            if (j > 0)
-#pragma unroll
-                for (int qd = 0; qd < 4; qd++)
-                    if (qd < nq)
-#pragma unroll
-                        for (int r = 4 * qd; r < 4 * qd + 4; r++) {
-                            isc[r] += __mul24(sc[j - 1], dot[(j - 1) & 1][r]);
-                            asm volatile("" : "+v"(isc[r]));
-                        }
-            __builtin_amdgcn_sched_barrier(0);
+            lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], blo, lo, 0, 0, 0);
+            hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bhi, hi, 0, 0, 0);
+            imn = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], v4i{mm[j], mm[j], mm[j], mm[j]}, imn, 0, 0, 0);
         }
 #pragma unroll
         for (int qd = 0; qd < 4; qd++)
@@ -811,7 +812,7 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
 #pragma unroll
                 for (int r = 4 * qd; r < 4 * qd + 4; r++) {
                     const int k = 8 * (r >> 2) + 4 * h + (r & 3);   // chunk pair of accumulator register r
-                    acc[r] = acc[r] + q4k_combine(o.hdr, s_dx[sb][k], isc[r], imn[r]);
+                    acc[r] = acc[r] + q4k_combine(o.hdr, s_dx[sb][k], lo[r] + 8 * hi[r], imn[r]);
                 }
     };
     for (int sb0 = 0; sb0 < nsb; sb0 += NB) {
