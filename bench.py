@@ -357,12 +357,14 @@ def bench_gemm(torch, timer, dev, args, ceil=None):
     traffic = read_traffic("gemm_i8_4096")
     roof = {"bound": "mfma", "achieved": tops, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
             "frac": tops / PEAK_INT8_TOPS, "traffic": traffic,
-            "kernel": "k_gemm_big<8, 2> (256x256 tile, 8 waves, 2 K stages per barrier)", "algorithmic_ops_per_launch": ops,
+            "kernel": "k_gemm_big<8, 2, true> (256x256 tile, 8 waves, 2 K stages per barrier, C += A.B)",
+            "algorithmic_ops_per_launch": ops,
             "rotating_sets": {"sets": 3, "bytes": 3 * (M * K + K * N + 4 * M * N), "us": msr * 1e3,
                               "TOPS": topsr, "frac": topsr / PEAK_INT8_TOPS},
             "overwrite_form": {"entry": "gemm_hip_i8_dev_set (C = A.B, C not read)", "us": mss * 1e3,
                                "TOPS": ops / mss / 1e9, "frac": ops / mss / 1e9 / PEAK_INT8_TOPS,
-                               "rotating_sets_us": mssr * 1e3, "rotating_sets_TOPS": ops / mssr / 1e9}}
+                               "rotating_sets_us": mssr * 1e3, "rotating_sets_TOPS": ops / mssr / 1e9,
+                               "traffic": read_traffic("gemm_i8_4096_set")}}
     if ceil is not None:
         mf = ceil.mfma(True)
         roof["measured_mfma_ceiling"] = {"TOPS": mf["TOPS"], "clock_GHz": mf["clock_GHz"],
