@@ -540,10 +540,19 @@ def bench_extra(torch, timer, dev, args, ceil):
     n_exp, d, ff, n_act = 128, 2048, 768, 8
     Wg, Wu, Wd = synth.moe_weights(n_exp, d, ff, seed=500)
     R = synth.moe_router(n_exp, d, seed=501)
-    layers = []
+    ggml = []
     base = [torch.from_numpy(np.ascontiguousarray(w).view(np.uint8).reshape(-1)).to(dev) for w in (Wg, Wu, Wd)]
     for li in range(3):   # 3 layers x 340 MB of experts: well beyond the 256 MB Infinity Cache
-        layers.append([b.clone() for b in base] if li else base)
+        ggml.append([b.clone() for b in base] if li else base)
+    # the timed layers read the experts in the tiled layout, regrouped once at load time
+    # (moe_pack_experts, like x100q_pack for the GEMV weights); the ggml layout is timed beside them
+    layers = []
+    for Ly in ggml:
+        t = [torch.empty_like(b) for b in Ly]
+        for k, (rows, K) in enumerate(((ff, d), (ff, d), (d, ff))):
+            x100hip.moe_pack_experts(n_exp, rows, K, Ly[k].data_ptr(), t[k].data_ptr())
+        layers.append(t)
+    torch.cuda.synchronize()
     dR = torch.from_numpy(R).to(dev)
     n_h = 48
     for M in (1, 4, 8):   # decode, and speculative verify of 4 and 8 rows (8: on the matrix cores)
@@ -555,27 +564,29 @@ def bench_extra(torch, timer, dev, args, ceil):
         wsb = x100hip.moe_workspace_bytes(M, d, ff, n_exp, n_act)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
 
-        def call(i, with_sel=False):
-            L = layers[i % 3]
+        def call(i, with_sel=False, tiled=True):
+            L = (layers if tiled else ggml)[i % 3]
             x100hip.moe_layer_ws(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
                                  L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False,
                                  sel[i].data_ptr() if with_sel else None, None, ws.data_ptr(), wsb,
-                                 torch.cuda.current_stream().cuda_stream)
+                                 torch.cuda.current_stream().cuda_stream, tiled=tiled)
 
         for i in range(n_h):
             call(i, True)
         torch.cuda.synchronize()
         U = np.array([len(set(r.ravel().tolist())) for r in sel.cpu().numpy()])
         us = timer.graph([lambda i=i: call(i) for i in range(n_h)])
+        us_ggml = timer.graph([lambda i=i: call(i, tiled=False) for i in range(n_h)])
         lat = timer.single(lambda: call(0))
         byts = float(n_exp * d * 4 + U.mean() * 3 * (ff * d // 256 * 144) + M * d * 4 * 2)
         cpu_us = cpu_time(lambda: ol.moe_layer(hns[0], R, Wg, Wu, Wd, n_act), min_s=0.3)
         key = "moe_layer_qwen3_30b_a3b_m%d" % M
         extra[key] = ceil.annotate({"us_per_layer": us, "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
                                     "single_launch_us": lat, "experts_union_mean": float(U.mean()),
-                                    "bytes_per_layer": byts, "cpu_us_1core": cpu_us}, byts, us)
-        log("%s: %.2f us/layer  U=%.1f  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us" % (
-            key, us, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us))
+                                    "bytes_per_layer": byts, "cpu_us_1core": cpu_us, "expert_layout": "tiled",
+                                    "ggml_layout_us_per_layer": us_ggml}, byts, us)
+        log("%s: %.2f us/layer  U=%.1f  %.0f GB/s (%.1f%% HBM)  single %.2f us  cpu %.0f us  (ggml layout %.2f us)" % (
+            key, us, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, lat, cpu_us, us_ggml))
     # many token rows (verify / prefill): pairs grouped by expert in chunks of 32, matrix cores
     for M in (64, 512):
         n_h = 6
@@ -586,28 +597,30 @@ def bench_extra(torch, timer, dev, args, ceil):
         wsb = x100hip.moe_workspace_bytes(M, d, ff, n_exp, n_act)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
 
-        def callm(i, with_sel=False):
-            L = layers[i % 3]
+        def callm(i, with_sel=False, tiled=True):
+            L = (layers if tiled else ggml)[i % 3]
             x100hip.moe_layer_ws(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
                                  L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False,
                                  sel[i].data_ptr() if with_sel else None, None, ws.data_ptr(), wsb,
-                                 torch.cuda.current_stream().cuda_stream)
+                                 torch.cuda.current_stream().cuda_stream, tiled=tiled)
 
         for i in range(n_h):
             callm(i, True)
         torch.cuda.synchronize()
         U = np.array([len(set(r.ravel().tolist())) for r in sel.cpu().numpy()])
         us = timer.graph([lambda i=i: callm(i) for i in range(n_h)])
+        us_ggml = timer.graph([lambda i=i: callm(i, tiled=False) for i in range(n_h)])
         byts = float(n_exp * d * 4 + U.mean() * 3 * (ff * d // 256 * 144) + M * d * 4 * 2)
         cpu_us = cpu_time(lambda: ol.moe_layer(hns[0][:8], R, Wg, Wu, Wd, n_act), min_s=0.3) * M / 8
         key = "moe_layer_qwen3_30b_a3b_m%d" % M
         extra[key] = ceil.annotate({"us_per_layer": us, "us_per_token": us / M, "tokens_per_s": M / us * 1e6,
                                     "GB/s": byts / us / 1e3, "hbm_frac": byts / us / 1e3 / PEAK_HBM_GBS,
                                     "experts_union_mean": float(U.mean()), "bytes_per_layer": byts,
-                                    "cpu_us_1core": cpu_us, "cpu_note": "8-row sample scaled to M rows"}, byts, us)
-        log("%s: %.2f us/layer (%.3f us/token)  U=%.1f  %.0f GB/s (%.1f%% HBM)  cpu %.0f us" % (
-            key, us, us / M, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, cpu_us))
-    del layers, base
+                                    "cpu_us_1core": cpu_us, "cpu_note": "8-row sample scaled to M rows",
+                                    "expert_layout": "tiled", "ggml_layout_us_per_layer": us_ggml}, byts, us)
+        log("%s: %.2f us/layer (%.3f us/token)  U=%.1f  %.0f GB/s (%.1f%% HBM)  cpu %.0f us  (ggml layout %.2f us)" % (
+            key, us, us / M, U.mean(), byts / us / 1e3, 100 * byts / us / 1e3 / PEAK_HBM_GBS, cpu_us, us_ggml))
+    del layers, ggml, base
 
     # ---- whole decoder layer (x100_decode_layer_hip), one token --------------------------------
     # Qwen3-30B-A3B: d 2048, 32 query / 4 KV heads of 128, attention weights as in the mixed
@@ -720,14 +733,21 @@ def probe_paths(torch, dev, s, reps=3):
     Wg, Wu, Wd = synth.moe_weights(n_exp, d, ff, seed=500)
     dR = torch.from_numpy(synth.moe_router(n_exp, d, seed=501)).to(dev)
     base = [torch.from_numpy(np.ascontiguousarray(w).view(np.uint8).reshape(-1)).to(dev) for w in (Wg, Wu, Wd)]
-    layers = [base] + [[b.clone() for b in base] for _ in range(reps - 1)]
+    layers = []
+    for _ in range(reps):   # tiled expert copies, as the benchmark times them
+        t = [torch.empty_like(b) for b in base]
+        for k, (rows, K) in enumerate(((ff, d), (ff, d), (d, ff))):
+            x100hip.moe_pack_experts(n_exp, rows, K, base[k].data_ptr(), t[k].data_ptr(), s)
+        layers.append(t)
+    del base
     for M in (1, 4, 8, 64):
         dh = torch.from_numpy(synth.normal_f32(900 + M, (reps, M, d))).to(dev)
         out = torch.empty((M, d), dtype=torch.float32, device=dev)
         for i in range(reps):
             L = layers[i]
             x100hip.moe_layer(M, d, ff, n_exp, n_act, dh[i].data_ptr(), dR.data_ptr(), L[0].data_ptr(),
-                              L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False, None, None, s)
+                              L[1].data_ptr(), L[2].data_ptr(), out.data_ptr(), False, None, None, s,
+                              tiled=True)
         torch.cuda.synchronize()
 
 

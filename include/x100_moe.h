@@ -5,9 +5,15 @@
  * M token rows (decode, speculative verify or prefill), one call per layer:
  *   logits = R . hn (fp32), softmax over all n_exp experts, top-n_act (ties -> lower expert id),
  *   renormalised weights; for each selected expert: g = Wg[e].hn, u = Wu[e].hn, act = silu(g)*u,
- *   y = Wd[e].act; out = sum_a w_a * y_a  (plus out's old value when residual != 0).
+ *   y = Wd[e].act; out = sum_a w_a * y_a  (plus out's old value with X100_MOE_RESIDUAL).
  * Experts are Q4_K blocks in the ggml 3-D layout, experts outermost (qwen_moe.c:220-222):
- *   Wg, Wu: [n_exp][ff][d/256] blocks, Wd: [n_exp][d][ff/256] blocks.
+ *   Wg, Wu: [n_exp][ff][d/256] blocks, Wd: [n_exp][d][ff/256] blocks,
+ * or the same bytes regrouped by moe_pack_experts (then X100_MOE_TILED in flags).
+ *
+ * flags (the `residual` argument): bit 0, X100_MOE_RESIDUAL, adds the result into out (the
+ * reference's x += moe(x)); bit 1, X100_MOE_TILED, says that Wg, Wu and Wd were written by
+ * moe_pack_experts.  Any other bit is rejected (X100_EINVAL).  The results are the same, bit for
+ * bit, in both layouts.
  * Activations are quantized to Q8_K per row (hn before gate/up, act before down) with the
  * scalar path's rounding; rows that pick the same expert share one pass over its weights (below
  * 5 token rows all rows at once; from 5 rows the (row, slot) pairs are grouped by expert into
@@ -35,6 +41,8 @@
 #include <stdint.h>
 
 #define X100_MOE_MAX_ROWS 512
+#define X100_MOE_RESIDUAL 1   /* flags: out += the layer's result (else out = it)                 */
+#define X100_MOE_TILED    2   /* flags: expert tensors in moe_pack_experts' layout               */
 /* Size of moe_layer_hip_noalloc's static scratch array (8 MiB per GPU): enough for up to 64
  * token rows at the Qwen3-30B-A3B shape (d 2048, ff 768, 128 experts, top 8) and 16 rows at
  * d = ff = 4096. */
@@ -71,6 +79,16 @@ int moe_layer_hip_ws(int M, int d, int ff, int n_exp, int n_act, const float *hn
 int moe_layer_hip_noalloc(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
                           int *sel, float *sw, void *stream);
+
+/* No counterpart in the reference: a load-time step, like x100q_pack for the GEMV weights.  Copies
+ * n_exp expert matrices of rows x K Q4_K weights (ggml layout, as above: Wg and Wu with rows = ff,
+ * K = d; Wd with rows = d, K = ff) from src to dst (device, 16-byte aligned, not overlapping, the
+ * same n_exp * rows * K / 256 * 144 bytes) in the tiled layout that moe_layer_hip* read with
+ * X100_MOE_TILED: per 8 rows and super-block, the 16-byte pieces of the 8 blocks grouped by
+ * position (the 8 headers, then bytes 0-15 of the 8 rows' qs, ...), so that the matrix-core path
+ * (5 or more token rows) reads whole cache lines.  rows % 8 == 0, K % 256 == 0.  Asynchronous on
+ * stream. */
+int moe_pack_experts(int n_exp, int rows, int K, const void *src, void *dst, void *stream);
 
 #ifdef __cplusplus
 }

@@ -612,6 +612,20 @@ int moe_layer_hip(int M, int d, int ff, int n_exp, int n_act, const float *hn, c
     return moe_run(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, stream);
 }
 
+int moe_pack_experts(int n_exp, int rows, int K, const void *src, void *dst, void *stream)
+{
+    if (n_exp < 1 || rows < 8 || rows % 8 || K < 256 || K % 256 || !src || !dst) return X100_EINVAL;
+    if (((uintptr_t)src | (uintptr_t)dst) & 15) return X100_EINVAL;
+    const size_t bytes = (size_t)n_exp * rows * (K / 256) * 144;
+    const uintptr_t s0 = (uintptr_t)src, d0 = (uintptr_t)dst;
+    if (s0 < d0 + bytes && d0 < s0 + bytes) return X100_EINVAL;   // the copy is not in place
+    int rc = check_device();
+    if (rc) return rc;
+    hipError_t e = x100_moe_tile_pack(n_exp, rows, K, src, dst, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e);
+    return X100_OK;
+}
+
 int moe_layer_hip_noalloc(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
                           float *sw, void *stream)

@@ -52,6 +52,41 @@ struct MoeWs {
 
 inline size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Expert weight layouts.  GGUF (TL = false): row-major, 144-byte Q4_K blocks, row r's super-block
+// sb at (r * nsb + sb) * 144.  Tiled (TL = true, written by k_moe_tile_pack): the same bytes
+// regrouped in tiles of 8 rows x one super-block (1152 bytes), tiles row-group major; inside a
+// tile, 16-byte granule g (0: the header d, dmin, scales; 1..8: qs bytes 16(g-1) .. +16) of row
+// r & 7 at 128 g + 16 (r & 7).  The 8 rows of a granule fill one 128-byte cache line, so a wave
+// reading granule g of 32 rows touches 4 whole lines instead of 32 partial ones, and the 8 rows
+// of a row group stay one contiguous span (nsb tiles), as in the GGUF layout.
+// Byte offset of granule g of row r, super-block sb, in a matrix of nsb super-blocks per row.
+template <bool TL>
+X100_DEV size_t q4k_gofs(size_t r, int sb, int g, int nsb)
+{
+    if constexpr (TL)
+        return (((r >> 3) * nsb + sb) * 9 + g) * 128 + 16 * (r & 7);
+    else
+        return (r * nsb + sb) * 144 + 16 * g;
+}
+// A unit's header and lane half h's qs granules (4h + 1 .. 4h + 4, in qv[0..3]) from weights
+// staged in LDS in the layout of TL: blk = the unit's 144-byte block (GGUF), or its granule 0
+// (tiled; the callers give the 8 units of 16 consecutive lanes the 8 rows of one tile, so that
+// each read of the 16 lanes covers 128 contiguous bytes per lane half).  Reading lane half 1's
+// granules rotated by one (so that the halves fall in opposite 128-byte halves of a 256-byte LDS
+// line) and restoring the order with selects measured slower: M = 1 19.4 us against 15.6 us.
+template <bool TL>
+X100_DEV void q4k_lds_unit(const uint8_t *blk, int h, v4i &hdr, v4i (&qv)[4])
+{
+    hdr = *(const v4i *)blk;
+    if constexpr (TL) {
+#pragma unroll
+        for (int pc = 0; pc < 4; pc++) qv[pc] = *(const v4i *)(blk + 128 * (1 + 4 * h + pc));
+    } else {
+#pragma unroll
+        for (int pc = 0; pc < 4; pc++) qv[pc] = *(const v4i *)(blk + 16 + 64 * h + 16 * pc);
+    }
+}
+
 // Bytes of one row's Q8_K record (nsb 256-element blocks).
 __host__ __device__ inline int q8k_rec_bytes(int nsb) { return (nsb * (256 + 64 + 4) + 15) & ~15; }
 
@@ -566,7 +601,7 @@ __global__ __launch_bounds__(512) void k_moe_topk_group(int M, int n_exp, int n_
 // cnt * GU_ROWS <= 32 values), so at the top of an item wave 0 lets its last store stay
 // outstanding.
 // ------------------------------------------------------------------------------------------------
-template <int UPL, int NWV>
+template <int UPL, int NWV, bool TL>
 __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff, int n_exp, int n_act,
                                                             const uint8_t *__restrict__ Wg,
                                                             const uint8_t *__restrict__ Wu, MoeWs ws,
@@ -632,14 +667,25 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
         const int tv_spare = 4 * 2 * GU_ROWS * nsb;
 #pragma unroll
         for (int c = 0; c < UPL; c++) {
-            const int un = c * 32 * NWV + w * 32 + (lane >> 1);
-            const bool valid = un < nunits;
-            const int sb = valid ? un % nsb : 0;
-            const uint8_t *blk = wl + (size_t)(valid ? un : 0) * 144;
-            const v4i hdr = *(const v4i *)blk;
-            v4i qv[4];
-#pragma unroll
-            for (int pc = 0; pc < 4; pc++) qv[pc] = *(const v4i *)(blk + 16 + 64 * h + 16 * pc);
+            // unit un = (matrix, row, super-block) in that order; tiled, the lanes take the units
+            // row-fastest (q = (matrix, super-block, row)), so that 8 consecutive lane pairs read
+            // the 8 rows of one LDS tile
+            const int q = c * 32 * NWV + w * 32 + (lane >> 1);
+            const bool valid = q < nunits;
+            int un, sb;
+            const uint8_t *blk;
+            if constexpr (TL) {
+                const int qq = valid ? q : 0, rest = qq >> 3, mat = rest / nsb;
+                sb = rest - mat * nsb;
+                un = (mat * GU_ROWS + (qq & 7)) * nsb + sb;
+                blk = wl + (size_t)mat * GU_ROWS * nsb * 144 + sb * 1152 + 16 * (qq & 7);
+            } else {
+                un = q;
+                sb = valid ? un % nsb : 0;
+                blk = wl + (size_t)(valid ? un : 0) * 144;
+            }
+            v4i hdr, qv[4];
+            q4k_lds_unit<TL>(blk, h, hdr, qv);
             Q4kHalf uh;
             q4k_scales_gguf(hdr, h, uh);
             q4k_unpack(qv, uh);
@@ -703,7 +749,7 @@ constexpr int MF_PCH = 32;   // pairs per chunk of the MFMA path
 // Super-blocks in the first staged half of k_moe_mfma's activations (even, at most nsb).
 __host__ __device__ inline int mf_half(int nsb) { return min(nsb, ((nsb + 1) / 2 + 1) & ~1); }
 
-template <bool GU>
+template <bool GU, bool TL>
 __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, const uint8_t *__restrict__ Wa,
                                                   const uint8_t *__restrict__ Wb, MoeWs ws)
 {
@@ -737,7 +783,10 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     const int mat = GU ? (w & 1) : 0, nrows = GU ? ff : d;
     const int r0 = GU ? blockIdx.y * 64 + 32 * (w >> 1) : blockIdx.y * 128 + 32 * w;
     const size_t erow = (size_t)nsb * 144;
-    const uint8_t *wr = (mat ? Wb : Wa) + (size_t)ex * erow * nrows + (size_t)(r0 + col) * erow;
+    const uint8_t *wr = (mat ? Wb : Wa) + (size_t)ex * erow * nrows;
+    // granule g of this lane's row in super-block sb: wr + wofs + sb * sbs + g * gs
+    const size_t wofs = q4k_gofs<TL>((size_t)(r0 + col), 0, 0, nsb);
+    constexpr int sbs = TL ? 1152 : 144, gs = TL ? 128 : 16;
 
     // Weight operands in a ring of NB register buffers: the loads run NB - 1 super-blocks ahead
     // of the math (the last ones reload the final super-block, in bounds).
@@ -747,9 +796,10 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     constexpr int NB = 2;
     Wt wb[NB];
     auto wload = [&](int sb, Wt &o) {
-        o.hdr = *(const v4i *)(wr + sb * 144);
+        const uint8_t *b = wr + wofs + sb * sbs;
+        o.hdr = *(const v4i *)b;
 #pragma unroll
-        for (int p = 0; p < 4; p++) o.q[p] = *(const v4i *)(wr + sb * 144 + 16 + 32 * p + 16 * h);
+        for (int p = 0; p < 4; p++) o.q[p] = *(const v4i *)(b + (1 + 2 * p + h) * gs);
     };
 #pragma unroll
     for (int i = 0; i < NB - 1; i++) wload(min(i, nsb - 1), wb[i]);
@@ -856,7 +906,7 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
 // ------------------------------------------------------------------------------------------------
 // grid (U_max, d / DN_ROWS).  Units (row, super-block) = DN_ROWS*nsf, 8 lanes each.
 // ------------------------------------------------------------------------------------------------
-template <int UPL>
+template <int UPL, bool TL>
 __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *__restrict__ Wd, MoeWs ws)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -878,9 +928,9 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
     for (int c = 0; c < UPL; c++) {
         const int un = min(c * 32 + w * 8 + (lane >> 3), nunits - 1);   // clamped, as in gate/up
         const int r = un / nsf, sb = un - r * nsf;
-        const uint8_t *blk = Wd + (size_t)ex * emat + (size_t)(r0 + r) * erow + sb * 144;
-        hdr[c] = *(const v4i *)blk;
-        qs[c] = __builtin_nontemporal_load((const v4i *)(blk + 16 + 16 * i));
+        const uint8_t *wm = Wd + (size_t)ex * emat;
+        hdr[c] = *(const v4i *)(wm + q4k_gofs<TL>((size_t)(r0 + r), sb, 0, nsf));
+        qs[c] = __builtin_nontemporal_load((const v4i *)(wm + q4k_gofs<TL>((size_t)(r0 + r), sb, 1 + i, nsf)));
     }
 
     // Q8_K of this expert's activation rows (one wave per 256-element block) -> LDS.
@@ -950,7 +1000,7 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
 // ------------------------------------------------------------------------------------------------
 constexpr int FD_DN = 8;     // output rows per block
 
-template <int UPL>
+template <int UPL, bool TL>
 __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, int n_exp, int n_act, uint32_t mnsf,
                                                         uint32_t mdn, uint32_t mspan, const uint8_t *__restrict__ Wd, MoeWs ws,
                                                         float *__restrict__ out, int residual)
@@ -1007,16 +1057,27 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, i
 
 #pragma unroll
     for (int c = 0; c < UPL; c++) {
-        const int un = c * 32 * nw + w * 32 + (lane >> 1);
-        const bool valid = un < nunits;
-        const int unc = valid ? un : 0;
-        const int p = (int)udiv16((uint32_t)unc, (uint32_t)(DN * nsf), mdn), rem = unc - p * DN * nsf;
-        const int sb = rem - (int)udiv16((uint32_t)rem, (uint32_t)nsf, mnsf) * nsf;
-        const uint8_t *blk = wl + (size_t)unc * 144;
-        const v4i hdr = *(const v4i *)blk;
-        v4i qv[4];
-#pragma unroll
-        for (int pc = 0; pc < 4; pc++) qv[pc] = *(const v4i *)(blk + 16 + 64 * h + 16 * pc);
+        // unit un = (pair, row, super-block) in that order; tiled, the lanes take the units
+        // row-fastest (q = (pair, super-block, row)), so that 8 consecutive lane pairs read the 8
+        // rows (DN = 8) of one LDS tile
+        const int q = c * 32 * nw + w * 32 + (lane >> 1);
+        const bool valid = q < nunits;
+        const int qc = valid ? q : 0;
+        const int p = (int)udiv16((uint32_t)qc, (uint32_t)(DN * nsf), mdn), rem = qc - p * DN * nsf;
+        int un, sb;
+        const uint8_t *blk;
+        if constexpr (TL) {
+            static_assert(DN == 8, "a tiled span holds 8 rows");
+            sb = rem >> 3;
+            un = (p * DN + (rem & 7)) * nsf + sb;
+            blk = wl + (size_t)p * DN * nsf * 144 + sb * 1152 + 16 * (rem & 7);
+        } else {
+            un = qc;
+            sb = rem - (int)udiv16((uint32_t)rem, (uint32_t)nsf, mnsf) * nsf;
+            blk = wl + (size_t)qc * 144;
+        }
+        v4i hdr, qv[4];
+        q4k_lds_unit<TL>(blk, h, hdr, qv);
         Q4kHalf uh;
         q4k_scales_gguf(hdr, h, uh);
         q4k_unpack(qv, uh);
@@ -1113,6 +1174,7 @@ void route_rows(int M, int d, int n_exp, const float *hn, const float *R, MoeWs 
 // Five or more token rows, on the matrix cores: router logits and Q8_K records per 4-row chunk,
 // softmax / top-k per 8-row chunk, the pairs grouped by expert into chunks of 32, gate/up + SwiGLU
 // and the down projection by k_moe_mfma, then the weighted combine.
+template <bool TL>
 hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                            const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
                            float *sw, MoeWs ws, hipStream_t s)
@@ -1126,36 +1188,23 @@ hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const flo
         hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
         hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
     }
-    hipLaunchKernelGGL(k_moe_mfma<true>, dim3(Vmax, ff / 64), dim3(256), (size_t)mf_half(nsb) * 8192, s, d, ff, n_act,
+    hipLaunchKernelGGL((k_moe_mfma<true, TL>), dim3(Vmax, ff / 64), dim3(256), (size_t)mf_half(nsb) * 8192, s, d, ff, n_act,
                        (const uint8_t *)Wg, (const uint8_t *)Wu, ws);
     hipLaunchKernelGGL(k_moe_act_q8k, dim3((P * nsf + 3) / 4), dim3(256), 0, s, P, ff, ws);
-    hipLaunchKernelGGL(k_moe_mfma<false>, dim3(Vmax, d / 128), dim3(256), (size_t)mf_half(nsf) * 8192, s, d, ff, n_act,
+    hipLaunchKernelGGL((k_moe_mfma<false, TL>), dim3(Vmax, d / 128), dim3(256), (size_t)mf_half(nsf) * 8192, s, d, ff, n_act,
                        (const uint8_t *)Wd, (const uint8_t *)nullptr, ws);
     hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
     return hipGetLastError();
 }
 
-}  // namespace
-
-size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act)
+// Below MF_MIN_ROWS token rows: routing, gate/up (persistent), down (+ combine).
+template <bool TL>
+hipError_t moe_launch_few(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                          const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
+                          float *sw, MoeWs ws, hipStream_t s)
 {
-    size_t total = 0;
-    carve(0, M, d, ff, n_exp, n_act, &total);
-    return total;
-}
-
-hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
-                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
-                           int *sel, float *sw, void *workspace, hipStream_t s)
-{
-    if (M < 1 || M > X100_MOE_MAX_ROWS || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256)
-        return hipErrorInvalidValue;
-    if (d % 256 || ff % 256 || d > 4096 || ff > 4096 || d % DN_ROWS || ff % GU_ROWS) return hipErrorInvalidValue;
     const int nsb = d / 256, nsf = ff / 256;
-    if (2 * GU_ROWS * nsb > 8 * 8 * GU_NWV || DN_ROWS * nsf > 8 * 32) return hipErrorInvalidValue;
-    MoeWs ws = carve((uintptr_t)workspace, M, d, ff, n_exp, n_act, nullptr);
     const int Umax = min(M * n_act, n_exp);
-    if (M >= MF_MIN_ROWS) return moe_launch_mfma(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
 
     const int nwaves = n_exp * M + (M * nsb + 3) / 4;   // router waves, then quantizer waves of four records
     hipLaunchKernelGGL(k_moe_route, dim3((nwaves + RT_WPB - 1) / RT_WPB), dim3(64 * RT_WPB), (size_t)M * d * 4, s, M, d, n_exp,
@@ -1173,8 +1222,8 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     const int upl_gu = (2 * 2 * GU_ROWS * nsb + 64 * GU_NWV - 1) / (64 * GU_NWV);   // two lanes per unit
 #define X100_GU(U)                                                                                       \
     do {                                                                                                 \
-        const int nb = min(Umax * (ff / GU_ROWS), resident_blocks(k_moe_gate_up_p<U, GU_NWV>, 64 * GU_NWV, lds_gp)); \
-        hipLaunchKernelGGL((k_moe_gate_up_p<U, GU_NWV>), dim3(nb), dim3(64 * GU_NWV), lds_gp, s, M, d, ff, n_exp, \
+        const int nb = min(Umax * (ff / GU_ROWS), resident_blocks(k_moe_gate_up_p<U, GU_NWV, TL>, 64 * GU_NWV, lds_gp)); \
+        hipLaunchKernelGGL((k_moe_gate_up_p<U, GU_NWV, TL>), dim3(nb), dim3(64 * GU_NWV), lds_gp, s, M, d, ff, n_exp, \
                            n_act, wg, wu, ws, sel, sw);                                                   \
     } while (0)
     if (upl_gu == 1)
@@ -1199,10 +1248,10 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
             const uint32_t mnsf = udiv16_magic((uint32_t)nsf), mdn = udiv16_magic((uint32_t)(dn * nsf));
             const uint32_t mspan = udiv16_magic((uint32_t)(dn * nsf * 9));
             if (upl == 1)
-                hipLaunchKernelGGL((k_moe_down_fused<1>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn, mspan,
+                hipLaunchKernelGGL((k_moe_down_fused<1, TL>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn, mspan,
                                    (const uint8_t *)Wd, ws, out, residual);
             else
-                hipLaunchKernelGGL((k_moe_down_fused<2>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn, mspan,
+                hipLaunchKernelGGL((k_moe_down_fused<2, TL>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn, mspan,
                                    (const uint8_t *)Wd, ws, out, residual);
             return hipGetLastError();
         }
@@ -1212,14 +1261,66 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
     const dim3 g_dn(Umax, d / DN_ROWS);
     const uint8_t *wd = (const uint8_t *)Wd;
     switch (upl_dn) {
-    case 1: hipLaunchKernelGGL((k_moe_down<1>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    case 2: hipLaunchKernelGGL((k_moe_down<2>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    case 3: case 4: hipLaunchKernelGGL((k_moe_down<4>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
-    default: hipLaunchKernelGGL((k_moe_down<8>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 1: hipLaunchKernelGGL((k_moe_down<1, TL>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 2: hipLaunchKernelGGL((k_moe_down<2, TL>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    case 3: case 4: hipLaunchKernelGGL((k_moe_down<4, TL>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
+    default: hipLaunchKernelGGL((k_moe_down<8, TL>), g_dn, dim3(256), lds_dn, s, d, ff, wd, ws); break;
     }
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
     hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
+    return hipGetLastError();
+}
+
+// Tiled expert layout (q4k_gofs<true>): thread t writes 16-byte granule t of dst, whose tile
+// position (row group, super-block, granule, row) names the granule of src it copies.
+__global__ __launch_bounds__(256) void k_moe_tile_pack(size_t ngran, int nsb, const v4i *__restrict__ src,
+                                                       v4i *__restrict__ dst)
+{
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= ngran) return;
+    const size_t tile = t / 72;   // 8 rows x 9 granules
+    const int in = (int)(t - tile * 72), g = in >> 3, r7 = in & 7;
+    const size_t rg = tile / nsb;
+    const int sb = (int)(tile - rg * nsb);
+    dst[t] = src[((8 * rg + r7) * nsb + sb) * 9 + g];
+}
+
+}  // namespace
+
+size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act)
+{
+    size_t total = 0;
+    carve(0, M, d, ff, n_exp, n_act, &total);
+    return total;
+}
+
+hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
+                           const void *Wg, const void *Wu, const void *Wd, float *out, int flags,
+                           int *sel, float *sw, void *workspace, hipStream_t s)
+{
+    if (M < 1 || M > X100_MOE_MAX_ROWS || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256)
+        return hipErrorInvalidValue;
+    if (d % 256 || ff % 256 || d > 4096 || ff > 4096 || d % DN_ROWS || ff % GU_ROWS) return hipErrorInvalidValue;
+    if (flags & ~(X100_MOE_RESIDUAL | X100_MOE_TILED)) return hipErrorInvalidValue;
+    const int nsb = d / 256, nsf = ff / 256;
+    if (2 * GU_ROWS * nsb > 8 * 8 * GU_NWV || DN_ROWS * nsf > 8 * 32) return hipErrorInvalidValue;
+    MoeWs ws = carve((uintptr_t)workspace, M, d, ff, n_exp, n_act, nullptr);
+    const int residual = flags & X100_MOE_RESIDUAL;
+    const bool tiled = (flags & X100_MOE_TILED) != 0;
+    if (M >= MF_MIN_ROWS)
+        return tiled ? moe_launch_mfma<true>(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s)
+                     : moe_launch_mfma<false>(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
+    return tiled ? moe_launch_few<true>(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s)
+                 : moe_launch_few<false>(M, d, ff, n_exp, n_act, hn, R, Wg, Wu, Wd, out, residual, sel, sw, ws, s);
+}
+
+hipError_t x100_moe_tile_pack(int n_exp, int rows, int K, const void *src, void *dst, hipStream_t s)
+{
+    if (n_exp < 1 || rows < 8 || rows % 8 || K < 256 || K % 256 || !src || !dst) return hipErrorInvalidValue;
+    const size_t ngran = (size_t)n_exp * rows * (K / 256) * 9;
+    hipLaunchKernelGGL(k_moe_tile_pack, dim3((unsigned)((ngran + 255) / 256)), dim3(256), 0, s, ngran, K / 256,
+                       (const v4i *)src, (v4i *)dst);
     return hipGetLastError();
 }

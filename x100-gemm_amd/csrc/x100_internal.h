@@ -31,9 +31,11 @@ bool x100_qgemv_supported(int qtype, int M, int N, int K);
 hipError_t x100_check_quant_div_launch(uint32_t lo, uint32_t hi, unsigned long long *cnt, hipStream_t s);
 
 size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act);
+// flags: X100_MOE_RESIDUAL, X100_MOE_TILED (x100_moe.h).
 hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
-                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual,
+                           const void *Wg, const void *Wu, const void *Wd, float *out, int flags,
                            int *sel, float *sw, void *workspace, hipStream_t s);
+hipError_t x100_moe_tile_pack(int n_exp, int rows, int K, const void *src, void *dst, hipStream_t s);
 
 hipError_t x100_gemv_tile_launch(int int4, int M, int N, int K, const void *W, const int8_t *x, int32_t *y,
                                  hipStream_t s);

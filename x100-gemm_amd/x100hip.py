@@ -10,7 +10,8 @@ Entry points and what they replace in the reference:
   qgemv_hip (+ x100q_pack)                      lin_mm of qwen_moe.c:101-107 on Q4_0/Q4_K/Q3_K;
                                                 lin_mm_i8_x of qwen_moe_q3k.c:1075 on Q8_0/Q5_K/Q6_K
   moe_layer_hip / moe_layer_hip_ws              the MoE block of qwen_moe.c:294-311 (library or
-                                                caller scratch)
+                                                caller scratch); moe_pack_experts: load-time
+                                                regrouping of the expert tensors (tiled=True)
   gemv_int4_hip / gemv_int8_hip (+ packers)     gemv_nb_int4 / gemv_nb_int8 of bench/q4_gemv.c:67-99
 """
 import ctypes
@@ -35,6 +36,7 @@ EXPORTS = (
     "x100_tile_bytes", "x100_pack_w_int4", "x100_pack_w_int8", "gemv_int4_hip", "gemv_int8_hip",
     "x100q_gguf_bytes", "x100q_packed_bytes", "x100q_pack", "qgemv_hip", "x100q_check_quant_div",
     "moe_layer_hip", "moe_layer_workspace_bytes", "moe_layer_hip_ws", "moe_layer_hip_noalloc",
+    "moe_pack_experts",
     "x100_gguf_open", "x100_gguf_close", "x100_gguf_version", "x100_gguf_n_tensors", "x100_gguf_n_kv",
     "x100_gguf_alignment", "x100_gguf_data_offset", "x100_gguf_tensor_at", "x100_gguf_find",
     "x100_gguf_kv_at", "x100_gguf_get_int", "x100_gguf_get_float", "x100_gguf_get_str",
@@ -112,6 +114,7 @@ def lib():
     L.moe_layer_workspace_bytes.restype = sz
     L.moe_layer_hip_ws.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p, sz, p]
     L.moe_layer_hip_noalloc.argtypes = [i, i, i, i, i, p, p, p, p, p, p, i, p, p, p]
+    L.moe_pack_experts.argtypes = [i, i, i, p, p, p]
     L.x100_tile_bytes.argtypes = [i, i, i]
     L.x100_tile_bytes.restype = sz
     L.x100_pack_w_int4.argtypes = [i, i, p, p]
@@ -161,6 +164,7 @@ def lib():
     L.x100_decode_layer_hip_ws.restype = i
     for name in ("gemm_hip_i8", "gemm_hip_i8_dev", "gemm_hip_i8_dev_set", "gemm_hip_i8_dev_variant", "x100_hip_detect",
                  "x100q_pack", "qgemv_hip", "x100q_check_quant_div", "moe_layer_hip", "moe_layer_hip_ws", "moe_layer_hip_noalloc",
+                 "moe_pack_experts",
                  "x100_pack_w_int4",
                  "x100_pack_w_int8",
                  "gemv_int4_hip", "gemv_int8_hip"):
@@ -235,19 +239,31 @@ def check_quant_div(lo_bits, hi_bits, d_counts, stream=None):
 
 
 # ---- MoE layer ---------------------------------------------------------------------------------
+MOE_RESIDUAL, MOE_TILED = 1, 2
+
+
+def _moe_flags(residual, tiled):
+    return (MOE_RESIDUAL if residual else 0) | (MOE_TILED if tiled else 0)
+
+
+def moe_pack_experts(n_exp, rows, K, d_src, d_dst, stream=None):
+    """Q4_K expert tensor (n_exp x rows x K, ggml layout) -> the tiled layout (same size)."""
+    return _check("moe_pack_experts", lib().moe_pack_experts(n_exp, rows, K, d_src, d_dst, stream))
+
+
 def moe_layer(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residual=False,
-              d_sel=None, d_sw=None, stream=None):
+              d_sel=None, d_sw=None, stream=None, tiled=False):
     return _check("moe_layer_hip",
                   lib().moe_layer_hip(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out,
-                                      1 if residual else 0, d_sel, d_sw, stream))
+                                      _moe_flags(residual, tiled), d_sel, d_sw, stream))
 
 
 def moe_layer_noalloc(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residual=False,
-                      d_sel=None, d_sw=None, stream=None):
+                      d_sel=None, d_sw=None, stream=None, tiled=False):
     """moe_layer with the library's static per-GPU scratch (allocates nothing)."""
     return _check("moe_layer_hip_noalloc",
                   lib().moe_layer_hip_noalloc(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out,
-                                              1 if residual else 0, d_sel, d_sw, stream))
+                                              _moe_flags(residual, tiled), d_sel, d_sw, stream))
 
 
 def moe_workspace_bytes(M, d, ff, n_exp, n_act):
@@ -255,11 +271,11 @@ def moe_workspace_bytes(M, d, ff, n_exp, n_act):
 
 
 def moe_layer_ws(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out, residual, d_sel, d_sw, d_ws, ws_bytes,
-                 stream=None):
+                 stream=None, tiled=False):
     """moe_layer on caller scratch (d_ws: device buffer of ws_bytes >= moe_workspace_bytes)."""
     return _check("moe_layer_hip_ws",
                   lib().moe_layer_hip_ws(M, d, ff, n_exp, n_act, d_hn, d_R, d_Wg, d_Wu, d_Wd, d_out,
-                                         1 if residual else 0, d_sel, d_sw, d_ws, ws_bytes, stream))
+                                         _moe_flags(residual, tiled), d_sel, d_sw, d_ws, ws_bytes, stream))
 
 
 # ---- integer tile GEMV (int4 / int8 weights) ---------------------------------------------------
