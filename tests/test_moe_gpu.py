@@ -124,7 +124,8 @@ def test_moe_many_rows_qwen3_shape(dev, M):
 
 @pytest.mark.parametrize("M,n_exp,d,ff,n_act", [(100, 8, 256, 256, 8),     # every expert in every row: 13 chunks each
                                                 (40, 16, 512, 256, 4), (17, 64, 1024, 512, 2),
-                                                (33, 200, 256, 256, 6)])
+                                                (33, 200, 256, 256, 6),
+                                                (12, 8, 3072, 512, 2)])   # d of 12 blocks: the router's general form
 def test_moe_many_rows_small_shapes(dev, M, n_exp, d, ff, n_act):
     check(M, n_exp, d, ff, n_act, seed=620 + M + n_exp, dev=dev)
 

@@ -203,23 +203,23 @@ __global__ __launch_bounds__(64 * RT_WPB) void k_moe_route(int M, int d, int n_e
 
 // ------------------------------------------------------------------------------------------------
 // Router of many token rows: the logits of k_moe_route (same per-lane order and butterfly, so the
-// same bits) from blocks of RR_ROWS token rows x 4 * epw experts, so that each staged hn row serves
+// same bits) from blocks of RR_ROWS token rows x 4 * epw experts, so that each loaded hn row serves
 // up to 32 experts instead of 4 (epw grows with M: more experts per block, fewer blocks).  Wave w
-// computes experts 4 * epw * bx + epw * w .. +epw, the router rows of the next two experts loaded
-// while the current one's dots run.  Blocks bx >= ceil(n_exp / (4 * epw)) quantize the chunk's hn rows to
-// Q8_K (one wave per 256-element block, from global memory).
+// computes experts 4 * epw * bx + epw * w .. +epw.  Blocks bx >= ceil(n_exp / (4 * epw)) quantize
+// the chunk's hn rows to Q8_K (one wave per 256-element block, from global memory).
 // grid (ceil(n_exp / (4 * epw)) + ceil(RR_ROWS * d / 1024), ceil(M / RR_ROWS)).
 // ------------------------------------------------------------------------------------------------
 constexpr int RR_ROWS = 4;
 
-template <int NJ>   // 256-element blocks of d held per lane (d <= 256 * NJ)
+// NJ: 256-element blocks of d held per lane (d <= 256 * NJ); EXACT: d == 256 * NJ, so the block
+// loop needs no range tests (a test per block split each dot into branches and kept the RB rows'
+// sums from interleaving).
+template <int NJ, bool EXACT>
 __global__ __launch_bounds__(256) void k_moe_route_rows(int M, int d, int n_exp, int epw, const float *__restrict__ hn,
                                                         const float *__restrict__ R, MoeWs ws)
 {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const float4 *s_hn = (const float4 *)smem;   // [RR_ROWS][d / 4]
     const int lane = threadIdx.x & 63, w = wave_id();
-    const int nsb = d / 256;
+    const int nsb = EXACT ? NJ : d / 256;
     const int row0 = blockIdx.y * RR_ROWS, nr = min(RR_ROWS, M - row0);
     const int ngrp = (n_exp + 4 * epw - 1) / (4 * epw);
     if ((int)blockIdx.x >= ngrp) {
@@ -232,42 +232,57 @@ __global__ __launch_bounds__(256) void k_moe_route_rows(int M, int d, int n_exp,
         return;
     }
 
-    // The wave's first router row, then the chunk's hn rows -> LDS.
+    // The block's hn rows in registers, RB at a time (all four at d <= 2048), and the wave's router
+    // rows streamed through a two-row register ring, the next expert's row loading while the
+    // current one's RB dot products run: no LDS, and no load between an expert's dots.
+    constexpr int RB = NJ <= 8 ? RR_ROWS : 1;   // hn rows held per pass (RB * NJ float4 registers)
     const int e0 = blockIdx.x * 4 * epw + epw * w;
     auto rload = [&](int e, float4 *rv) {
         const rsrc_t rr = buf_rsrc(R + (size_t)min(e, n_exp - 1) * d, (uint32_t)d * 4u);   // clamped expert
 #pragma unroll
         for (int j = 0; j < NJ; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
     };
-    float4 rv[3][NJ];   // ring: router rows of experts i, i + 1, i + 2
-    rload(e0, rv[0]);
-    if (epw > 1) rload(e0 + 1, rv[1]);
-    for (int ch = w; ch < nr * nsb; ch += 4)
-        dma_1k(hn + (size_t)row0 * d + (size_t)ch * 256 + 4 * lane, smem + ch * 1024);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
+    for (int mb = 0; mb < nr; mb += RB) {
+        float4 rv[2][NJ];   // ring: router rows of experts i, i + 1
+        rload(e0, rv[0]);
+        float4 hv[RB][NJ];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int e = e0 + i;
-        if (i >= epw) break;
-        if (i + 2 < epw) rload(e + 2, rv[(i + 2) % 3]);
-        if (e < n_exp)
-            for (int m = 0; m < nr; m++) {
-                const float4 *hr = s_hn + m * (d / 4);
-                float sum = 0.0f;
+        for (int m = 0; m < RB; m++) {
+            const rsrc_t hr = buf_rsrc(hn + (size_t)(row0 + min(mb + m, nr - 1)) * d, (uint32_t)d * 4u);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) hv[m][j] = buf_load_f4(hr, (uint32_t)(4 * lane + 256 * j) * 4u);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int e = e0 + i;
+            if (i >= epw) break;
+            if (i + 1 < epw) rload(e + 1, rv[(i + 1) & 1]);
+            if (e < n_exp) {
+                // each row's sum in k_moe_route's order (blocks j ascending, then x, y, z, w); the
+                // RB rows' independent sums interleaved
+                float sum[RB];
+#pragma unroll
+                for (int m = 0; m < RB; m++) sum[m] = 0.0f;
 #pragma unroll
                 for (int j = 0; j < NJ; j++)
-                    if (j < nsb) {
-                        const float4 hv = hr[lane + 64 * j];
-                        sum += rv[i % 3][j].x * hv.x;
-                        sum += rv[i % 3][j].y * hv.y;
-                        sum += rv[i % 3][j].z * hv.z;
-                        sum += rv[i % 3][j].w * hv.w;
+                    if (EXACT || j < nsb) {
+#pragma unroll
+                        for (int m = 0; m < RB; m++) sum[m] += rv[i & 1][j].x * hv[m][j].x;
+#pragma unroll
+                        for (int m = 0; m < RB; m++) sum[m] += rv[i & 1][j].y * hv[m][j].y;
+#pragma unroll
+                        for (int m = 0; m < RB; m++) sum[m] += rv[i & 1][j].z * hv[m][j].z;
+#pragma unroll
+                        for (int m = 0; m < RB; m++) sum[m] += rv[i & 1][j].w * hv[m][j].w;
                     }
-                sum = wave_sum_bfly_f(sum);
-                if (lane == 0) ws.logits[(size_t)(row0 + m) * n_exp + e] = sum;
+#pragma unroll
+                for (int m = 0; m < RB; m++)
+                    if (mb + m < nr) {
+                        const float v = wave_sum_bfly_f(sum[m]);
+                        if (lane == 0) ws.logits[(size_t)(row0 + mb + m) * n_exp + e] = v;
+                    }
             }
+        }
     }
 }
 
@@ -512,9 +527,16 @@ X100_DEV void group_pairs(int P, int n_exp, Sel sel, MoeWs ws)
         s_cnt[t] = 0;
         s_cur[t] = 0;
     }
+    // Thread t's pairs t, t + 256, ... (P <= 4096: at most 16) have their experts loaded at once,
+    // before the first count: a load per counting step made each step a round trip to memory.
+    constexpr int PPT = X100_MOE_MAX_ROWS * 8 / 256;
+    int ex[PPT];
+#pragma unroll
+    for (int i = 0; i < PPT; i++) ex[i] = (on && t + 256 * i < P) ? sel(t + 256 * i) : -1;
     __syncthreads();
-    if (on)
-        for (int p = t; p < P; p += 256) atomicAdd(&s_cnt[sel(p)], 1);
+#pragma unroll
+    for (int i = 0; i < PPT; i++)
+        if (ex[i] >= 0) atomicAdd(&s_cnt[ex[i]], 1);
     __syncthreads();
     if (t < 64) {
         // chunk bases: exclusive prefix sum of ceil(count / PCH) over the experts, wave 0 with four
@@ -552,11 +574,11 @@ X100_DEV void group_pairs(int P, int n_exp, Sel sel, MoeWs ws)
             ws.ucnt[v0 + k] = min(PCH, c - PCH * k);
         }
     }
-    if (on)
-        for (int p = t; p < P; p += 256) {
-            const int e = sel(p);
-            const int k = atomicAdd(&s_cur[e], 1);
-            ws.upairs[(s_vbase[e] + k / PCH) * PCH + (k % PCH)] = p;
+#pragma unroll
+    for (int i = 0; i < PPT; i++)
+        if (ex[i] >= 0) {
+            const int k = atomicAdd(&s_cur[ex[i]], 1);
+            ws.upairs[(s_vbase[ex[i]] + k / PCH) * PCH + (k % PCH)] = t + 256 * i;
         }
 }
 
@@ -746,8 +768,10 @@ __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 // r0 + 32 * w .. +32.  grid (chunks, ff / 64 or d / 128).
 // ------------------------------------------------------------------------------------------------
 constexpr int MF_PCH = 32;   // pairs per chunk of the MFMA path
-// Super-blocks in the first staged half of k_moe_mfma's activations (even, at most nsb).
-__host__ __device__ inline int mf_half(int nsb) { return min(nsb, ((nsb + 1) / 2 + 1) & ~1); }
+// Super-blocks in the first staged part of k_moe_mfma's activations: all of them up to 4 (one
+// staging round trip; the down projection of ff = 768 has 3), else the first half rounded up to
+// even, so that the halves meet between two ring steps.
+__host__ __device__ inline int mf_half(int nsb) { return nsb <= 4 ? nsb : min(nsb, ((nsb + 1) / 2 + 1) & ~1); }
 
 template <bool GU, bool TL>
 __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, const uint8_t *__restrict__ Wa,
@@ -805,7 +829,7 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     for (int i = 0; i < NB - 1; i++) wload(min(i, nsb - 1), wb[i]);
     // DMA lane l fetches pair l % 32, bytes 16 * (l / 32) .. +16 of each sub-block.
     const uint8_t *src = X + (size_t)arow * rec + 16 * h;
-    const int nh1 = mf_half(nsb);   // even, so the halves meet between two ring steps
+    const int nh1 = mf_half(nsb);   // nsb, or even: the halves meet between two ring steps
     auto stage = [&](int sb0, int sb1) {
         for (int c = 8 * sb0 + w; c < 8 * sb1; c += 4) dma_1k(src + 32 * c, smem + (c - 8 * sb0) * 1024);
     };
@@ -1164,11 +1188,14 @@ void route_rows(int M, int d, int n_exp, const float *hn, const float *R, MoeWs 
     const int epw = max(1, min(8, M / 64));   // experts per wave
     const int ngrp = (n_exp + 4 * epw - 1) / (4 * epw), nq = (RR_ROWS * (d / 256) + 3) / 4;
     const dim3 g(ngrp + nq, (M + RR_ROWS - 1) / RR_ROWS);
-    if (d <= 2048)
-        hipLaunchKernelGGL(k_moe_route_rows<8>, g, dim3(256), (size_t)RR_ROWS * d * 4, s, M, d, n_exp, epw, hn, R, ws);
+    if (d == 2048)
+        hipLaunchKernelGGL((k_moe_route_rows<8, true>), g, dim3(256), 0, s, M, d, n_exp, epw, hn, R, ws);
+    else if (d < 2048)
+        hipLaunchKernelGGL((k_moe_route_rows<8, false>), g, dim3(256), 0, s, M, d, n_exp, epw, hn, R, ws);
+    else if (d == 4096)
+        hipLaunchKernelGGL((k_moe_route_rows<16, true>), g, dim3(256), 0, s, M, d, n_exp, epw, hn, R, ws);
     else
-        hipLaunchKernelGGL(k_moe_route_rows<16>, g, dim3(256), (size_t)RR_ROWS * d * 4, s, M, d, n_exp, epw, hn, R,
-                           ws);
+        hipLaunchKernelGGL((k_moe_route_rows<16, false>), g, dim3(256), 0, s, M, d, n_exp, epw, hn, R, ws);
 }
 
 // Five or more token rows, on the matrix cores: router logits and Q8_K records per 4-row chunk,
