@@ -752,15 +752,15 @@ __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 // ------------------------------------------------------------------------------------------------
 // Expert-grouped Q4_K x Q8_K products on the matrix cores (many token rows).  The pairs of one
 // expert come in chunks of up to 32 (k_moe_group<32>); a wave computes a 32 x 32 tile (chunk pairs
-// x weight rows) with one v_mfma_i32_32x32x32_i8 per 32-element sub-block j:
+// x weight rows) with v_mfma_i32_32x32x32_i8 per 32-element sub-block j:
 //   A = the pairs' Q8_K bytes of sub-block j (lane l: pair l % 32, elements 16 * (l / 32) .. +16),
-//   B = the weight rows' 4-bit values of sub-block j (lane l: row l % 32, the same elements),
-// so the accumulator holds dot_j(pair, row) exactly.  Lane l owns weight row l % 32 in every
-// accumulator register, so isc += sc_j(row) * dot_j is one multiply-add per register; the min term
-// sum_j m_j * (sum of the activation bytes of sub-block j) is a second MFMA chain whose B holds m_j in
-// every byte.  These integers equal those of the one-row kernels, and the fp32 combine per
-// super-block (q4k_combine) and the sum over super-blocks run in the same order, so every output
-// is bit-identical to theirs.
+//   B = the weight rows' 4-bit values of sub-block j times the low or the high 3 bits of the
+//       row's 6-bit scale (lane l: row l % 32, the same elements),
+// so the two accumulators hold sum_j sc_lo_j dot_j and sum_j sc_hi_j dot_j exactly; a third
+// chain whose B holds m_j in every byte gives the min term sum_j m_j * (sum of the activation
+// bytes of sub-block j).  These integers equal those of the one-row kernels, and the fp32 combine
+// per super-block (q4k_combine) and the sum over super-blocks run in the same order, so every
+// output is bit-identical to theirs.
 //
 // GU: gate and up (A = the hn records, pair p reads row p / n_act); wave w computes matrix w & 1
 // (gate, up) for ff rows r0 + 32 * (w >> 1) .. +32, and SwiGLU pairs them through LDS.
