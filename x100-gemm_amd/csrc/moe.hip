@@ -768,15 +768,22 @@ __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 // r0 + 32 * w .. +32.  grid (chunks, ff / 64 or d / 128).
 // ------------------------------------------------------------------------------------------------
 constexpr int MF_PCH = 32;   // pairs per chunk of the MFMA path
+#ifndef MF_DN_RT
+#define MF_DN_RT 2           // row tiles per wave of the down projection (one staging part)
+#endif
 // Super-blocks in the first staged part of k_moe_mfma's activations: all of them up to 4 (one
 // staging round trip; the down projection of ff = 768 has 3), else the first half rounded up to
 // even, so that the halves meet between two ring steps.
 __host__ __device__ inline int mf_half(int nsb) { return nsb <= 4 ? nsb : min(nsb, ((nsb + 1) / 2 + 1) & ~1); }
 
-template <bool GU, bool TL>
+template <bool GU, bool TL, int RT>
 __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, const uint8_t *__restrict__ Wa,
                                                   const uint8_t *__restrict__ Wb, MoeWs ws)
 {
+    // RT (down projection only, with every super-block staged at once): a wave walks RT tiles of
+    // 32 weight rows, 128 rows apart, one after the other on the same staged activations; the
+    // weight loads run ahead across the tile boundaries.
+    static_assert(RT == 1 || !GU, "row tiles in sequence: down projection only");
     // The chunk's activation bytes, staged per block in two halves (super-blocks 0 .. nh1-1, then
     // nh1 .. nsb-1, so that the LDS of a block is half the chunk's and more blocks fit a CU):
     // 1 KiB per sub-block c = 8 * sb + j, laid out [h][pair][16 B] so that the A operand of lane l
@@ -805,7 +812,7 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
         s_dx[sb][col] = ((const float *)(X + (size_t)arow * rec + nsb * 320))[sb];
 
     const int mat = GU ? (w & 1) : 0, nrows = GU ? ff : d;
-    const int r0 = GU ? blockIdx.y * 64 + 32 * (w >> 1) : blockIdx.y * 128 + 32 * w;
+    const int r0 = GU ? blockIdx.y * 64 + 32 * (w >> 1) : blockIdx.y * 128 * RT + 32 * w;
     const size_t erow = (size_t)nsb * 144;
     const uint8_t *wr = (mat ? Wb : Wa) + (size_t)ex * erow * nrows;
     // granule g of this lane's row in super-block sb: wr + wofs + sb * sbs + g * gs
@@ -819,8 +826,10 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
     };
     constexpr int NB = 2;
     Wt wb[NB];
-    auto wload = [&](int sb, Wt &o) {
-        const uint8_t *b = wr + wofs + sb * sbs;
+    // step k: tile k / nsb (128 * tile rows further on, in both layouts), super-block k % nsb
+    auto wload = [&](int k, Wt &o) {
+        const int tile = RT > 1 ? k / nsb : 0, sb = k - tile * nsb;
+        const uint8_t *b = wr + wofs + (size_t)tile * 128 * erow + sb * sbs;
         o.hdr = *(const v4i *)b;
 #pragma unroll
         for (int p = 0; p < 4; p++) o.q[p] = *(const v4i *)(b + (1 + 2 * p + h) * gs);
@@ -889,8 +898,9 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
                     acc[r] = acc[r] + q4k_combine(o.hdr, s_dx[sb][k], lo[r] + 8 * hi[r], imn[r]);
                 }
     };
-    for (int sb0 = 0; sb0 < nsb; sb0 += NB) {
-        if (sb0 == nh1) {   // second half of the activations into the same LDS
+    const int nstep = RT * nsb;
+    for (int k0 = 0; k0 < nstep; k0 += NB) {
+        if (RT == 1 && k0 == nh1) {   // second half of the activations into the same LDS
             __syncthreads();
             stage(nh1, nsb);
             __builtin_amdgcn_s_waitcnt(0);
@@ -898,11 +908,22 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
-            const int sb = sb0 + i;
-            if (sb < nsb) {
-                wload(min(sb + NB - 1, nsb - 1), wb[(i + NB - 1) % NB]);
+            const int k = k0 + i;
+            if (k < nstep) {
+                wload(min(k + NB - 1, nstep - 1), wb[(i + NB - 1) % NB]);
                 __builtin_amdgcn_sched_barrier(0);
+                const int sb = RT > 1 ? k % nsb : k;
                 compute(sb, wb[i]);
+                if constexpr (RT > 1)
+                    if (sb == nsb - 1 && k < nstep - 1) {   // a tile done: store it, start the next
+                        const int rt = r0 + 128 * (k / nsb);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int kk = 8 * (r >> 2) + 4 * h + (r & 3);
+                            if (kk < cnt) ws.ydn[(size_t)s_pairs[kk] * d + rt + col] = acc[r];
+                            acc[r] = 0.0f;
+                        }
+                    }
             }
         }
     }
@@ -922,7 +943,7 @@ __global__ __launch_bounds__(256) void k_moe_mfma(int d, int ff, int n_act, cons
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int k = 8 * (r >> 2) + 4 * h + (r & 3);
-            if (k < cnt) ws.ydn[(size_t)s_pairs[k] * d + r0 + col] = acc[r];
+            if (k < cnt) ws.ydn[(size_t)s_pairs[k] * d + r0 + 128 * (RT - 1) + col] = acc[r];
         }
     }
 }
@@ -1215,11 +1236,16 @@ hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const flo
         hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
         hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
     }
-    hipLaunchKernelGGL((k_moe_mfma<true, TL>), dim3(Vmax, ff / 64), dim3(256), (size_t)mf_half(nsb) * 8192, s, d, ff, n_act,
-                       (const uint8_t *)Wg, (const uint8_t *)Wu, ws);
+    hipLaunchKernelGGL((k_moe_mfma<true, TL, 1>), dim3(Vmax, ff / 64), dim3(256), (size_t)mf_half(nsb) * 8192, s, d,
+                       ff, n_act, (const uint8_t *)Wg, (const uint8_t *)Wu, ws);
     hipLaunchKernelGGL(k_moe_act_q8k, dim3((P * nsf + 3) / 4), dim3(256), 0, s, P, ff, ws);
-    hipLaunchKernelGGL((k_moe_mfma<false, TL>), dim3(Vmax, d / 128), dim3(256), (size_t)mf_half(nsf) * 8192, s, d, ff, n_act,
-                       (const uint8_t *)Wd, (const uint8_t *)nullptr, ws);
+    // down: MF_DN_RT row tiles per wave when one staging part holds every super-block
+    if (MF_DN_RT > 1 && mf_half(nsf) == nsf && d % (128 * MF_DN_RT) == 0)
+        hipLaunchKernelGGL((k_moe_mfma<false, TL, MF_DN_RT>), dim3(Vmax, d / (128 * MF_DN_RT)), dim3(256),
+                           (size_t)nsf * 8192, s, d, ff, n_act, (const uint8_t *)Wd, (const uint8_t *)nullptr, ws);
+    else
+        hipLaunchKernelGGL((k_moe_mfma<false, TL, 1>), dim3(Vmax, d / 128), dim3(256), (size_t)mf_half(nsf) * 8192, s, d,
+                           ff, n_act, (const uint8_t *)Wd, (const uint8_t *)nullptr, ws);
     hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
     return hipGetLastError();
 }
