@@ -892,7 +892,7 @@ static int layer_ok(const orc_layer_cfg *c)
  * qwen_moe.c:289-292 up to rounding. */
 static void attn_chunks(int n_pos, int n_kv, int *CH, int *nch)
 {
-    const int target = n_kv >= 512 ? 1 : 512 / n_kv;
+    const int target = n_kv >= 256 ? 1 : 256 / n_kv;
     int ch = (n_pos + target - 1) / target;
     ch = (ch + 7) / 8 * 8;
     if (ch < 8) ch = 8;

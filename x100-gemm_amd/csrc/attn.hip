@@ -241,9 +241,12 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     att[(size_t)h * HD + t] = O / L;
 }
 
-// Chunking of 0..pos: about 512 blocks over the KV heads, at least 8 positions per chunk.  Since
-// CH >= n_pos / target and CH >= 8, nch <= min(target, ceil(n_pos / 8)) for every n_pos.
-int chunk_target(int n_kv) { return n_kv >= 512 ? 1 : 512 / n_kv; }
+// Chunking of 0..pos: about 256 blocks over the KV heads, at least 8 positions per chunk (512
+// blocks made each block's fixed cost, the merge and the partial stores, and the combine's chunk
+// loop weigh more: a Qwen3 layer took 51.0 / 54.2 us at 1024 / 4096 positions against 48.1 /
+// 52.9 us; 128 blocks: 48.5 / 58.4 us).  Since CH >= n_pos / target and CH >= 8,
+// nch <= min(target, ceil(n_pos / 8)) for every n_pos.
+int chunk_target(int n_kv) { return n_kv >= 256 ? 1 : 256 / n_kv; }
 void chunks(int n_pos, int n_kv, int &CH, int &nch)
 {
     const int target = chunk_target(n_kv);
