@@ -45,40 +45,6 @@ __global__ __launch_bounds__(NT) void k_rmsnorm(float *__restrict__ x, const flo
     for (int i = threadIdx.x; i < n; i += NT) out[i] = x[i] * s * w[i];
 }
 
-// Per-head RMSNorm and RoPE (qwen_moe.c:284-285; rope table qwen_moe_hp.c:799-804) and the KV-cache
-// write.  Block b < n_head: query head b, in place.  Block n_head + j: key head j, written to
-// kc[j][pos]; value head j copied to vc[j][pos].  Lane i rotates the pair (i, i + HD/2).
-// fr = base^(-2i/hd) with the exponent in fp32 and a = pos*fr in fp32, as the reference; pow, cos
-// and sin are evaluated in double and rounded once.
-__global__ __launch_bounds__(64) void k_qk_rope(float *__restrict__ q, const float *__restrict__ k,
-                                                const float *__restrict__ v, const float *__restrict__ q_norm,
-                                                const float *__restrict__ k_norm, int n_head, int ctx, int pos,
-                                                float eps, float base, float *__restrict__ kc,
-                                                float *__restrict__ vc)
-{
-    const int b = blockIdx.x, i = threadIdx.x;
-    const bool is_q = b < n_head;
-    const int j = b - n_head;
-    const float *src = is_q ? q + (size_t)b * HD : k + (size_t)j * HD;
-    float *dst = is_q ? q + (size_t)b * HD : kc + ((size_t)j * ctx + pos) * HD;
-    const float *w = is_q ? q_norm : k_norm;
-    const float x = src[i], y = src[i + HD / 2];
-    const float ss = wave_sum_bfly_f(x * x + y * y);
-    const float s = 1.0f / sqrtf(ss / (float)HD + eps);
-    const float a0 = x * s * w[i], a1 = y * s * w[i + HD / 2];
-    const float e = -2.0f * (float)i / (float)HD;
-    const float fr = (float)pow((double)base, (double)e);
-    const float ang = (float)pos * fr;
-    const float c = (float)cos((double)ang), sn = (float)sin((double)ang);
-    dst[i] = a0 * c - a1 * sn;
-    dst[i + HD / 2] = a0 * sn + a1 * c;
-    if (!is_q) {
-        float *vd = vc + ((size_t)j * ctx + pos) * HD;
-        vd[i] = v[(size_t)j * HD + i];
-        vd[i + HD / 2] = v[(size_t)j * HD + i + HD / 2];
-    }
-}
-
 // e^x evaluated in double and rounded once (the oracle does the same; libm's expf differs by at most
 // one ulp).
 X100_DEV float exp_r(float x) { return (float)exp((double)x); }
@@ -101,31 +67,19 @@ X100_DEV float sum8_all(float v)
 // head (online softmax).  The 8 groups are then merged, and lanes 0-7 write (m, l, o[128]) of each
 // head to part[head][c].
 template <int QPW>
-__global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, const float *__restrict__ kc,
-                                                   const float *__restrict__ vc, int gpr, int ctx, int n_pos, int CH,
-                                                   float scale, float *__restrict__ part)
+__global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, const float *__restrict__ k,
+                                                   const float *__restrict__ v, const float *__restrict__ q_norm,
+                                                   const float *__restrict__ k_norm, float eps, float base,
+                                                   float *__restrict__ kc, float *__restrict__ vc, int gpr, int ctx,
+                                                   int n_pos, int CH, float scale, float *__restrict__ part)
 {
     constexpr int DL = HD / 8;
-    const int kvh = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
+    __shared__ float s_q[4 * QPW][HD];   // the block's query heads after RMSNorm and RoPE
+    const int kvh = blockIdx.x, c = blockIdx.y, nch = gridDim.y, pos = n_pos - 1;
     const int lane = threadIdx.x & 63, w = wave_id(), grp = lane >> 3, sl = lane & 7;
     const int j0 = c * CH, j1 = min(j0 + CH, n_pos);
+    const bool has_pos = c == nch - 1;   // the chunk holding pos writes this KV head's cache rows
     const float *K = kc + (size_t)kvh * ctx * HD + sl * DL, *V = vc + (size_t)kvh * ctx * HD + sl * DL;
-
-    float qr[QPW][DL], m[QPW], l[QPW], o[QPW][DL];
-#pragma unroll
-    for (int g = 0; g < QPW; g++) {
-        const int hq = w + 4 * g;
-        const float *qh = q + ((size_t)kvh * gpr + min(hq, gpr - 1)) * HD + sl * DL;
-#pragma unroll
-        for (int t = 0; t < DL; t += 4) {
-            const float4 v4 = *(const float4 *)(qh + t);
-            qr[g][t] = v4.x; qr[g][t + 1] = v4.y; qr[g][t + 2] = v4.z; qr[g][t + 3] = v4.w;
-        }
-        m[g] = -FLT_MAX;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < DL; t++) o[g][t] = 0.0f;
-    }
 
     // The K / V rows of the next step are loaded before the current step is computed.
     float kr[DL], vr[DL], kn[DL], vn[DL];
@@ -139,7 +93,60 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, 
             vv[t] = b4.x; vv[t + 1] = b4.y; vv[t + 2] = b4.z; vv[t + 3] = b4.w;
         }
     };
-    load_rows(j0, kr, vr);
+    if (!has_pos) load_rows(j0, kr, vr);   // rows written before this launch: load at once
+
+    // Per-head RMSNorm and RoPE (qwen_moe.c:284-285; rope table qwen_moe_hp.c:799-804): lane i
+    // rotates the pair (i, i + HD/2), fr = base^(-2i/hd) with the exponent in fp32 and a = pos*fr in
+    // fp32, as the reference; pow, cos and sin are evaluated in double and rounded once.  Wave w takes the block's query heads w, w+4, ... (clamped: heads past gpr repeat the
+    // last and are not stored); in the chunk holding pos, wave 0 also writes this KV head's key row
+    // (normalised and rotated) and value row into the cache at pos and waits for the stores, which
+    // the barrier below orders before every wave's loads of that row.
+    {
+        const int i = lane;
+        const float e = -2.0f * (float)i / (float)HD;
+        const float fr = (float)pow((double)base, (double)e);
+        const float ang = (float)pos * fr;
+        const float cs = (float)cos((double)ang), sn = (float)sin((double)ang);
+        auto norm_rope = [&](const float *src, const float *wn, float &o0, float &o1) {
+            const float x = src[i], y = src[i + HD / 2];
+            const float ss = wave_sum_bfly_f(x * x + y * y);
+            const float s = 1.0f / sqrtf(ss / (float)HD + eps);
+            const float a0 = x * s * wn[i], a1 = y * s * wn[i + HD / 2];
+            o0 = a0 * cs - a1 * sn;
+            o1 = a0 * sn + a1 * cs;
+        };
+#pragma unroll
+        for (int g = 0; g < QPW; g++) {
+            const int hq = w + 4 * g;
+            float o0, o1;
+            norm_rope(q + ((size_t)kvh * gpr + min(hq, gpr - 1)) * HD, q_norm, o0, o1);
+            s_q[hq][i] = o0;
+            s_q[hq][i + HD / 2] = o1;
+        }
+        if (has_pos && w == 0) {
+            float o0, o1;
+            norm_rope(k + (size_t)kvh * HD, k_norm, o0, o1);
+            float *kd = kc + ((size_t)kvh * ctx + pos) * HD, *vd = vc + ((size_t)kvh * ctx + pos) * HD;
+            kd[i] = o0;
+            kd[i + HD / 2] = o1;
+            vd[i] = v[(size_t)kvh * HD + i];
+            vd[i + HD / 2] = v[(size_t)kvh * HD + i + HD / 2];
+            __builtin_amdgcn_s_waitcnt(0);   // the cache row is in memory before the barrier
+        }
+    }
+    __syncthreads();
+    if (has_pos) load_rows(j0, kr, vr);
+
+    float qr[QPW][DL], m[QPW], l[QPW], o[QPW][DL];
+#pragma unroll
+    for (int g = 0; g < QPW; g++) {
+#pragma unroll
+        for (int t = 0; t < DL; t++) qr[g][t] = s_q[w + 4 * g][sl * DL + t];
+        m[g] = -FLT_MAX;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < DL; t++) o[g][t] = 0.0f;
+    }
     for (int jb = j0; jb < j1; jb += 8) {
         const bool more = jb + 8 < j1;
         if (more) load_rows(jb + 8, kn, vn);
@@ -280,21 +287,21 @@ hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w
     if ((e = x100_qgemv_launch(c->wq_type, 1, qd, d, w->wq, hn, q, s)) != hipSuccess) return e;
     if ((e = x100_qgemv_launch(c->wk_type, 1, kvd, d, w->wk, hn, k, s)) != hipSuccess) return e;
     if ((e = x100_qgemv_launch(c->wv_type, 1, kvd, d, w->wv, hn, v, s)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_qk_rope, dim3(nh + nkv), dim3(64), 0, s, q, k, v, w->q_norm, w->k_norm, nh, c->ctx, pos,
-                       c->eps, c->rope_base, w->k_cache, w->v_cache);
+    // head norms, RoPE and the KV-cache write at pos run inside the attention blocks (k_attn_part)
     int CH, nch;
     chunks(pos + 1, nkv, CH, nch);
     const float scale = 1.0f / sqrtf((float)HD);
     const dim3 grid(nkv, nch);
+#define X100_ATTN(QPW)                                                                                  \
+    hipLaunchKernelGGL(k_attn_part<QPW>, grid, dim3(256), 0, s, q, k, v, w->q_norm, w->k_norm, c->eps,   \
+                       c->rope_base, w->k_cache, w->v_cache, gpr, c->ctx, pos + 1, CH, scale, part)
     if (gpr <= 4)
-        hipLaunchKernelGGL(k_attn_part<1>, grid, dim3(256), 0, s, q, w->k_cache, w->v_cache, gpr, c->ctx, pos + 1,
-                           CH, scale, part);
+        X100_ATTN(1);
     else if (gpr <= 8)
-        hipLaunchKernelGGL(k_attn_part<2>, grid, dim3(256), 0, s, q, w->k_cache, w->v_cache, gpr, c->ctx, pos + 1,
-                           CH, scale, part);
+        X100_ATTN(2);
     else
-        hipLaunchKernelGGL(k_attn_part<4>, grid, dim3(256), 0, s, q, w->k_cache, w->v_cache, gpr, c->ctx, pos + 1,
-                           CH, scale, part);
+        X100_ATTN(4);
+#undef X100_ATTN
     hipLaunchKernelGGL(k_attn_combine, dim3(nh), dim3(HD), 0, s, part, nch, att);
     if ((e = x100_qgemv_launch(c->wo_type, 1, d, qd, w->wo, att, o, s)) != hipSuccess) return e;
     // h += o, and hn = rmsnorm(h, ffn_norm) for the MoE block that follows (skipped without ffn_norm)
