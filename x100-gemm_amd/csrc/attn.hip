@@ -284,9 +284,15 @@ hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w
     hipLaunchKernelGGL(k_rmsnorm<1024>, dim3(1), dim3(1024), 0, s, h, (const float *)nullptr, w->attn_norm, c->eps,
                        d, hn);
     hipError_t e;
-    if ((e = x100_qgemv_launch(c->wq_type, 1, qd, d, w->wq, hn, q, s)) != hipSuccess) return e;
+    // q and v in one launch when they share a weight type that has the merged form (Q3_K in the
+    // mixed checkpoint), else one launch each
+    e = c->wq_type == c->wv_type ? x100_qgemv2_launch(c->wq_type, qd, w->wq, q, kvd, w->wv, v, d, hn, s)
+                                 : hipErrorNotSupported;
+    if (e != hipSuccess && e != hipErrorNotSupported) return e;
+    const bool qv = e == hipSuccess;
+    if (!qv && (e = x100_qgemv_launch(c->wq_type, 1, qd, d, w->wq, hn, q, s)) != hipSuccess) return e;
     if ((e = x100_qgemv_launch(c->wk_type, 1, kvd, d, w->wk, hn, k, s)) != hipSuccess) return e;
-    if ((e = x100_qgemv_launch(c->wv_type, 1, kvd, d, w->wv, hn, v, s)) != hipSuccess) return e;
+    if (!qv && (e = x100_qgemv_launch(c->wv_type, 1, kvd, d, w->wv, hn, v, s)) != hipSuccess) return e;
     // head norms, RoPE and the KV-cache write at pos run inside the attention blocks (k_attn_part)
     int CH, nch;
     chunks(pos + 1, nkv, CH, nch);

@@ -453,8 +453,9 @@ __global__ __launch_bounds__(1024) void k_q3_K4(const KqArgs a)
 // of row_shr:2 steps inside the wave, starting from 0.0f + t0 as the oracle does, and the row's
 // last unit writes y: no terms in LDS and no second barrier.  The weight loads of a wave cover
 // 32 / nsb consecutive rows of every super-block section (whole 128-byte lines).
+// bx: the block's index within its matrix (blockIdx.x, or less in k_kq_rm2).
 template <int MR, bool Q3>
-__global__ __launch_bounds__(512) void k_kq_rm(const KqArgs a)
+X100_DEV void kq_rm_body(const KqArgs &a, int bx)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int M = a.M, N = a.N, K = a.K, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
@@ -464,7 +465,7 @@ __global__ __launch_bounds__(512) void k_kq_rm(const KqArgs a)
     const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1;
     uint8_t *recs = smem;
     const int u0 = 32 * w + (lane >> 1), lgn = __builtin_ctz((unsigned)nsb);
-    const int rib = u0 >> lgn, sb = u0 & (nsb - 1), row0 = blockIdx.x * RB;
+    const int rib = u0 >> lgn, sb = u0 & (nsb - 1), row0 = bx * RB;
     const bool valid = rib < RB && row0 + rib < N;
     const int row = min(row0 + min(rib, RB - 1), N - 1);
 
@@ -571,6 +572,23 @@ __global__ __launch_bounds__(512) void k_kq_rm(const KqArgs a)
             }
         if (m < M && valid && h == 0 && sb == nsb - 1) y[(size_t)m * N + row] = acc;
     }
+}
+
+template <int MR, bool Q3>
+__global__ __launch_bounds__(512) void k_kq_rm(const KqArgs a)
+{
+    kq_rm_body<MR, Q3>(a, blockIdx.x);
+}
+
+// Two one-row products of one weight type and the same x in one launch (the decode layer's q and
+// v projections): blocks 0 .. nb0-1 compute a0, the rest a1, each block with its job's plan.
+// Every row's result is that of k_kq_rm (the quantizer's records do not depend on which waves
+// quantize them, and a row's sum is inside one wave).
+template <bool Q3>
+__global__ __launch_bounds__(512) void k_kq_rm2(const KqArgs a0, const KqArgs a1, int nb0)
+{
+    const bool first = (int)blockIdx.x < nb0;
+    kq_rm_body<1, Q3>(first ? a0 : a1, first ? (int)blockIdx.x : (int)blockIdx.x - nb0);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1071,6 +1089,26 @@ hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *
     return hipGetLastError();
 }
 
+// y0 = W0 x and y1 = W1 x for one token row, both Q4_K or both Q3_K with K / 256 in {1, 2, 4, 8},
+// in one launch of k_kq_rm2 (hipErrorNotSupported otherwise: the caller launches them one by one).
+template <bool Q3>
+hipError_t launch_kq2(int N0, const void *w0, float *y0, int N1, const void *w1, float *y1, int K, const float *x,
+                      hipStream_t s)
+{
+    const int nsb = K / 256;
+    KqPlan p0, p1;
+    if (K % 256 || !(nsb == 1 || nsb == 2 || nsb == 4 || nsb == 8) || !kq_plan(1, N0, K, p0) || !kq_plan(1, N1, K, p1))
+        return hipErrorNotSupported;
+    const KqArgs a0{1, N0, K, p0.rb, nsb, udiv16_magic((uint32_t)p0.rb), udiv16_magic((uint32_t)nsb),
+                    (const uint8_t *)w0, x, y0};
+    const KqArgs a1{1, N1, K, p1.rb, nsb, udiv16_magic((uint32_t)p1.rb), udiv16_magic((uint32_t)nsb),
+                    (const uint8_t *)w1, x, y1};
+    const int nb0 = (N0 + p0.rb - 1) / p0.rb, nb1 = (N1 + p1.rb - 1) / p1.rb;
+    hipLaunchKernelGGL(k_kq_rm2<Q3>, dim3(nb0 + nb1), dim3(64 * max(p0.nw, p1.nw)), (size_t)(nsb + 1) * KREC, s, a0,
+                       a1, nb0);
+    return hipGetLastError();
+}
+
 // Exhaustive check of the activation quantizer's division-free arithmetic (x100_common.h) on the
 // device: for every float u in [lo, hi] (bit patterns), cnt[0] counts rcp_rn_any(u) != 1.0f / u
 // (rcp_rn_any is rcp_rn from 2^-126 up, so this covers both), cnt[1] div127_rn(u) != u / 127.0f
@@ -1093,6 +1131,15 @@ __global__ __launch_bounds__(256) void k_check_quant_div(uint32_t lo, uint32_t h
 }
 
 }  // namespace
+
+hipError_t x100_qgemv2_launch(int qtype, int N0, const void *w0, float *y0, int N1, const void *w1, float *y1, int K,
+                              const float *x, hipStream_t s)
+{
+    if (N0 < 1 || N1 < 1) return hipErrorNotSupported;
+    if (qtype == X100_Q4_K) return launch_kq2<false>(N0, w0, y0, N1, w1, y1, K, x, s);
+    if (qtype == X100_Q3_K) return launch_kq2<true>(N0, w0, y0, N1, w1, y1, K, x, s);
+    return hipErrorNotSupported;
+}
 
 hipError_t x100_check_quant_div_launch(uint32_t lo, uint32_t hi, unsigned long long *cnt, hipStream_t s)
 {

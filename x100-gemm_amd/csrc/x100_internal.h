@@ -26,6 +26,11 @@ size_t x100_q_packed_bytes(int qtype, int N, int K);
 hipError_t x100_q_pack_launch(int qtype, int N, int K, const void *src, void *dst, hipStream_t s);
 hipError_t x100_qgemv_launch(int qtype, int M, int N, int K, const void *w, const float *x, float *y,
                              hipStream_t s);
+// Two one-row GEMVs of one weight type on the same x (packed weights w0: N0 x K, w1: N1 x K) in one
+// launch, each row's result that of x100_qgemv_launch; hipErrorNotSupported (nothing launched)
+// for shapes or types that have no merged form.
+hipError_t x100_qgemv2_launch(int qtype, int N0, const void *w0, float *y0, int N1, const void *w1, float *y1, int K,
+                              const float *x, hipStream_t s);
 // True when x100_qgemv_launch accepts the shape (it then launches without further checks).
 bool x100_qgemv_supported(int qtype, int M, int N, int K);
 hipError_t x100_check_quant_div_launch(uint32_t lo, uint32_t hi, unsigned long long *cnt, hipStream_t s);
