@@ -15,8 +15,8 @@
  * moe_pack_experts.  Any other bit is rejected (X100_EINVAL).  The results are the same, bit for
  * bit, in both layouts.
  * Activations are quantized to Q8_K per row (hn before gate/up, act before down) with the
- * scalar path's rounding; rows that pick the same expert share one pass over its weights (below
- * 5 token rows all rows at once; from 5 rows the (row, slot) pairs are grouped by expert into
+ * scalar path's rounding; rows that pick the same expert share one pass over its weights (up to
+ * 8 token rows all rows at once; from 9 rows the (row, slot) pairs are grouped by expert into
  * chunks of 32 on the matrix cores, the MUL_MAT_ID grouping of ime.cpp:667-697).  Each row's
  * result is the same as a one-row call's, bit for bit.
  *
@@ -86,7 +86,7 @@ int moe_layer_hip_noalloc(int M, int d, int ff, int n_exp, int n_act, const floa
  * same n_exp * rows * K / 256 * 144 bytes) in the tiled layout that moe_layer_hip* read with
  * X100_MOE_TILED: per 8 rows and super-block, the 16-byte pieces of the 8 blocks grouped by
  * position (the 8 headers, then bytes 0-15 of the 8 rows' qs, ...), so that the matrix-core path
- * (5 or more token rows) reads whole cache lines.  rows % 8 == 0, K % 256 == 0.  Asynchronous on
+ * (9 or more token rows) reads whole cache lines.  rows % 8 == 0, K % 256 == 0.  Asynchronous on
  * stream. */
 int moe_pack_experts(int n_exp, int rows, int K, const void *src, void *dst, void *stream);
 

@@ -82,6 +82,13 @@ def test_moe_m8_and_residual(dev):
     check(8, 128, 2048, 768, 8, seed=500, dev=dev, residual=True)
 
 
+@pytest.mark.parametrize("M", [5, 6, 7])
+def test_moe_five_to_seven_rows_qwen3_shape(dev, M):
+    # above 4 rows: two routing rows per wave, up to 56 union slots, and the fused down projection
+    # in two row groups of at most 32 pairs (7 rows: groups of 4 and 3)
+    check(M, 128, 2048, 768, 8, seed=540 + M, dev=dev)
+
+
 @pytest.mark.parametrize("M,n_exp,d,ff,n_act", [(1, 16, 512, 256, 4), (3, 16, 512, 256, 4),
                                                 (2, 8, 256, 512, 8), (5, 64, 1024, 512, 2),
                                                 (4, 200, 256, 256, 6),
@@ -103,8 +110,8 @@ def test_moe_repeat_calls_stable(dev):
 
 @pytest.mark.parametrize("M", [2, 4, 8])
 def test_moe_batched_rows_equal_single_rows(dev, M):
-    # Several token rows (union grouping, one-block top-k, fused or separate down + combine) must
-    # give every row exactly what a one-row call gives it (per-row routing and Q8_K quantization)
+    # Several token rows (union grouping, fused down in one or two row groups) must give every
+    # row exactly what a one-row call gives it (per-row routing and Q8_K quantization)
     L = layer(128, 2048, 768, 500, dev)
     hn = synth.normal_f32(800 + M, (M, 2048))
     out, sel, sw = gpu_moe(hn, L, 8, dev)
@@ -115,7 +122,7 @@ def test_moe_batched_rows_equal_single_rows(dev, M):
         assert np.array_equal(out[m].view(np.uint32), o1[0].view(np.uint32)), "row %d differs" % m
 
 
-# ---- 8 or more token rows: routing per 8-row chunk, pairs grouped by expert into chunks of 32 on
+# ---- 9 or more token rows: routing per 8-row chunk, pairs grouped by expert into chunks of 32 on
 # the matrix cores ----
 @pytest.mark.parametrize("M", [9, 12, 15, 16, 64, 512])
 def test_moe_many_rows_qwen3_shape(dev, M):
@@ -130,11 +137,13 @@ def test_moe_many_rows_small_shapes(dev, M, n_exp, d, ff, n_act):
     check(M, n_exp, d, ff, n_act, seed=620 + M + n_exp, dev=dev)
 
 
-@pytest.mark.parametrize("M,n_exp,d,ff,n_act", [(8, 16, 512, 4096, 4),    # 16 super-blocks of ff, two halves
-                                                (8, 200, 256, 256, 6)])
+@pytest.mark.parametrize("M,n_exp,d,ff,n_act", [(8, 16, 512, 4096, 4),    # union-slot down (ff of 16 super-blocks)
+                                                (8, 200, 256, 256, 6),     # fused down, two row groups
+                                                (6, 16, 512, 4096, 8)])    # 48 pairs, union-slot down
 def test_moe_eight_rows_small_shapes(dev, M, n_exp, d, ff, n_act):
-    # 8 rows on the matrix cores at small shapes (ff of 16 super-blocks: activations in two halves)
-    check(M, n_exp, d, ff, n_act, seed=780 + n_exp, dev=dev)
+    # 6 and 8 rows at small shapes: the fused down projection in row groups where it fits LDS,
+    # else the union-slot down kernel and the separate combine
+    check(M, n_exp, d, ff, n_act, seed=780 + n_exp + M, dev=dev)
 
 
 def test_moe_few_rows_large_ff(dev):
@@ -143,7 +152,7 @@ def test_moe_few_rows_large_ff(dev):
     check(3, 16, 512, 4096, 8, seed=790, dev=dev)
 
 
-@pytest.mark.parametrize("M", [3, 16])
+@pytest.mark.parametrize("M", [3, 8, 16])
 def test_moe_largest_hidden_and_ff(dev, M):
     # d = ff = 4096, the largest the kernels take: 16 super-blocks per row (router rows of 16
     # blocks per lane, 128 KiB of staged activations per matrix-core block)

@@ -1,8 +1,8 @@
 """Tiled expert layout (moe_pack_experts + X100_MOE_TILED): the regrouping against an independent
 numpy statement of the layout, and the MoE layer on tiled experts against the same layer on the
-ggml-layout experts, bit for bit, on every kernel path (few rows: persistent gate/up, fused down,
-union-slot down for large ff; 5 or more rows: the matrix-core kernels, activations in one or two
-halves), with and without the residual add."""
+ggml-layout experts, bit for bit, on every kernel path (up to 8 rows: persistent gate/up, fused
+down in one or two row groups, union-slot down for large ff; 9 or more rows: the matrix-core
+kernels, activations in one or two halves), with and without the residual add."""
 import numpy as np
 import pytest
 
@@ -93,11 +93,12 @@ def test_pack_rejects_bad_arguments(dev):
 CASES = [
     # (M, n_exp, d, ff, n_act): the Qwen3-30B-A3B layer on both paths
     (1, 128, 2048, 768, 8), (2, 128, 2048, 768, 8), (4, 128, 2048, 768, 8), (5, 128, 2048, 768, 8),
-    (8, 128, 2048, 768, 8), (33, 128, 2048, 768, 8), (64, 128, 2048, 768, 8),
+    (7, 128, 2048, 768, 8), (8, 128, 2048, 768, 8), (9, 128, 2048, 768, 8), (33, 128, 2048, 768, 8),
+    (64, 128, 2048, 768, 8),
     # small shapes, few and many rows
     (3, 16, 512, 256, 4), (4, 200, 256, 256, 6), (17, 64, 1024, 512, 2), (100, 8, 256, 256, 8),
     # ff of 16 super-blocks: union-slot down (few rows), two activation halves (matrix cores)
-    (3, 16, 512, 4096, 8), (8, 16, 512, 4096, 4),
+    (3, 16, 512, 4096, 8), (6, 16, 512, 4096, 8), (8, 16, 512, 4096, 4), (12, 16, 512, 4096, 4),
     # d = ff = 4096
     (3, 4, 4096, 4096, 2), (16, 4, 4096, 4096, 2),
 ]

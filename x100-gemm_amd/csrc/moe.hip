@@ -1,9 +1,9 @@
 // Qwen3-MoE decode layer (the FFN block of qwen_moe.c:294-311) for M token rows: the kernels below
-// for M < 5, and from 5 rows (moe_launch_mfma) the (row, slot) pairs grouped by expert into
+// for up to 8 rows, and from 9 rows (moe_launch_mfma) the (row, slot) pairs grouped by expert into
 // chunks of 32 on the matrix cores (k_moe_mfma).  Both give each row the same bits as a one-row
 // call.
 //
-// Below 5 rows, three or four launches on one stream; each kernel only reads what an earlier launch
+// Up to 8 rows, three or four launches on one stream; each kernel only reads what an earlier launch
 // wrote, so no block ever waits for, or signals, another block (no fences, no atomics):
 //   k_moe_route       router logits R.hn (one wave per expert and token row) and the Q8_K form of
 //                     every hn row.
@@ -14,9 +14,9 @@
 //                     MUL_MAT_ID grouping of ime.cpp:667-697), the next item's weights in flight
 //                     while the current one is computed, and writes SwiGLU(g, u) per (token row,
 //                     slot) pair.
-//   k_moe_down_fused  grid (FD_DN rows of d): every pair's activation row quantized to Q8_K in
-//                     LDS, the down projection of those rows for all pairs, and the weighted
-//                     combine in slot order, written to out.
+//   k_moe_down_fused  grid (FD_DN rows of d, row groups of at most 32 pairs): every pair's
+//                     activation row quantized to Q8_K in LDS, the down projection of those rows
+//                     for the group's pairs, and the weighted combine in slot order, written to out.
 //   k_moe_down        (when the fused form does not fit: large ff) grid (union slot, DN_ROWS rows
 //   + k_moe_combine   of d): the expert's activation rows in Q8_K, down projection, y per pair;
 //                     then out[m] (+)= sum_a w_a * y_a.
@@ -30,7 +30,7 @@ typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 constexpr int GU_ROWS = 8;    // gate/up rows of ff per work item
 constexpr int GU_NWV = 4;     // waves per block of k_moe_gate_up_p (one per token row for the routing)
 constexpr int DN_ROWS = 16;   // down rows of d per block
-constexpr int MF_MIN_ROWS = 5;   // token rows from which the expert products run on the matrix cores
+constexpr int MF_MIN_ROWS = 9;   // token rows from which the expert products run on the matrix cores
 
 // Workspace layout (device memory owned by the library, sized by x100_moe_workspace_bytes).
 struct MoeWs {
@@ -40,14 +40,14 @@ struct MoeWs {
     int *nuniq;           // [1]
     int *uniq;            // [P]          expert id of union slot u (P = M*n_act)
     int *ucnt;            // [P]          pairs in union slot u
-    int *upairs;          // [slot][8] pair ids (m*n_act + a) of union slot u, m ascending (M < 5);
-                          // [chunk][32] from 5 rows (chunks of up to 32 pairs per expert)
-    uint8_t *xrec;        // Q8_K of the hn rows: below 5 rows the records [M][nsb] (KREC bytes
-                          // each, x100_common.h); from 5 rows [M][rec] = q[nsb][256] |
+    int *upairs;          // [slot][8] pair ids (m*n_act + a) of union slot u, m ascending (up to
+                          // 8 rows); [chunk][32] from 9 rows (chunks of up to 32 pairs per expert)
+    uint8_t *xrec;        // Q8_K of the hn rows: up to 8 rows the records [M][nsb] (KREC bytes
+                          // each, x100_common.h); from 9 rows [M][rec] = q[nsb][256] |
                           // bsum[nsb][16] (int) | d[nsb] (float), rec rounded up to 16 bytes
     float *act;           // [P][ff]
     float *ydn;           // [P][d]
-    uint8_t *xact;        // [P][recf]: Q8_K of act row p (5 or more token rows), layout of xrec
+    uint8_t *xact;        // [P][recf]: Q8_K of act row p (9 or more token rows), layout of xrec
 };
 
 inline size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -491,7 +491,7 @@ X100_DEV void publish_routing(int M, int n_act, const RouteLds &rl, MoeWs ws, in
 }
 
 // ------------------------------------------------------------------------------------------------
-// 5 or more token rows (verify / prefill).  Routing per 8-row chunk of the grid (the same
+// 9 or more token rows (verify / prefill).  Routing per 8-row chunk of the grid (the same
 // route_block as above), written per row; then the pairs (row, slot) are grouped by expert (the
 // MUL_MAT_ID grouping of ime.cpp:667-697, qwen_moe_hp.c:1674-1700) into chunks of at most PCH
 // pairs per expert, in the union-slot format (uniq, ucnt, upairs) that k_moe_mfma reads.
@@ -589,28 +589,12 @@ __global__ __launch_bounds__(256) void k_moe_group(int P, int n_exp, MoeWs ws)
     group_pairs<PCH>(P, n_exp, [&](int p) { return ws.sel[p]; }, ws);
 }
 
-// Up to 8 token rows: k_moe_topk_rows and k_moe_group in one block (one launch fewer), the
-// grouping reading the selections from LDS.
-template <int PCH>
-__global__ __launch_bounds__(512) void k_moe_topk_group(int M, int n_exp, int n_act, MoeWs ws,
-                                                        int *__restrict__ sel_out, float *__restrict__ sw_out)
-{
-    __shared__ RouteLds rl;
-    route_block<8>(M, n_exp, n_act, ws.logits, rl);
-    const int t = threadIdx.x, P = M * n_act;
-    if (t < P) {
-        ws.sel[t] = rl.sel[t];
-        ws.sw[t] = rl.w[t];
-        if (sel_out) sel_out[t] = rl.sel[t];
-        if (sw_out) sw_out[t] = rl.w[t];
-    }
-    group_pairs<PCH>(P, n_exp, [&](int p) { return rl.sel[p]; }, ws);
-}
 
 // ------------------------------------------------------------------------------------------------
-// Gate/up for 1 .. 4 token rows, persistent: each block derives the routing of all M rows from the
-// logits once (route_block, one wave per row; block 0 publishes it for the down projection and the
-// caller) and stages the Q8_K records of all M rows in LDS, then walks the work items it =
+// Gate/up for 1 .. 8 token rows, persistent: each block derives the routing of all M rows from the
+// logits once (route_block, one wave per row, two per wave above 4 rows; block 0 publishes it for
+// the down projection and the caller) and stages the Q8_K records of all M rows in LDS (above 4
+// rows that makes 2 blocks per CU instead of 3), then walks the work items it =
 // blockIdx.x, + gridDim.x, ... (item = union slot u, GU_ROWS rows of ff).  The next item's weights
 // are staged into the second of two LDS buffers while the current item is computed, so a block
 // always has one item's weights in flight.  An item's expert rows of one matrix are one contiguous
@@ -620,7 +604,7 @@ __global__ __launch_bounds__(512) void k_moe_topk_group(int M, int n_exp, int n_
 // order and SwiGLU(g, u) written per (token row, slot) pair.
 // The weight DMA is issued from inline asm (dma16v) and waited for with an exact s_waitcnt: on
 // this GPU global stores count in vmcnt too, and only wave 0 stores act (one instruction per item,
-// cnt * GU_ROWS <= 32 values), so at the top of an item wave 0 lets its last store stay
+// cnt * GU_ROWS <= 64 values), so at the top of an item wave 0 lets its last store stay
 // outstanding.
 // ------------------------------------------------------------------------------------------------
 template <int UPL, int NWV, bool TL>
@@ -631,7 +615,6 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ RouteLds rl;
-    __shared__ int s_cnt[32], s_pairs[32 * 8];
     const int nsb = d / 256, P = M * n_act;
     const int t = threadIdx.x, lane = t & 63, w = wave_id(), h = lane & 1;
 
@@ -644,7 +627,9 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
     const int nch = nunits * 9, span = GU_ROWS * nsb * 9;   // 16-byte chunks: item, one matrix
     const uint32_t wbytes = (uint32_t)((nch + 63) / 64 * 1024);
     uint8_t *wl0 = smem + ((size_t)M * nsb * KREC + 1023) / 1024 * 1024;
-    float *tv = (float *)(wl0 + 2 * (size_t)wbytes);   // [4][2][GU_ROWS][nsb] + one spare
+    float *tv = (float *)(wl0 + 2 * (size_t)wbytes);   // [M][2][GU_ROWS][nsb] + one spare
+    int *s_cnt = (int *)(tv + M * 2 * GU_ROWS * nsb + 1);   // [union slot]: its number of pairs
+    int *s_pairs = s_cnt + min(P, n_exp);                    // [union slot][8]: its pairs
     const uint32_t wlds = lds_addr(wl0);
 
     // Weight blocks of item `it` into buffer b: DMA op i copies chunks 64i .. 64i+63 of the gate
@@ -686,7 +671,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
 
         const int u = it / nrg, r0 = (it - u * nrg) * GU_ROWS, cnt = s_cnt[u];
         const uint8_t *wl = wl0 + (size_t)b * wbytes;
-        const int tv_spare = 4 * 2 * GU_ROWS * nsb;
+        const int tv_spare = M * 2 * GU_ROWS * nsb;
 #pragma unroll
         for (int c = 0; c < UPL; c++) {
             // unit un = (matrix, row, super-block) in that order; tiled, the lanes take the units
@@ -721,7 +706,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
             }
         }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        // g, u sequential over super-blocks; SwiGLU (qwen_moe.c:309): wave 0 only (cnt * GU_ROWS <= 32)
+        // g, u sequential over super-blocks; SwiGLU (qwen_moe.c:309): wave 0 only (cnt * GU_ROWS <= 64)
         if (t < cnt * GU_ROWS) {
             const int k = t / GU_ROWS, r = t - k * GU_ROWS;
             const float *tg = tv + k * 2 * GU_ROWS * nsb + r * nsb;
@@ -737,7 +722,7 @@ __global__ __launch_bounds__(64 * NWV) void k_moe_gate_up_p(int M, int d, int ff
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Q8_K of every pair's activation row, once (5 or more token rows): wave q quantizes block
+// Q8_K of every pair's activation row, once (9 or more token rows): wave q quantizes block
 // q % nsf of pair q / nsf with q8_K_wave, into the pair's record of ws.xact.
 __global__ __launch_bounds__(256) void k_moe_act_q8k(int P, int ff, MoeWs ws)
 {
@@ -1033,8 +1018,9 @@ __global__ __launch_bounds__(256) void k_moe_down(int d, int ff, const uint8_t *
 }
 
 // ------------------------------------------------------------------------------------------------
-// Down projection and weighted combine in one launch.  grid = d / DN blocks; a block owns DN output
-// rows for every (token row m, slot a) pair p = m*n_act + a.  Units (pair p, row r, super-block
+// Down projection and weighted combine in one launch.  grid (d / DN, row groups of rg token rows);
+// a block owns DN output rows for every (token row m, slot a) pair p = m*n_act + a of its row group
+// (at most 32 pairs; the pairs below are the group's).  Units (pair p, row r, super-block
 // sb) = P*DN*nsf in that order, two lanes each (halves of the Q4_K block), UPL units per lane
 // pair: the unit's expert is sel[p] and its activation row is act[p] (an expert chosen by several
 // token rows is read once per pair, the repeats mostly from cache), so the activation loads depend
@@ -1060,7 +1046,7 @@ X100_DEV void vm_wait_upto(int n)
 }
 
 template <int UPL, bool TL>
-__global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, int n_exp, int n_act, uint32_t mnsf,
+__global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int rg, int d, int ff, int n_exp, int n_act, uint32_t mnsf,
                                                         uint32_t mdn, uint32_t mspan, const uint8_t *__restrict__ Wd, MoeWs ws,
                                                         float *__restrict__ out, int residual)
 {
@@ -1069,7 +1055,8 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, i
     __shared__ float s_y[32][FD_DN];
     __shared__ float s_w[32];
     const int lane = threadIdx.x & 63, w = wave_id(), h = lane & 1, nw = blockDim.x >> 6;
-    const int P = M * n_act;
+    const int m0 = blockIdx.y * rg, Mg = min(rg, M - m0);   // the group's token rows
+    const int P = Mg * n_act, p0 = m0 * n_act;               // its pairs: p0 .. p0 + P - 1
     const int nsf = ff / 256;
     const int r0 = blockIdx.x * DN;
     const int nunits = P * DN * nsf, nq = P * nsf;
@@ -1090,7 +1077,7 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, i
         // The activation rows were written by the previous launch, so every load is a round trip
         // to memory: the loads of four passes are issued before the first is quantized (passes past
         // the last record read out of range, which returns zeros and touches no memory).
-        const rsrc_t ar = buf_rsrc(ws.act, (uint32_t)(P * ff) * 4u);
+        const rsrc_t ar = buf_rsrc(ws.act + (size_t)p0 * ff, (uint32_t)(P * ff) * 4u);
         const int step = 4 * max(nwq, 1);
         for (int qb0 = 4 * w; qb0 < nq; qb0 += 4 * step) {
             float4 v[4][4];
@@ -1115,7 +1102,7 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, i
     const int I1 = min(nops, (pa * span + 63) / 64);                // operations those pairs need
     int nlate = 0;
     if (w >= nwq) {
-        const int selv = (int)min((unsigned)ws.sel[min(lane, P - 1)], (unsigned)(n_exp - 1));
+        const int selv = (int)min((unsigned)ws.sel[p0 + min(lane, P - 1)], (unsigned)(n_exp - 1));
         const int j = w - nwq;
         for (int i = j; i < nops; i += ndw) {
             const int c = min(i * 64 + lane, nch - 1);
@@ -1132,7 +1119,7 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, i
             nlate = i0 < nops ? (nops - 1 - i0) / ndw + 1 : 0;
         }
     }
-    if ((int)threadIdx.x < P) s_w[threadIdx.x] = ws.sw[threadIdx.x];
+    if ((int)threadIdx.x < P) s_w[threadIdx.x] = ws.sw[p0 + threadIdx.x];
     if constexpr (SPLIT) {
         vm_wait_upto(nlate);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -1192,11 +1179,11 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int d, int ff, i
     }
     __syncthreads();
     // out[m][row] (+)= sum over slots a of w_a * y_a, a ascending (qwen_moe.c:310-311)
-    for (int t = threadIdx.x; t < M * DN; t += blockDim.x) {
+    for (int t = threadIdx.x; t < Mg * DN; t += blockDim.x) {
         const int m = t / DN, r = t - m * DN;
         float eo = 0.0f;
         for (int a = 0; a < n_act; a++) eo = eo + s_w[m * n_act + a] * s_y[m * n_act + a][r];
-        float *o = out + (size_t)m * d + r0 + r;
+        float *o = out + (size_t)(m0 + m) * d + r0 + r;
         *o = residual ? *o + eo : eo;
     }
 }
@@ -1241,10 +1228,10 @@ MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *
     ws.nuniq = (int *)take(sizeof(int));
     ws.uniq = (int *)take(sizeof(int) * P);
     ws.ucnt = (int *)take(sizeof(int) * P);
-    // union slots of 8 (M < 5: at most P of them) or chunks of 32 (at most P/32 + n_exp + 1, and
+    // union slots of 8 (up to 8 rows: at most P of them) or chunks of 32 (at most P/32 + n_exp + 1, and
     // at most P)
     ws.upairs = (int *)take(sizeof(int) * ((size_t)P * 8 + 32 * (size_t)n_exp + 32));
-    // hn records: Q8_K records [M][nsb] (below 5 rows) or per-row records (the matrix-core path)
+    // hn records: Q8_K records [M][nsb] (up to 8 rows) or per-row records (the matrix-core path)
     ws.xrec = (uint8_t *)take(max((size_t)M * q8k_rec_bytes(nsb), (size_t)M * nsb * KREC));
     ws.act = (float *)take(sizeof(float) * (size_t)P * ff);
     ws.ydn = (float *)take(sizeof(float) * (size_t)P * d);
@@ -1268,7 +1255,7 @@ void route_rows(int M, int d, int n_exp, const float *hn, const float *R, MoeWs 
         hipLaunchKernelGGL((k_moe_route_rows<16, false>), g, dim3(256), 0, s, M, d, n_exp, epw, hn, R, ws);
 }
 
-// Five or more token rows, on the matrix cores: router logits and Q8_K records per 4-row chunk,
+// Nine or more token rows, on the matrix cores: router logits and Q8_K records per 4-row chunk,
 // softmax / top-k per 8-row chunk, the pairs grouped by expert into chunks of 32, gate/up + SwiGLU
 // and the down projection by k_moe_mfma, then the weighted combine.
 template <bool TL>
@@ -1279,12 +1266,8 @@ hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const flo
     const int nsb = d / 256, nsf = ff / 256, P = M * n_act, nrc = (M + 7) / 8;
     const int Vmax = min(P, (P + MF_PCH - 1) / MF_PCH + n_exp);
     route_rows(M, d, n_exp, hn, R, ws, s);
-    if (M <= 8) {
-        hipLaunchKernelGGL(k_moe_topk_group<MF_PCH>, dim3(1), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
-    } else {
-        hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
-        hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
-    }
+    hipLaunchKernelGGL(k_moe_topk_rows, dim3(nrc), dim3(512), 0, s, M, n_exp, n_act, ws, sel, sw);
+    hipLaunchKernelGGL(k_moe_group<MF_PCH>, dim3(1), dim3(256), 0, s, P, n_exp, ws);
     hipLaunchKernelGGL((k_moe_mfma<true, TL, 1>), dim3(Vmax, ff / 64), dim3(256), (size_t)mf_half(nsb) * 8192, s, d,
                        ff, n_act, (const uint8_t *)Wg, (const uint8_t *)Wu, ws);
     hipLaunchKernelGGL(k_moe_act_q8k, dim3((P * nsf + 3) / 4), dim3(256), 0, s, P, ff, ws);
@@ -1320,7 +1303,8 @@ hipError_t moe_launch_few(int M, int d, int ff, int n_exp, int n_act, const floa
     const uint8_t *wg = (const uint8_t *)Wg, *wu = (const uint8_t *)Wu;
     const size_t lds_gp = ((size_t)M * nsb * KREC + 1023) / 1024 * 1024 +                // hn records
                           2 * (((size_t)2 * GU_ROWS * nsb * 9 + 63) / 64 * 1024) +       // weight blocks x 2
-                          ((size_t)4 * 2 * GU_ROWS * nsb + 1) * 4;                        // terms
+                          ((size_t)M * 2 * GU_ROWS * nsb + 1) * 4 +                       // terms
+                          (size_t)Umax * 9 * 4;                                           // slot lists
     const int upl_gu = (2 * 2 * GU_ROWS * nsb + 64 * GU_NWV - 1) / (64 * GU_NWV);   // two lanes per unit
 #define X100_GU(U)                                                                                       \
     do {                                                                                                 \
@@ -1338,23 +1322,25 @@ hipError_t moe_launch_few(int M, int d, int ff, int n_exp, int n_act, const floa
 
     {
         // down + combine in one launch (k_moe_down_fused) when the units fit two per lane pair in
-        // 16 waves and the activation records fit LDS (every block quantizes all P rows);
-        // otherwise k_moe_down, then k_moe_combine
+        // 16 waves and the activation records fit LDS (every block quantizes all pairs of its row
+        // group); otherwise k_moe_down, then k_moe_combine.  Row groups: the fewest groups of at
+        // most 32 pairs, rows spread evenly over them (8 rows of 8 slots: two groups of 4).
         const int dn = FD_DN;
-        const int P = M * n_act, nq = P * nsf, nun = P * dn * nsf;
+        const int ng = (M * n_act + 31) / 32, rg = (M + ng - 1) / ng;
+        const int P = rg * n_act, nq = P * nsf, nun = P * dn * nsf;
         const int upl = (2 * nun + 1023) / 1024;
         const int nwf = (2 * nun + 64 * upl - 1) / (64 * upl);
         const size_t ldsf = (size_t)nq * KREC + ((size_t)nun * 9 + 63) / 64 * 1024 + ((size_t)nun + 1) * 4;
-        if (M <= 4 && P <= 32 && d % dn == 0 && upl <= 2 && ldsf <= 160 * 1024) {
-            const dim3 gf(d / dn), bf(64 * nwf);
+        if (P <= 32 && d % dn == 0 && upl <= 2 && ldsf <= 160 * 1024) {
+            const dim3 gf(d / dn, (M + rg - 1) / rg), bf(64 * nwf);
             const uint32_t mnsf = udiv16_magic((uint32_t)nsf), mdn = udiv16_magic((uint32_t)(dn * nsf));
             const uint32_t mspan = udiv16_magic((uint32_t)(dn * nsf * 9));
             if (upl == 1)
-                hipLaunchKernelGGL((k_moe_down_fused<1, TL>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn, mspan,
-                                   (const uint8_t *)Wd, ws, out, residual);
+                hipLaunchKernelGGL((k_moe_down_fused<1, TL>), gf, bf, ldsf, s, M, rg, d, ff, n_exp, n_act, mnsf, mdn,
+                                   mspan, (const uint8_t *)Wd, ws, out, residual);
             else
-                hipLaunchKernelGGL((k_moe_down_fused<2, TL>), gf, bf, ldsf, s, M, d, ff, n_exp, n_act, mnsf, mdn, mspan,
-                                   (const uint8_t *)Wd, ws, out, residual);
+                hipLaunchKernelGGL((k_moe_down_fused<2, TL>), gf, bf, ldsf, s, M, rg, d, ff, n_exp, n_act, mnsf, mdn,
+                                   mspan, (const uint8_t *)Wd, ws, out, residual);
             return hipGetLastError();
         }
     }
