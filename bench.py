@@ -119,6 +119,38 @@ class Timer:
         t.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (replays * len(fns))
 
+    def graph_ab(self, fns_a, fns_b, rounds=5, replays=3):
+        """Two captured graphs timed in alternation (rounds x replays each): the medians of their
+        microseconds per fn, so that neither gains from going first on a clock that is still
+        settling."""
+        t = self.torch
+        graphs = []
+        for fns in (fns_a, fns_b):
+            for f in fns[:2]:
+                f()
+            t.cuda.synchronize()
+            g = t.cuda.CUDAGraph()
+            side = t.cuda.Stream()
+            with t.cuda.stream(side):
+                with t.cuda.graph(g, stream=side):
+                    for f in fns:
+                        f()
+            t.cuda.synchronize()
+            g.replay()
+            t.cuda.synchronize()
+            graphs.append((g, len(fns)))
+        res = ([], [])
+        for _ in range(rounds):
+            for k, (g, n) in enumerate(graphs):
+                e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(replays):
+                    g.replay()
+                e1.record()
+                t.cuda.synchronize()
+                res[k].append(e0.elapsed_time(e1) * 1e3 / (replays * n))
+        return float(np.median(res[0])), float(np.median(res[1]))
+
     def single(self, fn, reps=10):
         """Isolated-launch latency: synchronise around every call."""
         t = self.torch
@@ -555,7 +587,7 @@ def bench_extra(torch, timer, dev, args, ceil):
     torch.cuda.synchronize()
     dR = torch.from_numpy(R).to(dev)
     n_h = 48
-    for M in (1, 4, 8):   # decode, and speculative verify of 4 and 8 rows (8: on the matrix cores)
+    for M in (1, 4, 8):   # decode, and speculative verify of 4 and 8 rows
         hns = synth.normal_f32(900 + M, (n_h, M, d))
         dh = torch.from_numpy(hns).to(dev)
         out = torch.empty((M, d), dtype=torch.float32, device=dev)
@@ -575,8 +607,8 @@ def bench_extra(torch, timer, dev, args, ceil):
             call(i, True)
         torch.cuda.synchronize()
         U = np.array([len(set(r.ravel().tolist())) for r in sel.cpu().numpy()])
-        us = timer.graph([lambda i=i: call(i) for i in range(n_h)])
-        us_ggml = timer.graph([lambda i=i: call(i, tiled=False) for i in range(n_h)])
+        us, us_ggml = timer.graph_ab([lambda i=i: call(i) for i in range(n_h)],
+                                    [lambda i=i: call(i, tiled=False) for i in range(n_h)])
         lat = timer.single(lambda: call(0))
         byts = float(n_exp * d * 4 + U.mean() * 3 * (ff * d // 256 * 144) + M * d * 4 * 2)
         cpu_us = cpu_time(lambda: ol.moe_layer(hns[0], R, Wg, Wu, Wd, n_act), min_s=0.3)
@@ -608,8 +640,8 @@ def bench_extra(torch, timer, dev, args, ceil):
             callm(i, True)
         torch.cuda.synchronize()
         U = np.array([len(set(r.ravel().tolist())) for r in sel.cpu().numpy()])
-        us = timer.graph([lambda i=i: callm(i) for i in range(n_h)])
-        us_ggml = timer.graph([lambda i=i: callm(i, tiled=False) for i in range(n_h)])
+        us, us_ggml = timer.graph_ab([lambda i=i: callm(i) for i in range(n_h)],
+                                    [lambda i=i: callm(i, tiled=False) for i in range(n_h)])
         byts = float(n_exp * d * 4 + U.mean() * 3 * (ff * d // 256 * 144) + M * d * 4 * 2)
         cpu_us = cpu_time(lambda: ol.moe_layer(hns[0][:8], R, Wg, Wu, Wd, n_act), min_s=0.3) * M / 8
         key = "moe_layer_qwen3_30b_a3b_m%d" % M
