@@ -96,8 +96,9 @@ class Timer:
         t.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / reps   # microseconds per call
 
-    def graph(self, fns, replays=3):
-        """Capture fns back to back in one graph; microseconds per fn, averaged over replays."""
+    def graph(self, fns, replays=3, rounds=5):
+        """Capture fns back to back in one graph; microseconds per fn: the median over rounds of the
+        average over replays."""
         t = self.torch
         for f in fns[:2]:
             f()
@@ -111,13 +112,16 @@ class Timer:
         t.cuda.synchronize()
         g.replay()
         t.cuda.synchronize()
-        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(replays):
-            g.replay()
-        e1.record()
-        t.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (replays * len(fns))
+        res = []
+        for _ in range(rounds):
+            e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(replays):
+                g.replay()
+            e1.record()
+            t.cuda.synchronize()
+            res.append(e0.elapsed_time(e1) * 1e3 / (replays * len(fns)))
+        return float(np.median(res))
 
     def graph_ab(self, fns_a, fns_b, rounds=5, replays=3):
         """Two captured graphs timed in alternation (rounds x replays each): the medians of their
