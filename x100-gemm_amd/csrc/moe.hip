@@ -149,17 +149,20 @@ X100_DEV float swiglu(float g, float u)
 // pulls its router rows and hn through its own load path): M = 1 15.85 -> 15.67 us against 4
 // waves per block; 1 wave per block was as fast at M = 1 but slower at M = 4.  A block that holds
 // both kinds of wave (n_exp * M odd) works as before: its quantizer wave loads no router row, takes
-// part in the hn DMA and the barrier, and skips the dot.
+// part in the hn DMA and the barrier, and skips the dot.  A block stages only the hn rows of its
+// own waves (at most RT_WPB rows; all M rows had made M = 8 1.5 us slower: 64 KiB of DMA per block).
 // ------------------------------------------------------------------------------------------------
 constexpr int RT_WPB = 2;
 __global__ __launch_bounds__(64 * RT_WPB) void k_moe_route(int M, int d, int n_exp, uint32_t mnsb, const float *__restrict__ hn,
                                                    const float *__restrict__ R, MoeWs ws)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    float4 *s_hn = (float4 *)smem;   // [M][d/4]
+    float4 *s_hn = (float4 *)smem;   // [min(M, RT_WPB)][d/4]: the hn rows of the block's router waves
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * RT_WPB + wave_id();
+    const int g0 = blockIdx.x * RT_WPB, wave = g0 + wave_id();
     const int nsb = d / 256, nq = M * nsb, nrw = n_exp * M;
+    // wave g works on token row g % M, so the block's waves need rows g0 % M, (g0 + 1) % M, ...:
+    // min(M, RT_WPB) of them
 
     if (wave >= nrw) {   // quantizer waves (wave-uniform)
         const int qb = 4 * (wave - nrw);
@@ -179,13 +182,22 @@ __global__ __launch_bounds__(64 * RT_WPB) void k_moe_route(int M, int d, int n_e
 #pragma unroll
     for (int j = 0; j < 16; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
 
-    // hn -> LDS (all M rows; M*d/256 chunks of 1 KiB, one wave each), asynchronous.
-    for (int ch = wave_id(); ch < M * nsb; ch += RT_WPB)
-        dma_1k(hn + (size_t)ch * 256 + 4 * lane, smem + ch * 1024);
+    // hn -> LDS (the block's rows: nrb * d/256 chunks of 1 KiB, one wave each), asynchronous.  Up to
+    // RT_WPB rows these are all M rows in order (slot = row); above, slot i holds row (g0 + i) % M.
+    if (M <= RT_WPB) {
+        for (int ch = wave_id(); ch < M * nsb; ch += RT_WPB)
+            dma_1k(hn + (size_t)ch * 256 + 4 * lane, smem + ch * 1024);
+    } else {
+        const int r0 = g0 % M;
+        for (int ch = wave_id(); ch < RT_WPB * nsb; ch += RT_WPB) {
+            const int sl = (int)udiv16((uint32_t)ch, (uint32_t)nsb, mnsb), r = r0 + sl;
+            dma_1k(hn + (size_t)(r < M ? r : r - M) * d + (ch - sl * nsb) * 256 + 4 * lane, smem + ch * 1024);
+        }
+    }
     __syncthreads();
 
     if (wave < nrw) {
-        const float4 *h = s_hn + m * (d / 4);
+        const float4 *h = s_hn + (M <= RT_WPB ? m : wave_id()) * (d / 4);
         float sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; j++)
@@ -1292,7 +1304,7 @@ hipError_t moe_launch_few(int M, int d, int ff, int n_exp, int n_act, const floa
     const int Umax = min(M * n_act, n_exp);
 
     const int nwaves = n_exp * M + (M * nsb + 3) / 4;   // router waves, then quantizer waves of four records
-    hipLaunchKernelGGL(k_moe_route, dim3((nwaves + RT_WPB - 1) / RT_WPB), dim3(64 * RT_WPB), (size_t)M * d * 4, s, M, d, n_exp,
+    hipLaunchKernelGGL(k_moe_route, dim3((nwaves + RT_WPB - 1) / RT_WPB), dim3(64 * RT_WPB), (size_t)min(M, RT_WPB) * d * 4, s, M, d, n_exp,
                        udiv16_magic((uint32_t)nsb), hn, R, ws);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
