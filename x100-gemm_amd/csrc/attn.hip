@@ -9,6 +9,8 @@
 
 #include <algorithm>
 
+#include <cmath>
+
 #include "x100_common.h"
 #include "x100_internal.h"
 
@@ -66,10 +68,17 @@ X100_DEV float sum8_all(float v)
 // dimensions of K_j and V_j, keeping a running maximum m, sum l and output o per position group and
 // head (online softmax).  The 8 groups are then merged, and lanes 0-7 write (m, l, o[128]) of each
 // head to part[head][c].
+// The rotation of the token's position for every pair (i, i + HD/2), passed by value in the kernel
+// arguments: the launcher builds it on the host once per call, as the reference builds its rope
+// table there (qwen_moe_hp.c:799-804).
+struct RopeTab {
+    float cs[HD / 2], sn[HD / 2];
+};
+
 template <int QPW>
 __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, const float *__restrict__ k,
                                                    const float *__restrict__ v, const float *__restrict__ q_norm,
-                                                   const float *__restrict__ k_norm, float eps, float base,
+                                                   const float *__restrict__ k_norm, float eps, const RopeTab rt,
                                                    float *__restrict__ kc, float *__restrict__ vc, int gpr, int ctx,
                                                    int n_pos, int CH, float scale, float *__restrict__ part)
 {
@@ -96,17 +105,13 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ q, 
     if (!has_pos) load_rows(j0, kr, vr);   // rows written before this launch: load at once
 
     // Per-head RMSNorm and RoPE (qwen_moe.c:284-285; rope table qwen_moe_hp.c:799-804): lane i
-    // rotates the pair (i, i + HD/2), fr = base^(-2i/hd) with the exponent in fp32 and a = pos*fr in
-    // fp32, as the reference; pow, cos and sin are evaluated in double and rounded once.  Wave w takes the block's query heads w, w+4, ... (clamped: heads past gpr repeat the
+    // rotates the pair (i, i + HD/2) by the table's cos and sin.  Wave w takes the block's query heads w, w+4, ... (clamped: heads past gpr repeat the
     // last and are not stored); in the chunk holding pos, wave 0 also writes this KV head's key row
     // (normalised and rotated) and value row into the cache at pos and waits for the stores, which
     // the barrier below orders before every wave's loads of that row.
     {
         const int i = lane;
-        const float e = -2.0f * (float)i / (float)HD;
-        const float fr = (float)pow((double)base, (double)e);
-        const float ang = (float)pos * fr;
-        const float cs = (float)cos((double)ang), sn = (float)sin((double)ang);
+        const float cs = rt.cs[i], sn = rt.sn[i];
         auto norm_rope = [&](const float *src, const float *wn, float &o0, float &o1) {
             const float x = src[i], y = src[i + HD / 2];
             const float ss = wave_sum_bfly_f(x * x + y * y);
@@ -265,6 +270,21 @@ void chunks(int n_pos, int n_kv, int &CH, int &nch)
 
 constexpr size_t seg(size_t floats) { return (floats + 63) / 64 * 64; }   // 256-byte segments
 
+// fr = base^(-2i/hd) with the exponent in fp32, a = pos*fr in fp32, as the reference; pow, cos and
+// sin evaluated in double and rounded once (the oracle's orc_rope_table).
+RopeTab rope_table(int pos, float base)
+{
+    RopeTab t;
+    for (int i = 0; i < HD / 2; i++) {
+        const float e = -2.0f * (float)i / (float)HD;
+        const float fr = (float)std::pow((double)base, (double)e);
+        const float a = (float)pos * fr;
+        t.cs[i] = (float)std::cos((double)a);
+        t.sn[i] = (float)std::sin((double)a);
+    }
+    return t;
+}
+
 }  // namespace
 
 // Workspace floats: hn[d] q[qd] k[kvd] v[kvd] att[qd] o[d] part[n_head][nch_max][HD + 2].
@@ -297,10 +317,11 @@ hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w
     int CH, nch;
     chunks(pos + 1, nkv, CH, nch);
     const float scale = 1.0f / sqrtf((float)HD);
+    const RopeTab rt = rope_table(pos, c->rope_base);
     const dim3 grid(nkv, nch);
 #define X100_ATTN(QPW)                                                                                  \
-    hipLaunchKernelGGL(k_attn_part<QPW>, grid, dim3(256), 0, s, q, k, v, w->q_norm, w->k_norm, c->eps,   \
-                       c->rope_base, w->k_cache, w->v_cache, gpr, c->ctx, pos + 1, CH, scale, part)
+    hipLaunchKernelGGL(k_attn_part<QPW>, grid, dim3(256), 0, s, q, k, v, w->q_norm, w->k_norm, c->eps, rt, \
+                       w->k_cache, w->v_cache, gpr, c->ctx, pos + 1, CH, scale, part)
     if (gpr <= 4)
         X100_ATTN(1);
     else if (gpr <= 8)
