@@ -304,14 +304,20 @@ hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w
     hipLaunchKernelGGL(k_rmsnorm<1024>, dim3(1), dim3(1024), 0, s, h, (const float *)nullptr, w->attn_norm, c->eps,
                        d, hn);
     hipError_t e;
-    // q and v in one launch when they share a weight type that has the merged form (Q3_K in the
-    // mixed checkpoint), else one launch each
-    e = c->wq_type == c->wv_type ? x100_qgemv2_launch(c->wq_type, qd, w->wq, q, kvd, w->wv, v, d, hn, s)
-                                 : hipErrorNotSupported;
+    // q, v and k in one launch when q and v share a K-quant type and k is on the int8 path (Q3_K
+    // and Q8_0 in the mixed checkpoint, d = 2048); else q and v in one launch when they share a
+    // weight type that has the merged form; else one launch each
+    e = c->wq_type == c->wv_type
+            ? x100_qgemv3_launch(c->wq_type, qd, w->wq, q, kvd, w->wv, v, c->wk_type, kvd, w->wk, k, d, hn, s)
+            : hipErrorNotSupported;
     if (e != hipSuccess && e != hipErrorNotSupported) return e;
-    const bool qv = e == hipSuccess;
+    const bool qvk = e == hipSuccess;
+    e = !qvk && c->wq_type == c->wv_type ? x100_qgemv2_launch(c->wq_type, qd, w->wq, q, kvd, w->wv, v, d, hn, s)
+                                         : hipErrorNotSupported;
+    if (e != hipSuccess && e != hipErrorNotSupported) return e;
+    const bool qv = qvk || e == hipSuccess;
     if (!qv && (e = x100_qgemv_launch(c->wq_type, 1, qd, d, w->wq, hn, q, s)) != hipSuccess) return e;
-    if ((e = x100_qgemv_launch(c->wk_type, 1, kvd, d, w->wk, hn, k, s)) != hipSuccess) return e;
+    if (!qvk && (e = x100_qgemv_launch(c->wk_type, 1, kvd, d, w->wk, hn, k, s)) != hipSuccess) return e;
     if (!qv && (e = x100_qgemv_launch(c->wv_type, 1, kvd, d, w->wv, hn, v, s)) != hipSuccess) return e;
     // head norms, RoPE and the KV-cache write at pos run inside the attention blocks (k_attn_part)
     int CH, nch;

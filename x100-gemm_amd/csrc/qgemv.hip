@@ -650,10 +650,12 @@ X100_DEV float slot_sum(float v)
     return v;
 }
 
+// bx, gx: the block's index and the number of blocks among those that run this product (blockIdx.x
+// and gridDim.x, or less in k_kq_rm2_q8); the block takes row groups bx, bx + gx, ...
 template <int MR, int LPR, int RPW, int BPL, int XPT, int NT>
-__global__ __launch_bounds__(NT) void k_q8_0(int M, int N, int K, int ngroups, const uint16_t *__restrict__ wd,
-                                              const int8_t *__restrict__ wq, const float *__restrict__ x,
-                                              float *__restrict__ y)
+X100_DEV void q8_0_body(int M, int N, int K, int ngroups, const uint16_t *__restrict__ wd,
+                        const int8_t *__restrict__ wq, const float *__restrict__ x, float *__restrict__ y, int bx,
+                        int gx)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nb = K / 32;
@@ -673,7 +675,7 @@ __global__ __launch_bounds__(NT) void k_q8_0(int M, int N, int K, int ngroups, c
     float4 xv[XPT];
     x_load<XPT, NT>(xr, 0, xv);
 
-    int g = blockIdx.x;
+    int g = bx;
     I8Group<RPW, BPL> cur;
     i8_load_group<LPR, RPW, BPL, NT>(cur, g, N, nb, qr, dr, nblk);
 
@@ -685,9 +687,9 @@ __global__ __launch_bounds__(NT) void k_q8_0(int M, int N, int K, int ngroups, c
     }
     __syncthreads();
 
-    for (; g < ngroups; g += gridDim.x) {
+    for (; g < ngroups; g += gx) {
         I8Group<RPW, BPL> nxt;
-        i8_load_group<LPR, RPW, BPL, NT>(nxt, g + (int)gridDim.x, N, nb, qr, dr, nblk);
+        i8_load_group<LPR, RPW, BPL, NT>(nxt, g + gx, N, nb, qr, dr, nblk);
 
         float acc[RPW][MR];
 #pragma unroll
@@ -731,6 +733,30 @@ __global__ __launch_bounds__(NT) void k_q8_0(int M, int N, int K, int ngroups, c
         }
         cur = nxt;
     }
+}
+
+template <int MR, int LPR, int RPW, int BPL, int XPT, int NT>
+__global__ __launch_bounds__(NT) void k_q8_0(int M, int N, int K, int ngroups, const uint16_t *__restrict__ wd,
+                                              const int8_t *__restrict__ wq, const float *__restrict__ x,
+                                              float *__restrict__ y)
+{
+    q8_0_body<MR, LPR, RPW, BPL, XPT, NT>(M, N, K, ngroups, wd, wq, x, y, blockIdx.x, gridDim.x);
+}
+
+// A decoder layer's q, v and k projections in one launch: blocks 0 .. nb0-1 compute a0 and
+// nb0 .. nb01-1 a1 (one-row K-quant products, as k_kq_rm2), the rest the int8-path product of
+// one token row with the plan of k_q8_0<1, 16, 1, 4, 2, 256> (33 to 64 blocks of 32 per row); each
+// block does what it does in its own launch, so every result is that launch's.  256 threads.
+template <bool Q3>
+__global__ __launch_bounds__(256) void k_kq_rm2_q8(const KqArgs a0, const KqArgs a1, int nb0, int nb01, int N2,
+                                                   int ngroups2, const uint16_t *__restrict__ wd2,
+                                                   const int8_t *__restrict__ wq2, float *__restrict__ y2)
+{
+    const int b = blockIdx.x;
+    if (b < nb01)
+        kq_rm_body<1, Q3>(b < nb0 ? a0 : a1, b < nb0 ? b : b - nb0);
+    else
+        q8_0_body<1, 16, 1, 4, 2, 256>(1, N2, a0.K, ngroups2, wd2, wq2, a0.x, y2, b - nb01, (int)gridDim.x - nb01);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1109,6 +1135,34 @@ hipError_t launch_kq2(int N0, const void *w0, float *y0, int N1, const void *w1,
     return hipGetLastError();
 }
 
+// y0 = W0 x, y1 = W1 x (both Q4_K or both Q3_K) and y2 = W2 x (int8 path) for one token row in one
+// launch of k_kq_rm2_q8, when K = 2048 (the K-quant row-major form with 8 super-blocks and the
+// int8 plan that kernel instantiates) and both K-quant plans use 4 waves; hipErrorNotSupported
+// otherwise (nothing launched).
+template <bool Q3>
+hipError_t launch_kq2_q8(int N0, const void *w0, float *y0, int N1, const void *w1, float *y1, int N2, const void *w2,
+                         float *y2, int K, const float *x, hipStream_t s)
+{
+    const int nsb = K / 256, nb = K / 32;
+    KqPlan p0, p1;
+    if (K != 2048 || N2 < 1 || (size_t)N2 * nb >= ((size_t)1 << 27) || !kq_plan(1, N0, K, p0) || !kq_plan(1, N1, K, p1) ||
+        max(p0.nw, p1.nw) != 4)
+        return hipErrorNotSupported;
+    const KqArgs a0{1, N0, K, p0.rb, nsb, udiv16_magic((uint32_t)p0.rb), udiv16_magic((uint32_t)nsb),
+                    (const uint8_t *)w0, x, y0};
+    const KqArgs a1{1, N1, K, p1.rb, nsb, udiv16_magic((uint32_t)p1.rb), udiv16_magic((uint32_t)nsb),
+                    (const uint8_t *)w1, x, y1};
+    const int nb0 = (N0 + p0.rb - 1) / p0.rb, nb1 = (N1 + p1.rb - 1) / p1.rb;
+    // the int8 product as launch_q8_0_b lays it out: 16 rows per group (4 waves x 64 / 16 lanes),
+    // one block per group (fewer groups than resident blocks)
+    const size_t ngrp = (size_t)N2 * nb;
+    const int ngroups = (N2 + 15) / 16;
+    const size_t lds = max((size_t)(nsb + 1) * KREC, ((size_t)nb + 1) * 40);
+    hipLaunchKernelGGL(k_kq_rm2_q8<Q3>, dim3(nb0 + nb1 + ngroups), dim3(256), lds, s, a0, a1, nb0, nb0 + nb1, N2,
+                       ngroups, (const uint16_t *)w2, (const int8_t *)w2 + align256(ngrp * 2), y2);
+    return hipGetLastError();
+}
+
 // Exhaustive check of the activation quantizer's division-free arithmetic (x100_common.h) on the
 // device: for every float u in [lo, hi] (bit patterns), cnt[0] counts rcp_rn_any(u) != 1.0f / u
 // (rcp_rn_any is rcp_rn from 2^-126 up, so this covers both), cnt[1] div127_rn(u) != u / 127.0f
@@ -1138,6 +1192,16 @@ hipError_t x100_qgemv2_launch(int qtype, int N0, const void *w0, float *y0, int 
     if (N0 < 1 || N1 < 1) return hipErrorNotSupported;
     if (qtype == X100_Q4_K) return launch_kq2<false>(N0, w0, y0, N1, w1, y1, K, x, s);
     if (qtype == X100_Q3_K) return launch_kq2<true>(N0, w0, y0, N1, w1, y1, K, x, s);
+    return hipErrorNotSupported;
+}
+
+hipError_t x100_qgemv3_launch(int qtype, int N0, const void *w0, float *y0, int N1, const void *w1, float *y1,
+                              int qtype2, int N2, const void *w2, float *y2, int K, const float *x, hipStream_t s)
+{
+    if (N0 < 1 || N1 < 1 || !(qtype2 == X100_Q8_0 || qtype2 == X100_Q5_K || qtype2 == X100_Q6_K))
+        return hipErrorNotSupported;
+    if (qtype == X100_Q4_K) return launch_kq2_q8<false>(N0, w0, y0, N1, w1, y1, N2, w2, y2, K, x, s);
+    if (qtype == X100_Q3_K) return launch_kq2_q8<true>(N0, w0, y0, N1, w1, y1, N2, w2, y2, K, x, s);
     return hipErrorNotSupported;
 }
 
