@@ -301,17 +301,20 @@ hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w
     const int d = c->d, nh = c->n_head, nkv = c->n_head_kv, gpr = nh / nkv, qd = nh * HD, kvd = nkv * HD;
     float *hn = ws, *q = hn + seg(d), *k = q + seg(qd), *v = k + seg(kvd), *att = v + seg(kvd),
           *o = att + seg(qd), *part = o + seg(d);
-    hipLaunchKernelGGL(k_rmsnorm<1024>, dim3(1), dim3(1024), 0, s, h, (const float *)nullptr, w->attn_norm, c->eps,
-                       d, hn);
     hipError_t e;
     // q, v and k in one launch when q and v share a K-quant type and k is on the int8 path (Q3_K
-    // and Q8_0 in the mixed checkpoint, d = 2048); else q and v in one launch when they share a
-    // weight type that has the merged form; else one launch each
-    e = c->wq_type == c->wv_type
-            ? x100_qgemv3_launch(c->wq_type, qd, w->wq, q, kvd, w->wv, v, c->wk_type, kvd, w->wk, k, d, hn, s)
+    // and Q8_0 in the mixed checkpoint, d = 2048), with the attention RMSNorm of h inside it; else
+    // the norm launch, then q and v in one launch when they share a weight type that has the
+    // merged form, else one launch each
+    e = c->wq_type == c->wv_type && w->attn_norm
+            ? x100_qgemv3_launch(c->wq_type, qd, w->wq, q, kvd, w->wv, v, c->wk_type, kvd, w->wk, k, d, h,
+                                 w->attn_norm, c->eps, s)
             : hipErrorNotSupported;
     if (e != hipSuccess && e != hipErrorNotSupported) return e;
     const bool qvk = e == hipSuccess;
+    if (!qvk)
+        hipLaunchKernelGGL(k_rmsnorm<1024>, dim3(1), dim3(1024), 0, s, h, (const float *)nullptr, w->attn_norm,
+                           c->eps, d, hn);
     e = !qvk && c->wq_type == c->wv_type ? x100_qgemv2_launch(c->wq_type, qd, w->wq, q, kvd, w->wv, v, d, hn, s)
                                          : hipErrorNotSupported;
     if (e != hipSuccess && e != hipErrorNotSupported) return e;

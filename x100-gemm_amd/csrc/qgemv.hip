@@ -453,9 +453,61 @@ __global__ __launch_bounds__(1024) void k_q3_K4(const KqArgs a)
 // of row_shr:2 steps inside the wave, starting from 0.0f + t0 as the oracle does, and the row's
 // last unit writes y: no terms in LDS and no second barrier.  The weight loads of a wave cover
 // 32 / nsb consecutive rows of every super-block section (whole 128-byte lines).
+// ------------------------------------------------------------------------------------------------
+// RMSNorm of one 2048-element row inside a 256-thread block, with the operations and order of
+// k_rmsnorm<1024> (attn.hip): virtual thread T < 1024 sums h[T]^2 and h[T + 1024]^2 from 0, the 64
+// virtual threads of a virtual wave reduce by wave_sum_bfly_f's butterfly, and the 16 wave sums are
+// added in order; s = 1 / sqrtf(sum / 2048 + eps) and hn = h * s * w.  Thread t holds virtual
+// threads 4t .. 4t+3 (its float4s at elements 4t and 1024 + 4t), so virtual lane 4 (t % 16) + j
+// pairs with its butterfly partners l^32, l^16, l^8, l^4 in threads t^8, t^4, t^2, t^1 (component
+// j) and with l^2, l^1 inside the thread.  Used where a row's norm is folded into its consumer.
+// ------------------------------------------------------------------------------------------------
+struct RmsRow {
+    float4 a, b;
+};
+X100_DEV void rms_load(const float *__restrict__ h, RmsRow &r)
+{
+    r.a = *(const float4 *)(h + 4 * threadIdx.x);
+    r.b = *(const float4 *)(h + 1024 + 4 * threadIdx.x);
+}
+// red: 16 floats of LDS; every thread of the block calls it (one barrier).
+X100_DEV float rms_scale(const RmsRow &r, float eps, float *red)
+{
+    float v[4] = {0.0f + r.a.x * r.a.x, 0.0f + r.a.y * r.a.y, 0.0f + r.a.z * r.a.z, 0.0f + r.a.w * r.a.w};
+    v[0] += r.b.x * r.b.x;
+    v[1] += r.b.y * r.b.y;
+    v[2] += r.b.z * r.b.z;
+    v[3] += r.b.w * r.b.w;
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] += dpp_f<0x128>(0.0f, v[j]);   // t^8 (row_ror:8 within 16)
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] += dpp_f<0x124>(0.0f, v[j]);   // t^4 (values now depend on t % 8)
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] += dpp_f<0x4E>(0.0f, v[j]);    // t^2
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] += dpp_f<0xB1>(0.0f, v[j]);    // t^1
+    const float u0 = v[0] + v[2], u1 = v[1] + v[3];                // virtual l^2
+    const float tot16 = u0 + u1;                                   // virtual l^1
+    if ((threadIdx.x & 15) == 0) red[threadIdx.x >> 4] = tot16;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) tot += red[k];
+    return 1.0f / sqrtf(tot / 2048.0f + eps);
+}
+X100_DEV void rms_apply(float4 &v, float s, const float4 g)
+{
+    v.x = v.x * s * g.x;
+    v.y = v.y * s * g.y;
+    v.z = v.z * s * g.z;
+    v.w = v.w * s * g.w;
+}
+
 // bx: the block's index within its matrix (blockIdx.x, or less in k_kq_rm2).
-template <int MR, bool Q3>
-X100_DEV void kq_rm_body(const KqArgs &a, int bx)
+// NORM (one token row, K = 2048, every record in the first two passes): a.x is the raw row h, and
+// the block applies RMSNorm with weights nrm (rms_scale, LDS at byte 4096) to the values it quantizes.
+template <int MR, bool Q3, bool NORM = false>
+X100_DEV void kq_rm_body(const KqArgs &a, int bx, const float *__restrict__ nrm = nullptr, float eps = 0.0f)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int M = a.M, N = a.N, K = a.K, RB = a.RB, nsb = a.nsb, nw = blockDim.x >> 6, nq = M * nsb;
@@ -476,8 +528,21 @@ X100_DEV void kq_rm_body(const KqArgs &a, int bx)
     // rotation is a permutation of the waves, so every record is still quantized once.
     const int qw = (w + nw - 2) % nw;
     const bool wq = 4 * qw < nq;   // the wave has records to quantize (wave-uniform)
+    RmsRow rr;
+    if constexpr (NORM) rms_load(x, rr);
     Q8kFirst xf;
     if (wq) q8k_first(xr, a, nq, nw, xf, qw);
+    float4 g0[4], g1[4];   // the norm weights of the values in xf (elements as q8k_load takes them)
+    if constexpr (NORM)
+        if (wq) {
+            const int e = 16 * (lane & 15);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int q0 = min(4 * qw + (lane >> 4), nq - 1), q1 = min(4 * (qw + nw) + (lane >> 4), nq - 1);
+                g0[c] = *(const float4 *)(nrm + q0 * 256 + e + 4 * c);
+                g1[c] = *(const float4 *)(nrm + q1 * 256 + e + 4 * c);
+            }
+        }
 
     v4i qv[4], hm = {};
     uint2 sv;
@@ -500,6 +565,16 @@ X100_DEV void kq_rm_body(const KqArgs &a, int bx)
     }
 
     __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the quantizer
+    if constexpr (NORM) {
+        const float sc = rms_scale(rr, eps, (float *)(smem + 4096));
+        if (wq) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) rms_apply(xf.v0[c], sc, g0[c]);
+            if (4 * (qw + nw) < nq)
+#pragma unroll
+                for (int c = 0; c < 4; c++) rms_apply(xf.v1[c], sc, g1[c]);
+        }
+    }
     if (wq) q8k_rest(xr, a, nq, nw, xf, recs, qw);
     __syncthreads();
     if (32 * w >= RB * nsb) return;   // waves past the block's units only quantized (wave-uniform)
@@ -652,10 +727,12 @@ X100_DEV float slot_sum(float v)
 
 // bx, gx: the block's index and the number of blocks among those that run this product (blockIdx.x
 // and gridDim.x, or less in k_kq_rm2_q8); the block takes row groups bx, bx + gx, ...
-template <int MR, int LPR, int RPW, int BPL, int XPT, int NT>
+// NORM (one token row, K = 2048, one pass of NT * XPT float4): x is the raw row h, and the block
+// applies RMSNorm with weights nrm (rms_scale, LDS at byte 4096) to the values it quantizes.
+template <int MR, int LPR, int RPW, int BPL, int XPT, int NT, bool NORM = false>
 X100_DEV void q8_0_body(int M, int N, int K, int ngroups, const uint16_t *__restrict__ wd,
                         const int8_t *__restrict__ wq, const float *__restrict__ x, float *__restrict__ y, int bx,
-                        int gx)
+                        int gx, const float *__restrict__ nrm = nullptr, float eps = 0.0f)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nb = K / 32;
@@ -672,14 +749,25 @@ X100_DEV void q8_0_body(int M, int N, int K, int ngroups, const uint16_t *__rest
 
     const int total4 = M * K / 4;
     const rsrc_t xr = buf_rsrc(x, (uint32_t)total4 * 16u);
+    RmsRow rr;
+    if constexpr (NORM) rms_load(x, rr);
     float4 xv[XPT];
     x_load<XPT, NT>(xr, 0, xv);
+    float4 gv[XPT];   // the norm weights of xv's elements
+    if constexpr (NORM)
+#pragma unroll
+        for (int i = 0; i < XPT; i++) gv[i] = *(const float4 *)(nrm + 4 * (threadIdx.x + NT * i));
 
     int g = bx;
     I8Group<RPW, BPL> cur;
     i8_load_group<LPR, RPW, BPL, NT>(cur, g, N, nb, qr, dr, nblk);
 
     __builtin_amdgcn_sched_barrier(0);   // keep the first group's loads ahead of the quantizer
+    if constexpr (NORM) {
+        const float sc = rms_scale(rr, eps, (float *)(smem + 4096));
+#pragma unroll
+        for (int i = 0; i < XPT; i++) rms_apply(xv[i], sc, gv[i]);
+    }
     q8_0_from_regs<XPT, NT, false, false>(xv, 0, total4, K, xlo, xhi, xd, xs);
     for (int c0 = NT * XPT; c0 < total4; c0 += NT * XPT) {
         x_load<XPT, NT>(xr, c0, xv);
@@ -747,16 +835,20 @@ __global__ __launch_bounds__(NT) void k_q8_0(int M, int N, int K, int ngroups, c
 // nb0 .. nb01-1 a1 (one-row K-quant products, as k_kq_rm2), the rest the int8-path product of
 // one token row with the plan of k_q8_0<1, 16, 1, 4, 2, 256> (33 to 64 blocks of 32 per row); each
 // block does what it does in its own launch, so every result is that launch's.  256 threads.
-template <bool Q3>
+// NORM: x (a0.x) is the layer's raw row h, and every block applies the attention RMSNorm (weights
+// nrm, k_rmsnorm<1024>'s order) to the values it quantizes, in place of a norm launch before.
+template <bool Q3, bool NORM>
 __global__ __launch_bounds__(256) void k_kq_rm2_q8(const KqArgs a0, const KqArgs a1, int nb0, int nb01, int N2,
                                                    int ngroups2, const uint16_t *__restrict__ wd2,
-                                                   const int8_t *__restrict__ wq2, float *__restrict__ y2)
+                                                   const int8_t *__restrict__ wq2, float *__restrict__ y2,
+                                                   const float *__restrict__ nrm, float eps)
 {
     const int b = blockIdx.x;
     if (b < nb01)
-        kq_rm_body<1, Q3>(b < nb0 ? a0 : a1, b < nb0 ? b : b - nb0);
+        kq_rm_body<1, Q3, NORM>(b < nb0 ? a0 : a1, b < nb0 ? b : b - nb0, nrm, eps);
     else
-        q8_0_body<1, 16, 1, 4, 2, 256>(1, N2, a0.K, ngroups2, wd2, wq2, a0.x, y2, b - nb01, (int)gridDim.x - nb01);
+        q8_0_body<1, 16, 1, 4, 2, 256, NORM>(1, N2, a0.K, ngroups2, wd2, wq2, a0.x, y2, b - nb01,
+                                              (int)gridDim.x - nb01, nrm, eps);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1141,7 +1233,7 @@ hipError_t launch_kq2(int N0, const void *w0, float *y0, int N1, const void *w1,
 // otherwise (nothing launched).
 template <bool Q3>
 hipError_t launch_kq2_q8(int N0, const void *w0, float *y0, int N1, const void *w1, float *y1, int N2, const void *w2,
-                         float *y2, int K, const float *x, hipStream_t s)
+                         float *y2, int K, const float *x, const float *nrm, float eps, hipStream_t s)
 {
     const int nsb = K / 256, nb = K / 32;
     KqPlan p0, p1;
@@ -1157,9 +1249,15 @@ hipError_t launch_kq2_q8(int N0, const void *w0, float *y0, int N1, const void *
     // one block per group (fewer groups than resident blocks)
     const size_t ngrp = (size_t)N2 * nb;
     const int ngroups = (N2 + 15) / 16;
-    const size_t lds = max((size_t)(nsb + 1) * KREC, ((size_t)nb + 1) * 40);
-    hipLaunchKernelGGL(k_kq_rm2_q8<Q3>, dim3(nb0 + nb1 + ngroups), dim3(256), lds, s, a0, a1, nb0, nb0 + nb1, N2,
-                       ngroups, (const uint16_t *)w2, (const int8_t *)w2 + align256(ngrp * 2), y2);
+    const size_t lds = max(max((size_t)(nsb + 1) * KREC, ((size_t)nb + 1) * 40), (size_t)4096 + 16 * 4);
+    const uint16_t *wd = (const uint16_t *)w2;
+    const int8_t *wq = (const int8_t *)w2 + align256(ngrp * 2);
+    if (nrm)
+        hipLaunchKernelGGL((k_kq_rm2_q8<Q3, true>), dim3(nb0 + nb1 + ngroups), dim3(256), lds, s, a0, a1, nb0,
+                           nb0 + nb1, N2, ngroups, wd, wq, y2, nrm, eps);
+    else
+        hipLaunchKernelGGL((k_kq_rm2_q8<Q3, false>), dim3(nb0 + nb1 + ngroups), dim3(256), lds, s, a0, a1, nb0,
+                           nb0 + nb1, N2, ngroups, wd, wq, y2, nrm, eps);
     return hipGetLastError();
 }
 
@@ -1196,12 +1294,13 @@ hipError_t x100_qgemv2_launch(int qtype, int N0, const void *w0, float *y0, int 
 }
 
 hipError_t x100_qgemv3_launch(int qtype, int N0, const void *w0, float *y0, int N1, const void *w1, float *y1,
-                              int qtype2, int N2, const void *w2, float *y2, int K, const float *x, hipStream_t s)
+                              int qtype2, int N2, const void *w2, float *y2, int K, const float *x, const float *nrm,
+                              float eps, hipStream_t s)
 {
     if (N0 < 1 || N1 < 1 || !(qtype2 == X100_Q8_0 || qtype2 == X100_Q5_K || qtype2 == X100_Q6_K))
         return hipErrorNotSupported;
-    if (qtype == X100_Q4_K) return launch_kq2_q8<false>(N0, w0, y0, N1, w1, y1, N2, w2, y2, K, x, s);
-    if (qtype == X100_Q3_K) return launch_kq2_q8<true>(N0, w0, y0, N1, w1, y1, N2, w2, y2, K, x, s);
+    if (qtype == X100_Q4_K) return launch_kq2_q8<false>(N0, w0, y0, N1, w1, y1, N2, w2, y2, K, x, nrm, eps, s);
+    if (qtype == X100_Q3_K) return launch_kq2_q8<true>(N0, w0, y0, N1, w1, y1, N2, w2, y2, K, x, nrm, eps, s);
     return hipErrorNotSupported;
 }
 

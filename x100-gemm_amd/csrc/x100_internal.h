@@ -33,8 +33,11 @@ hipError_t x100_qgemv2_launch(int qtype, int N0, const void *w0, float *y0, int 
                               const float *x, hipStream_t s);
 // The same two plus a third one-row GEMV on the int8 path (qtype2: Q8_0, Q5_K or Q6_K, packed
 // w2: N2 x K) in one launch; hipErrorNotSupported (nothing launched) outside the shapes it has.
+// With nrm, x is a raw row and the products take RMSNorm(x) with weights nrm and eps (the
+// operations of the norm launch it replaces, bit for bit).
 hipError_t x100_qgemv3_launch(int qtype, int N0, const void *w0, float *y0, int N1, const void *w1, float *y1,
-                              int qtype2, int N2, const void *w2, float *y2, int K, const float *x, hipStream_t s);
+                              int qtype2, int N2, const void *w2, float *y2, int K, const float *x, const float *nrm,
+                              float eps, hipStream_t s);
 // True when x100_qgemv_launch accepts the shape (it then launches without further checks).
 bool x100_qgemv_supported(int qtype, int M, int N, int K);
 hipError_t x100_check_quant_div_launch(uint32_t lo, uint32_t hi, unsigned long long *cnt, hipStream_t s);
