@@ -157,6 +157,29 @@ def test_decode_layer_qwen3_30b_a3b(dev):
         close(gl.vc.cpu().numpy()[:, pos], rv[:, pos], "v row")
 
 
+@pytest.mark.parametrize("types,n_exp,n_act,ff", [
+    ((synth.Q4_K, synth.Q4_K, synth.Q4_K, synth.Q4_0), 33, 3, 512),   # odd expert count: a block holds a
+    ((synth.Q3_K, synth.Q8_0, synth.Q3_K, synth.Q5_K), 9, 8, 256),     # router and a quantizer wave
+    ((synth.Q4_0, synth.Q8_0, synth.Q4_0, synth.Q4_K), 64, 1, 1024),
+])
+def test_decode_layer_d2048_moe_variants(dev, types, n_exp, n_act, ff):
+    """Whole layers at d = 2048 (where the step before the MoE block, h += o and its RMSNorm, runs
+    inside the MoE router kernel) with other expert counts, slot counts, ff and weight types."""
+    cfg = make_cfg(types, d=2048, n_head=16, n_head_kv=4, ff=ff, n_exp=n_exp, n_act=n_act, ctx=256)
+    L = synth.decode_layer_weights(2048, 16, 4, 128, ff, n_exp, types, seed=170 + n_exp)
+    gl = GpuLayer(cfg, L, types, dev)
+    for pos in (0, 255):
+        kc, vc = caches(cfg, pos, 700 + pos + n_exp)
+        h = synth.normal_f32(710 + pos + n_exp, (cfg.d,)) * np.float32(1 + pos % 7)
+        gl.set_cache(kc, vc)
+        got, gsel, gsw = gl.run(pos, h, whole=True)
+        rh, rk, rv = h.copy(), kc.copy(), vc.copy()
+        rsel, rsw = ol.decode_layer(cfg, L, rk, rv, pos, rh)
+        assert np.array_equal(gsel, rsel)
+        close(gsw, rsw, "router weights pos %d" % pos)
+        close(got, rh, "layer pos %d" % pos)
+
+
 def test_decode_rejects_bad_configs(dev):
     cfg = make_cfg()
     L = synth.decode_layer_weights(512, 4, 2, 128, 256, 8, TYPES, seed=150)

@@ -296,7 +296,7 @@ size_t x100_attn_workspace_bytes(const x100_layer_cfg *c)
 }
 
 hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h,
-                            float *ws, float **hn_out, hipStream_t s)
+                            float *ws, float **hn_out, hipStream_t s, float **o_out)
 {
     const int d = c->d, nh = c->n_head, nkv = c->n_head_kv, gpr = nh / nkv, qd = nh * HD, kvd = nkv * HD;
     float *hn = ws, *q = hn + seg(d), *k = q + seg(qd), *v = k + seg(kvd), *att = v + seg(kvd),
@@ -340,6 +340,10 @@ hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w
 #undef X100_ATTN
     hipLaunchKernelGGL(k_attn_combine, dim3(nh), dim3(HD), 0, s, part, nch, att);
     if ((e = x100_qgemv_launch(c->wo_type, 1, d, qd, w->wo, att, o, s)) != hipSuccess) return e;
+    if (o_out) {   // the caller's MoE launch adds o and forms the norm itself
+        *o_out = o;
+        return hipGetLastError();
+    }
     // h += o, and hn = rmsnorm(h, ffn_norm) for the MoE block that follows (skipped without ffn_norm)
     hipLaunchKernelGGL(k_rmsnorm<1024>, dim3(1), dim3(1024), 0, s, h, (const float *)o, w->ffn_norm, c->eps, d, hn);
     if (hn_out) *hn_out = hn;

@@ -702,14 +702,28 @@ static int attn_decode(const x100_layer_cfg *c, const x100_layer_weights *w, int
     return attn_half(c, &w2, pos, h, nullptr, ws, stream);
 }
 
+// A layer: the attention half, then the MoE block on rmsnorm(h, ffn_norm) with the residual add.
+// Where x100_moe_norm_launch takes the shape (d = 2048), h += o and the norm run inside its router
+// kernel instead of a launch of their own (same bits).
 static int decode_layer(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, int *sel, float *sw,
                         void *ws, void *stream)
 {
+    void *mws = (uint8_t *)ws + attn_ws_bytes(c);
+    if (w->ffn_norm && x100_moe_norm_supported(c->d, c->ff, c->n_exp, c->n_act, X100_MOE_RESIDUAL)) {
+        float *o = nullptr;
+        hipError_t e = x100_attn_launch(c, w, pos, h, (float *)ws, nullptr, (hipStream_t)stream, &o);
+        if (e == hipSuccess)
+            e = x100_moe_norm_launch(c->d, c->ff, c->n_exp, c->n_act, h, o, w->ffn_norm, c->eps, w->router, w->wg,
+                                     w->wu, w->wd, X100_MOE_RESIDUAL, sel, sw, mws, (hipStream_t)stream);
+        if (e == hipErrorInvalidValue) return X100_EINVAL;
+        if (e != hipSuccess) return hip_fail(e);
+        return X100_OK;
+    }
     float *hn = nullptr;
     int rc = attn_half(c, w, pos, h, &hn, ws, stream);
     if (rc) return rc;
-    return moe_run(1, c->d, c->ff, c->n_exp, c->n_act, hn, w->router, w->wg, w->wu, w->wd, h, 1, sel, sw,
-                   (uint8_t *)ws + attn_ws_bytes(c), stream);
+    return moe_run(1, c->d, c->ff, c->n_exp, c->n_act, hn, w->router, w->wg, w->wu, w->wd, h, X100_MOE_RESIDUAL, sel,
+                   sw, mws, stream);
 }
 
 int x100_attn_decode_hip_ws(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, void *ws,

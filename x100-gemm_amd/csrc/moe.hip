@@ -6,7 +6,9 @@
 // Up to 8 rows, three or four launches on one stream; each kernel only reads what an earlier launch
 // wrote, so no block ever waits for, or signals, another block (no fences, no atomics):
 //   k_moe_route       router logits R.hn (one wave per expert and token row) and the Q8_K form of
-//                     every hn row.
+//                     every hn row.  In a decoder layer at d = 2048, k_moe_route_norm instead: the row
+//                     hn = rmsnorm(h + o) formed in every block first, and the residual add of o
+//                     left to the combine.
 //   k_moe_gate_up_p   persistent blocks over the work items (union slot, GU_ROWS rows of ff).  Every
 //                     block derives the routing of all rows itself (cheaper than another launch;
 //                     block 0 publishes it), then streams the items' rows of the expert's gate and
@@ -211,6 +213,110 @@ __global__ __launch_bounds__(64 * RT_WPB) void k_moe_route(int M, int d, int n_e
         sum = wave_sum_bfly_f(sum);
         if (lane == 0) ws.logits[m * n_exp + e] = sum;
     }
+}
+
+// ------------------------------------------------------------------------------------------------
+// A decoder layer's step before the MoE block, folded into the router (one token row, d = 2048):
+// every 128-thread block forms hn = rmsnorm(h + o, nrm) itself with the operations and order of
+// k_rmsnorm<1024> (attn.hip): virtual thread T < 1024 sums (h + o)[T]^2 and (h + o)[T + 1024]^2
+// from 0, the 64 virtual threads of a virtual wave reduce by wave_sum_bfly_f's butterfly, the 16
+// wave sums are added in order, s = 1 / sqrtf(sum / 2048 + eps) and hn = (h + o) * s * nrm.
+// Thread t holds virtual threads 8t .. 8t+7, so virtual lane 8 (t % 8) + j meets its partners
+// l^32, l^16, l^8 in threads t^4, t^2, t^1 and l^4, l^2, l^1 inside the thread.
+// ------------------------------------------------------------------------------------------------
+X100_DEV void rms_row_2048_128(const float *__restrict__ h, const float *__restrict__ o,
+                               const float *__restrict__ nrm, float eps, float *s_hn, float *red)
+{
+    const int t = threadIdx.x;
+    float a[8], b[8];
+    float4 g[4];   // the norm weights of the thread's elements, loaded with h and o
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        g[k] = *(const float4 *)(nrm + 8 * t + 4 * k);
+        g[2 + k] = *(const float4 *)(nrm + 1024 + 8 * t + 4 * k);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const float4 ha = *(const float4 *)(h + 8 * t + 4 * k), oa = *(const float4 *)(o + 8 * t + 4 * k);
+        const float4 hb = *(const float4 *)(h + 1024 + 8 * t + 4 * k);
+        const float4 ob = *(const float4 *)(o + 1024 + 8 * t + 4 * k);
+        a[4 * k] = ha.x + oa.x; a[4 * k + 1] = ha.y + oa.y; a[4 * k + 2] = ha.z + oa.z; a[4 * k + 3] = ha.w + oa.w;
+        b[4 * k] = hb.x + ob.x; b[4 * k + 1] = hb.y + ob.y; b[4 * k + 2] = hb.z + ob.z; b[4 * k + 3] = hb.w + ob.w;
+    }
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        v[j] = 0.0f + a[j] * a[j];
+        v[j] += b[j] * b[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] += __shfl_xor(v[j], 4, 64);   // virtual l^32: thread t^4
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] += dpp_f<0x4E>(0.0f, v[j]);   // virtual l^16: t^2
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] += dpp_f<0xB1>(0.0f, v[j]);   // virtual l^8: t^1
+    const float w0 = v[0] + v[4], w1 = v[1] + v[5], w2 = v[2] + v[6], w3 = v[3] + v[7];   // l^4
+    const float x0 = w0 + w2, x1 = w1 + w3;                                                 // l^2
+    if ((t & 7) == 0) red[t >> 3] = x0 + x1;                                               // l^1
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) tot += red[k];
+    const float sc = 1.0f / sqrtf(tot / 2048.0f + eps);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const float4 ga = g[k], gb = g[2 + k];
+        *(float4 *)(s_hn + 8 * t + 4 * k) = make_float4(a[4 * k] * sc * ga.x, a[4 * k + 1] * sc * ga.y,
+                                                        a[4 * k + 2] * sc * ga.z, a[4 * k + 3] * sc * ga.w);
+        *(float4 *)(s_hn + 1024 + 8 * t + 4 * k) = make_float4(b[4 * k] * sc * gb.x, b[4 * k + 1] * sc * gb.y,
+                                                               b[4 * k + 2] * sc * gb.z, b[4 * k + 3] * sc * gb.w);
+    }
+    __syncthreads();
+}
+
+// k_moe_route for one token row with the pre-MoE step folded in: hn = rmsnorm(h + o, nrm) in every
+// block's LDS (rms_row_2048_128), then wave g < n_exp computes expert g's logit and the waves past
+// them quantize the row's Q8_K records, with k_moe_route's operations.  d = 2048, blocks of 2 waves.
+__global__ __launch_bounds__(64 * RT_WPB) void k_moe_route_norm(int n_exp, const float *__restrict__ h,
+                                                                const float *__restrict__ o,
+                                                                const float *__restrict__ nrm, float eps,
+                                                                const float *__restrict__ R, MoeWs ws)
+{
+    static_assert(RT_WPB == 2, "rms_row_2048_128 takes 128 threads");
+    __shared__ __attribute__((aligned(16))) float s_hn[2048];
+    __shared__ float red[16];
+    constexpr int d = 2048, nsb = 8;
+    const int lane = threadIdx.x & 63, wave = blockIdx.x * RT_WPB + wave_id();
+    // the router row first: these are the kernel's critical loads (none for quantizer waves)
+    const int e = min(wave, n_exp - 1);
+    const rsrc_t rr = buf_rsrc(R + (size_t)e * d, wave < n_exp ? (uint32_t)d * 4u : 0u);
+    float4 rv[nsb];
+#pragma unroll
+    for (int j = 0; j < nsb; j++) rv[j] = buf_load_f4(rr, (uint32_t)(4 * lane + 256 * j) * 4u);
+    rms_row_2048_128(h, o, nrm, eps, s_hn, red);
+    if (wave >= n_exp) {   // quantizer waves (wave-uniform): records 4 (wave - n_exp) .. +3
+        const int qb = 4 * (wave - n_exp), q = qb + (lane >> 4);
+        if (qb < nsb) {
+            float4 v[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                v[c] = q < nsb ? *(const float4 *)(s_hn + q * 256 + 16 * (lane & 15) + 4 * c) : make_float4(0, 0, 0, 0);
+            q8k_quant(v, nsb, qb, ws.xrec);
+        }
+        return;
+    }
+    const float4 *hv4 = (const float4 *)s_hn;
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < nsb; j++) {
+        const float4 hv = hv4[lane + 64 * j];
+        sum += rv[j].x * hv.x;
+        sum += rv[j].y * hv.y;
+        sum += rv[j].z * hv.z;
+        sum += rv[j].w * hv.w;
+    }
+    sum = wave_sum_bfly_f(sum);
+    if (lane == 0) ws.logits[e] = sum;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1060,7 +1166,8 @@ X100_DEV void vm_wait_upto(int n)
 template <int UPL, bool TL>
 __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int rg, int d, int ff, int n_exp, int n_act, uint32_t mnsf,
                                                         uint32_t mdn, uint32_t mspan, const uint8_t *__restrict__ Wd, MoeWs ws,
-                                                        float *__restrict__ out, int residual)
+                                                        float *__restrict__ out, int residual,
+                                                        const float *__restrict__ oadd)
 {
     constexpr int DN = FD_DN;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1195,16 +1302,19 @@ __global__ __launch_bounds__(1024) void k_moe_down_fused(int M, int rg, int d, i
         const int m = t / DN, r = t - m * DN;
         float eo = 0.0f;
         for (int a = 0; a < n_act; a++) eo = eo + s_w[m * n_act + a] * s_y[m * n_act + a][r];
-        float *o = out + (size_t)(m0 + m) * d + r0 + r;
-        *o = residual ? *o + eo : eo;
+        const size_t i = (size_t)(m0 + m) * d + r0 + r;
+        out[i] = residual ? (oadd ? out[i] + oadd[i] : out[i]) + eo : eo;
     }
 }
 
 // ------------------------------------------------------------------------------------------------
-// out[m][j] (+)= sum_a sw[m][a] * y[m*n_act + a][j], a ascending (qwen_moe.c:310-311).
+// out[m][j] (+)= sum_a sw[m][a] * y[m*n_act + a][j], a ascending (qwen_moe.c:310-311).  With oadd
+// (the decoder layer's attention output, whose residual add a folded router left undone) the
+// residual is (out + oadd) + the sum, the order of the unfolded layer.
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_moe_combine(int M, int d, int n_act, MoeWs ws,
-                                                     float *__restrict__ out, int residual)
+                                                     float *__restrict__ out, int residual,
+                                                     const float *__restrict__ oadd)
 {
     const int t = blockIdx.x * 256 + threadIdx.x;
     if (t >= M * d) return;
@@ -1220,7 +1330,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(int M, int d, int n_act, Mo
 #pragma unroll
     for (int a = 0; a < 8; a++)
         if (a < n_act) eo = eo + wv[a] * yv[a];
-    out[t] = residual ? out[t] + eo : eo;
+    out[t] = residual ? (oadd ? out[t] + oadd[t] : out[t]) + eo : eo;
 }
 
 MoeWs carve(uintptr_t base, int M, int d, int ff, int n_exp, int n_act, size_t *total)
@@ -1290,22 +1400,30 @@ hipError_t moe_launch_mfma(int M, int d, int ff, int n_exp, int n_act, const flo
     else
         hipLaunchKernelGGL((k_moe_mfma<false, TL, 1>), dim3(Vmax, d / 128), dim3(256), (size_t)mf_half(nsf) * 8192, s, d,
                            ff, n_act, (const uint8_t *)Wd, (const uint8_t *)nullptr, ws);
-    hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
+    hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual,
+                       (const float *)nullptr);
     return hipGetLastError();
 }
 
-// Below MF_MIN_ROWS token rows: routing, gate/up (persistent), down (+ combine).
+// Below MF_MIN_ROWS token rows: routing, gate/up (persistent), down (+ combine).  With nrm (one
+// row, d = 2048), hn is the layer's h: the router forms rmsnorm(h + oadd, nrm) itself
+// (k_moe_route_norm) and the residual output is (h + oadd) + the MoE sum.
 template <bool TL>
 hipError_t moe_launch_few(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                           const void *Wg, const void *Wu, const void *Wd, float *out, int residual, int *sel,
-                          float *sw, MoeWs ws, hipStream_t s)
+                          float *sw, MoeWs ws, hipStream_t s, const float *oadd = nullptr,
+                          const float *nrm = nullptr, float eps = 0.0f)
 {
     const int nsb = d / 256, nsf = ff / 256;
     const int Umax = min(M * n_act, n_exp);
 
     const int nwaves = n_exp * M + (M * nsb + 3) / 4;   // router waves, then quantizer waves of four records
-    hipLaunchKernelGGL(k_moe_route, dim3((nwaves + RT_WPB - 1) / RT_WPB), dim3(64 * RT_WPB), (size_t)min(M, RT_WPB) * d * 4, s, M, d, n_exp,
-                       udiv16_magic((uint32_t)nsb), hn, R, ws);
+    if (nrm)
+        hipLaunchKernelGGL(k_moe_route_norm, dim3((nwaves + RT_WPB - 1) / RT_WPB), dim3(64 * RT_WPB), 0, s, n_exp,
+                           hn, oadd, nrm, eps, R, ws);
+    else
+        hipLaunchKernelGGL(k_moe_route, dim3((nwaves + RT_WPB - 1) / RT_WPB), dim3(64 * RT_WPB),
+                           (size_t)min(M, RT_WPB) * d * 4, s, M, d, n_exp, udiv16_magic((uint32_t)nsb), hn, R, ws);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
 
@@ -1349,10 +1467,10 @@ hipError_t moe_launch_few(int M, int d, int ff, int n_exp, int n_act, const floa
             const uint32_t mspan = udiv16_magic((uint32_t)(dn * nsf * 9));
             if (upl == 1)
                 hipLaunchKernelGGL((k_moe_down_fused<1, TL>), gf, bf, ldsf, s, M, rg, d, ff, n_exp, n_act, mnsf, mdn,
-                                   mspan, (const uint8_t *)Wd, ws, out, residual);
+                                   mspan, (const uint8_t *)Wd, ws, out, residual, oadd);
             else
                 hipLaunchKernelGGL((k_moe_down_fused<2, TL>), gf, bf, ldsf, s, M, rg, d, ff, n_exp, n_act, mnsf, mdn,
-                                   mspan, (const uint8_t *)Wd, ws, out, residual);
+                                   mspan, (const uint8_t *)Wd, ws, out, residual, oadd);
             return hipGetLastError();
         }
     }
@@ -1369,7 +1487,7 @@ hipError_t moe_launch_few(int M, int d, int ff, int n_exp, int n_act, const floa
     err = hipGetLastError();
     if (err != hipSuccess) return err;
 
-    hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual);
+    hipLaunchKernelGGL(k_moe_combine, dim3((M * d + 255) / 256), dim3(256), 0, s, M, d, n_act, ws, out, residual, oadd);
     return hipGetLastError();
 }
 
@@ -1396,16 +1514,35 @@ size_t x100_moe_workspace_bytes(int M, int d, int ff, int n_exp, int n_act)
     return total;
 }
 
+static bool moe_shape_ok(int M, int d, int ff, int n_exp, int n_act, int flags)
+{
+    if (M < 1 || M > X100_MOE_MAX_ROWS || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256) return false;
+    if (d % 256 || ff % 256 || d > 4096 || ff > 4096 || d % DN_ROWS || ff % GU_ROWS) return false;
+    if (flags & ~(X100_MOE_RESIDUAL | X100_MOE_TILED)) return false;
+    return 2 * GU_ROWS * (d / 256) <= 8 * 8 * GU_NWV && DN_ROWS * (ff / 256) <= 8 * 32;
+}
+
+bool x100_moe_norm_supported(int d, int ff, int n_exp, int n_act, int flags)
+{
+    return d == 2048 && (flags & X100_MOE_RESIDUAL) && moe_shape_ok(1, d, ff, n_exp, n_act, flags);
+}
+
+hipError_t x100_moe_norm_launch(int d, int ff, int n_exp, int n_act, float *h, const float *o, const float *nrm,
+                                float eps, const float *R, const void *Wg, const void *Wu, const void *Wd, int flags,
+                                int *sel, float *sw, void *workspace, hipStream_t s)
+{
+    if (!x100_moe_norm_supported(d, ff, n_exp, n_act, flags) || !o || !nrm) return hipErrorInvalidValue;
+    MoeWs ws = carve((uintptr_t)workspace, 1, d, ff, n_exp, n_act, nullptr);
+    return (flags & X100_MOE_TILED)
+               ? moe_launch_few<true>(1, d, ff, n_exp, n_act, h, R, Wg, Wu, Wd, h, 1, sel, sw, ws, s, o, nrm, eps)
+               : moe_launch_few<false>(1, d, ff, n_exp, n_act, h, R, Wg, Wu, Wd, h, 1, sel, sw, ws, s, o, nrm, eps);
+}
+
 hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,
                            const void *Wg, const void *Wu, const void *Wd, float *out, int flags,
                            int *sel, float *sw, void *workspace, hipStream_t s)
 {
-    if (M < 1 || M > X100_MOE_MAX_ROWS || n_act < 1 || n_act > 8 || n_exp < n_act || n_exp > 256)
-        return hipErrorInvalidValue;
-    if (d % 256 || ff % 256 || d > 4096 || ff > 4096 || d % DN_ROWS || ff % GU_ROWS) return hipErrorInvalidValue;
-    if (flags & ~(X100_MOE_RESIDUAL | X100_MOE_TILED)) return hipErrorInvalidValue;
-    const int nsb = d / 256, nsf = ff / 256;
-    if (2 * GU_ROWS * nsb > 8 * 8 * GU_NWV || DN_ROWS * nsf > 8 * 32) return hipErrorInvalidValue;
+    if (!moe_shape_ok(M, d, ff, n_exp, n_act, flags)) return hipErrorInvalidValue;
     MoeWs ws = carve((uintptr_t)workspace, M, d, ff, n_exp, n_act, nullptr);
     const int residual = flags & X100_MOE_RESIDUAL;
     const bool tiled = (flags & X100_MOE_TILED) != 0;

@@ -48,13 +48,21 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
                            const void *Wg, const void *Wu, const void *Wd, float *out, int flags,
                            int *sel, float *sw, void *workspace, hipStream_t s);
 hipError_t x100_moe_tile_pack(int n_exp, int rows, int K, const void *src, void *dst, hipStream_t s);
+// One token row of a decoder layer with the step before the MoE block folded in: h <- (h + o) +
+// MoE(rmsnorm(h + o, nrm)), the bits of h += o, hn = rmsnorm(h, nrm), x100_moe_launch(hn, out = h,
+// residual).  Supported (x100_moe_norm_supported) for d = 2048 with X100_MOE_RESIDUAL.
+bool x100_moe_norm_supported(int d, int ff, int n_exp, int n_act, int flags);
+hipError_t x100_moe_norm_launch(int d, int ff, int n_exp, int n_act, float *h, const float *o, const float *nrm,
+                                float eps, const float *R, const void *Wg, const void *Wu, const void *Wd, int flags,
+                                int *sel, float *sw, void *workspace, hipStream_t s);
 
 hipError_t x100_gemv_tile_launch(int int4, int M, int N, int K, const void *W, const int8_t *x, int32_t *y,
                                  hipStream_t s);
 
 // Attention half of a decoder layer (attn.hip).  ws holds x100_attn_workspace_bytes(c) bytes; with
-// w->ffn_norm set, *hn_out receives rmsnorm(h, ffn_norm) (inside ws) for the MoE block.
+// w->ffn_norm set, *hn_out receives rmsnorm(h, ffn_norm) (inside ws) for the MoE block.  With
+// o_out, h += o and the norm are left to the caller (x100_moe_norm_launch): *o_out receives o.
 size_t x100_attn_workspace_bytes(const x100_layer_cfg *c);
 hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h,
-                            float *ws, float **hn_out, hipStream_t s);
+                            float *ws, float **hn_out, hipStream_t s, float **o_out = nullptr);
 
