@@ -180,6 +180,36 @@ def test_decode_layer_d2048_moe_variants(dev, types, n_exp, n_act, ff):
         close(got, rh, "layer pos %d" % pos)
 
 
+def test_decode_layer_unaligned_h(dev):
+    """h 4 bytes past a 16-byte boundary: the layer takes the unfolded norm launches (the folded
+    norms load h as float4) and still matches the oracle bit for bit."""
+    import torch
+    types = (synth.Q3_K, synth.Q8_0, synth.Q3_K, synth.Q5_K)
+    cfg = make_cfg(types, d=2048, n_head=32, n_head_kv=4, ff=768, n_exp=128, n_act=8, ctx=64)
+    L = synth.decode_layer_weights(2048, 32, 4, 128, 768, 128, types, seed=190)
+    gl = GpuLayer(cfg, L, types, dev)
+    pos = 40
+    kc, vc = caches(cfg, pos, 800)
+    h = synth.normal_f32(801, (cfg.d,))
+    gl.set_cache(kc, vc)
+    buf = torch.zeros(cfg.d + 4, dtype=torch.float32, device=dev)
+    buf[1:cfg.d + 1] = torch.from_numpy(h).to(dev)
+    sel = torch.full((cfg.n_act,), -1, dtype=torch.int32, device=dev)
+    sw = torch.zeros((cfg.n_act,), dtype=torch.float32, device=dev)
+    assert (buf.data_ptr() + 4) % 16 == 4
+    x100hip.decode_layer(gl.gcfg, gl.w, pos, buf.data_ptr() + 4, sel.data_ptr(), sw.data_ptr(),
+                         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = buf.cpu().numpy()
+    rh, rk, rv = h.copy(), kc.copy(), vc.copy()
+    rsel, rsw = ol.decode_layer(cfg, L, rk, rv, pos, rh)
+    assert np.array_equal(sel.cpu().numpy(), rsel)
+    close(sw.cpu().numpy(), rsw, "router weights")
+    close(got[1:cfg.d + 1], rh, "layer")
+    assert got[0] == 0 and not got[cfg.d + 1:].any()
+    close(gl.kc.cpu().numpy()[:, pos], rk[:, pos], "k row")
+
+
 def test_decode_rejects_bad_configs(dev):
     cfg = make_cfg()
     L = synth.decode_layer_weights(512, 4, 2, 128, 256, 8, TYPES, seed=150)

@@ -303,10 +303,11 @@ hipError_t x100_attn_launch(const x100_layer_cfg *c, const x100_layer_weights *w
           *o = att + seg(qd), *part = o + seg(d);
     hipError_t e;
     // q, v and k in one launch when q and v share a K-quant type and k is on the int8 path (Q3_K
-    // and Q8_0 in the mixed checkpoint, d = 2048), with the attention RMSNorm of h inside it; else
+    // and Q8_0 in the mixed checkpoint, d = 2048), with the attention RMSNorm of h inside it (its
+    // 16-byte loads of h and the norm weights need both 16-byte aligned); else
     // the norm launch, then q and v in one launch when they share a weight type that has the
     // merged form, else one launch each
-    e = c->wq_type == c->wv_type && w->attn_norm
+    e = c->wq_type == c->wv_type && w->attn_norm && !(((uintptr_t)h | (uintptr_t)w->attn_norm) & 15)
             ? x100_qgemv3_launch(c->wq_type, qd, w->wq, q, kvd, w->wv, v, c->wk_type, kvd, w->wk, k, d, h,
                                  w->attn_norm, c->eps, s)
             : hipErrorNotSupported;

@@ -703,13 +703,15 @@ static int attn_decode(const x100_layer_cfg *c, const x100_layer_weights *w, int
 }
 
 // A layer: the attention half, then the MoE block on rmsnorm(h, ffn_norm) with the residual add.
-// Where x100_moe_norm_launch takes the shape (d = 2048), h += o and the norm run inside its router
-// kernel instead of a launch of their own (same bits).
+// Where x100_moe_norm_launch takes the shape (d = 2048) and h and ffn_norm are 16-byte aligned (its
+// router loads them as float4), h += o and the norm run inside its router kernel instead of a
+// launch of their own (same bits).
 static int decode_layer(const x100_layer_cfg *c, const x100_layer_weights *w, int pos, float *h, int *sel, float *sw,
                         void *ws, void *stream)
 {
     void *mws = (uint8_t *)ws + attn_ws_bytes(c);
-    if (w->ffn_norm && x100_moe_norm_supported(c->d, c->ff, c->n_exp, c->n_act, X100_MOE_RESIDUAL)) {
+    if (w->ffn_norm && !(((uintptr_t)h | (uintptr_t)w->ffn_norm) & 15) &&
+        x100_moe_norm_supported(c->d, c->ff, c->n_exp, c->n_act, X100_MOE_RESIDUAL)) {
         float *o = nullptr;
         hipError_t e = x100_attn_launch(c, w, pos, h, (float *)ws, nullptr, (hipStream_t)stream, &o);
         if (e == hipSuccess)
