@@ -1207,6 +1207,21 @@ hipError_t launch_kq(int M, int N, int K, const void *w, const float *x, float *
     return hipGetLastError();
 }
 
+// Plans of two matrices in one launch: both take the larger rows per block of the two.  kq_plan
+// sizes a matrix for a launch of its own (about 256 blocks), and every block of a shared launch
+// quantizes all of x, so the smaller matrix (the 512 rows of a v projection beside 4096 of q: 256
+// blocks of 2 rows) would add as many blocks of that fixed work as the larger one for a tenth of
+// its weights.
+inline void kq_plan_shared(int K, KqPlan &p0, KqPlan &p1)
+{
+    const int nsb = K / 256, rb = max(p0.rb, p1.rb);
+    for (KqPlan *p : {&p0, &p1}) {
+        p->rb = rb;
+        p->nw = min(8, max((2 * rb * nsb + 63) / 64, (nsb + 3) / 4));
+        p->lds = kq_lds(1, rb, nsb);
+    }
+}
+
 // y0 = W0 x and y1 = W1 x for one token row, both Q4_K or both Q3_K with K / 256 in {1, 2, 4, 8},
 // in one launch of k_kq_rm2 (hipErrorNotSupported otherwise: the caller launches them one by one).
 template <bool Q3>
@@ -1217,6 +1232,7 @@ hipError_t launch_kq2(int N0, const void *w0, float *y0, int N1, const void *w1,
     KqPlan p0, p1;
     if (K % 256 || !(nsb == 1 || nsb == 2 || nsb == 4 || nsb == 8) || !kq_plan(1, N0, K, p0) || !kq_plan(1, N1, K, p1))
         return hipErrorNotSupported;
+    kq_plan_shared(K, p0, p1);
     const KqArgs a0{1, N0, K, p0.rb, nsb, udiv16_magic((uint32_t)p0.rb), udiv16_magic((uint32_t)nsb),
                     (const uint8_t *)w0, x, y0};
     const KqArgs a1{1, N1, K, p1.rb, nsb, udiv16_magic((uint32_t)p1.rb), udiv16_magic((uint32_t)nsb),
@@ -1237,9 +1253,10 @@ hipError_t launch_kq2_q8(int N0, const void *w0, float *y0, int N1, const void *
 {
     const int nsb = K / 256, nb = K / 32;
     KqPlan p0, p1;
-    if (K != 2048 || N2 < 1 || (size_t)N2 * nb >= ((size_t)1 << 27) || !kq_plan(1, N0, K, p0) || !kq_plan(1, N1, K, p1) ||
-        max(p0.nw, p1.nw) != 4)
+    if (K != 2048 || N2 < 1 || (size_t)N2 * nb >= ((size_t)1 << 27) || !kq_plan(1, N0, K, p0) || !kq_plan(1, N1, K, p1))
         return hipErrorNotSupported;
+    kq_plan_shared(K, p0, p1);
+    if (max(p0.nw, p1.nw) != 4) return hipErrorNotSupported;
     const KqArgs a0{1, N0, K, p0.rb, nsb, udiv16_magic((uint32_t)p0.rb), udiv16_magic((uint32_t)nsb),
                     (const uint8_t *)w0, x, y0};
     const KqArgs a1{1, N1, K, p1.rb, nsb, udiv16_magic((uint32_t)p1.rb), udiv16_magic((uint32_t)nsb),
