@@ -304,7 +304,7 @@ class Ceilings:
 
 
 # ------------------------------------------------------------------------------------------------
-# CPU baseline (oracle / reference build; the checker, never the product)
+# CPU baseline (oracle / reference build: test infrastructure, timed here as a baseline only)
 # ------------------------------------------------------------------------------------------------
 def cpu_gemm_baseline(K=4096, N=4096, target_s=10.0):
     import oracle_lib as ol

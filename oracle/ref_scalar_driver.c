@@ -1,5 +1,5 @@
 /*
- * Driver for the reference's own scalar format functions (checker only, never the product).
+ * Driver for the reference's own scalar format functions (test infrastructure, never the product).
  *
  * oracle/ref_scalar.py copies the named definitions out of the reference's qwen_moe_q3k.c into a
  * temporary file REF_SCALAR_SRC and compiles this driver with it into oracle/_ref/libref_scalar.so

@@ -1,4 +1,4 @@
-"""ctypes binding of oracle/liboracle.so -- the CPU restatement used as the parity checker.
+"""ctypes binding of oracle/liboracle.so -- the CPU restatement the parity tests compare against.
 
 Test infrastructure only: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
 leg, never by the product path.

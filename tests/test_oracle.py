@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/x100_oracle.c) before it is trusted as the parity checker.
+"""Pins the CPU oracle (oracle/x100_oracle.c) before the parity tests trust it.
 
 Each oracle function is checked against something other than itself:
   gemm_ref_i8         numpy int64 matmul (closed form), the reference's own gemm_ref_i8 built from

@@ -123,8 +123,8 @@ def test_quantizer_division_free_arithmetic_is_exact(dev):
     # IEEE division.  Exhaustively on this GPU: 1/d over every positive d up to FLT_MAX / 127
     # (subnormal d included: the Q8_K quantizers have no amax floor), amax / 127 over every
     # positive amax, and the fp16 truncation over every positive float; zero mismatches against
-    # the correctly rounded quotients and the reference's conversion (the checker runs the
-    # quantizers' own device functions).
+    # the correctly rounded quotients and the reference's conversion (the check kernel runs
+    # the quantizers' own device functions).
     import torch
     fmax = 0x7f7fffff
     d_hi = _fbits(np.float32(3.4028234663852886e38 / 127.0))
