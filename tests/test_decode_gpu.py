@@ -133,8 +133,19 @@ def test_attn_decode_qwen3_shape_long_context(dev):
     cfg = make_cfg(types, d=2048, n_head=32, n_head_kv=4, ctx=4096)
     L = synth.decode_layer_weights(2048, 32, 4, 128, 256, 8, types, seed=130)
     gl = None
-    for pos in (1000, 4095):
+    # chunks of 16, 24, 32, 40 and 64 positions (2 to 8 steps of 8 positions per block)
+    for pos in (1000, 1300, 2000, 2500, 4095):
         gl = check_attn(cfg, types, L, pos, 500 + pos, dev, gl)
+
+
+def test_attn_decode_qwen3_shape_8192_positions(dev):
+    # 128 positions per chunk (16 steps of 8 positions per block)
+    types = (synth.Q3_K, synth.Q8_0, synth.Q3_K, synth.Q5_K)
+    cfg = make_cfg(types, d=2048, n_head=32, n_head_kv=4, ctx=8192)
+    L = synth.decode_layer_weights(2048, 32, 4, 128, 256, 8, types, seed=135)
+    gl = None
+    for pos in (5000, 8191):
+        gl = check_attn(cfg, types, L, pos, 900 + pos, dev, gl)
 
 
 def test_decode_layer_qwen3_30b_a3b(dev):
