@@ -1524,7 +1524,7 @@ static bool moe_shape_ok(int M, int d, int ff, int n_exp, int n_act, int flags)
 
 bool x100_moe_norm_supported(int d, int ff, int n_exp, int n_act, int flags)
 {
-    return d == 2048 && (flags & X100_MOE_RESIDUAL) && moe_shape_ok(1, d, ff, n_exp, n_act, flags);
+    return d == 2048 && flags == X100_MOE_RESIDUAL && moe_shape_ok(1, d, ff, n_exp, n_act, flags);
 }
 
 hipError_t x100_moe_norm_launch(int d, int ff, int n_exp, int n_act, float *h, const float *o, const float *nrm,
@@ -1533,9 +1533,7 @@ hipError_t x100_moe_norm_launch(int d, int ff, int n_exp, int n_act, float *h, c
 {
     if (!x100_moe_norm_supported(d, ff, n_exp, n_act, flags) || !o || !nrm) return hipErrorInvalidValue;
     MoeWs ws = carve((uintptr_t)workspace, 1, d, ff, n_exp, n_act, nullptr);
-    return (flags & X100_MOE_TILED)
-               ? moe_launch_few<true>(1, d, ff, n_exp, n_act, h, R, Wg, Wu, Wd, h, 1, sel, sw, ws, s, o, nrm, eps)
-               : moe_launch_few<false>(1, d, ff, n_exp, n_act, h, R, Wg, Wu, Wd, h, 1, sel, sw, ws, s, o, nrm, eps);
+    return moe_launch_few<false>(1, d, ff, n_exp, n_act, h, R, Wg, Wu, Wd, h, 1, sel, sw, ws, s, o, nrm, eps);
 }
 
 hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const float *hn, const float *R,

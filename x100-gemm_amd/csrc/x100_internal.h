@@ -50,7 +50,8 @@ hipError_t x100_moe_launch(int M, int d, int ff, int n_exp, int n_act, const flo
 hipError_t x100_moe_tile_pack(int n_exp, int rows, int K, const void *src, void *dst, hipStream_t s);
 // One token row of a decoder layer with the step before the MoE block folded in: h <- (h + o) +
 // MoE(rmsnorm(h + o, nrm)), the bits of h += o, hn = rmsnorm(h, nrm), x100_moe_launch(hn, out = h,
-// residual).  Supported (x100_moe_norm_supported) for d = 2048 with X100_MOE_RESIDUAL.
+// residual).  Supported (x100_moe_norm_supported) for d = 2048, flags X100_MOE_RESIDUAL (ggml-layout
+// experts, as the decoder layer keeps them).
 bool x100_moe_norm_supported(int d, int ff, int n_exp, int n_act, int flags);
 hipError_t x100_moe_norm_launch(int d, int ff, int n_exp, int n_act, float *h, const float *o, const float *nrm,
                                 float eps, const float *R, const void *Wg, const void *Wu, const void *Wd, int flags,
